@@ -1,0 +1,189 @@
+"""GRPO logprob + loss fwd+bwd benchmark on one MI355X.
+
+A step is one pass of the GRPO loss head over one batch held in HBM: group
+advantages from rewards, per-sequence lengths, the fused per-row kernel (policy +
+reference log-softmax, token gather, clipped-ratio + k3-KL loss, dlogits =
+c*(onehot - softmax) written in bf16, zero rows for masked tokens) and the
+deterministic loss reduction. Default workload: configuration 2 (Qwen2.5-0.5B
+vocabulary, 64 sequences x 512 tokens, V=151936, bf16).
+
+Prints one JSON line. value = valid (mask=1) tokens per second over the whole
+step. roofline: algorithmic bytes of the fused row kernel per launch divided by
+its mean duration, timed with HIP events recorded by the library on the launch
+stream. cpu_baseline: the CPU oracle (fp32, reference op order, OpenMP) on a
+bounded sample of the same rows.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+
+
+def algorithmic_bytes(cfg, lengths, mode_clip_kl: bool, zero_fill: bool = True) -> dict:
+    """Bytes the fused row kernel must move: per live row one read of the policy row,
+    one of the reference row (clip-KL mode) and one write of dlogits; per masked row
+    the zero-fill write; per row 28 B of token scalars (id 8, mask 4, old logp 4,
+    logp 4, ref logp 4, token loss 4)."""
+    import numpy as np
+
+    s_in = 2 if cfg.dtype == "bf16" else 4
+    s_out = s_in
+    V = cfg.V
+    live = int(np.minimum(lengths, cfg.T).sum())
+    rows = cfg.S * cfg.T
+    dead = rows - live
+    per_live = (2 if mode_clip_kl else 1) * V * s_in + V * s_out
+    per_dead = V * s_out if zero_fill else 0
+    total = live * per_live + dead * per_dead + rows * 28
+    return {"live_rows": live, "rows": rows, "per_live": per_live, "per_dead": per_dead, "bytes": total}
+
+
+def cpu_baseline(inp, cfg, mode_clip_kl: bool, budget_s: float = 12.0, chunk: int = 256) -> dict:
+    """Time the CPU oracle (fp32 reference op order, all threads) on consecutive row
+    chunks of the same inputs until about budget_s of compute has been spent."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as orc
+
+    threads = min(os.cpu_count() or 1, 16)
+    V, T = cfg.V, cfg.T
+    flat = inp["logits"].view(-1, V)
+    rflat = inp["ref_logits"].view(-1, V)
+    ids = inp["ids"].view(-1).cpu().numpy()
+    mask = inp["mask"].cpu().numpy()
+    w = mask.reshape(-1)
+    adv = orc.advantages(inp["rewards"].cpu().numpy(), cfg.group)
+    Ls = orc.seq_lengths(mask, T, 0)
+    old = inp["old_logp"].view(-1).cpu().numpy()
+    nrows = flat.shape[0]
+    # Visit rows in a fixed pseudo-random order so the sample has the workload's live fraction.
+    order = np.random.default_rng(0).permutation(nrows)
+    spent, done, live_done = 0.0, 0, 0
+    while spent < budget_s and done < nrows:
+        idx = np.sort(order[done:done + chunk])
+        ti = torch.as_tensor(idx, device=flat.device)
+        L = flat.index_select(0, ti)
+        R = rflat.index_select(0, ti)
+        if L.dtype == torch.bfloat16:
+            L = L.view(torch.int16).cpu().numpy().view(np.uint16)
+            R = R.view(torch.int16).cpu().numpy().view(np.uint16)
+            dt = orc.BF16
+        else:
+            L, R, dt = L.cpu().numpy(), R.cpu().numpy(), orc.F32
+        seq = idx // T
+        t0 = time.perf_counter()
+        orc.grpo_rows(L, ids[idx], w[idx], adv[seq], Ls[seq], float(cfg.S), ref_logits=R if mode_clip_kl else None,
+                      old_logp=old[idx], loss_mode=orc.CLIP_KL if mode_clip_kl else orc.REINFORCE,
+                      clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, precision=orc.REF_F32, dtype=dt,
+                      nthreads=threads)
+        spent += time.perf_counter() - t0
+        done += len(idx)
+        live_done += int((w[idx] != 0).sum())
+    return {"value": live_done / spent, "unit": "valid tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of {nrows} rows ({live_done} valid) in {spent:.1f} s: oracle fp32 reference-op-order "
+                      f"fwd+bwd (grpo_oracle.cpp, OpenMP {threads} threads)"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
+    ap.add_argument("--force-streaming", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the GRPO loss head shards by whole "
+                                   "sequence groups, but no multi-GPU path is built; use --gpus 1"}))
+        sys.exit(2)
+
+    import ctypes
+
+    import torch
+
+    from pcp_amd import grpo, synth
+    from pcp_amd._lib import LossMode, check, lib
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    cfg = synth.CONFIGS[args.config]
+    clip = args.mode == "clip_kl"
+    mode = LossMode.GRPO_CLIP_KL if clip else LossMode.REINFORCE
+    t_setup = time.perf_counter()
+    inp = synth.make_device_inputs(cfg, dev)
+    torch.cuda.synchronize()
+    t_setup = time.perf_counter() - t_setup
+    ctx = grpo.default_context(0)
+    kw = dict(rewards=inp["rewards"], group_size=cfg.group, ref_logits=inp["ref_logits"] if clip else None,
+              old_logp=inp["old_logp"], loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta,
+              force_streaming=args.force_streaming, ctx=ctx)
+    out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], **kw)  # allocates outputs
+    for _ in range(args.warmup):
+        grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], outputs=out, sync=False, **kw)
+    ctx.sync()
+    torch.cuda.synchronize()
+
+    check(lib().pcp_profile_start(ctx.handle, args.steps), ctx.handle)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], outputs=out, sync=False, **kw)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx.sync()
+    n_l = ctypes.c_int(0)
+    tot = ctypes.c_double(0)
+    check(lib().pcp_profile_stop(ctx.handle, ctypes.byref(n_l), ctypes.byref(tot)), ctx.handle)
+    kernel_ms = tot.value / max(n_l.value, 1)
+
+    ab = algorithmic_bytes(cfg, inp["lengths"], clip)
+    ms_step = elapsed * 1e3 / args.steps
+    value = ab["live_rows"] / (ms_step / 1e3)
+    achieved = ab["bytes"] / (kernel_ms / 1e3) / 1e9
+    line = {
+        "metric": "GRPO logprob+loss fwd+bwd tokens/s and achieved HBM GB/s, V=151936 bf16",
+        "value": value,
+        "unit": "valid tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg.dtype,
+        "data": "synthetic (seeded Philox/PCG64 inputs of the configuration)",
+        "config": {"workload": f"config{cfg.key} {cfg.name}: {cfg.prompts} prompts x G={cfg.group}, T={cfg.T}, "
+                               f"V={cfg.V}, {cfg.dtype} logits, loss={args.mode}",
+                   "rows": ab["rows"], "valid_rows": ab["live_rows"], "global_batch": cfg.S, "seq_len": cfg.T},
+        "step_gbs": ab["bytes"] / (ms_step / 1e3) / 1e9,
+        "rows_per_s": ab["rows"] / (ms_step / 1e3),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "grpo_resident_kernel" if not args.force_streaming else "grpo_stream_kernel",
+                     "kernel_ms": kernel_ms, "algorithmic_bytes": ab["bytes"]},
+        "setup_s": t_setup,
+    }
+    tfile = os.path.join(ROOT, "profiles", f"traffic_config{cfg.key}_{args.mode}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(inp, cfg, clip, budget_s=args.cpu_budget)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,237 @@
+"""TEST INFRASTRUCTURE — Python face of the CPU oracle (oracle/libpcp_oracle.so).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only as the checker (or the timed CPU baseline); the product
+path (pcp_amd) never does.
+
+What each function restates (reference file:line):
+  advantages   src/nodes/controllers/rl_shepherd.zig:462-479 (bit-exact f32)
+  logprob      tools/export_qwen_forward.py:154-156, models/tests/qwen_test.mlir:257-277
+  grpo_rows    export_qwen_forward.py:156-163 (REINFORCE), its autodiff backward
+               (src/compiler/graph_builder.zig:302-426, src/autodiff/vjp_rules.zig rules
+               cited in grpo_oracle.cpp) and the clipped-ratio + k3-KL loss
+  grpo_full    the whole loss head over [S, T, V] with the kernels' row layout
+               (seq lengths = clamp(mask.sum(1), min=1), export_qwen_forward.py:160)
+
+Pinning: every function is checked in tests/test_oracle.py against the reference's
+known-answer tests (src/examples/isolated_vjp_tests.zig), closed forms, brute force
+in float64, finite differences and torch CPU autograd.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libpcp_oracle.so")
+
+F16, BF16, F32 = 0, 1, 2
+EXACT, REF_F32, FAITHFUL = 0, 1, 2
+REINFORCE, CLIP_KL = 0, 1
+IGNORE_INDEX = -100
+
+
+class _RowsArgs(ctypes.Structure):
+    _fields_ = [
+        ("nrows", ctypes.c_int64), ("vocab", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("logits", ctypes.c_void_p), ("ref_logits", ctypes.c_void_p),
+        ("ids", ctypes.c_void_p), ("w", ctypes.c_void_p), ("adv", ctypes.c_void_p),
+        ("seq_len", ctypes.c_void_p), ("old_logp", ctypes.c_void_p),
+        ("loss_norm", ctypes.c_float), ("loss_mode", ctypes.c_int32),
+        ("clip_eps", ctypes.c_float), ("kl_beta", ctypes.c_float),
+        ("precision", ctypes.c_int32), ("nthreads", ctypes.c_int32),
+        ("lp", ctypes.c_void_p), ("lr", ctypes.c_void_p), ("token_loss", ctypes.c_void_p),
+        ("coef", ctypes.c_void_p), ("dlogits", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(_LIB_PATH)
+        L.oracle_f32_to_bf16_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.oracle_advantages.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float,
+                                        ctypes.c_void_p]
+        L.oracle_logprob.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+                                     ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                     ctypes.c_void_p]
+        L.oracle_grpo_rows.argtypes = [ctypes.POINTER(_RowsArgs)]
+        L.oracle_grpo_rows.restype = ctypes.c_int
+        L.oracle_max_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray | None) -> int | None:
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ---- element codecs --------------------------------------------------------
+
+def bf16_from_f32(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even f32 -> bf16 bit patterns (uint16)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_bf16_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    """Exact widening of bf16 bit patterns to f32."""
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def widen(x: np.ndarray, dtype: int) -> np.ndarray:
+    """Logits array in its storage form (uint16 for bf16, float16, float32) -> float64."""
+    if dtype == BF16:
+        return bf16_to_f32(x).astype(np.float64)
+    return np.asarray(x).astype(np.float64)
+
+
+def storage_dtype_code(x: np.ndarray, bf16: bool = False) -> int:
+    if bf16 or x.dtype == np.uint16:
+        return BF16
+    if x.dtype == np.float16:
+        return F16
+    if x.dtype == np.float32:
+        return F32
+    raise TypeError(f"unsupported logits storage {x.dtype}")
+
+
+# ---- a3: advantages ---------------------------------------------------------
+
+def advantages(rewards: np.ndarray, group_size: int, eps: float = 1e-8) -> np.ndarray:
+    r = np.ascontiguousarray(rewards, dtype=np.float32)
+    out = np.empty_like(r)
+    lib().oracle_advantages(_ptr(r), r.size, int(group_size), ctypes.c_float(eps), _ptr(out))
+    return out
+
+
+# ---- a1: log-prob gather ------------------------------------------------------
+
+def logprob(logits: np.ndarray, ids: np.ndarray, dtype: int | None = None, precision: int = EXACT,
+            nthreads: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """logits [N, V] in storage form; ids [N]. Returns (lp, lse) in float64."""
+    x = np.ascontiguousarray(logits)
+    dt = storage_dtype_code(x) if dtype is None else dtype
+    N, V = x.shape
+    ids64 = np.ascontiguousarray(ids, dtype=np.int64)
+    lp = np.empty(N, np.float64)
+    lse = np.empty(N, np.float64)
+    lib().oracle_logprob(_ptr(x), dt, N, V, _ptr(ids64), precision, nthreads, _ptr(lp), _ptr(lse))
+    return lp, lse
+
+
+# ---- a2+a4+a5: rows ---------------------------------------------------------------
+
+@dataclass
+class RowsResult:
+    lp: np.ndarray
+    lr: np.ndarray
+    token_loss: np.ndarray
+    coef: np.ndarray
+    dlogits: np.ndarray | None
+
+
+def grpo_rows(logits: np.ndarray, ids: np.ndarray, w: np.ndarray, adv: np.ndarray, seq_len: np.ndarray,
+              loss_norm: float, *, ref_logits: np.ndarray | None = None, old_logp: np.ndarray | None = None,
+              loss_mode: int = REINFORCE, clip_eps: float = 0.2, kl_beta: float = 0.04,
+              precision: int = EXACT, want_dlogits: bool = True, dtype: int | None = None,
+              nthreads: int = 0) -> RowsResult:
+    """Loss terms of independent rows. Per-row metadata: ids, mask weight w, the
+    advantage and clamped length of the row's sequence, old log-prob."""
+    x = np.ascontiguousarray(logits)
+    dt = storage_dtype_code(x) if dtype is None else dtype
+    N, V = x.shape
+    ref = None if ref_logits is None else np.ascontiguousarray(ref_logits)
+    ids64 = np.ascontiguousarray(ids, dtype=np.int64).reshape(N)
+    wf = np.ascontiguousarray(w, dtype=np.float32).reshape(N)
+    af = np.ascontiguousarray(adv, dtype=np.float32).reshape(N)
+    lf = np.ascontiguousarray(seq_len, dtype=np.float32).reshape(N)
+    of = None if old_logp is None else np.ascontiguousarray(old_logp, dtype=np.float32).reshape(N)
+    res = RowsResult(np.empty(N), np.empty(N), np.empty(N), np.empty(N),
+                     np.empty((N, V), np.float32) if want_dlogits else None)
+    a = _RowsArgs(N, V, dt, _ptr(x), _ptr(ref), _ptr(ids64), _ptr(wf), _ptr(af), _ptr(lf), _ptr(of),
+                  float(loss_norm), loss_mode, clip_eps, kl_beta, precision, nthreads,
+                  _ptr(res.lp), _ptr(res.lr), _ptr(res.token_loss), _ptr(res.coef), _ptr(res.dlogits))
+    rc = lib().oracle_grpo_rows(ctypes.byref(a))
+    if rc != 0:
+        raise ValueError("oracle_grpo_rows rejected its arguments")
+    return res
+
+
+# ---- full problem -------------------------------------------------------------------
+
+@dataclass
+class FullResult:
+    loss: float
+    lp: np.ndarray          # [S, TS] indexed like ids (unaddressed entries 0)
+    lr: np.ndarray
+    token_loss: np.ndarray
+    coef: np.ndarray
+    adv: np.ndarray         # [S] f32
+    seq_len: np.ndarray     # [S] f32
+    dlogits: np.ndarray | None  # [S, LS, V] f32
+
+
+def seq_lengths(mask: np.ndarray, rows: int, tok_offset: int) -> np.ndarray:
+    """max(sum_t mask[s, tok_offset + t], 1) over the rows that carry tokens (f32)."""
+    m = np.asarray(mask, dtype=np.float32)[:, tok_offset:tok_offset + rows]
+    return np.maximum(m.astype(np.float64).sum(axis=1), 1.0).astype(np.float32)
+
+
+def grpo_full(logits: np.ndarray, ids: np.ndarray, mask: np.ndarray | None, *, rows: int, tok_offset: int = 0,
+              advantages_in: np.ndarray | None = None, rewards: np.ndarray | None = None, group_size: int = 1,
+              ref_logits: np.ndarray | None = None, old_logp: np.ndarray | None = None,
+              loss_mode: int = REINFORCE, clip_eps: float = 0.2, kl_beta: float = 0.04,
+              loss_norm: float = 0.0, std_eps: float = 1e-8, precision: int = EXACT,
+              want_dlogits: bool = True, dtype: int | None = None, nthreads: int = 0) -> FullResult:
+    """The loss head over logits [S, LS, V] (storage form) and token arrays [S, TS]:
+    row (s, t < rows) scores ids[s, tok_offset + t]; rows >= rows are pad rows."""
+    x = np.asarray(logits)
+    S, LS, V = x.shape
+    ids = np.asarray(ids)
+    TS = ids.shape[1]
+    m = np.ones(ids.shape, np.float32) if mask is None else np.asarray(mask, dtype=np.float32)
+    if advantages_in is not None:
+        adv = np.ascontiguousarray(advantages_in, dtype=np.float32)
+    else:
+        adv = advantages(rewards, group_size, std_eps)
+    L = seq_lengths(m, rows, tok_offset)
+    G = float(loss_norm) if loss_norm > 0 else float(S)
+    sel_rows = x[:, :rows, :].reshape(S * rows, V)
+    sel_ref = None if ref_logits is None else np.asarray(ref_logits)[:, :rows, :].reshape(S * rows, V)
+    tix = slice(tok_offset, tok_offset + rows)
+    r = grpo_rows(sel_rows, ids[:, tix].reshape(-1), m[:, tix].reshape(-1),
+                  np.repeat(adv, rows), np.repeat(L, rows), G, ref_logits=sel_ref,
+                  old_logp=None if old_logp is None else np.asarray(old_logp)[:, tix].reshape(-1),
+                  loss_mode=loss_mode, clip_eps=clip_eps, kl_beta=kl_beta, precision=precision,
+                  want_dlogits=want_dlogits, dtype=dtype, nthreads=nthreads)
+
+    def place(v):
+        out = np.zeros((S, TS), np.float64)
+        out[:, tix] = v.reshape(S, rows)
+        return out
+
+    tl = r.token_loss.reshape(S, rows)
+    seq = tl.sum(axis=1) / L.astype(np.float64)
+    if loss_mode == REINFORCE:
+        seq = seq * adv.astype(np.float64)
+    loss = float(seq.sum() / G)
+    dl = None
+    if want_dlogits:
+        dl = np.zeros((S, LS, V), np.float32)
+        dl[:, :rows, :] = r.dlogits.reshape(S, rows, V)
+    return FullResult(loss, place(r.lp), place(r.lr), place(r.token_loss), place(r.coef), adv, L, dl)

@@ -1,0 +1,72 @@
+// Library context and status helpers shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "pcp_grpo.h"
+
+struct pcp_ctx {
+  int device = 0;
+  int backend = PCP_BACKEND_ROCM;
+  std::string last_error;
+  int* d_err = nullptr;          // device error word (kErr* bits)
+  void* scratch = nullptr;       // per-call work buffers, grown on demand
+  size_t scratch_bytes = 0;
+  std::set<hipStream_t> pending;  // streams holding PCP_FLAG_ASYNC work
+  // Row-kernel timing (pcp_profile_start/stop): event pairs, next free pair.
+  std::vector<hipEvent_t> prof_start, prof_stop;
+  int prof_used = 0;
+  bool prof_on = false;
+};
+
+namespace pcp {
+
+// Last failure message of the calling thread; pcp_last_error(NULL) returns it,
+// so argument errors are reported even when no context exists.
+std::string& thread_error();
+
+inline int fail(pcp_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  thread_error() = buf;
+  if (ctx) ctx->last_error = buf;
+  return code;
+}
+
+inline int hip_fail(pcp_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, PCP_ERR_DEVICE, "%s: %s (%d)", what, hipGetErrorString(e), static_cast<int>(e));
+}
+
+inline bool mul_overflows(int64_t a, int64_t b, int64_t* out) {
+  return __builtin_mul_overflow(a, b, out);
+}
+
+inline int dtype_bytes(int dt) {
+  switch (dt) {
+    case PCP_F16: return 2;
+    case PCP_BF16: return 2;
+    case PCP_F32: return 4;
+    case PCP_F64: return 8;
+    case PCP_I32: return 4;
+    case PCP_I64: return 8;
+    case PCP_BOOL: return 1;
+  }
+  return 0;
+}
+
+// Make `bytes` of scratch available on ctx (grow-only; synchronises before a free).
+int ensure_scratch(pcp_ctx* ctx, size_t bytes);
+
+// After synchronising: read and clear the device error word, map it to a status.
+int collect_device_errors(pcp_ctx* ctx);
+
+}  // namespace pcp

@@ -1,0 +1,389 @@
+// Device-pointer entry points of the C ABI: context lifetime, argument
+// validation and the launch sequence of the GRPO loss head.
+//
+// Mirrors the device-resident half of IreeBackend (src/backends/iree.zig:84,
+// :166-333): the caller owns HBM buffers; the library owns only small scratch
+// (advantages, per-sequence lengths and sums, per-token losses, error word).
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+
+#include "context.hpp"
+#include "grpo_device.hpp"
+#include "grpo_launch.hpp"
+#include "pcp_grpo.h"
+
+namespace pcp {
+
+std::string& thread_error() {
+  static thread_local std::string msg;
+  return msg;
+}
+
+int ensure_scratch(pcp_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->scratch_bytes) return PCP_OK;
+  if (ctx->scratch) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipDeviceSynchronize");
+    (void)hipFree(ctx->scratch);
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+  }
+  const size_t want = (bytes + 0xFFFFF) & ~static_cast<size_t>(0xFFFFF);
+  hipError_t e = hipMalloc(&ctx->scratch, want);
+  if (e != hipSuccess) {
+    ctx->scratch = nullptr;
+    (void)hipGetLastError();
+    return fail(ctx, PCP_ERR_OOM, "hipMalloc(%zu bytes of scratch) failed: %s", want,
+                hipGetErrorString(e));
+  }
+  ctx->scratch_bytes = want;
+  return PCP_OK;
+}
+
+int collect_device_errors(pcp_ctx* ctx) {
+  int h = 0;
+  hipError_t e = hipMemcpy(&h, ctx->d_err, sizeof(int), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(ctx, e, "reading the device error word");
+  if (h == 0) return PCP_OK;
+  const int zero = 0;
+  e = hipMemcpy(ctx->d_err, &zero, sizeof(int), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(ctx, e, "clearing the device error word");
+  if (h & kErrTokenRange)
+    return fail(ctx, PCP_ERR_TOKEN_RANGE, "a live token id is outside [0, vocab) and is not -100");
+  return fail(ctx, PCP_ERR_NONFINITE, "a live row has a non-finite log-sum-exp (NaN/Inf logits)");
+}
+
+namespace {
+
+// Resolved geometry of a request.
+struct Geo {
+  int64_t n_seq, rows, vocab, group, lstride, tstride, toff, nrows;
+  float loss_norm;
+};
+
+enum Op { kLogprob = 0, kLoss = 1 };
+
+int validate(const pcp_grpo_args* a, Op op, Geo* g) {
+  if (!a) return fail(nullptr, PCP_ERR_INVALID_ARG, "args is NULL");
+  if (a->n_seq < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "n_seq must be >= 1 (got %lld)", (long long)a->n_seq);
+  if (a->rows < 0) return fail(nullptr, PCP_ERR_INVALID_ARG, "rows must be >= 0");
+  if (a->vocab < 1 || a->vocab > INT32_MAX)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab must be in [1, 2^31) (got %lld)", (long long)a->vocab);
+  if (a->group_size < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "group_size must be >= 1");
+  g->n_seq = a->n_seq;
+  g->rows = a->rows;
+  g->vocab = a->vocab;
+  g->group = a->group_size;
+  g->lstride = a->logit_seq_stride ? a->logit_seq_stride : a->rows;
+  g->tstride = a->tok_seq_stride ? a->tok_seq_stride : a->rows;
+  g->toff = a->tok_offset;
+  if (g->lstride < g->rows || g->lstride < 1)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "logit_seq_stride (%lld) must be >= max(rows, 1)", (long long)g->lstride);
+  if (g->toff < 0 || g->toff + g->rows > g->tstride)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "tok_offset + rows must fit in tok_seq_stride");
+  int64_t tmp;
+  if (mul_overflows(g->n_seq, g->lstride, &g->nrows) || g->nrows > INT32_MAX)
+    return fail(nullptr, PCP_ERR_OVERFLOW, "n_seq * logit_seq_stride exceeds 2^31-1 rows");
+  if (mul_overflows(g->nrows, g->vocab, &tmp) || mul_overflows(tmp, 4, &tmp))
+    return fail(nullptr, PCP_ERR_OVERFLOW, "logits byte size overflows int64");
+  if (mul_overflows(g->n_seq, g->tstride, &tmp))
+    return fail(nullptr, PCP_ERR_OVERFLOW, "token array size overflows int64");
+  if (a->logits_dtype != PCP_BF16 && a->logits_dtype != PCP_F16 && a->logits_dtype != PCP_F32)
+    return fail(nullptr, PCP_ERR_DTYPE, "logits dtype must be bf16, f16 or f32 (got %d)", a->logits_dtype);
+  if (a->ids_dtype != PCP_I64 && a->ids_dtype != PCP_I32)
+    return fail(nullptr, PCP_ERR_DTYPE, "ids dtype must be i64 or i32 (got %d)", a->ids_dtype);
+  if (a->mask && a->mask_dtype != PCP_F32 && a->mask_dtype != PCP_BOOL)
+    return fail(nullptr, PCP_ERR_DTYPE, "mask dtype must be f32 or bool (got %d)", a->mask_dtype);
+  if (!a->logits) return fail(nullptr, PCP_ERR_INVALID_ARG, "logits is NULL");
+  if (!a->ids && g->rows > 0) return fail(nullptr, PCP_ERR_INVALID_ARG, "ids is NULL");
+  if (op == kLoss) {
+    if (a->dlogits) {
+      if (a->dlogits_dtype != a->logits_dtype && a->dlogits_dtype != PCP_F32)
+        return fail(nullptr, PCP_ERR_DTYPE, "dlogits dtype must equal the logits dtype or be f32");
+    }
+    if (a->loss_mode != PCP_LOSS_REINFORCE && a->loss_mode != PCP_LOSS_GRPO_CLIP_KL)
+      return fail(nullptr, PCP_ERR_INVALID_ARG, "unknown loss_mode %d", a->loss_mode);
+    if (a->loss_mode == PCP_LOSS_GRPO_CLIP_KL && !a->ref_logits)
+      return fail(nullptr, PCP_ERR_INVALID_ARG, "GRPO_CLIP_KL needs ref_logits");
+    if (!a->advantages && !a->rewards)
+      return fail(nullptr, PCP_ERR_INVALID_ARG, "advantages and rewards are both NULL");
+    if (!(a->clip_eps >= 0.f && a->clip_eps < 1.f))
+      return fail(nullptr, PCP_ERR_INVALID_ARG, "clip_eps must be in [0, 1)");
+    if (!(a->loss_norm >= 0.f)) return fail(nullptr, PCP_ERR_INVALID_ARG, "loss_norm must be >= 0");
+  }
+  g->loss_norm = a->loss_norm > 0.f ? a->loss_norm : static_cast<float>(g->n_seq);
+  return PCP_OK;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline size_t round256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+int finish(pcp_ctx* ctx, const pcp_grpo_args* a, hipStream_t st) {
+  if (a->flags & PCP_FLAG_ASYNC) {
+    ctx->pending.insert(st);
+    return PCP_OK;
+  }
+  hipError_t e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+  return collect_device_errors(ctx);
+}
+
+int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op) {
+  Geo g;
+  int rc = validate(a, op, &g);
+  if (rc != PCP_OK) {
+    if (ctx) ctx->last_error = thread_error();
+    return rc;
+  }
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  hipStream_t st = static_cast<hipStream_t>(a->stream);
+
+  // Scratch: adv | seq_len | seq_scale | seq_val | loss | token_loss.
+  const size_t sv = round256(sizeof(float) * g.n_seq);
+  const bool need_tl = (op == kLoss) && a->token_loss == nullptr;
+  const size_t tl_bytes = need_tl ? round256(sizeof(float) * g.n_seq * g.tstride) : 0;
+  rc = ensure_scratch(ctx, 4 * sv + 256 + tl_bytes);
+  if (rc != PCP_OK) return rc;
+  char* sp = static_cast<char*>(ctx->scratch);
+  float* s_adv = reinterpret_cast<float*>(sp);
+  float* s_len = reinterpret_cast<float*>(sp + sv);
+  float* s_scale = reinterpret_cast<float*>(sp + 2 * sv);
+  float* s_val = reinterpret_cast<float*>(sp + 3 * sv);
+  float* s_loss = reinterpret_cast<float*>(sp + 4 * sv);
+  float* s_tl = need_tl ? reinterpret_cast<float*>(sp + 4 * sv + 256) : a->token_loss;
+
+  RowArgs ra;
+  std::memset(&ra, 0, sizeof(ra));
+  ra.logits = a->logits;
+  ra.ids = a->ids;
+  ra.mask = a->mask;
+  ra.err = ctx->d_err;
+  ra.vocab = g.vocab;
+  ra.rows = g.rows;
+  ra.logit_stride = g.lstride;
+  ra.tok_stride = g.tstride;
+  ra.tok_offset = g.toff;
+  ra.ids_i64 = a->ids_dtype == PCP_I64;
+  ra.mask_u8 = a->mask_dtype == PCP_BOOL;
+  ra.zero_fill = (a->flags & PCP_FLAG_NO_ZERO_FILL) ? 0 : 1;
+  ra.logp = a->logp;
+  ra.ref_logp = a->ref_logp;
+
+  if (op == kLoss) {
+    const float* adv = a->advantages;
+    if (!adv) {
+      e = launch_advantages(a->rewards, g.n_seq, g.group, a->std_eps, s_adv, st);
+      if (e != hipSuccess) return hip_fail(ctx, e, "advantages launch");
+      adv = s_adv;
+    }
+    if (a->advantages_out && a->advantages_out != adv) {
+      e = hipMemcpyAsync(a->advantages_out, adv, sizeof(float) * g.n_seq, hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return hip_fail(ctx, e, "copying advantages");
+    }
+    e = launch_seq_prep(a->mask, ra.mask_u8, g.n_seq, g.rows, g.tstride, g.toff, g.loss_norm, s_len,
+                        s_scale, st);
+    if (e != hipSuccess) return hip_fail(ctx, e, "seq_prep launch");
+    ra.ref_logits = (a->loss_mode == PCP_LOSS_GRPO_CLIP_KL) ? a->ref_logits : nullptr;
+    ra.old_logp = a->old_logp;
+    ra.adv = adv;
+    ra.seq_scale = s_scale;
+    ra.dlogits = a->dlogits;
+    ra.token_loss = s_tl;
+    ra.loss_mode = a->loss_mode;
+    ra.clip_eps = a->clip_eps;
+    ra.kl_beta = a->kl_beta;
+  } else {
+    ra.ref_logits = a->ref_logits;
+  }
+
+  const int in_bytes = dtype_bytes(a->logits_dtype);
+  const bool al = aligned16(a->logits) && (!ra.ref_logits || aligned16(ra.ref_logits)) &&
+                  (!ra.dlogits || aligned16(ra.dlogits));
+  const RowPlan plan = plan_rows(in_bytes, g.vocab, al, ra.dlogits != nullptr,
+                                 (a->flags & PCP_FLAG_FORCE_STREAMING) != 0);
+  const int out_dt = ra.dlogits ? a->dlogits_dtype : a->logits_dtype;
+  const bool timed = ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
+  if (timed) {
+    e = hipEventRecord(ctx->prof_start[ctx->prof_used], st);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
+  }
+  e = launch_rows(plan, a->logits_dtype, out_dt == PCP_F32 ? PCP_F32 : a->logits_dtype, ra, g.nrows, st);
+  if (e != hipSuccess) return hip_fail(ctx, e, "row kernel launch");
+  if (timed) {
+    e = hipEventRecord(ctx->prof_stop[ctx->prof_used++], st);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
+  }
+
+  if (op == kLoss) {
+    float* loss = a->loss ? a->loss : s_loss;
+    e = launch_loss_reduce(s_tl, g.n_seq, g.rows, g.tstride, g.toff, s_len, ra.adv,
+                           a->loss_mode == PCP_LOSS_REINFORCE, g.loss_norm, s_val, loss, st);
+    if (e != hipSuccess) return hip_fail(ctx, e, "loss reduction launch");
+  }
+  return finish(ctx, a, st);
+}
+
+}  // namespace
+}  // namespace pcp
+
+using namespace pcp;
+
+extern "C" {
+
+void pcp_grpo_args_init(pcp_grpo_args* a) {
+  if (!a) return;
+  std::memset(a, 0, sizeof(*a));
+  a->group_size = 1;
+  a->logits_dtype = PCP_BF16;
+  a->dlogits_dtype = PCP_BF16;
+  a->ids_dtype = PCP_I64;
+  a->mask_dtype = PCP_F32;
+  a->loss_mode = PCP_LOSS_REINFORCE;
+  a->clip_eps = 0.2f;
+  a->kl_beta = 0.04f;
+  a->std_eps = 1e-8f;
+}
+
+int pcp_init(int backend, int device_ordinal, pcp_ctx** out) {
+  if (!out) return fail(nullptr, PCP_ERR_INVALID_ARG, "out is NULL");
+  *out = nullptr;
+  if (backend != PCP_BACKEND_ROCM)
+    return fail(nullptr, PCP_ERR_UNSUPPORTED, "backend %d: this library implements PCP_BACKEND_ROCM only", backend);
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    return fail(nullptr, PCP_ERR_DEVICE, "no HIP device available (%s)", hipGetErrorString(e));
+  }
+  if (device_ordinal < 0 || device_ordinal >= n)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "device ordinal %d out of range [0, %d)", device_ordinal, n);
+  e = hipSetDevice(device_ordinal);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
+  pcp_ctx* c = new (std::nothrow) pcp_ctx();
+  if (!c) return fail(nullptr, PCP_ERR_OOM, "allocating the context");
+  c->device = device_ordinal;
+  e = hipMalloc(&c->d_err, sizeof(int));
+  if (e != hipSuccess) {
+    delete c;
+    return fail(nullptr, PCP_ERR_OOM, "hipMalloc(error word): %s", hipGetErrorString(e));
+  }
+  e = hipMemset(c->d_err, 0, sizeof(int));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    (void)hipFree(c->d_err);
+    delete c;
+    return hip_fail(nullptr, e, "initialising the error word");
+  }
+  *out = c;
+  return PCP_OK;
+}
+
+static void release_profile_events(pcp_ctx* ctx) {
+  for (hipEvent_t ev : ctx->prof_start) (void)hipEventDestroy(ev);
+  for (hipEvent_t ev : ctx->prof_stop) (void)hipEventDestroy(ev);
+  ctx->prof_start.clear();
+  ctx->prof_stop.clear();
+  ctx->prof_used = 0;
+  ctx->prof_on = false;
+}
+
+int pcp_profile_start(pcp_ctx* ctx, int max_launches) {
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  if (max_launches < 1 || max_launches > 1 << 20) return fail(ctx, PCP_ERR_INVALID_ARG, "max_launches out of range");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  release_profile_events(ctx);
+  for (int i = 0; i < max_launches; ++i) {
+    hipEvent_t a, b;
+    if ((e = hipEventCreate(&a)) != hipSuccess) return hip_fail(ctx, e, "hipEventCreate");
+    if ((e = hipEventCreate(&b)) != hipSuccess) {
+      (void)hipEventDestroy(a);
+      return hip_fail(ctx, e, "hipEventCreate");
+    }
+    ctx->prof_start.push_back(a);
+    ctx->prof_stop.push_back(b);
+  }
+  ctx->prof_on = true;
+  return PCP_OK;
+}
+
+int pcp_profile_stop(pcp_ctx* ctx, int* n_launches, double* total_ms) {
+  if (!ctx || !n_launches || !total_ms) return fail(ctx, PCP_ERR_INVALID_ARG, "NULL argument");
+  *n_launches = 0;
+  *total_ms = 0.0;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  double tot = 0.0;
+  for (int i = 0; i < ctx->prof_used; ++i) {
+    if ((e = hipEventSynchronize(ctx->prof_stop[i])) != hipSuccess) return hip_fail(ctx, e, "hipEventSynchronize");
+    float ms = 0.f;
+    if ((e = hipEventElapsedTime(&ms, ctx->prof_start[i], ctx->prof_stop[i])) != hipSuccess)
+      return hip_fail(ctx, e, "hipEventElapsedTime");
+    tot += ms;
+  }
+  *n_launches = ctx->prof_used;
+  *total_ms = tot;
+  release_profile_events(ctx);
+  return PCP_OK;
+}
+
+void pcp_destroy(pcp_ctx* ctx) {
+  if (!ctx) return;
+  if (hipSetDevice(ctx->device) == hipSuccess) {
+    (void)hipDeviceSynchronize();
+    release_profile_events(ctx);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->d_err) (void)hipFree(ctx->d_err);
+  }
+  delete ctx;
+}
+
+int pcp_get_backend_type(const pcp_ctx* ctx) { return ctx ? ctx->backend : PCP_ERR_INVALID_ARG; }
+
+const char* pcp_last_error(const pcp_ctx* ctx) {
+  return ctx ? ctx->last_error.c_str() : thread_error().c_str();
+}
+
+int pcp_sync(pcp_ctx* ctx) {
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  for (hipStream_t s : ctx->pending) {
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      ctx->pending.clear();
+      return hip_fail(ctx, e, "hipStreamSynchronize");
+    }
+  }
+  ctx->pending.clear();
+  return collect_device_errors(ctx);
+}
+
+int pcp_grpo_logprob_fwd(pcp_ctx* ctx, const pcp_grpo_args* a) { return run(ctx, a, kLogprob); }
+
+int pcp_grpo_loss_fwd_bwd(pcp_ctx* ctx, const pcp_grpo_args* a) { return run(ctx, a, kLoss); }
+
+int pcp_grpo_advantages(pcp_ctx* ctx, const float* rewards, int64_t n, int64_t group_size,
+                        float std_eps, float* adv, void* stream) {
+  if (n < 1) return fail(ctx, PCP_ERR_INVALID_ARG, "n must be >= 1");
+  if (group_size < 1) return fail(ctx, PCP_ERR_INVALID_ARG, "group_size must be >= 1");
+  if (!rewards || !adv) return fail(ctx, PCP_ERR_INVALID_ARG, "rewards / adv is NULL");
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  e = launch_advantages(rewards, n, group_size, std_eps, adv, st);
+  if (e != hipSuccess) return hip_fail(ctx, e, "advantages launch");
+  e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+  return PCP_OK;
+}
+
+const char* pcp_version(void) { return "pcp_grpo 0.1.0 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,398 @@
+// Host-bytes entry point of the C ABI: pcp_execute / pcp_free.
+//
+// Mirrors WorkerBackend.executeFunction (src/backends/worker_backend.zig:27-33)
+// as implemented by IreeBackend.execute (src/backends/iree.zig:336-442): borrowed
+// host byte slices with i64 shapes and DType codes in, every input copied to the
+// device, the function run synchronously, every output copied back into a
+// caller-owned host buffer. Argument checks run before any device call.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "context.hpp"
+#include "pcp_grpo.h"
+
+namespace pcp {
+namespace {
+
+struct In {
+  const void* data;
+  size_t nbytes;
+  std::vector<int64_t> shape;
+  int dtype;
+  int64_t numel;
+};
+
+struct OutSpec {
+  size_t nbytes;
+};
+
+int check_inputs(int n_in, const void* const* data, const size_t* nbytes,
+                 const int64_t* const* shapes, const int* ranks, const int* dtypes,
+                 const int* defaults, std::vector<In>* ins) {
+  ins->resize(n_in);
+  for (int i = 0; i < n_in; ++i) {
+    In& t = (*ins)[i];
+    t.data = data[i];
+    t.nbytes = nbytes[i];
+    t.dtype = dtypes ? dtypes[i] : defaults[i];
+    if (dtype_bytes(t.dtype) == 0) return fail(nullptr, PCP_ERR_DTYPE, "input %d: unknown dtype %d", i, t.dtype);
+    if (ranks[i] < 0 || ranks[i] > 8) return fail(nullptr, PCP_ERR_INVALID_ARG, "input %d: bad rank %d", i, ranks[i]);
+    if (ranks[i] > 0 && !shapes[i]) return fail(nullptr, PCP_ERR_INVALID_ARG, "input %d: shape is NULL", i);
+    t.shape.assign(shapes[i], shapes[i] + ranks[i]);
+    int64_t n = 1;
+    for (int64_t d : t.shape) {
+      if (d < 0) return fail(nullptr, PCP_ERR_INVALID_ARG, "input %d: negative dimension", i);
+      if (mul_overflows(n, d, &n)) return fail(nullptr, PCP_ERR_OVERFLOW, "input %d: element count overflows", i);
+    }
+    t.numel = n;
+    int64_t b;
+    if (mul_overflows(n, dtype_bytes(t.dtype), &b)) return fail(nullptr, PCP_ERR_OVERFLOW, "input %d: byte size overflows", i);
+    if (static_cast<size_t>(b) != t.nbytes)
+      return fail(nullptr, PCP_ERR_INVALID_ARG, "input %d: %zu bytes given, shape x dtype needs %lld", i, t.nbytes, (long long)b);
+    if (b > 0 && !t.data) return fail(nullptr, PCP_ERR_INVALID_ARG, "input %d: data is NULL", i);
+  }
+  return PCP_OK;
+}
+
+int expect_dtype(const In& t, int i, std::initializer_list<int> ok, const char* what) {
+  for (int d : ok)
+    if (t.dtype == d) return PCP_OK;
+  return fail(nullptr, PCP_ERR_DTYPE, "input %d (%s): dtype %d not supported", i, what, t.dtype);
+}
+
+int expect_shape(const In& t, int i, std::initializer_list<int64_t> dims, const char* what) {
+  if (t.shape.size() != dims.size())
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "input %d (%s): rank %zu, expected %zu", i, what, t.shape.size(), dims.size());
+  size_t k = 0;
+  for (int64_t d : dims) {
+    if (d >= 0 && t.shape[k] != d)
+      return fail(nullptr, PCP_ERR_INVALID_ARG, "input %d (%s): dim %zu is %lld, expected %lld", i, what, k,
+                  (long long)t.shape[k], (long long)d);
+    ++k;
+  }
+  return PCP_OK;
+}
+
+int64_t id_at(const In& ids, int64_t i) {
+  return ids.dtype == PCP_I64 ? static_cast<const int64_t*>(ids.data)[i]
+                              : static_cast<const int32_t*>(ids.data)[i];
+}
+bool mask_at(const In* m, int64_t i) {
+  if (!m) return true;
+  return m->dtype == PCP_BOOL ? static_cast<const uint8_t*>(m->data)[i] != 0
+                              : static_cast<const float*>(m->data)[i] != 0.f;
+}
+
+// Host check of the targets the kernels will gather (shifted: positions 1..T-1).
+int check_ids(const In& ids, const In* mask, int64_t S, int64_t T, int64_t V) {
+  for (int64_t s = 0; s < S; ++s)
+    for (int64_t t = 1; t < T; ++t) {
+      const int64_t i = s * T + t;
+      const int64_t id = id_at(ids, i);
+      if (mask_at(mask, i) && id != PCP_IGNORE_INDEX && (id < 0 || id >= V))
+        return fail(nullptr, PCP_ERR_TOKEN_RANGE, "token id %lld at [%lld, %lld] outside [0, %lld)", (long long)id,
+                    (long long)s, (long long)t, (long long)V);
+    }
+  return PCP_OK;
+}
+
+// Device allocations of one call, released on every exit path.
+struct DevArena {
+  std::vector<void*> ptrs;
+  ~DevArena() {
+    for (void* p : ptrs) (void)hipFree(p);
+  }
+  int alloc(pcp_ctx* ctx, size_t bytes, void** out) {
+    *out = nullptr;
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(out, bytes);
+    if (e != hipSuccess) {
+      *out = nullptr;
+      (void)hipGetLastError();
+      return fail(ctx, PCP_ERR_OOM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    }
+    ptrs.push_back(*out);
+    return PCP_OK;
+  }
+  int upload(pcp_ctx* ctx, const In& t, void** out) {
+    int rc = alloc(ctx, t.nbytes, out);
+    if (rc != PCP_OK) return rc;
+    if (t.nbytes == 0) return PCP_OK;
+    hipError_t e = hipMemcpy(*out, t.data, t.nbytes, hipMemcpyHostToDevice);
+    return e == hipSuccess ? PCP_OK : hip_fail(ctx, e, "host-to-device copy");
+  }
+  int zeroed(pcp_ctx* ctx, size_t bytes, void** out) {
+    int rc = alloc(ctx, bytes, out);
+    if (rc != PCP_OK) return rc;
+    hipError_t e = hipMemset(*out, 0, bytes ? bytes : 16);
+    return e == hipSuccess ? PCP_OK : hip_fail(ctx, e, "hipMemset");
+  }
+};
+
+struct Outputs {
+  std::vector<void*> dev;
+  std::vector<size_t> bytes;
+};
+
+int download(pcp_ctx* ctx, const Outputs& o, int* n_out, void*** out_data, size_t** out_nbytes) {
+  const int n = static_cast<int>(o.dev.size());
+  void** od = static_cast<void**>(std::calloc(n, sizeof(void*)));
+  size_t* ob = static_cast<size_t*>(std::calloc(n, sizeof(size_t)));
+  if (!od || !ob) {
+    std::free(od);
+    std::free(ob);
+    return fail(ctx, PCP_ERR_OOM, "allocating the output list");
+  }
+  for (int i = 0; i < n; ++i) {
+    od[i] = std::malloc(o.bytes[i] ? o.bytes[i] : 1);
+    ob[i] = o.bytes[i];
+    hipError_t e = od[i] ? hipMemcpy(od[i], o.dev[i], o.bytes[i], hipMemcpyDeviceToHost) : hipErrorOutOfMemory;
+    if (e != hipSuccess) {
+      for (int k = 0; k <= i; ++k) std::free(od[k]);
+      std::free(od);
+      std::free(ob);
+      return e == hipErrorOutOfMemory ? fail(ctx, PCP_ERR_OOM, "allocating output %d", i)
+                                      : hip_fail(ctx, e, "device-to-host copy");
+    }
+  }
+  *n_out = n;
+  *out_data = od;
+  *out_nbytes = ob;
+  return PCP_OK;
+}
+
+// ---- functions ------------------------------------------------------------
+
+enum Fn { kLossFwdBwd, kClipKl, kLogprob, kAdvantages, kUnknown };
+
+Fn lookup(const char* fn) {
+  if (!std::strcmp(fn, "grpo_loss_fwd_bwd") || !std::strcmp(fn, "main")) return kLossFwdBwd;
+  if (!std::strcmp(fn, "grpo_clip_kl_fwd_bwd")) return kClipKl;
+  if (!std::strcmp(fn, "grpo_logprob_fwd")) return kLogprob;
+  if (!std::strcmp(fn, "grpo_advantages")) return kAdvantages;
+  return kUnknown;
+}
+
+// Shifted layout of the reference graph over [S, T] token arrays.
+void shifted_layout(pcp_grpo_args* a, int64_t S, int64_t T, int64_t V) {
+  a->n_seq = S;
+  a->rows = T > 0 ? T - 1 : 0;
+  a->vocab = V;
+  a->logit_seq_stride = T;
+  a->tok_seq_stride = T;
+  a->tok_offset = T > 0 ? 1 : 0;
+}
+
+}  // namespace
+
+int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, const size_t* nbytes,
+            const int64_t* const* shapes, const int* ranks, const int* dtypes, int* n_out,
+            void*** out_data, size_t** out_nbytes) {
+  if (!fn || !n_out || !out_data || !out_nbytes || n_in < 0 || (n_in > 0 && (!data || !nbytes || !shapes || !ranks)))
+    return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_execute: NULL argument");
+  *n_out = 0;
+  *out_data = nullptr;
+  *out_nbytes = nullptr;
+  const Fn f = lookup(fn);
+  if (f == kUnknown) return fail(ctx, PCP_ERR_UNKNOWN_FUNCTION, "no function named '%s'", fn);
+
+  static const int kDefLoss[] = {PCP_F32, PCP_I64, PCP_F32, PCP_F32};
+  static const int kDefClip[] = {PCP_F32, PCP_F32, PCP_I64, PCP_F32, PCP_F32, PCP_F32, PCP_F32};
+  static const int kDefLp2[] = {PCP_F32, PCP_I64};
+  static const int kDefLp3[] = {PCP_F32, PCP_F32, PCP_I64};
+  static const int kDefAdv[] = {PCP_F32, PCP_I64};
+  const int* defaults = nullptr;
+  int want = 0;
+  switch (f) {
+    case kLossFwdBwd: want = 4; defaults = kDefLoss; break;
+    case kClipKl: want = 7; defaults = kDefClip; break;
+    case kLogprob: want = (n_in == 3) ? 3 : 2; defaults = (n_in == 3) ? kDefLp3 : kDefLp2; break;
+    case kAdvantages: want = 2; defaults = kDefAdv; break;
+    default: break;
+  }
+  if (n_in != want) return fail(ctx, PCP_ERR_COUNT_MISMATCH, "'%s' takes %d inputs, got %d", fn, want, n_in);
+
+  std::vector<In> in;
+  int rc = check_inputs(n_in, data, nbytes, shapes, ranks, dtypes, defaults, &in);
+  if (rc != PCP_OK) goto arg_error;
+
+  {
+    pcp_grpo_args a;
+    pcp_grpo_args_init(&a);
+    Outputs outs;
+    DevArena arena;
+
+    if (f == kAdvantages) {
+      if ((rc = expect_dtype(in[0], 0, {PCP_F32}, "rewards")) || (rc = expect_shape(in[0], 0, {-1}, "rewards")) ||
+          (rc = expect_dtype(in[1], 1, {PCP_I64, PCP_I32}, "group_size")) ||
+          (rc = expect_shape(in[1], 1, {}, "group_size")))
+        goto arg_error;
+      const int64_t n = in[0].numel;
+      const int64_t G = id_at(in[1], 0);
+      if (n < 1 || G < 1) {
+        rc = fail(nullptr, PCP_ERR_INVALID_ARG, "grpo_advantages: need n >= 1 and group_size >= 1");
+        goto arg_error;
+      }
+      if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+      void *dr, *da;
+      if ((rc = arena.upload(ctx, in[0], &dr)) || (rc = arena.alloc(ctx, n * sizeof(float), &da))) return rc;
+      if ((rc = pcp_grpo_advantages(ctx, static_cast<float*>(dr), n, G, 1e-8f, static_cast<float*>(da), nullptr)))
+        return rc;
+      outs.dev.push_back(da);
+      outs.bytes.push_back(n * sizeof(float));
+      return download(ctx, outs, n_out, out_data, out_nbytes);
+    }
+
+    // [S, T, V] functions.
+    const int ix_ids = (f == kLossFwdBwd || f == kLogprob) ? (f == kLogprob && n_in == 3 ? 2 : 1) : 2;
+    const In& L = in[0];
+    if ((rc = expect_dtype(L, 0, {PCP_BF16, PCP_F16, PCP_F32}, "logits")) || (rc = expect_shape(L, 0, {-1, -1, -1}, "logits")))
+      goto arg_error;
+    const int64_t S = L.shape[0], T = L.shape[1], V = L.shape[2];
+    if (S < 1 || T < 1 || V < 1) {
+      rc = fail(nullptr, PCP_ERR_INVALID_ARG, "logits dims must be >= 1");
+      goto arg_error;
+    }
+    const In& ids = in[ix_ids];
+    if ((rc = expect_dtype(ids, ix_ids, {PCP_I64, PCP_I32}, "input_ids")) || (rc = expect_shape(ids, ix_ids, {S, T}, "input_ids")))
+      goto arg_error;
+    const bool has_ref = (f == kClipKl) || (f == kLogprob && n_in == 3);
+    if (has_ref) {
+      if ((rc = expect_dtype(in[1], 1, {L.dtype}, "ref_logits")) || (rc = expect_shape(in[1], 1, {S, T, V}, "ref_logits")))
+        goto arg_error;
+    }
+    const In* mask = nullptr;
+    if (f == kLossFwdBwd || f == kClipKl) {
+      const int im = ix_ids + 1;
+      mask = &in[im];
+      if ((rc = expect_dtype(*mask, im, {PCP_F32, PCP_BOOL}, "attention_mask")) ||
+          (rc = expect_shape(*mask, im, {S, T}, "attention_mask")))
+        goto arg_error;
+    }
+    if (f == kLossFwdBwd) {
+      if ((rc = expect_dtype(in[3], 3, {PCP_F32}, "advantages")) || (rc = expect_shape(in[3], 3, {S}, "advantages")))
+        goto arg_error;
+    }
+    float hyper[4] = {1.f, 0.2f, 0.04f, 0.f};
+    if (f == kClipKl) {
+      if ((rc = expect_dtype(in[4], 4, {PCP_F32}, "old_logp")) || (rc = expect_shape(in[4], 4, {S, T}, "old_logp")) ||
+          (rc = expect_dtype(in[5], 5, {PCP_F32}, "rewards")) || (rc = expect_shape(in[5], 5, {S}, "rewards")) ||
+          (rc = expect_dtype(in[6], 6, {PCP_F32}, "hyper")) || (rc = expect_shape(in[6], 6, {4}, "hyper")))
+        goto arg_error;
+      std::memcpy(hyper, in[6].data, sizeof(hyper));
+      const float G = hyper[0];
+      if (!(G >= 1.f) || G != static_cast<float>(static_cast<int64_t>(G))) {
+        rc = fail(nullptr, PCP_ERR_INVALID_ARG, "hyper[0] (group_size) must be a positive integer");
+        goto arg_error;
+      }
+    }
+    if ((rc = check_ids(ids, mask, S, T, V))) goto arg_error;
+    if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+
+    shifted_layout(&a, S, T, V);
+    a.logits_dtype = L.dtype;
+    a.dlogits_dtype = L.dtype;
+    a.ids_dtype = ids.dtype;
+    void* p;
+    if ((rc = arena.upload(ctx, L, &p))) return rc;
+    a.logits = p;
+    if (has_ref) {
+      if ((rc = arena.upload(ctx, in[1], &p))) return rc;
+      a.ref_logits = p;
+    }
+    if ((rc = arena.upload(ctx, ids, &p))) return rc;
+    a.ids = p;
+    if (mask) {
+      if ((rc = arena.upload(ctx, *mask, &p))) return rc;
+      a.mask = p;
+      a.mask_dtype = mask->dtype;
+    }
+    const size_t tok_bytes = sizeof(float) * S * T;
+    if (f == kLogprob) {
+      if ((rc = arena.zeroed(ctx, tok_bytes, &p))) return rc;
+      a.logp = static_cast<float*>(p);
+      outs.dev.push_back(p);
+      outs.bytes.push_back(tok_bytes);
+      if (has_ref) {
+        if ((rc = arena.zeroed(ctx, tok_bytes, &p))) return rc;
+        a.ref_logp = static_cast<float*>(p);
+        outs.dev.push_back(p);
+        outs.bytes.push_back(tok_bytes);
+      }
+      if ((rc = pcp_grpo_logprob_fwd(ctx, &a))) return rc;
+      return download(ctx, outs, n_out, out_data, out_nbytes);
+    }
+
+    if ((rc = arena.alloc(ctx, sizeof(float), &p))) return rc;
+    a.loss = static_cast<float*>(p);
+    outs.dev.push_back(p);
+    outs.bytes.push_back(sizeof(float));
+    if ((rc = arena.alloc(ctx, L.nbytes, &p))) return rc;
+    a.dlogits = p;
+    outs.dev.push_back(p);
+    outs.bytes.push_back(L.nbytes);
+    if (f == kLossFwdBwd) {
+      if ((rc = arena.upload(ctx, in[3], &p))) return rc;
+      a.advantages = static_cast<float*>(p);
+      a.group_size = S;
+      a.loss_mode = PCP_LOSS_REINFORCE;
+    } else {
+      if ((rc = arena.upload(ctx, in[4], &p))) return rc;
+      a.old_logp = static_cast<float*>(p);
+      if ((rc = arena.upload(ctx, in[5], &p))) return rc;
+      a.rewards = static_cast<float*>(p);
+      a.group_size = static_cast<int64_t>(hyper[0]);
+      a.clip_eps = hyper[1];
+      a.kl_beta = hyper[2];
+      a.loss_norm = hyper[3];
+      a.loss_mode = PCP_LOSS_GRPO_CLIP_KL;
+      for (int k = 0; k < 2; ++k) {
+        if ((rc = arena.zeroed(ctx, tok_bytes, &p))) return rc;
+        (k == 0 ? a.logp : a.ref_logp) = static_cast<float*>(p);
+        outs.dev.push_back(p);
+        outs.bytes.push_back(tok_bytes);
+      }
+      if ((rc = arena.alloc(ctx, sizeof(float) * S, &p))) return rc;
+      a.advantages_out = static_cast<float*>(p);
+      outs.dev.push_back(p);
+      outs.bytes.push_back(sizeof(float) * S);
+    }
+    if ((rc = pcp_grpo_loss_fwd_bwd(ctx, &a))) return rc;
+    return download(ctx, outs, n_out, out_data, out_nbytes);
+  }
+
+arg_error:
+  if (ctx) ctx->last_error = thread_error();
+  return rc;
+}
+
+}  // namespace pcp
+
+extern "C" {
+
+int pcp_execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, const size_t* nbytes,
+                const int64_t* const* shapes, const int* ranks, const int* dtypes, int* n_out,
+                void*** out_data, size_t** out_nbytes) {
+  if (ctx) {
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return pcp::hip_fail(ctx, e, "hipSetDevice");
+  }
+  return pcp::execute(ctx, fn, n_in, data, nbytes, shapes, ranks, dtypes, n_out, out_data, out_nbytes);
+}
+
+void pcp_free(pcp_ctx* ctx, int n_out, void** out_data, size_t* out_nbytes) {
+  (void)ctx;
+  if (out_data) {
+    for (int i = 0; i < n_out; ++i) std::free(out_data[i]);
+    std::free(out_data);
+  }
+  std::free(out_nbytes);
+}
+
+}  // extern "C"

@@ -1,0 +1,308 @@
+// Device-side building blocks of the GRPO loss-head kernels (gfx950, wave64).
+//
+// Element codecs, vector row I/O, the online (max, sum-exp) pair and its wave /
+// workgroup merge, and the per-token GRPO math shared by every kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pcp_grpo.h"
+
+namespace pcp {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kLn2 = 0.69314718055994530942f;
+constexpr float kNegInf = -__builtin_inff();
+
+// Device error bits, OR-ed into the context's flag word; the host maps them to
+// pcp_status codes after the stream is synchronised.
+constexpr int kErrTokenRange = 1;
+constexpr int kErrNonFinite = 2;
+
+// v_exp_f32: 2^x. Used only for the per-element softmax terms, where results
+// below the fp32 normal range are irrelevant (they multiply a coefficient < 1).
+__device__ __forceinline__ float hw_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
+// Element codecs. `unpack(w, j)` reads element j of a packed little-endian word
+// array; `load1` reads one element of a row.
+// ---------------------------------------------------------------------------
+struct F32T {
+  static constexpr int kBytes = 4;
+  __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
+    return __uint_as_float(w[j]);
+  }
+  __device__ static __forceinline__ float load1(const void* p, int64_t i) {
+    return static_cast<const float*>(p)[i];
+  }
+};
+
+struct BF16T {
+  static constexpr int kBytes = 2;
+  __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
+    const uint32_t x = w[j >> 1];
+    return __uint_as_float((j & 1) ? (x & 0xffff0000u) : (x << 16));
+  }
+  __device__ static __forceinline__ float load1(const void* p, int64_t i) {
+    return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]) << 16);
+  }
+};
+
+struct F16T {
+  static constexpr int kBytes = 2;
+  __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
+    const uint32_t x = w[j >> 1];
+    const uint16_t h = (j & 1) ? static_cast<uint16_t>(x >> 16) : static_cast<uint16_t>(x & 0xffffu);
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+  }
+  __device__ static __forceinline__ float load1(const void* p, int64_t i) {
+    return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  }
+};
+
+// Pack two floats into one 32-bit word of the output element type (RNE).
+template <typename TO>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16T>(float lo, float hi) {
+  f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));  // v_cvt_pk_bf16_f32
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<F16T>(float lo, float hi) {
+  f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+}
+
+template <typename TO>
+__device__ __forceinline__ void store1(void* p, int64_t i, float v);
+template <>
+__device__ __forceinline__ void store1<F32T>(void* p, int64_t i, float v) {
+  static_cast<float*>(p)[i] = v;
+}
+template <>
+__device__ __forceinline__ void store1<BF16T>(void* p, int64_t i, float v) {
+  static_cast<__bf16*>(p)[i] = static_cast<__bf16>(v);
+}
+template <>
+__device__ __forceinline__ void store1<F16T>(void* p, int64_t i, float v) {
+  static_cast<_Float16*>(p)[i] = static_cast<_Float16>(v);
+}
+
+// Load one 16-byte vector (kBytes*EPV == 16) of a row; `nt` selects the
+// non-temporal (streaming) cache policy.
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16(const void* base, int64_t vec_idx) {
+  const u32x4* p = static_cast<const u32x4*>(base) + vec_idx;
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+// Store N floats as N output elements at element offset `elem` of `base`.
+// N * kBytes is 8, 16 or 32 bytes; `base + elem` is aligned to that size.
+template <typename TO, int N, bool NT>
+__device__ __forceinline__ void store_vals(void* base, int64_t elem, const float (&v)[N]) {
+  if constexpr (TO::kBytes == 4) {
+    static_assert(N % 4 == 0, "f32 output stores whole 16-byte vectors");
+    u32x4* p = reinterpret_cast<u32x4*>(static_cast<float*>(base) + elem);
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      u32x4 w = {__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]),
+                 __float_as_uint(v[4 * q + 2]), __float_as_uint(v[4 * q + 3])};
+      if constexpr (NT) __builtin_nontemporal_store(w, p + q);
+      else p[q] = w;
+    }
+  } else {
+    static_assert(N == 4 || N % 8 == 0, "16-bit output stores 8 or 16n bytes");
+    if constexpr (N == 4) {
+      u32x2* p = reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + elem);
+      u32x2 w = {pack2<TO>(v[0], v[1]), pack2<TO>(v[2], v[3])};
+      if constexpr (NT) __builtin_nontemporal_store(w, p);
+      else *p = w;
+    } else {
+      u32x4* p = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + elem);
+#pragma unroll
+      for (int q = 0; q < N / 8; ++q) {
+        u32x4 w = {pack2<TO>(v[8 * q], v[8 * q + 1]), pack2<TO>(v[8 * q + 2], v[8 * q + 3]),
+                   pack2<TO>(v[8 * q + 4], v[8 * q + 5]), pack2<TO>(v[8 * q + 6], v[8 * q + 7])};
+        if constexpr (NT) __builtin_nontemporal_store(w, p + q);
+        else p[q] = w;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Online log-sum-exp state in base-2 units: m = max(x) * log2(e),
+// s = sum 2^(x*log2(e) - m). m == -inf means "no element yet" (then s == 0).
+// merge() is commutative bit-for-bit, so an xor-butterfly leaves every lane of
+// a wave with the same value, and a fixed cross-wave order makes the result
+// identical on every thread and on every run.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
+  const float M = fmaxf(m, m2);
+  const float a = (m == kNegInf) ? 0.f : s * hw_exp2(m - M);
+  const float b = (m2 == kNegInf) ? 0.f : s2 * hw_exp2(m2 - M);
+  m = M;
+  s = a + b;
+}
+
+// log-sum-exp (natural units) of a merged state.
+__device__ __forceinline__ float ms_lse(float m, float s) { return (m + log2f(s)) * kLn2; }
+
+// Reduce two (m, s) pairs over the workgroup. `lds` holds 4 floats per wave.
+// Returns the same values on every thread.
+template <int BLOCK>
+__device__ __forceinline__ void block_merge2(float& m1, float& s1, float& m2, float& s2,
+                                             float* lds) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float om1 = __shfl_xor(m1, off), os1 = __shfl_xor(s1, off);
+    const float om2 = __shfl_xor(m2, off), os2 = __shfl_xor(s2, off);
+    ms_merge(m1, s1, om1, os1);
+    ms_merge(m2, s2, om2, os2);
+  }
+  constexpr int NW = BLOCK / 64;
+  if constexpr (NW > 1) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) {
+      lds[4 * wid + 0] = m1;
+      lds[4 * wid + 1] = s1;
+      lds[4 * wid + 2] = m2;
+      lds[4 * wid + 3] = s2;
+    }
+    __syncthreads();
+    m1 = lds[0];
+    s1 = lds[1];
+    m2 = lds[2];
+    s2 = lds[3];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+      ms_merge(m1, s1, lds[4 * w + 0], lds[4 * w + 1]);
+      ms_merge(m2, s2, lds[4 * w + 2], lds[4 * w + 3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel argument block (passed by value) and per-row metadata.
+// ---------------------------------------------------------------------------
+struct RowArgs {
+  const void* logits;
+  const void* ref_logits;  // nullptr => no reference pass
+  const void* ids;
+  const void* mask;        // nullptr => all ones
+  const float* old_logp;   // nullptr => on-policy
+  const float* adv;        // [n_seq]
+  const float* seq_scale;  // [n_seq]: 1 / (loss_norm * max(sum mask, 1))
+  void* dlogits;           // nullptr => forward only
+  float* logp;
+  float* ref_logp;
+  float* token_loss;
+  int* err;
+  int64_t vocab;
+  int64_t rows;
+  int64_t logit_stride;
+  int64_t tok_stride;
+  int64_t tok_offset;
+  int32_t ids_i64;
+  int32_t mask_u8;
+  int32_t loss_mode;
+  int32_t zero_fill;
+  float clip_eps;
+  float kl_beta;
+};
+
+struct RowMeta {
+  int64_t row;   // logits row index
+  int64_t tix;   // token index into ids/mask/per-token outputs (valid when tok)
+  int64_t id;    // target token
+  float w;       // mask weight
+  int32_t seq;
+  bool tok;      // row carries a token (t < rows)
+  bool live;     // tok && w != 0 && id != ignore && id in range
+};
+
+__device__ __forceinline__ RowMeta row_meta(const RowArgs& a, int64_t row) {
+  RowMeta r;
+  r.row = row;
+  const int64_t s = row / a.logit_stride;
+  const int64_t t = row - s * a.logit_stride;
+  r.seq = static_cast<int32_t>(s);
+  r.tok = t < a.rows;
+  r.tix = s * a.tok_stride + a.tok_offset + t;
+  r.id = 0;
+  r.w = 0.f;
+  r.live = false;
+  if (r.tok) {
+    r.id = a.ids_i64 ? static_cast<const int64_t*>(a.ids)[r.tix]
+                     : static_cast<int64_t>(static_cast<const int32_t*>(a.ids)[r.tix]);
+    if (a.mask == nullptr) r.w = 1.f;
+    else if (a.mask_u8) r.w = static_cast<const uint8_t*>(a.mask)[r.tix] ? 1.f : 0.f;
+    else r.w = static_cast<const float*>(a.mask)[r.tix];
+    const bool ignored = (r.id == PCP_IGNORE_INDEX);
+    const bool in_range = (r.id >= 0) && (r.id < a.vocab);
+    if (r.w != 0.f && !ignored && !in_range) {
+      if (threadIdx.x == 0) atomicOr(a.err, kErrTokenRange);
+    }
+    r.live = (r.w != 0.f) && in_range;
+  }
+  return r;
+}
+
+// Per-token loss term and d loss / d logp.
+struct TokenTerms {
+  float loss;  // m * l'
+  float coef;  // c = d loss / d logp (already includes m / (loss_norm * L_s))
+};
+
+__device__ __forceinline__ TokenTerms token_terms(const RowArgs& a, const RowMeta& r, float lp,
+                                                  float lr) {
+  TokenTerms o;
+  if (a.adv == nullptr) {  // forward-only request: no loss terms
+    o.loss = 0.f;
+    o.coef = 0.f;
+    return o;
+  }
+  const float A = a.adv[r.seq];
+  const float scale = a.seq_scale[r.seq] * r.w;
+  if (a.loss_mode == PCP_LOSS_REINFORCE) {
+    // token_losses = -logp * mask; seq_nll * adv; mean  (export_qwen_forward.py:156-163)
+    o.loss = r.w * (-lp);
+    o.coef = -A * scale;
+  } else {
+    const float old = a.old_logp ? a.old_logp[r.tix] : lp;
+    const float rho = expf(lp - old);
+    const float lo = 1.f - a.clip_eps, hi = 1.f + a.clip_eps;
+    const float rc = fminf(fmaxf(rho, lo), hi);
+    const float surr = fminf(rho * A, rc * A);
+    const float dlr = lr - lp;
+    const float e = expf(dlr);
+    const float k3 = e - dlr - 1.f;
+    o.loss = r.w * (-surr + a.kl_beta * k3);
+    // The min picks the unclipped branch (gradient -A*rho) unless the ratio left the
+    // trust region on the side the advantage's sign rewards.
+    const bool unclipped = (A >= 0.f) ? (rho <= hi) : (rho >= lo);
+    const float dsurr = unclipped ? -A * rho : 0.f;
+    o.coef = scale * (dsurr + a.kl_beta * (1.f - e));
+  }
+  return o;
+}
+
+// Write per-token outputs of a token row (thread 0 only).
+__device__ __forceinline__ void write_token_outputs(const RowArgs& a, const RowMeta& r, float lp,
+                                                    float lr, float tl) {
+  if (threadIdx.x != 0 || !r.tok) return;
+  if (a.logp) a.logp[r.tix] = lp;
+  if (a.ref_logp) a.ref_logp[r.tix] = lr;
+  if (a.token_loss) a.token_loss[r.tix] = tl;
+}
+
+}  // namespace pcp

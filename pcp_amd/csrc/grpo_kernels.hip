@@ -1,0 +1,544 @@
+// GRPO loss-head kernels for MI355X (gfx950).
+//
+// One workgroup owns one logits row. The hot kernel (grpo_resident_kernel) keeps
+// the policy row in VGPRs as packed 16-bit words (V=151936 bf16 = 19 x 16 B per
+// lane at 1024 lanes), so a live row costs exactly one read of the policy row,
+// one read of the reference row and one write of dlogits:
+//   1. issue every 16-byte load of the policy row (coalesced, 1 KiB per wave per
+//      chunk), then stream the reference row in batches;
+//   2. per-lane max and sum of 2^(x*log2e - m) over the resident values, online
+//      (max, sum) over the reference batches;
+//   3. one workgroup merge of both (m, s) pairs: xor-butterfly in the wave, then a
+//      fixed-order combine of the 16 wave results through LDS;
+//   4. token math (logp, ref logp, ratio, clip, k3-KL, coefficient c);
+//   5. dlogits = c * (onehot - 2^(x*log2e - lse2)) straight from the registers,
+//      packed to bf16 with v_cvt_pk_bf16_f32, stored 16 B per lane.
+// Rows whose token is masked, ignored or a pad row only zero-fill dlogits.
+//
+// Reference semantics: tools/export_qwen_forward.py:150-163 (loss),
+// models/tests/qwen_test.mlir:257-286 (cross-entropy lowering),
+// src/nodes/controllers/rl_shepherd.zig:462-479 (advantages).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "grpo_device.hpp"
+#include "grpo_launch.hpp"
+
+namespace pcp {
+
+// ---------------------------------------------------------------------------
+// Row helpers
+// ---------------------------------------------------------------------------
+template <typename TO, int EPV, int BLOCK>
+__device__ __forceinline__ void zero_row_vec(void* dl, int64_t row_elem, int nv) {
+  float z[EPV];
+#pragma unroll
+  for (int j = 0; j < EPV; ++j) z[j] = 0.f;
+  for (int vi = threadIdx.x; vi < nv; vi += BLOCK)
+    store_vals<TO, EPV, true>(dl, row_elem + static_cast<int64_t>(vi) * EPV, z);
+}
+
+template <typename TO, int BLOCK>
+__device__ __forceinline__ void zero_row_scalar(void* dl, int64_t row_elem, int64_t v) {
+  for (int64_t i = threadIdx.x; i < v; i += BLOCK) store1<TO>(dl, row_elem + i, 0.f);
+}
+
+__device__ __forceinline__ void flag_nonfinite(const RowArgs& a, float lse, float lr_lse) {
+  if (threadIdx.x == 0 && !(__builtin_isfinite(lse) && __builtin_isfinite(lr_lse)))
+    atomicOr(a.err, kErrNonFinite);
+}
+
+// ---------------------------------------------------------------------------
+// Register-resident fused forward+backward.
+//   TI/TO: input / output codecs; BLOCK lanes; NCH 16-byte chunks per lane
+//   (row capacity BLOCK*NCH*16 bytes); RB reference chunks per batch.
+// Requirements (checked on the host): V % EPV == 0, 16-byte aligned rows,
+// V <= BLOCK*NCH*EPV, dlogits != nullptr.
+// ---------------------------------------------------------------------------
+template <typename TI, typename TO, int BLOCK, int NCH, int RB>
+__global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
+  constexpr int EPV = 16 / TI::kBytes;
+  __shared__ float lds[4 * (BLOCK / 64)];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const RowMeta r = row_meta(a, row);
+  const int nv = static_cast<int>(a.vocab / EPV);
+  const int64_t row_elem = row * a.vocab;
+
+  if (!r.live) {
+    write_token_outputs(a, r, 0.f, 0.f, 0.f);
+    if (a.zero_fill) zero_row_vec<TO, EPV, BLOCK>(a.dlogits, row_elem, nv);
+    return;
+  }
+
+  const void* xrow = static_cast<const char*>(a.logits) + row_elem * TI::kBytes;
+  const bool has_ref = a.ref_logits != nullptr;
+  const void* rrow =
+      has_ref ? static_cast<const char*>(a.ref_logits) + row_elem * TI::kBytes : nullptr;
+
+  // Target logits: one broadcast load each, completing under the row stream.
+  const float xy = TI::load1(xrow, r.id);
+  const float ry = has_ref ? TI::load1(rrow, r.id) : 0.f;
+
+  // 1. Policy row -> registers.
+  u32x4 xv[NCH];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int vi = k * BLOCK + tid;
+    if (vi < nv) xv[k] = ld16<true>(xrow, vi);
+    else xv[k] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // 2a. Per-lane (max, sum) of the resident policy values.
+  float pm = kNegInf, ps = 0.f;
+  {
+    float mx = kNegInf;
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      if (k * BLOCK + tid < nv) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
+#pragma unroll
+        for (int j = 0; j < EPV; ++j) mx = fmaxf(mx, TI::unpack(w, j));
+      }
+    }
+    if (mx != kNegInf) {
+      const float m2 = mx * kLog2e;
+      float s = 0.f;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        if (k * BLOCK + tid < nv) {
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
+#pragma unroll
+          for (int j = 0; j < EPV; ++j) s += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -m2));
+        }
+      }
+      pm = m2;
+      ps = s;
+    }
+  }
+
+  // 2b. Reference row: online (max, sum) over batches of RB chunks.
+  float rm = kNegInf, rs = 0.f;
+  if (has_ref) {
+#pragma unroll
+    for (int kb = 0; kb < NCH; kb += RB) {
+      u32x4 rv[RB];
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+        const int vi = (kb + q) * BLOCK + tid;
+        if (kb + q < NCH && vi < nv) rv[q] = ld16<true>(rrow, vi);
+        else rv[q] = u32x4{0u, 0u, 0u, 0u};
+      }
+      float bm = kNegInf;
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+        if (kb + q < NCH && (kb + q) * BLOCK + tid < nv) {
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(&rv[q]);
+#pragma unroll
+          for (int j = 0; j < EPV; ++j) bm = fmaxf(bm, TI::unpack(w, j));
+        }
+      }
+      if (bm != kNegInf) {
+        const float nm = fmaxf(rm, bm * kLog2e);
+        float acc = (rm == kNegInf) ? 0.f : rs * hw_exp2(rm - nm);
+#pragma unroll
+        for (int q = 0; q < RB; ++q) {
+          if (kb + q < NCH && (kb + q) * BLOCK + tid < nv) {
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(&rv[q]);
+#pragma unroll
+            for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -nm));
+          }
+        }
+        rm = nm;
+        rs = acc;
+      }
+    }
+  }
+
+  // 3. Workgroup merge.
+  block_merge2<BLOCK>(pm, ps, rm, rs, lds);
+  const float lse2 = pm + log2f(ps);
+  const float lse = lse2 * kLn2;
+  const float rlse = has_ref ? ms_lse(rm, rs) : 0.f;
+  flag_nonfinite(a, lse, rlse);
+
+  // 4. Token math.
+  const float lp = xy - lse;
+  const float lr = ry - rlse;
+  const TokenTerms tt = token_terms(a, r, lp, lr);
+  write_token_outputs(a, r, lp, lr, tt.loss);
+
+  // 5. dlogits = c * (onehot - softmax) from the resident row.
+  const float c = tt.coef, nc = -tt.coef;
+  const int vid = static_cast<int>(r.id / EPV);
+  const int kid = vid / BLOCK, tid_id = vid - kid * BLOCK, jid = static_cast<int>(r.id) - vid * EPV;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int vi = k * BLOCK + tid;
+    if (vi < nv) {
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
+      float o[EPV];
+#pragma unroll
+      for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -lse2));
+      if (k == kid && tid == tid_id) {
+#pragma unroll
+        for (int j = 0; j < EPV; ++j)
+          if (j == jid) o[j] += c;
+      }
+      store_vals<TO, EPV, true>(a.dlogits, row_elem + static_cast<int64_t>(vi) * EPV, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming kernel: any V, any alignment (VEC = false uses element loads).
+// Forward only when dlogits == nullptr; otherwise a second read of the policy
+// row produces dlogits (3 row reads + 1 write per live row).
+// ---------------------------------------------------------------------------
+template <typename TI, bool VEC>
+struct StreamIO {
+  static constexpr int EPV = VEC ? 16 / TI::kBytes : 1;
+  struct Raw {
+    u32x4 v;
+    float f;
+  };
+  __device__ static __forceinline__ Raw load(const void* row, int vi) {
+    Raw r;
+    if constexpr (VEC) r.v = ld16<true>(row, vi);
+    else r.f = TI::load1(row, vi);
+    return r;
+  }
+  __device__ static __forceinline__ float get(const Raw& r, int j) {
+    if constexpr (VEC) return TI::unpack(reinterpret_cast<const uint32_t*>(&r.v), j);
+    else return r.f;
+  }
+};
+
+template <typename TI, typename TO, int BLOCK, int U, bool VEC>
+__global__ void __launch_bounds__(BLOCK) grpo_stream_kernel(RowArgs a) {
+  using IO = StreamIO<TI, VEC>;
+  constexpr int EPV = IO::EPV;
+  __shared__ float lds[4 * (BLOCK / 64)];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const RowMeta r = row_meta(a, row);
+  const int nv = static_cast<int>(a.vocab / EPV);
+  const int64_t row_elem = row * a.vocab;
+
+  if (!r.live) {
+    write_token_outputs(a, r, 0.f, 0.f, 0.f);
+    if (a.dlogits && a.zero_fill) {
+      if constexpr (VEC) zero_row_vec<TO, EPV, BLOCK>(a.dlogits, row_elem, nv);
+      else zero_row_scalar<TO, BLOCK>(a.dlogits, row_elem, a.vocab);
+    }
+    return;
+  }
+
+  const void* xrow = static_cast<const char*>(a.logits) + row_elem * TI::kBytes;
+  const bool has_ref = a.ref_logits != nullptr;
+  const void* rrow =
+      has_ref ? static_cast<const char*>(a.ref_logits) + row_elem * TI::kBytes : nullptr;
+  const float xy = TI::load1(xrow, r.id);
+  const float ry = has_ref ? TI::load1(rrow, r.id) : 0.f;
+
+  float pm = kNegInf, ps = 0.f, rm = kNegInf, rs = 0.f;
+  for (int base = 0; base < nv; base += BLOCK * U) {
+    typename IO::Raw xb[U], rb[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int vi = base + q * BLOCK + tid;
+      if (vi < nv) {
+        xb[q] = IO::load(xrow, vi);
+        if (has_ref) rb[q] = IO::load(rrow, vi);
+      }
+    }
+    float bx = kNegInf, br = kNegInf;
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      if (base + q * BLOCK + tid < nv) {
+#pragma unroll
+        for (int j = 0; j < EPV; ++j) {
+          bx = fmaxf(bx, IO::get(xb[q], j));
+          if (has_ref) br = fmaxf(br, IO::get(rb[q], j));
+        }
+      }
+    }
+    if (bx != kNegInf) {
+      const float nm = fmaxf(pm, bx * kLog2e);
+      float acc = (pm == kNegInf) ? 0.f : ps * hw_exp2(pm - nm);
+#pragma unroll
+      for (int q = 0; q < U; ++q)
+        if (base + q * BLOCK + tid < nv)
+#pragma unroll
+          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(IO::get(xb[q], j), kLog2e, -nm));
+      pm = nm;
+      ps = acc;
+    }
+    if (has_ref && br != kNegInf) {
+      const float nm = fmaxf(rm, br * kLog2e);
+      float acc = (rm == kNegInf) ? 0.f : rs * hw_exp2(rm - nm);
+#pragma unroll
+      for (int q = 0; q < U; ++q)
+        if (base + q * BLOCK + tid < nv)
+#pragma unroll
+          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(IO::get(rb[q], j), kLog2e, -nm));
+      rm = nm;
+      rs = acc;
+    }
+  }
+
+  block_merge2<BLOCK>(pm, ps, rm, rs, lds);
+  const float lse2 = pm + log2f(ps);
+  const float lse = lse2 * kLn2;
+  const float rlse = has_ref ? ms_lse(rm, rs) : 0.f;
+  flag_nonfinite(a, lse, rlse);
+  const float lp = xy - lse;
+  const float lr = ry - rlse;
+  const TokenTerms tt = token_terms(a, r, lp, lr);
+  write_token_outputs(a, r, lp, lr, tt.loss);
+  if (a.dlogits == nullptr) return;
+
+  const float c = tt.coef, nc = -tt.coef;
+  const int vid = static_cast<int>(r.id / EPV);
+  const int jid = static_cast<int>(r.id) - vid * EPV;
+  for (int base = 0; base < nv; base += BLOCK * U) {
+    typename IO::Raw xb[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int vi = base + q * BLOCK + tid;
+      if (vi < nv) xb[q] = IO::load(xrow, vi);
+    }
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int vi = base + q * BLOCK + tid;
+      if (vi < nv) {
+        float o[EPV];
+#pragma unroll
+        for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(IO::get(xb[q], j), kLog2e, -lse2));
+        if (vi == vid) {
+#pragma unroll
+          for (int j = 0; j < EPV; ++j)
+            if (j == jid) o[j] += c;
+        }
+        if constexpr (VEC) store_vals<TO, EPV, true>(a.dlogits, row_elem + static_cast<int64_t>(vi) * EPV, o);
+        else store1<TO>(a.dlogits, row_elem + vi, o[0]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Small kernels: sequence lengths, advantages, loss reduction.
+// ---------------------------------------------------------------------------
+
+// Deterministic workgroup sum: fixed per-lane order, xor butterfly (commutative,
+// so every lane agrees), fixed cross-wave order. Result on every thread.
+template <int BLOCK>
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  constexpr int NW = BLOCK / 64;
+  if constexpr (NW > 1) {
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = lds[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += lds[w];
+    __syncthreads();
+  }
+  return v;
+}
+
+// seq_len[s] = max(sum_t mask, 1)  (torch.clamp(shift_mask.sum(1), min=1.0),
+// export_qwen_forward.py:160); seq_scale[s] = 1 / (loss_norm * seq_len[s]).
+constexpr int kSmallBlock = 256;
+__global__ void __launch_bounds__(kSmallBlock)
+seq_prep_kernel(const void* mask, int32_t mask_u8, int64_t rows, int64_t tok_stride,
+                int64_t tok_offset, float loss_norm, float* seq_len, float* seq_scale) {
+  __shared__ float lds[kSmallBlock / 64];
+  const int64_t s = blockIdx.x;
+  float acc = 0.f;
+  const int64_t base = s * tok_stride + tok_offset;
+  for (int64_t t = threadIdx.x; t < rows; t += kSmallBlock) {
+    float m;
+    if (mask == nullptr) m = 1.f;
+    else if (mask_u8) m = static_cast<const uint8_t*>(mask)[base + t] ? 1.f : 0.f;
+    else m = static_cast<const float*>(mask)[base + t];
+    acc += m;
+  }
+  const float tot = block_sum<kSmallBlock>(acc, lds);
+  if (threadIdx.x == 0) {
+    const float L = fmaxf(tot, 1.f);
+    seq_len[s] = L;
+    seq_scale[s] = 1.f / (loss_norm * L);
+  }
+}
+
+// Group-relative advantages, restating rl_shepherd.zig:466-478 operation by
+// operation in IEEE fp32 with no contraction: sequential sum, mean = sum / n,
+// sequential sum of (r-mean)*(r-mean), std = sqrt(ssd / n) + eps, (r-mean)/std.
+__global__ void __launch_bounds__(64)
+advantages_kernel(const float* r, int64_t n, int64_t group, float eps, float* adv) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+  const int64_t i = g * group;
+  if (i >= n) return;
+  const int64_t e = (i + group < n) ? i + group : n;
+  const float cnt = static_cast<float>(e - i);
+  float sum = 0.f;
+  for (int64_t k = i; k < e; ++k) sum = __fadd_rn(sum, r[k]);
+  const float mean = __fdiv_rn(sum, cnt);
+  float ssd = 0.f;
+  for (int64_t k = i; k < e; ++k) {
+    const float d = __fsub_rn(r[k], mean);
+    ssd = __fadd_rn(ssd, __fmul_rn(d, d));
+  }
+  const float sd = __fadd_rn(__fsqrt_rn(__fdiv_rn(ssd, cnt)), eps);
+  for (int64_t k = i; k < e; ++k) adv[k] = __fdiv_rn(__fsub_rn(r[k], mean), sd);
+}
+
+// seq_val[s] = (sum_t token_loss) / seq_len[s] (* adv[s] in REINFORCE mode):
+// token_losses.sum(1) / seq_lengths; seq_nll * advantages (export_qwen_forward.py:161-162).
+__global__ void __launch_bounds__(kSmallBlock)
+seq_loss_kernel(const float* token_loss, int64_t rows, int64_t tok_stride, int64_t tok_offset,
+                const float* seq_len, const float* adv, int32_t reinforce, float* seq_val) {
+  __shared__ float lds[kSmallBlock / 64];
+  const int64_t s = blockIdx.x;
+  const int64_t base = s * tok_stride + tok_offset;
+  float acc = 0.f;
+  for (int64_t t = threadIdx.x; t < rows; t += kSmallBlock) acc += token_loss[base + t];
+  const float tot = block_sum<kSmallBlock>(acc, lds);
+  if (threadIdx.x == 0) {
+    const float v = tot / seq_len[s];
+    seq_val[s] = reinforce ? v * adv[s] : v;
+  }
+}
+
+// loss = sum_s seq_val[s] / loss_norm  (weighted_losses.mean(), export_qwen_forward.py:163).
+constexpr int kFinalBlock = 1024;
+__global__ void __launch_bounds__(kFinalBlock)
+loss_final_kernel(const float* seq_val, int64_t n_seq, float loss_norm, float* loss) {
+  __shared__ float lds[kFinalBlock / 64];
+  float acc = 0.f;
+  for (int64_t s = threadIdx.x; s < n_seq; s += kFinalBlock) acc += seq_val[s];
+  const float tot = block_sum<kFinalBlock>(acc, lds);
+  if (threadIdx.x == 0) *loss = tot / loss_norm;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launchers
+// ---------------------------------------------------------------------------
+namespace {
+
+template <typename TI, typename TO, int BLOCK, int NCH>
+hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
+  constexpr int RB = 4;
+  grpo_resident_kernel<TI, TO, BLOCK, NCH, RB>
+      <<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
+  return hipGetLastError();
+}
+
+template <typename TI, typename TO, bool VEC>
+hipError_t launch_stream(const RowArgs& a, int64_t nrows, hipStream_t st) {
+  constexpr int BLOCK = 1024, U = 4;
+  grpo_stream_kernel<TI, TO, BLOCK, U, VEC>
+      <<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
+  return hipGetLastError();
+}
+
+// Resident configurations: (BLOCK, NCH). A row of NV 16-byte vectors fits the
+// first configuration with BLOCK*NCH >= NV.
+struct ResCfg {
+  int block, nch;
+};
+// (1024, 24) would spill at the 128-VGPR budget of a 1024-lane workgroup, so rows
+// wider than 20480 16-byte vectors (V > 163840 for 16-bit logits) stream instead.
+constexpr ResCfg kResCfgs[] = {{256, 1},   {256, 2},   {256, 4},   {1024, 2}, {1024, 4},
+                               {1024, 8},  {1024, 12}, {1024, 16}, {1024, 19}, {1024, 20}};
+
+template <typename TI, typename TO>
+hipError_t dispatch_resident(int cfg, const RowArgs& a, int64_t nrows, hipStream_t st) {
+  switch (cfg) {
+    case 0: return launch_resident<TI, TO, 256, 1>(a, nrows, st);
+    case 1: return launch_resident<TI, TO, 256, 2>(a, nrows, st);
+    case 2: return launch_resident<TI, TO, 256, 4>(a, nrows, st);
+    case 3: return launch_resident<TI, TO, 1024, 2>(a, nrows, st);
+    case 4: return launch_resident<TI, TO, 1024, 4>(a, nrows, st);
+    case 5: return launch_resident<TI, TO, 1024, 8>(a, nrows, st);
+    case 6: return launch_resident<TI, TO, 1024, 12>(a, nrows, st);
+    case 7: return launch_resident<TI, TO, 1024, 16>(a, nrows, st);
+    case 8: return launch_resident<TI, TO, 1024, 19>(a, nrows, st);
+    case 9: return launch_resident<TI, TO, 1024, 20>(a, nrows, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <typename TI, typename TO>
+hipError_t dispatch_rows(const RowPlan& p, const RowArgs& a, int64_t nrows, hipStream_t st) {
+  if (p.kind == RowPlan::kResident) return dispatch_resident<TI, TO>(p.cfg, a, nrows, st);
+  if (p.kind == RowPlan::kStreamVec) return launch_stream<TI, TO, true>(a, nrows, st);
+  return launch_stream<TI, TO, false>(a, nrows, st);
+}
+
+}  // namespace
+
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool want_bwd, bool force_stream) {
+  RowPlan p;
+  const int epv = 16 / in_bytes;
+  const bool vec = aligned16 && (vocab % epv == 0);
+  p.kind = vec ? RowPlan::kStreamVec : RowPlan::kStreamScalar;
+  p.cfg = -1;
+  p.block = 1024;
+  if (!vec || !want_bwd || force_stream) return p;
+  const int64_t nv = vocab / epv;
+  for (int i = 0; i < static_cast<int>(sizeof(kResCfgs) / sizeof(kResCfgs[0])); ++i) {
+    if (static_cast<int64_t>(kResCfgs[i].block) * kResCfgs[i].nch >= nv) {
+      p.kind = RowPlan::kResident;
+      p.cfg = i;
+      p.block = kResCfgs[i].block;
+      p.nch = kResCfgs[i].nch;
+      return p;
+    }
+  }
+  return p;
+}
+
+hipError_t launch_rows(const RowPlan& p, int in_dtype, int out_dtype, const RowArgs& a,
+                       int64_t nrows, hipStream_t st) {
+  if (in_dtype == PCP_BF16 && out_dtype == PCP_BF16) return dispatch_rows<BF16T, BF16T>(p, a, nrows, st);
+  if (in_dtype == PCP_BF16 && out_dtype == PCP_F32) return dispatch_rows<BF16T, F32T>(p, a, nrows, st);
+  if (in_dtype == PCP_F16 && out_dtype == PCP_F16) return dispatch_rows<F16T, F16T>(p, a, nrows, st);
+  if (in_dtype == PCP_F16 && out_dtype == PCP_F32) return dispatch_rows<F16T, F32T>(p, a, nrows, st);
+  if (in_dtype == PCP_F32 && out_dtype == PCP_F32) return dispatch_rows<F32T, F32T>(p, a, nrows, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_seq_prep(const void* mask, int mask_u8, int64_t n_seq, int64_t rows,
+                           int64_t tok_stride, int64_t tok_offset, float loss_norm,
+                           float* seq_len, float* seq_scale, hipStream_t st) {
+  seq_prep_kernel<<<dim3(static_cast<unsigned>(n_seq)), dim3(kSmallBlock), 0, st>>>(
+      mask, mask_u8, rows, tok_stride, tok_offset, loss_norm, seq_len, seq_scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_advantages(const float* r, int64_t n, int64_t group, float eps, float* adv,
+                             hipStream_t st) {
+  const int64_t ngroups = (n + group - 1) / group;
+  const unsigned nb = static_cast<unsigned>((ngroups + 63) / 64);
+  advantages_kernel<<<dim3(nb), dim3(64), 0, st>>>(r, n, group, eps, adv);
+  return hipGetLastError();
+}
+
+hipError_t launch_loss_reduce(const float* token_loss, int64_t n_seq, int64_t rows,
+                              int64_t tok_stride, int64_t tok_offset, const float* seq_len,
+                              const float* adv, int reinforce, float loss_norm, float* seq_val,
+                              float* loss, hipStream_t st) {
+  seq_loss_kernel<<<dim3(static_cast<unsigned>(n_seq)), dim3(kSmallBlock), 0, st>>>(
+      token_loss, rows, tok_stride, tok_offset, seq_len, adv, reinforce, seq_val);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  loss_final_kernel<<<dim3(1), dim3(kFinalBlock), 0, st>>>(seq_val, n_seq, loss_norm, loss);
+  return hipGetLastError();
+}
+
+}  // namespace pcp

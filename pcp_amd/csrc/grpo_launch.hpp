@@ -1,0 +1,35 @@
+// Host-side launch interface of the GRPO kernels (implemented in grpo_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pcp {
+
+struct RowArgs;
+
+// Which row kernel serves a request.
+struct RowPlan {
+  enum Kind { kResident = 0, kStreamVec = 1, kStreamScalar = 2 };
+  int kind;
+  int cfg;    // resident configuration index
+  int block;  // lanes per workgroup
+  int nch;    // resident 16-byte chunks per lane
+};
+
+// in_bytes: logits element size; aligned16: every row base is 16-byte aligned.
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool want_bwd, bool force_stream);
+
+hipError_t launch_rows(const RowPlan& p, int in_dtype, int out_dtype, const RowArgs& a,
+                       int64_t nrows, hipStream_t st);
+hipError_t launch_seq_prep(const void* mask, int mask_u8, int64_t n_seq, int64_t rows,
+                           int64_t tok_stride, int64_t tok_offset, float loss_norm,
+                           float* seq_len, float* seq_scale, hipStream_t st);
+hipError_t launch_advantages(const float* r, int64_t n, int64_t group, float eps, float* adv,
+                             hipStream_t st);
+hipError_t launch_loss_reduce(const float* token_loss, int64_t n_seq, int64_t rows,
+                              int64_t tok_stride, int64_t tok_offset, const float* seq_len,
+                              const float* adv, int reinforce, float loss_norm, float* seq_val,
+                              float* loss, hipStream_t st);
+
+}  // namespace pcp

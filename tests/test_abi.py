@@ -1,0 +1,191 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+headers declare, the ctypes struct matches the C layout, and argument errors are
+reported with the right status before any device call (no context needed)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from pcp_amd import _lib
+from pcp_amd._lib import DType, PcpError
+from pcp_amd.backend import HipGrpoBackend, execute_raw
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def declared_functions():
+    names = []
+    for h in sorted(os.listdir(INCLUDE)):
+        if not h.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^[A-Za-z_][\w \*]*?\b(pcp_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(L, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (pcp_\w+)", out))
+    assert set(names) <= exported
+
+
+def test_struct_layout_matches_c(tmp_path):
+    fields = [f[0] for f in _lib.GrpoArgs._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "pcp_grpo.h"', "int main(void){",
+           'printf("%zu\\n", sizeof(pcp_grpo_args));']
+    src += [f'printf("%zu\\n", offsetof(pcp_grpo_args, {f}));' for f in fields]
+    src += ["return 0;}"]
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", INCLUDE, str(c), "-o", str(exe)], check=True)
+    vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(_lib.GrpoArgs)
+    for f, off in zip(fields, vals[1:]):
+        assert getattr(_lib.GrpoArgs, f).offset == off, f
+
+
+def test_c_host_links_against_the_library(tmp_path):
+    # A C caller (what a Zig @cImport binding compiles to) links and runs without a GPU.
+    src = r'''
+#include <stdio.h>
+#include "pcp_grpo.h"
+int main(void) {
+  pcp_grpo_args a; pcp_grpo_args_init(&a);
+  a.n_seq = 0;
+  int rc = pcp_grpo_loss_fwd_bwd(NULL, &a);
+  printf("%d %s|%s\n", rc, pcp_last_error(NULL), pcp_version());
+  return 0;
+}'''
+    c = tmp_path / "host.c"
+    c.write_text(src)
+    exe = tmp_path / "host"
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    subprocess.run(["gcc", "-std=c99", "-I", INCLUDE, str(c), "-L", libdir, "-lpcp_grpo", f"-Wl,-rpath,{libdir}",
+                    "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    assert out.startswith("-1 n_seq must be >= 1") and "gfx950" in out
+
+
+def test_args_defaults():
+    a = _lib.default_args()
+    assert a.logits_dtype == DType.bf16 and a.ids_dtype == DType.i64 and a.mask_dtype == DType.f32
+    assert abs(a.clip_eps - 0.2) < 1e-7 and abs(a.kl_beta - 0.04) < 1e-8 and abs(a.std_eps - 1e-8) < 1e-15
+    assert a.group_size == 1 and a.loss_norm == 0 and a.flags == 0
+
+
+def _valid_args():
+    a = _lib.default_args()
+    a.n_seq, a.rows, a.vocab, a.group_size = 2, 4, 16, 2
+    a.logits = 0x1000
+    a.ids = 0x2000
+    a.advantages = 0x3000
+    return a
+
+
+@pytest.mark.parametrize("mutate,code,text", [
+    (lambda a: setattr(a, "n_seq", 0), -1, "n_seq"),
+    (lambda a: setattr(a, "vocab", 0), -1, "vocab"),
+    (lambda a: setattr(a, "group_size", 0), -1, "group_size"),
+    (lambda a: setattr(a, "logit_seq_stride", 3), -1, "logit_seq_stride"),
+    (lambda a: setattr(a, "tok_offset", 1), -1, "tok_offset"),
+    (lambda a: setattr(a, "logits_dtype", int(DType.i32)), -2, "logits dtype"),
+    (lambda a: setattr(a, "ids_dtype", int(DType.f32)), -2, "ids dtype"),
+    (lambda a: (setattr(a, "mask", 0x10), setattr(a, "mask_dtype", int(DType.i64))), -2, "mask dtype"),
+    (lambda a: setattr(a, "logits", None), -1, "logits is NULL"),
+    (lambda a: setattr(a, "ids", None), -1, "ids is NULL"),
+    (lambda a: setattr(a, "loss_mode", 7), -1, "loss_mode"),
+    (lambda a: setattr(a, "loss_mode", 1), -1, "ref_logits"),
+    (lambda a: setattr(a, "advantages", None), -1, "both NULL"),
+    (lambda a: setattr(a, "clip_eps", 1.5), -1, "clip_eps"),
+    (lambda a: (setattr(a, "dlogits", 0x10), setattr(a, "dlogits_dtype", int(DType.f16))), -2, "dlogits dtype"),
+    (lambda a: (setattr(a, "n_seq", 1 << 40), setattr(a, "rows", 1 << 20)), -9, "2^31"),
+])
+def test_argument_errors_without_device(mutate, code, text):
+    L = _lib.lib()
+    a = _valid_args()
+    mutate(a)
+    rc = L.pcp_grpo_loss_fwd_bwd(None, ctypes.byref(a))
+    assert rc == code
+    assert text in L.pcp_last_error(None).decode()
+
+
+def test_valid_args_then_null_context():
+    L = _lib.lib()
+    a = _valid_args()
+    assert L.pcp_grpo_loss_fwd_bwd(None, ctypes.byref(a)) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()
+
+
+def test_init_rejects_other_backends_and_reports_missing_device():
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    assert L.pcp_init(int(_lib.Backend.cuda), 0, ctypes.byref(h)) == -10
+    if not torch.cuda.is_available():
+        with pytest.raises(PcpError) as e:
+            HipGrpoBackend.init(_lib.Backend.rocm, 0)
+        assert e.value.code == -6
+
+
+def _ref_inputs(S=2, T=5, V=11, ids=None):
+    rng = np.random.default_rng(0)
+    logits = rng.standard_normal((S, T, V)).astype(np.float32)
+    ids = rng.integers(0, V, (S, T)).astype(np.int64) if ids is None else ids
+    mask = np.ones((S, T), np.float32)
+    adv = np.array([1.0, -1.0], np.float32)[:S]
+    return [logits, ids, mask, adv], [logits.shape, ids.shape, mask.shape, adv.shape]
+
+
+def test_execute_argument_errors_without_device():
+    data, shapes = _ref_inputs()
+    dts = [DType.f32, DType.i64, DType.f32, DType.f32]
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "no_such_fn", data, shapes, dts)
+    assert e.value.code == -7
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "main", data[:3], shapes[:3], dts[:3])
+    assert e.value.code == -8
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "main", data, [shapes[0], (2, 4), shapes[2], shapes[3]], dts)
+    assert e.value.code == -1   # byte count does not match the shape
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "main", data, shapes, [DType.f64, DType.i64, DType.f32, DType.f32])
+    assert e.value.code == -1   # f64 bytes != f32 bytes for the same shape -> size mismatch first
+    bad = np.array(data[0], np.float64)
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "main", [bad] + data[1:], shapes, [DType.f64, DType.i64, DType.f32, DType.f32])
+    assert e.value.code == -2
+    ids = data[1].copy()
+    ids[1, 3] = 11                  # == V: out of range
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "main", [data[0], ids, data[2], data[3]], shapes, dts)
+    assert e.value.code == -3
+    ids[1, 3] = -100                # the ignore index is accepted
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "main", [data[0], ids, data[2], data[3]], shapes, dts)
+    assert e.value.code == -1 and "context is NULL" in str(e.value)
+    # dtypes == NULL selects the function's defaults (f32 / i64)
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "main", data, shapes, None)
+    assert "context is NULL" in str(e.value)
+
+
+def test_philox_known_answers():
+    # Random123 known-answer vectors for philox4x32-10.
+    from pcp_amd.synth import philox
+    assert philox([0, 0, 0, 0], [0, 0]) == [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]
+    assert philox([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2) == [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]
+    assert philox([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0]) == \
+        [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]

@@ -1,0 +1,273 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker of the HIP path.
+
+Each oracle function is checked against something it was not derived from:
+the reference's known-answer tests (src/examples/isolated_vjp_tests.zig), the
+committed golden fixtures (torch CPU float64 autograd, numpy float32 simulation),
+closed forms, brute force and finite differences in float64. The mutation tests
+at the end plant plausible mistakes in oracle outputs and show the checks catch
+them.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def load_cases():
+    z = np.load(os.path.join(GOLD, "cases.npz"))
+    cases = {}
+    for k in z.files:
+        name, field = k.split("/", 1)
+        cases.setdefault(name, {})[field] = z[k]
+    return cases
+
+
+CASES = load_cases()
+
+
+def run_oracle_case(orc, c, precision=0):
+    dt = orc.BF16 if c["logits"].dtype == np.uint16 else orc.F32
+    kw = {}
+    if "advantages" in c:
+        kw["advantages_in"] = c["advantages"]
+    else:
+        kw["rewards"] = c["rewards"]
+    return orc.grpo_full(c["logits"], c["ids"], c["mask"], rows=int(c["rows"]), tok_offset=int(c["tok_offset"]),
+                         group_size=int(c["group_size"]), ref_logits=c.get("ref_logits"),
+                         old_logp=c.get("old_logp"), loss_mode=int(c["loss_mode"]), clip_eps=float(c["clip_eps"]),
+                         kl_beta=float(c["kl_beta"]), loss_norm=float(c["loss_norm"]), precision=precision,
+                         dtype=dt, **kw)
+
+
+# ---- codecs ------------------------------------------------------------------------
+
+def test_bf16_rne_matches_torch(orc):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10,
+                        np.array([0.0, -0.0, 1.0, 1.00390625, 1.005859375, 1.0078125, 3.0e38, -1e-40, np.inf, -np.inf],
+                                 np.float32)])
+    # exact ties: mantissa ...1 1000 0000 0000 0000 and ...0 1000 ...
+    ties = (np.arange(1000, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    x = np.concatenate([x, ties])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = orc.bf16_from_f32(x)
+    assert np.array_equal(got, want)
+    back = orc.bf16_to_f32(got)
+    assert np.array_equal(back, torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy())
+
+
+# ---- a3 advantages -----------------------------------------------------------------
+
+def test_advantages_bit_exact_against_fixture(orc):
+    d = json.load(open(os.path.join(GOLD, "advantages.json")))
+    assert len(d["cases"]) >= 9
+    for c in d["cases"]:
+        r = np.array(c["rewards_bits"], np.uint32).view(np.float32)
+        want = np.array(c["adv_bits"], np.uint32)
+        got = orc.advantages(r, c["group"], d["eps"]).view(np.uint32)
+        assert np.array_equal(got, want), c["name"]
+
+
+def test_advantages_hand_values(orc):
+    # G=4, r=[1,0,0,0]: mean 0.25, std sqrt(0.1875) + 1e-8.
+    a = orc.advantages(np.array([1, 0, 0, 0], np.float32), 4)
+    sd = np.float32(np.sqrt(np.float32(0.1875))) + np.float32(1e-8)
+    assert a[0] == np.float32(np.float32(0.75) / sd)
+    assert a[1] == np.float32(np.float32(-0.25) / sd)
+    # binary all-equal groups give exactly 0; partial last group uses its own n
+    a = orc.advantages(np.array([1, 1, 1, 0, 1], np.float32), 3)
+    assert np.all(a[:3] == 0) and a[3] == -1 and a[4] == 1
+
+
+def test_advantages_degenerate_groups_are_rounding_noise(orc):
+    # The reference adds 1e-8 to the std *outside* the sqrt, so an all-equal group of
+    # non-representable rewards gives (r - mean)/(tiny + 1e-8), not 0.
+    a = orc.advantages(np.full(16, 0.7, np.float32), 16)
+    assert np.all(a == a[0]) and a[0] != 0 and abs(a[0]) < 1.0
+
+
+# ---- a1 log-prob ---------------------------------------------------------------------
+
+def test_logprob_closed_forms(orc):
+    V = 1000
+    x = np.full((3, V), 0.37, np.float32)
+    lp, lse = orc.logprob(x, np.array([0, 5, 999]))
+    assert np.allclose(lp, -np.log(V), rtol=0, atol=1e-12)
+    lp1, _ = orc.logprob(np.array([[3.5], [-7.0]], np.float32), np.array([0, 0]))
+    assert np.all(lp1 == 0.0)
+    rng = np.random.default_rng(1)
+    y = rng.standard_normal((5, 77)).astype(np.float32)
+    ids = rng.integers(0, 77, 5)
+    a, _ = orc.logprob(y, ids)
+    b, _ = orc.logprob((y + np.float32(40.0)).astype(np.float32), ids)  # shift invariance (exact shift in f32? not always)
+    assert np.allclose(a, b, atol=2e-5)
+
+
+def test_logprob_brute_force_and_torch(orc):
+    rng = np.random.default_rng(2)
+    y = (rng.standard_normal((64, 513)) * 3).astype(np.float32)
+    ids = rng.integers(0, 513, 64)
+    lp, lse = orc.logprob(y, ids)
+    y64 = y.astype(np.float64)
+    m = y64.max(1, keepdims=True)
+    brute = y64[np.arange(64), ids] - (m[:, 0] + np.log(np.exp(y64 - m).sum(1)))
+    assert np.allclose(lp, brute, rtol=0, atol=1e-12)
+    ce = torch.nn.functional.cross_entropy(torch.from_numpy(y), torch.from_numpy(ids), reduction="none").numpy()
+    lpf, _ = orc.logprob(y, ids, precision=orc.REF_F32)
+    assert np.allclose(-lpf, ce, rtol=1e-5, atol=1e-5)
+    assert np.allclose(lpf, lp, rtol=1e-5, atol=1e-5)
+
+
+def test_reference_kat_cross_entropy_stability(orc):
+    kat = json.load(open(os.path.join(GOLD, "reference_kats.json")))["cross_entropy_stability"]
+    x = np.array([kat["logits"]], np.float32)
+    ids = np.array([kat["target"]])
+    for prec in (orc.EXACT, orc.REF_F32, orc.FAITHFUL):
+        # loss = -lp with upstream 1: one sequence, A = 1, L = 1, G = 1.
+        r = orc.grpo_rows(x, ids, [1.0], [1.0], [1.0], 1.0, precision=prec)
+        assert abs(r.token_loss[0] - kat["expect_loss"]) <= kat["atol"]
+        assert np.all(np.abs(r.dlogits[0] - np.array(kat["expect_grad"])) <= kat["atol"])
+
+
+def test_reference_kat_reduce_max_routes_to_the_max(orc):
+    # reduceMaxVJP sends the upstream gradient to the element equal to the max
+    # ([1,5,3] -> [0,1,0]); in the faithful backward that is the only place the
+    # 1e-4 leak of the log guard appears.
+    kat = json.load(open(os.path.join(GOLD, "reference_kats.json")))["reduce_max_grad"]
+    x = np.array([kat["x"]], np.float32)
+    ex = orc.grpo_rows(x, np.array([2]), [1.0], [1.0], [1.0], 1.0, precision=orc.EXACT)
+    fa = orc.grpo_rows(x, np.array([2]), [1.0], [1.0], [1.0], 1.0, precision=orc.FAITHFUL)
+    diff = fa.dlogits[0] - ex.dlogits[0]
+    route = np.array(kat["expect_grad"])
+    leak = diff[np.argmax(route)]
+    assert leak != 0
+    others = diff - leak * route
+    assert np.all(np.abs(others) < 1e-4 * 2 * abs(ex.coef[0]))
+
+
+# ---- a2/a4/a5 against the torch-autograd fixtures ---------------------------------------
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_oracle_matches_golden(orc, name):
+    c = CASES[name]
+    r = run_oracle_case(orc, c)
+    np.testing.assert_allclose(r.loss, c["exp_loss"], rtol=1e-12, atol=1e-15)
+    np.testing.assert_allclose(r.lp, c["exp_lp"], rtol=1e-12, atol=1e-12)
+    if "ref_logits" in c:
+        np.testing.assert_allclose(r.lr, c["exp_lr"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(r.token_loss, c["exp_token_loss"], rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(r.coef, c["exp_coef"], rtol=1e-10, atol=1e-16)
+    assert np.array_equal(r.adv, c["exp_adv"])
+    scale = max(np.abs(c["exp_coef"]).max(), 1e-30)
+    np.testing.assert_allclose(r.dlogits, c["exp_dlogits"], rtol=1e-6, atol=1e-7 * scale)
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_oracle_f32_order_within_north_star_tolerance(orc, name):
+    c = CASES[name]
+    ex = run_oracle_case(orc, c, orc.EXACT)
+    f = run_oracle_case(orc, c, orc.REF_F32)
+    lse_scale = np.maximum(1.0, np.abs(ex.lp))
+    assert np.all(np.abs(f.lp - ex.lp) <= 1e-5 * lse_scale + 1e-5)
+    assert abs(f.loss - ex.loss) <= 1e-5 * max(1.0, abs(ex.loss))
+    assert np.abs(f.dlogits - ex.dlogits).max() <= 1e-4
+
+
+def test_faithful_reference_ad_within_dlogits_budget(orc):
+    for name in ("v7_ignore_empty", "v64_shifted", "v2_ties_large"):
+        c = CASES[name]
+        ex = run_oracle_case(orc, c, orc.EXACT)
+        fa = run_oracle_case(orc, c, orc.FAITHFUL)
+        gap = np.abs(fa.dlogits - ex.dlogits).max()
+        assert gap <= 1e-4
+        # the guards perturb each row by about 1e-4 relative to its coefficient
+        assert gap <= 3e-4 * np.abs(ex.coef).max() + 1e-7
+
+
+def test_dlogits_invariants(orc):
+    c = CASES["v1024_clip_kl"]
+    r = run_oracle_case(orc, c)
+    S, LS, V = r.dlogits.shape
+    row_sums = r.dlogits.astype(np.float64).sum(-1)
+    assert np.abs(row_sums).max() <= 1e-6 * np.abs(r.coef).max()
+    dead = c["mask"][:, :LS] == 0
+    assert np.all(r.dlogits[dead] == 0)
+
+
+def test_clip_kl_special_cases(orc):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((6, 50)) * 2).astype(np.float32)
+    ids = rng.integers(0, 50, 6)
+    w, A, L = np.ones(6), np.array([1, -1, 0.5, -2, 1, 1], np.float32), np.full(6, 3.0)
+    base = orc.grpo_rows(x, ids, w, A, L, 2.0)  # REINFORCE
+    # beta = 0 and old = lp (ratio 1): the clip-KL gradient reduces to the reference's.
+    on = orc.grpo_rows(x, ids, w, A, L, 2.0, ref_logits=x, loss_mode=orc.CLIP_KL, kl_beta=0.0)
+    np.testing.assert_allclose(on.coef, base.coef, rtol=1e-14)
+    np.testing.assert_allclose(on.dlogits, base.dlogits, rtol=1e-6, atol=1e-12)
+    # ref = policy: KL term and its gradient vanish for any beta.
+    kl = orc.grpo_rows(x, ids, w, A, L, 2.0, ref_logits=x, loss_mode=orc.CLIP_KL, kl_beta=0.5)
+    np.testing.assert_allclose(kl.coef, on.coef, rtol=1e-14)
+    # ratio beyond the trust region on the side the advantage rewards: zero gradient.
+    lp = base.lp
+    old = lp - np.where(A > 0, 1.0, -1.0)   # rho = e (A>0) or 1/e (A<0)
+    cl = orc.grpo_rows(x, ids, w, A, L, 2.0, ref_logits=x, old_logp=old, loss_mode=orc.CLIP_KL, kl_beta=0.0)
+    assert np.all(cl.coef == 0)
+    # ...and the unclipped side keeps -A*rho.
+    old2 = (lp + np.where(A > 0, 1.0, -1.0)).astype(np.float32)   # the ABI carries old_logp as f32
+    uc = orc.grpo_rows(x, ids, w, A, L, 2.0, ref_logits=x, old_logp=old2, loss_mode=orc.CLIP_KL, kl_beta=0.0)
+    rho = np.exp(lp - old2.astype(np.float64))
+    np.testing.assert_allclose(uc.coef, -A * rho / (2.0 * 3.0), rtol=1e-12)
+
+
+def test_finite_differences_tiny(orc):
+    rng = np.random.default_rng(4)
+    V = 9
+    x = (rng.standard_normal((1, V)) * 1.5).astype(np.float64)
+    ref = (x + rng.standard_normal((1, V)) * 0.3)
+    ids = np.array([4])
+    args = dict(ref_logits=ref.astype(np.float32), old_logp=np.array([-2.0], np.float32), loss_mode=orc.CLIP_KL,
+                kl_beta=0.3, clip_eps=0.2)
+
+    def loss_at(xx):
+        r = orc.grpo_rows(xx.astype(np.float32), ids, [1.0], [0.8], [1.0], 1.0, want_dlogits=False, **args)
+        return r.token_loss[0]
+
+    # f32 inputs: probe with steps large enough for f32 storage, central differences.
+    g = orc.grpo_rows(x.astype(np.float32), ids, [1.0], [0.8], [1.0], 1.0, **args).dlogits[0]
+    x32 = x.astype(np.float32).astype(np.float64)
+    h = 1e-2
+    fd = np.array([(loss_at(x32 + h * np.eye(V)[v]) - loss_at(x32 - h * np.eye(V)[v])) / (2 * h) for v in range(V)])
+    np.testing.assert_allclose(g, fd, rtol=2e-3, atol=2e-4)
+
+
+# ---- mutation tests: plausible mistakes in the oracle are caught -----------------
+
+def test_checks_catch_planted_mistakes(orc):
+    c = CASES["v1024_clip_kl"]
+    r = run_oracle_case(orc, c)
+    want = c["exp_dlogits"]
+    scale = np.abs(c["exp_coef"]).max()
+
+    def passes(d):
+        return np.allclose(d, want, rtol=1e-6, atol=1e-7 * scale)
+
+    assert passes(r.dlogits)
+    assert not passes(-r.dlogits)                                   # sign of the coefficient
+    shifted = np.roll(r.dlogits, 1, axis=-1)                        # off-by-one gather index
+    assert not passes(shifted)
+    no_onehot = r.dlogits.copy()                                    # dropped onehot term
+    S, LS, V = no_onehot.shape
+    for s in range(S):
+        for t in range(int(c["rows"])):
+            i = c["ids"][s, t]
+            if c["mask"][s, t] != 0:
+                no_onehot[s, t, i] -= r.coef[s, t]
+    assert not passes(no_onehot)
+    assert not np.allclose(r.loss * (1 + 1e-4), c["exp_loss"], rtol=1e-12)   # a dropped eps-level term
+    transposed = np.transpose(r.dlogits, (1, 0, 2)).reshape(r.dlogits.shape) if S != LS else None
+    if transposed is not None:
+        assert not passes(transposed)
