@@ -105,6 +105,57 @@ __device__ __forceinline__ u32x4 ld16(const void* base, int64_t vec_idx) {
   else return *p;
 }
 
+// Raw buffer resource over one row (base, size in bytes). The hardware range check
+// of a raw buffer access compares the lane (VGPR) offset with num_records (the
+// SGPR offset is not checked), so every access passes its full byte offset in the
+// VGPR: reads past the row end return 0 and writes past it are dropped. No lane
+// then needs a branch around its access (a branch around a load makes the
+// compiler wait for the pending load before the other path writes the same
+// registers, serialising the row), and the descriptor stays in SGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, uint32_t nbytes) {
+  // dword3 0x00020000: untyped 32-bit data format, as for any raw buffer access on gfx9.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0),
+                                           static_cast<int>(nbytes), 0x00020000);
+}
+
+// Cache-policy bits of buffer accesses: 2 = NT (streaming, not retained).
+constexpr int kBufNT = 2;
+
+// 16-byte load / store at byte offset `off` of a row buffer (range-checked).
+template <bool NT>
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, NT ? kBufNT : 0));
+}
+
+template <bool NT>
+__device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, u32x4 v, uint32_t off) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, off, 0, NT ? kBufNT : 0);
+}
+
+// Pack N floats into N output elements (N * kBytes = 16 or 32 bytes) and store them
+// through a row buffer at byte offset `off` (range-checked).
+template <typename TO, int N, bool NT>
+__device__ __forceinline__ void buf_store_vals(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&v)[N]) {
+  if constexpr (TO::kBytes == 4) {
+    static_assert(N % 4 == 0, "f32 output stores whole 16-byte vectors");
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      u32x4 w = {__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]), __float_as_uint(v[4 * q + 2]),
+                 __float_as_uint(v[4 * q + 3])};
+      buf_st16<NT>(r, w, off + 16 * q);
+    }
+  } else {
+    static_assert(N % 8 == 0, "16-bit output stores whole 16-byte vectors");
+#pragma unroll
+    for (int q = 0; q < N / 8; ++q) {
+      u32x4 w = {pack2<TO>(v[8 * q], v[8 * q + 1]), pack2<TO>(v[8 * q + 2], v[8 * q + 3]),
+                 pack2<TO>(v[8 * q + 4], v[8 * q + 5]), pack2<TO>(v[8 * q + 6], v[8 * q + 7])};
+      buf_st16<NT>(r, w, off + 16 * q);
+    }
+  }
+}
+
 // Store N floats as N output elements at element offset `elem` of `base`.
 // N * kBytes is 8, 16 or 32 bytes; `base + elem` is aligned to that size.
 template <typename TO, int N, bool NT>
@@ -141,17 +192,28 @@ __device__ __forceinline__ void store_vals(void* base, int64_t elem, const float
 
 // ---------------------------------------------------------------------------
 // Online log-sum-exp state in base-2 units: m = max(x) * log2(e),
-// s = sum 2^(x*log2(e) - m). m == -inf means "no element yet" (then s == 0).
-// merge() is commutative bit-for-bit, so an xor-butterfly leaves every lane of
-// a wave with the same value, and a fixed cross-wave order makes the result
-// identical on every thread and on every run.
+// s = sum 2^(x*log2(e) - m). s == 0 means "no element yet" (m is then -inf).
+// fmaxf ignores NaN, so NaN inputs never reach m; they reach s (2^NaN = NaN),
+// and every step below keeps a NaN s as NaN (NaN * 0 = NaN), so a NaN logit
+// always ends in a non-finite log-sum-exp. merge() is commutative bit-for-bit,
+// so an xor-butterfly leaves every lane of a wave with the same value, and a
+// fixed cross-wave order makes the result identical on every thread and run.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
   const float M = fmaxf(m, m2);
-  const float a = (m == kNegInf) ? 0.f : s * hw_exp2(m - M);
-  const float b = (m2 == kNegInf) ? 0.f : s2 * hw_exp2(m2 - M);
+  const float a = (s == 0.f) ? 0.f : s * hw_exp2(m - M);
+  const float b = (s2 == 0.f) ? 0.f : s2 * hw_exp2(m2 - M);
   m = M;
   s = a + b;
+}
+
+// Reference point for 2^(x*log2e - ref): the running max, or 0 while it is -inf
+// (all elements so far -inf or NaN), so -inf terms give 0 and NaN terms NaN.
+__device__ __forceinline__ float ms_ref(float m) { return (m == kNegInf) ? 0.f : m; }
+
+// Rescale a running sum from reference m to reference nm (nm >= m).
+__device__ __forceinline__ float ms_rescale(float s, float m, float nm) {
+  return (s == 0.f) ? 0.f : s * hw_exp2(m - ms_ref(nm));
 }
 
 // log-sum-exp (natural units) of a merged state.
@@ -257,6 +319,24 @@ __device__ __forceinline__ RowMeta row_meta(const RowArgs& a, int64_t row) {
   return r;
 }
 
+// k3 KL estimator exp(d) - d - 1 without cancellation: for |d| < 0.5 the series
+// d^2 * sum_k d^k / (k+2)! (truncated after d^7: relative error < 1e-9), else
+// expm1(d) - d (cancellation below a factor of 4 there).
+__device__ __forceinline__ float kl_k3(float d) {
+  if (fabsf(d) < 0.5f) {
+    float p = 1.f / 362880.f;
+    p = fmaf(p, d, 1.f / 40320.f);
+    p = fmaf(p, d, 1.f / 5040.f);
+    p = fmaf(p, d, 1.f / 720.f);
+    p = fmaf(p, d, 1.f / 120.f);
+    p = fmaf(p, d, 1.f / 24.f);
+    p = fmaf(p, d, 1.f / 6.f);
+    p = fmaf(p, d, 0.5f);
+    return d * d * p;
+  }
+  return expm1f(d) - d;
+}
+
 // Per-token loss term and d loss / d logp.
 struct TokenTerms {
   float loss;  // m * l'
@@ -284,14 +364,13 @@ __device__ __forceinline__ TokenTerms token_terms(const RowArgs& a, const RowMet
     const float rc = fminf(fmaxf(rho, lo), hi);
     const float surr = fminf(rho * A, rc * A);
     const float dlr = lr - lp;
-    const float e = expf(dlr);
-    const float k3 = e - dlr - 1.f;
-    o.loss = r.w * (-surr + a.kl_beta * k3);
+    o.loss = r.w * (-surr + a.kl_beta * kl_k3(dlr));
     // The min picks the unclipped branch (gradient -A*rho) unless the ratio left the
     // trust region on the side the advantage's sign rewards.
     const bool unclipped = (A >= 0.f) ? (rho <= hi) : (rho >= lo);
     const float dsurr = unclipped ? -A * rho : 0.f;
-    o.coef = scale * (dsurr + a.kl_beta * (1.f - e));
+    // d k3 / d logp = 1 - exp(ref - logp) = -expm1(ref - logp)
+    o.coef = scale * (dsurr - a.kl_beta * expm1f(dlr));
   }
   return o;
 }

@@ -59,16 +59,27 @@ __device__ __forceinline__ void flag_nonfinite(const RowArgs& a, float lse, floa
 template <typename TI, typename TO, int BLOCK, int NCH, int RB>
 __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   constexpr int EPV = 16 / TI::kBytes;
+  constexpr uint32_t kChunkBytes = BLOCK * 16;          // one chunk: 16 bytes per lane
+  constexpr uint32_t kOutVec = EPV * TO::kBytes;        // output bytes per input vector
   __shared__ float lds[4 * (BLOCK / 64)];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const RowMeta r = row_meta(a, row);
   const int nv = static_cast<int>(a.vocab / EPV);
   const int64_t row_elem = row * a.vocab;
+  const uint32_t in_bytes = static_cast<uint32_t>(a.vocab) * TI::kBytes;
+  const uint32_t out_bytes = static_cast<uint32_t>(a.vocab) * TO::kBytes;
+  const __amdgpu_buffer_rsrc_t drow = row_rsrc(static_cast<char*>(a.dlogits) + row_elem * TO::kBytes, out_bytes);
 
   if (!r.live) {
     write_token_outputs(a, r, 0.f, 0.f, 0.f);
-    if (a.zero_fill) zero_row_vec<TO, EPV, BLOCK>(a.dlogits, row_elem, nv);
+    if (a.zero_fill) {
+      float z[EPV];
+#pragma unroll
+      for (int j = 0; j < EPV; ++j) z[j] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) buf_store_vals<TO, EPV, true>(drow, (k * BLOCK + tid) * kOutVec, z);
+    }
     return;
   }
 
@@ -81,17 +92,16 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   const float xy = TI::load1(xrow, r.id);
   const float ry = has_ref ? TI::load1(rrow, r.id) : 0.f;
 
-  // 1. Policy row -> registers.
+  // 1. Policy row -> registers: all NCH loads back to back through one row
+  //    descriptor (lanes past the row end read 0 and are skipped below).
+  const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xrow, in_bytes);
+  const uint32_t voff = tid * 16u;
   u32x4 xv[NCH];
 #pragma unroll
-  for (int k = 0; k < NCH; ++k) {
-    const int vi = k * BLOCK + tid;
-    if (vi < nv) xv[k] = ld16<true>(xrow, vi);
-    else xv[k] = u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int k = 0; k < NCH; ++k) xv[k] = buf_ld16<true>(xbuf, voff + k * kChunkBytes);
 
   // 2a. Per-lane (max, sum) of the resident policy values.
-  float pm = kNegInf, ps = 0.f;
+  float pm, ps;
   {
     float mx = kNegInf;
 #pragma unroll
@@ -102,34 +112,30 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
         for (int j = 0; j < EPV; ++j) mx = fmaxf(mx, TI::unpack(w, j));
       }
     }
-    if (mx != kNegInf) {
-      const float m2 = mx * kLog2e;
-      float s = 0.f;
+    pm = mx * kLog2e;
+    const float m2 = ms_ref(pm);
+    float s = 0.f;
 #pragma unroll
-      for (int k = 0; k < NCH; ++k) {
-        if (k * BLOCK + tid < nv) {
-          const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
+    for (int k = 0; k < NCH; ++k) {
+      if (k * BLOCK + tid < nv) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
 #pragma unroll
-          for (int j = 0; j < EPV; ++j) s += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -m2));
-        }
+        for (int j = 0; j < EPV; ++j) s += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -m2));
       }
-      pm = m2;
-      ps = s;
     }
+    ps = s;
   }
 
   // 2b. Reference row: online (max, sum) over batches of RB chunks.
   float rm = kNegInf, rs = 0.f;
   if (has_ref) {
+    const __amdgpu_buffer_rsrc_t rbuf = row_rsrc(rrow, in_bytes);
 #pragma unroll
     for (int kb = 0; kb < NCH; kb += RB) {
       u32x4 rv[RB];
 #pragma unroll
-      for (int q = 0; q < RB; ++q) {
-        const int vi = (kb + q) * BLOCK + tid;
-        if (kb + q < NCH && vi < nv) rv[q] = ld16<true>(rrow, vi);
-        else rv[q] = u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int q = 0; q < RB; ++q)
+        if (kb + q < NCH) rv[q] = buf_ld16<true>(rbuf, voff + (kb + q) * kChunkBytes);
       float bm = kNegInf;
 #pragma unroll
       for (int q = 0; q < RB; ++q) {
@@ -139,20 +145,19 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
           for (int j = 0; j < EPV; ++j) bm = fmaxf(bm, TI::unpack(w, j));
         }
       }
-      if (bm != kNegInf) {
-        const float nm = fmaxf(rm, bm * kLog2e);
-        float acc = (rm == kNegInf) ? 0.f : rs * hw_exp2(rm - nm);
+      const float nm = fmaxf(rm, bm * kLog2e);
+      const float ref = ms_ref(nm);
+      float acc = ms_rescale(rs, rm, nm);
 #pragma unroll
-        for (int q = 0; q < RB; ++q) {
-          if (kb + q < NCH && (kb + q) * BLOCK + tid < nv) {
-            const uint32_t* w = reinterpret_cast<const uint32_t*>(&rv[q]);
+      for (int q = 0; q < RB; ++q) {
+        if (kb + q < NCH && (kb + q) * BLOCK + tid < nv) {
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(&rv[q]);
 #pragma unroll
-            for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -nm));
-          }
+          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -ref));
         }
-        rm = nm;
-        rs = acc;
       }
+      rm = nm;
+      rs = acc;
     }
   }
 
@@ -169,25 +174,23 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   const TokenTerms tt = token_terms(a, r, lp, lr);
   write_token_outputs(a, r, lp, lr, tt.loss);
 
-  // 5. dlogits = c * (onehot - softmax) from the resident row.
+  // 5. dlogits = c * (onehot - softmax) from the resident row; stores past the
+  //    row end are dropped by the buffer range check.
   const float c = tt.coef, nc = -tt.coef;
   const int vid = static_cast<int>(r.id / EPV);
   const int kid = vid / BLOCK, tid_id = vid - kid * BLOCK, jid = static_cast<int>(r.id) - vid * EPV;
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
-    const int vi = k * BLOCK + tid;
-    if (vi < nv) {
-      const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
-      float o[EPV];
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
+    float o[EPV];
 #pragma unroll
-      for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -lse2));
-      if (k == kid && tid == tid_id) {
+    for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -lse2));
+    if (k == kid && tid == tid_id) {
 #pragma unroll
-        for (int j = 0; j < EPV; ++j)
-          if (j == jid) o[j] += c;
-      }
-      store_vals<TO, EPV, true>(a.dlogits, row_elem + static_cast<int64_t>(vi) * EPV, o);
+      for (int j = 0; j < EPV; ++j)
+        if (j == jid) o[j] += c;
     }
+    buf_store_vals<TO, EPV, true>(drow, (k * BLOCK + tid) * kOutVec, o);
   }
 }
 
@@ -203,9 +206,12 @@ struct StreamIO {
     u32x4 v;
     float f;
   };
+  // NT: non-temporal (streaming) policy; a temporal load leaves the line in the
+  // caches for a re-read.
+  template <bool NT = true>
   __device__ static __forceinline__ Raw load(const void* row, int vi) {
     Raw r;
-    if constexpr (VEC) r.v = ld16<true>(row, vi);
+    if constexpr (VEC) r.v = ld16<NT>(row, vi);
     else r.f = TI::load1(row, vi);
     return r;
   }
@@ -215,7 +221,9 @@ struct StreamIO {
   }
 };
 
-template <typename TI, typename TO, int BLOCK, int U, bool VEC>
+// NT1: cache policy of the first policy read. When the row is re-read for
+// dlogits, a temporal first read lets the re-read hit the caches.
+template <typename TI, typename TO, int BLOCK, int U, bool VEC, bool NT1>
 __global__ void __launch_bounds__(BLOCK) grpo_stream_kernel(RowArgs a) {
   using IO = StreamIO<TI, VEC>;
   constexpr int EPV = IO::EPV;
@@ -249,7 +257,7 @@ __global__ void __launch_bounds__(BLOCK) grpo_stream_kernel(RowArgs a) {
     for (int q = 0; q < U; ++q) {
       const int vi = base + q * BLOCK + tid;
       if (vi < nv) {
-        xb[q] = IO::load(xrow, vi);
+        xb[q] = IO::template load<NT1>(xrow, vi);
         if (has_ref) rb[q] = IO::load(rrow, vi);
       }
     }
@@ -264,25 +272,27 @@ __global__ void __launch_bounds__(BLOCK) grpo_stream_kernel(RowArgs a) {
         }
       }
     }
-    if (bx != kNegInf) {
+    {
       const float nm = fmaxf(pm, bx * kLog2e);
-      float acc = (pm == kNegInf) ? 0.f : ps * hw_exp2(pm - nm);
+      const float ref = ms_ref(nm);
+      float acc = ms_rescale(ps, pm, nm);
 #pragma unroll
       for (int q = 0; q < U; ++q)
         if (base + q * BLOCK + tid < nv)
 #pragma unroll
-          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(IO::get(xb[q], j), kLog2e, -nm));
+          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(IO::get(xb[q], j), kLog2e, -ref));
       pm = nm;
       ps = acc;
     }
-    if (has_ref && br != kNegInf) {
+    if (has_ref) {
       const float nm = fmaxf(rm, br * kLog2e);
-      float acc = (rm == kNegInf) ? 0.f : rs * hw_exp2(rm - nm);
+      const float ref = ms_ref(nm);
+      float acc = ms_rescale(rs, rm, nm);
 #pragma unroll
       for (int q = 0; q < U; ++q)
         if (base + q * BLOCK + tid < nv)
 #pragma unroll
-          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(IO::get(rb[q], j), kLog2e, -nm));
+          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(IO::get(rb[q], j), kLog2e, -ref));
       rm = nm;
       rs = acc;
     }
@@ -376,25 +386,31 @@ seq_prep_kernel(const void* mask, int32_t mask_u8, int64_t rows, int64_t tok_str
 }
 
 // Group-relative advantages, restating rl_shepherd.zig:466-478 operation by
-// operation in IEEE fp32 with no contraction: sequential sum, mean = sum / n,
-// sequential sum of (r-mean)*(r-mean), std = sqrt(ssd / n) + eps, (r-mean)/std.
+// operation in IEEE fp32: sequential sum, mean = sum / n, sequential sum of
+// (r-mean)*(r-mean), std = sqrt(ssd / n) + eps, (r-mean)/std. hipcc contracts
+// a*b+c into an FMA by default (also inside the __fmul_rn/__fadd_rn helpers,
+// which are compiled outside this scope), so the arithmetic is written with
+// plain operators under contract(off); fp32 '/' and sqrtf are correctly rounded
+// (hipcc's default -fhip-fp32-correctly-rounded-divide-sqrt).
 __global__ void __launch_bounds__(64)
 advantages_kernel(const float* r, int64_t n, int64_t group, float eps, float* adv) {
+#pragma clang fp contract(off)
   const int64_t g = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
   const int64_t i = g * group;
   if (i >= n) return;
   const int64_t e = (i + group < n) ? i + group : n;
   const float cnt = static_cast<float>(e - i);
   float sum = 0.f;
-  for (int64_t k = i; k < e; ++k) sum = __fadd_rn(sum, r[k]);
-  const float mean = __fdiv_rn(sum, cnt);
+  for (int64_t k = i; k < e; ++k) sum = sum + r[k];
+  const float mean = sum / cnt;
   float ssd = 0.f;
   for (int64_t k = i; k < e; ++k) {
-    const float d = __fsub_rn(r[k], mean);
-    ssd = __fadd_rn(ssd, __fmul_rn(d, d));
+    const float d = r[k] - mean;
+    const float d2 = d * d;
+    ssd = ssd + d2;
   }
-  const float sd = __fadd_rn(__fsqrt_rn(__fdiv_rn(ssd, cnt)), eps);
-  for (int64_t k = i; k < e; ++k) adv[k] = __fdiv_rn(__fsub_rn(r[k], mean), sd);
+  const float sd = sqrtf(ssd / cnt) + eps;
+  for (int64_t k = i; k < e; ++k) adv[k] = (r[k] - mean) / sd;
 }
 
 // seq_val[s] = (sum_t token_loss) / seq_len[s] (* adv[s] in REINFORCE mode):
@@ -432,7 +448,9 @@ namespace {
 
 template <typename TI, typename TO, int BLOCK, int NCH>
 hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
-  constexpr int RB = 4;
+  // RB = 2: the largest reference batch that needs no register spill next to a
+  // 19-chunk resident row at 128 VGPRs (4 spills 9 VGPRs and measured ~1% slower).
+  constexpr int RB = 2;
   grpo_resident_kernel<TI, TO, BLOCK, NCH, RB>
       <<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
   return hipGetLastError();
@@ -441,8 +459,14 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
 template <typename TI, typename TO, bool VEC>
 hipError_t launch_stream(const RowArgs& a, int64_t nrows, hipStream_t st) {
   constexpr int BLOCK = 1024, U = 4;
-  grpo_stream_kernel<TI, TO, BLOCK, U, VEC>
-      <<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
+  // Forward only: every byte is read once, so stream it past the caches. With a
+  // backward pass the first policy read stays cacheable for the re-read.
+  if (a.dlogits)
+    grpo_stream_kernel<TI, TO, BLOCK, U, VEC, false>
+        <<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
+  else
+    grpo_stream_kernel<TI, TO, BLOCK, U, VEC, true>
+        <<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
   return hipGetLastError();
 }
 
