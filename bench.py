@@ -103,6 +103,9 @@ def main() -> None:
     ap.add_argument("--force-streaming", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--copy-calibration-gib", type=float, default=0.0,
+                    help="run one device-to-device copy of this many GiB first: under rocprofv3 --pmc its "
+                         "FETCH_SIZE / WRITE_SIZE give the counters' scale factors")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the GRPO loss head shards by whole "
@@ -118,6 +121,12 @@ def main() -> None:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
+    if args.copy_calibration_gib > 0:
+        n = int(args.copy_calibration_gib * (1 << 30)) // 2
+        src = torch.ones(n, dtype=torch.bfloat16, device=dev)
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        del src
     cfg = synth.CONFIGS[args.config]
     clip = args.mode == "clip_kl"
     mode = LossMode.GRPO_CLIP_KL if clip else LossMode.REINFORCE
