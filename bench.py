@@ -93,6 +93,136 @@ def cpu_baseline(inp, cfg, mode_clip_kl: bool, budget_s: float = 12.0, chunk: in
                       f"fwd+bwd (grpo_oracle.cpp, OpenMP {threads} threads)"}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, 2.5 PFLOP/s
+
+
+def cpu_baseline_lmhead(inp, cfg, mode_clip_kl: bool, budget_s: float = 12.0, chunk: int = 64) -> dict:
+    """Time a CPU port of the fused LM-head step on token chunks of the same inputs:
+    fp32 logits hidden.W^T (and W_ref) on BLAS, the oracle's loss rows with dlogits
+    (fp32, reference op order), then dhidden = D.W and dW += D^T.hidden on BLAS."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from oracle import oracle as orc
+
+    threads = min(os.cpu_count() or 1, 16)
+    V, T = cfg.V, cfg.T
+    W = inp["weight"].float().cpu().numpy()
+    Wr = inp["ref_weight"].float().cpu().numpy() if mode_clip_kl else None
+    h_all = inp["hidden"]
+    ids = inp["ids"].view(-1).cpu().numpy()
+    mask = inp["mask"].cpu().numpy()
+    w = mask.reshape(-1)
+    adv = orc.advantages(inp["rewards"].cpu().numpy(), cfg.group)
+    Ls = orc.seq_lengths(mask, T, 0)
+    old = inp["old_logp"].view(-1).cpu().numpy()
+    dW = np.zeros_like(W)
+    order = np.random.default_rng(0).permutation(len(ids))
+    spent, done, live_done = 0.0, 0, 0
+    with threadpool_limits(threads):
+        while spent < budget_s and done < len(ids):
+            idx = np.sort(order[done:done + chunk])
+            hc = h_all.index_select(0, torch.as_tensor(idx, device=h_all.device)).float().cpu().numpy()
+            seq = idx // T
+            t0 = time.perf_counter()
+            Lc = hc @ W.T
+            Rc = hc @ Wr.T if mode_clip_kl else None
+            r = orc.grpo_rows(Lc, ids[idx], w[idx], adv[seq], Ls[seq], float(cfg.S), ref_logits=Rc,
+                              old_logp=old[idx], loss_mode=orc.CLIP_KL if mode_clip_kl else orc.REINFORCE,
+                              clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, precision=orc.REF_F32, dtype=orc.F32,
+                              nthreads=threads)
+            _dh = r.dlogits @ W
+            dW += r.dlogits.T @ hc
+            spent += time.perf_counter() - t0
+            done += len(idx)
+            live_done += int((w[idx] != 0).sum())
+    return {"value": live_done / spent, "unit": "valid tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of {len(ids)} tokens ({live_done} valid) in {spent:.1f} s: fp32 BLAS logits + "
+                      f"oracle loss rows (reference op order) + fp32 BLAS dhidden/dW, {threads} threads"}
+
+
+def bench_lmhead(args) -> None:
+    """Configuration 5: the fused LM-head + GRPO loss step (logits never stored)."""
+    import ctypes
+
+    import torch
+
+    from pcp_amd import grpo, synth
+    from pcp_amd._lib import LossMode, check, lib
+
+    cfg = synth.LMHEAD
+    dev = torch.device("cuda:0")
+    clip = args.mode == "clip_kl"
+    mode = LossMode.GRPO_CLIP_KL if clip else LossMode.REINFORCE
+    t_setup = time.perf_counter()
+    inp = synth.make_lmhead_inputs(cfg, dev)
+    ctx = grpo.default_context(0)
+    fwd = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], rewards=inp["rewards"],
+                              group_size=cfg.group, want_grads=False, ctx=ctx)
+    inp["old_logp"] = (fwd.logp + inp["old_shift"]).contiguous()
+    torch.cuda.synchronize()
+    t_setup = time.perf_counter() - t_setup
+    kw = dict(ref_weight=inp["ref_weight"] if clip else None, rewards=inp["rewards"], group_size=cfg.group,
+              old_logp=inp["old_logp"], loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, ctx=ctx)
+    out = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], **kw)
+    for _ in range(args.warmup):
+        grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], outputs=out, sync=False, **kw)
+    ctx.sync()
+    torch.cuda.synchronize()
+    check(lib().pcp_profile_start(ctx.handle, args.steps), ctx.handle)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], outputs=out, sync=False, **kw)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx.sync()
+    n_l = ctypes.c_int(0)
+    tot = ctypes.c_double(0)
+    check(lib().pcp_profile_stop(ctx.handle, ctypes.byref(n_l), ctypes.byref(tot)), ctx.handle)
+    kernel_ms = tot.value / max(n_l.value, 1)
+
+    N, H, V = cfg.N, cfg.H, cfg.V
+    live = int(inp["mask"].sum().item())
+    ms_step = elapsed * 1e3 / args.steps
+    # Dense products per step: forward logits per model, recomputed logits, dhidden, dW.
+    products = (2 if clip else 1) + 3
+    step_flops = products * 2.0 * N * H * V
+    tile_flops = 2.0 * N * H * V
+    achieved = tile_flops / (kernel_ms / 1e3) / 1e12
+    line = {
+        "metric": "GRPO fused LM-head + loss fwd+bwd tokens/s, H=4096, V=151936 bf16",
+        "value": live / (ms_step / 1e3),
+        "unit": "valid tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Philox/PCG64 inputs of the configuration)",
+        "config": {"workload": f"config5 {cfg.name}: {cfg.prompts} prompts x G={cfg.group}, T={cfg.T}, "
+                               f"hidden {H}, V={V}, bf16 hidden/weights, loss={args.mode}",
+                   "tokens": N, "valid_tokens": live, "global_batch": cfg.S, "seq_len": cfg.T},
+        "step_tflops": step_flops / (ms_step / 1e3) / 1e12,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "lm_tile_kernel<kLmFwd> (policy logits tiles)", "kernel_ms": kernel_ms,
+                     "algorithmic_flops": tile_flops},
+        "setup_s": t_setup,
+    }
+    tfile = os.path.join(ROOT, "profiles", f"traffic_config5_{args.mode}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_lmhead(inp, cfg, clip, budget_s=args.cpu_budget)
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +250,9 @@ def main() -> None:
     from pcp_amd._lib import LossMode, check, lib
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.config == 5:
+        bench_lmhead(args)
+        return
     dev = torch.device("cuda:0")
     if args.copy_calibration_gib > 0:
         n = int(args.copy_calibration_gib * (1 << 30)) // 2

@@ -215,6 +215,54 @@ int pcp_grpo_advantages(pcp_ctx* ctx, const float* rewards, int64_t n, int64_t g
 int pcp_grpo_loss_fwd_bwd(pcp_ctx* ctx, const pcp_grpo_args* a);
 
 /*
+ * a6: fused LM-head + GRPO loss (the LM head of tools/export_qwen_forward.py:146-147
+ * and its VJP, src/autodiff/vjp_rules.zig:426-497). Tokens use the aligned layout:
+ * token t of sequence s is row s*rows + t of hidden_states and scores ids[s*rows+t].
+ * logits = hidden_states * weight^T are computed in 128 x 128 tiles on bf16 MFMA and
+ * reduced in-tile (per-token log-sum-exp and target logit); full logits are never
+ * stored. The backward recomputes logit tiles per vocab chunk into bf16 dlogits and
+ * runs dhidden = dlogits * weight and dweight = dlogits^T * hidden_states (fp32).
+ */
+typedef struct pcp_lmhead_args {
+  int64_t n_seq;              /* sequences                                                */
+  int64_t rows;               /* tokens per sequence                                      */
+  int64_t hidden;             /* H; multiple of 64                                        */
+  int64_t vocab;              /* V                                                        */
+  int64_t group_size;         /* sequences per advantage group                            */
+  int64_t vocab_chunk;        /* backward chunk width; 0 => 16384 (multiple of 128)       */
+  int32_t ids_dtype;          /* PCP_I64 | PCP_I32                                        */
+  int32_t mask_dtype;         /* PCP_F32 | PCP_BOOL                                       */
+  const void* hidden_states;  /* [n_seq*rows, H] bf16                                     */
+  const void* weight;         /* [V, H] bf16 (policy LM head)                             */
+  const void* ref_weight;     /* [V, H] bf16; required for PCP_LOSS_GRPO_CLIP_KL          */
+  const void* ids;            /* [n_seq*rows]                                             */
+  const void* mask;           /* [n_seq*rows] or NULL (all ones)                          */
+  const float* old_logp;      /* [n_seq*rows] or NULL (on-policy)                         */
+  const float* advantages;    /* [n_seq] or NULL (from rewards)                           */
+  const float* rewards;       /* [n_seq]                                                  */
+  float* logp;                /* optional [n_seq*rows] outputs                            */
+  float* ref_logp;
+  float* token_loss;
+  float* advantages_out;      /* optional [n_seq]                                         */
+  float* loss;                /* optional device scalar                                   */
+  float* dhidden;             /* [n_seq*rows, H] f32, or NULL                             */
+  float* dweight;             /* [V, H] f32, or NULL                                      */
+  int32_t loss_mode;
+  float clip_eps;
+  float kl_beta;
+  float std_eps;
+  float loss_norm;            /* 0 => n_seq                                               */
+  uint32_t flags;             /* PCP_FLAG_ASYNC                                           */
+  void* stream;
+} pcp_lmhead_args;
+
+/* Defaults as pcp_grpo_args_init (ids i64, mask f32, eps 0.2, beta 0.04, std_eps 1e-8). */
+void pcp_lmhead_args_init(pcp_lmhead_args* a);
+/* Forward loss (+ logp / ref logp / token losses) and, when dhidden / dweight are
+ * given, their gradients. */
+int pcp_grpo_lmhead_fwd_bwd(pcp_ctx* ctx, const pcp_lmhead_args* a);
+
+/*
  * Kernel timing (no reference counterpart: the reference never times its step).
  * Between pcp_profile_start and pcp_profile_stop, every row-kernel launch of
  * pcp_grpo_loss_fwd_bwd / pcp_grpo_logprob_fwd is bracketed by HIP events recorded

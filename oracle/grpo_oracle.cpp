@@ -34,7 +34,7 @@
 
 namespace {
 
-enum Dtype { kF16 = 0, kBF16 = 1, kF32 = 2 };
+enum Dtype { kF16 = 0, kBF16 = 1, kF32 = 2, kF64 = 3 };
 enum Precision { kExact = 0, kRefOrderF32 = 1, kFaithful = 2 };
 enum LossMode { kReinforce = 0, kClipKl = 1 };
 
@@ -81,13 +81,18 @@ inline float f16_to_f32(uint16_t h) {
   return f;
 }
 
-inline float load(const void* p, int dt, int64_t i) {
+// Element i of a logits array as a double (exact for every supported dtype);
+// kF64 inputs carry logits computed exactly elsewhere (e.g. hidden * W^T in f64).
+inline double loadd(const void* p, int dt, int64_t i) {
   switch (dt) {
     case kBF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
     case kF16: return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    case kF64: return static_cast<const double*>(p)[i];
     default: return static_cast<const float*>(p)[i];
   }
 }
+// The same element rounded to f32 (the reference graph runs in f32).
+inline float load(const void* p, int dt, int64_t i) { return static_cast<float>(loadd(p, dt, i)); }
 
 // Guard + clamp of one gradient edge (engine.zig:622-681): non-finite -> 0,
 // then clamp to [-100, 100].
@@ -107,11 +112,11 @@ template <typename R>
 RowLse<R> row_lse(const void* p, int dt, int64_t base, int64_t V) {
   R m = -INFINITY;
   for (int64_t v = 0; v < V; ++v) {
-    const R x = static_cast<R>(load(p, dt, base + v));
+    const R x = static_cast<R>(loadd(p, dt, base + v));
     if (x > m) m = x;
   }
   R S = 0;
-  for (int64_t v = 0; v < V; ++v) S += std::exp(static_cast<R>(load(p, dt, base + v)) - m);
+  for (int64_t v = 0; v < V; ++v) S += std::exp(static_cast<R>(loadd(p, dt, base + v)) - m);
   return {m, S, m + std::log(S)};
 }
 
@@ -121,7 +126,7 @@ extern "C" {
 
 typedef struct oracle_rows_args {
   int64_t nrows, vocab;
-  int32_t dtype;             // 0 f16, 1 bf16, 2 f32 (pcp_dtype codes)
+  int32_t dtype;             // 0 f16, 1 bf16, 2 f32, 3 f64 (pcp_dtype codes)
   const void* logits;        // [nrows, V]
   const void* ref_logits;    // [nrows, V] or NULL
   const int64_t* ids;        // [nrows]; -100 = ignore
@@ -178,7 +183,7 @@ void oracle_logprob(const void* logits, int32_t dtype, int64_t nrows, int64_t vo
     if (precision == kExact) {
       const RowLse<double> r = row_lse<double>(logits, dtype, base, vocab);
       l = r.lse;
-      x = (id >= 0 && id < vocab) ? static_cast<double>(load(logits, dtype, base + id)) : 0.0;
+      x = (id >= 0 && id < vocab) ? loadd(logits, dtype, base + id) : 0.0;
       if (lp) lp[n] = (id >= 0 && id < vocab) ? x - l : 0.0;
     } else {
       const RowLse<float> r = row_lse<float>(logits, dtype, base, vocab);
@@ -215,11 +220,11 @@ int oracle_grpo_rows(const oracle_rows_args* a) {
     const double w = a->w[n], A = a->adv[n], L = a->seq_len[n], G = a->loss_norm;
     if (a->precision == kExact) {
       const RowLse<double> p = row_lse<double>(a->logits, a->dtype, base, V);
-      const double lp = static_cast<double>(load(a->logits, a->dtype, base + id)) - p.lse;
+      const double lp = loadd(a->logits, a->dtype, base + id) - p.lse;
       double lr = 0.0;
       if (a->ref_logits) {
         const RowLse<double> q = row_lse<double>(a->ref_logits, a->dtype, base, V);
-        lr = static_cast<double>(load(a->ref_logits, a->dtype, base + id)) - q.lse;
+        lr = loadd(a->ref_logits, a->dtype, base + id) - q.lse;
       }
       double tl, c;
       const double scale = w / (G * L);
@@ -243,7 +248,7 @@ int oracle_grpo_rows(const oracle_rows_args* a) {
       if (a->coef) a->coef[n] = c;
       if (d) {
         for (int64_t v = 0; v < V; ++v) {
-          const double sm = std::exp(static_cast<double>(load(a->logits, a->dtype, base + v)) - p.lse);
+          const double sm = std::exp(loadd(a->logits, a->dtype, base + v) - p.lse);
           d[v] = static_cast<float>(c * ((v == id ? 1.0 : 0.0) - sm));
         }
       }

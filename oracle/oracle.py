@@ -28,7 +28,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libpcp_oracle.so")
 
-F16, BF16, F32 = 0, 1, 2
+F16, BF16, F32, F64 = 0, 1, 2, 3
 EXACT, REF_F32, FAITHFUL = 0, 1, 2
 REINFORCE, CLIP_KL = 0, 1
 IGNORE_INDEX = -100
@@ -93,6 +93,25 @@ def bf16_to_f32(h: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def lmhead_logits(hidden_bits: np.ndarray, weight_bits: np.ndarray) -> np.ndarray:
+    """Exact float64 logits hidden * W^T of bf16 operands (bit patterns, uint16): the
+    LM head of tools/export_qwen_forward.py:147 evaluated without rounding."""
+    return bf16_to_f32(hidden_bits).astype(np.float64) @ bf16_to_f32(weight_bits).astype(np.float64).T
+
+
+def lmhead_grads(hidden_bits: np.ndarray, weight_bits: np.ndarray, logits: np.ndarray, lse: np.ndarray,
+                 coef: np.ndarray, ids: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """float64 (dhidden, dW) of the LM head: D = c * (onehot - softmax), dhidden = D W,
+    dW = D^T hidden (matmulVJP, src/autodiff/vjp_rules.zig:426-497)."""
+    N, V = logits.shape
+    D = -np.exp(logits - lse[:, None]) * coef[:, None]
+    live = (coef != 0) & (ids >= 0) & (ids < V)
+    D[np.nonzero(live)[0], ids[live]] += coef[live]
+    h = bf16_to_f32(hidden_bits).astype(np.float64)
+    W = bf16_to_f32(weight_bits).astype(np.float64)
+    return D @ W, D.T @ h
+
+
 def widen(x: np.ndarray, dtype: int) -> np.ndarray:
     """Logits array in its storage form (uint16 for bf16, float16, float32) -> float64."""
     if dtype == BF16:
@@ -107,6 +126,8 @@ def storage_dtype_code(x: np.ndarray, bf16: bool = False) -> int:
         return F16
     if x.dtype == np.float32:
         return F32
+    if x.dtype == np.float64:
+        return F64
     raise TypeError(f"unsupported logits storage {x.dtype}")
 
 

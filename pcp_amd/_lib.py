@@ -90,6 +90,24 @@ class GrpoArgs(ctypes.Structure):
     ]
 
 
+class LmheadArgs(ctypes.Structure):
+    """pcp_lmhead_args (field order and types as in include/pcp_grpo.h)."""
+    _fields_ = [
+        ("n_seq", ctypes.c_int64), ("rows", ctypes.c_int64), ("hidden", ctypes.c_int64),
+        ("vocab", ctypes.c_int64), ("group_size", ctypes.c_int64), ("vocab_chunk", ctypes.c_int64),
+        ("ids_dtype", ctypes.c_int32), ("mask_dtype", ctypes.c_int32),
+        ("hidden_states", ctypes.c_void_p), ("weight", ctypes.c_void_p), ("ref_weight", ctypes.c_void_p),
+        ("ids", ctypes.c_void_p), ("mask", ctypes.c_void_p), ("old_logp", ctypes.c_void_p),
+        ("advantages", ctypes.c_void_p), ("rewards", ctypes.c_void_p),
+        ("logp", ctypes.c_void_p), ("ref_logp", ctypes.c_void_p), ("token_loss", ctypes.c_void_p),
+        ("advantages_out", ctypes.c_void_p), ("loss", ctypes.c_void_p),
+        ("dhidden", ctypes.c_void_p), ("dweight", ctypes.c_void_p),
+        ("loss_mode", ctypes.c_int32), ("clip_eps", ctypes.c_float), ("kl_beta", ctypes.c_float),
+        ("std_eps", ctypes.c_float), ("loss_norm", ctypes.c_float), ("flags", ctypes.c_uint32),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
 # Every symbol the headers in include/ declare, with its ctypes signature.
 _VP, _I, _I64, _F, _U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint64
 SIGNATURES = {
@@ -107,6 +125,8 @@ SIGNATURES = {
     "pcp_grpo_logprob_fwd": (_I, [_VP, ctypes.POINTER(GrpoArgs)]),
     "pcp_grpo_advantages": (_I, [_VP, _VP, _I64, _I64, _F, _VP, _VP]),
     "pcp_grpo_loss_fwd_bwd": (_I, [_VP, ctypes.POINTER(GrpoArgs)]),
+    "pcp_lmhead_args_init": (None, [ctypes.POINTER(LmheadArgs)]),
+    "pcp_grpo_lmhead_fwd_bwd": (_I, [_VP, ctypes.POINTER(LmheadArgs)]),
     "pcp_profile_start": (_I, [_VP, _I]),
     "pcp_profile_stop": (_I, [_VP, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double)]),
     "pcp_version": (ctypes.c_char_p, []),

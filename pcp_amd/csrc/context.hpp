@@ -23,6 +23,7 @@ struct pcp_ctx {
   std::vector<hipEvent_t> prof_start, prof_stop;
   int prof_used = 0;
   bool prof_on = false;
+  void* blas = nullptr;           // rocblas_handle, created on first LM-head backward
 };
 
 namespace pcp {
@@ -68,5 +69,8 @@ int ensure_scratch(pcp_ctx* ctx, size_t bytes);
 
 // After synchronising: read and clear the device error word, map it to a status.
 int collect_device_errors(pcp_ctx* ctx);
+
+// Release the context's BLAS handle (defined with the LM-head path).
+void release_blas(pcp_ctx* ctx);
 
 }  // namespace pcp

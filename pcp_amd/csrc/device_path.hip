@@ -337,6 +337,7 @@ void pcp_destroy(pcp_ctx* ctx) {
   if (hipSetDevice(ctx->device) == hipSuccess) {
     (void)hipDeviceSynchronize();
     release_profile_events(ctx);
+    release_blas(ctx);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->d_err) (void)hipFree(ctx->d_err);
   }

@@ -1,0 +1,53 @@
+// Host-side launch interface of the fused LM-head kernels (lmhead_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pcp {
+
+struct RowArgs;
+
+enum { kLmFwd = 0, kLmBwd = 1 };
+
+// One launch covers token tiles [0, ntt) x vocab tiles [vt0, vt0 + nvt) of 128 x 128.
+struct LmTileArgs {
+  const void* A;        // hidden [N, H] bf16, row-major
+  const void* B;        // weight [V, H] bf16, row-major
+  int N, V, H;          // H % 64 == 0
+  int vt0, nvt, ntt;
+  const void* ids;      // [N] target ids
+  int ids_i64;
+  // kLmFwd
+  float2* part;         // [N, ldp]: per vocab tile (max * log2e, sum 2^(x*log2e - max))
+  int ldp;
+  float* tgt;           // [N] target logit
+  // kLmBwd
+  const float* lse2;    // [N] base-2 log-sum-exp
+  const float* coef;    // [N] d loss / d logp
+  void* dchunk;         // [N, ldd] bf16 dlogits of vocab [vc0, vc0 + ldd)
+  int vc0, ldd;
+};
+
+struct LmReduceArgs {
+  const float2* part;
+  int64_t N;
+  int ldp, nvt;
+  float* lse2;          // out
+};
+
+struct LmTermsArgs {
+  int64_t N;
+  const float* tgt;
+  const float* lse2;
+  const float* ref_tgt;   // nullptr: no reference model
+  const float* ref_lse2;
+  float* coef;            // out
+};
+
+size_t lm_tile_smem_bytes();
+hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st);
+hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st);
+hipError_t launch_lm_terms(const RowArgs& ra, const LmTermsArgs& a, hipStream_t st);
+
+}  // namespace pcp

@@ -1,0 +1,258 @@
+// Device-pointer entry point of the fused LM-head + GRPO loss (pcp_grpo_lmhead_fwd_bwd).
+//
+// Forward, per model (policy, then reference): MFMA logits tiles reduced in-tile to
+// per-(token, vocab tile) log-sum-exp partials and the target logit; one wave per
+// token merges the partials. Then the GRPO terms per token and the loss reduction
+// (the same kernels as the logits-input path). Backward, per vocab chunk: logits
+// tiles recomputed into bf16 dlogits, then two plain GEMMs on rocBLAS:
+//   dhidden (+)= dlogits_chunk * W_chunk,   dW_chunk = dlogits_chunk^T * hidden.
+// This mirrors the LM head's VJP (src/autodiff/vjp_rules.zig:426-497, matmulVJP).
+
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <cstdint>
+#include <cstring>
+
+#include "context.hpp"
+#include "grpo_device.hpp"
+#include "grpo_launch.hpp"
+#include "lmhead_launch.hpp"
+#include "pcp_grpo.h"
+
+namespace pcp {
+namespace {
+
+constexpr int kTile = 128;
+constexpr int64_t kDefaultChunk = 16384;
+
+inline size_t r256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+int validate_lm(const pcp_lmhead_args* a) {
+  if (!a) return fail(nullptr, PCP_ERR_INVALID_ARG, "args is NULL");
+  if (a->n_seq < 1 || a->rows < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "n_seq and rows must be >= 1");
+  if (a->hidden < 64 || a->hidden % 64 != 0 || a->hidden > (1 << 20))
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden must be a positive multiple of 64 (got %lld)", (long long)a->hidden);
+  if (a->vocab < 1 || a->vocab > (1 << 30)) return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab out of range");
+  if (a->group_size < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "group_size must be >= 1");
+  int64_t n;
+  if (mul_overflows(a->n_seq, a->rows, &n) || n > (1 << 28))
+    return fail(nullptr, PCP_ERR_OVERFLOW, "n_seq * rows exceeds 2^28 tokens");
+  if (a->vocab_chunk < 0 || a->vocab_chunk % kTile != 0)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab_chunk must be a multiple of 128");
+  if (!a->hidden_states || !a->weight || !a->ids) return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden_states / weight / ids is NULL");
+  if (a->ids_dtype != PCP_I64 && a->ids_dtype != PCP_I32) return fail(nullptr, PCP_ERR_DTYPE, "ids dtype must be i64 or i32");
+  if (a->mask && a->mask_dtype != PCP_F32 && a->mask_dtype != PCP_BOOL)
+    return fail(nullptr, PCP_ERR_DTYPE, "mask dtype must be f32 or bool");
+  if (a->loss_mode != PCP_LOSS_REINFORCE && a->loss_mode != PCP_LOSS_GRPO_CLIP_KL)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "unknown loss_mode %d", a->loss_mode);
+  if (a->loss_mode == PCP_LOSS_GRPO_CLIP_KL && !a->ref_weight)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "GRPO_CLIP_KL needs ref_weight");
+  if (!a->advantages && !a->rewards) return fail(nullptr, PCP_ERR_INVALID_ARG, "advantages and rewards are both NULL");
+  if (!(a->clip_eps >= 0.f && a->clip_eps < 1.f)) return fail(nullptr, PCP_ERR_INVALID_ARG, "clip_eps must be in [0, 1)");
+  if (!(a->loss_norm >= 0.f)) return fail(nullptr, PCP_ERR_INVALID_ARG, "loss_norm must be >= 0");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(a->hidden_states) | reinterpret_cast<uintptr_t>(a->weight) |
+                       reinterpret_cast<uintptr_t>(a->ref_weight);
+  if (al & 15u) return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden_states / weights must be 16-byte aligned");
+  return PCP_OK;
+}
+
+int blas_status(pcp_ctx* ctx, rocblas_status s, const char* what) {
+  if (s == rocblas_status_success) return PCP_OK;
+  return fail(ctx, PCP_ERR_DEVICE, "%s: rocBLAS status %d", what, static_cast<int>(s));
+}
+
+int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
+  int rc = validate_lm(a);
+  if (rc != PCP_OK) {
+    if (ctx) ctx->last_error = thread_error();
+    return rc;
+  }
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  hipStream_t st = static_cast<hipStream_t>(a->stream);
+
+  const int64_t S = a->n_seq, T = a->rows, N = S * T, H = a->hidden, V = a->vocab;
+  const int nvt = static_cast<int>((V + kTile - 1) / kTile);
+  const int ntt = static_cast<int>((N + kTile - 1) / kTile);
+  const bool ref = a->loss_mode == PCP_LOSS_GRPO_CLIP_KL;
+  const bool bwd = a->dhidden || a->dweight;
+  const int64_t chunk = a->vocab_chunk ? a->vocab_chunk : kDefaultChunk;
+  const float loss_norm = a->loss_norm > 0.f ? a->loss_norm : static_cast<float>(S);
+
+  // Scratch layout.
+  size_t off = 0;
+  auto take = [&](size_t bytes) { const size_t o = off; off += r256(bytes); return o; };
+  const size_t o_adv = take(4 * S), o_len = take(4 * S), o_scale = take(4 * S), o_val = take(4 * S), o_loss = take(4);
+  const size_t o_tl = a->token_loss ? 0 : take(4 * N);
+  const size_t o_part = take(8 * static_cast<size_t>(N) * nvt);
+  const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
+  const size_t o_chunk = bwd ? take(2 * static_cast<size_t>(N) * chunk) : 0;
+  rc = ensure_scratch(ctx, off);
+  if (rc != PCP_OK) return rc;
+  char* sp = static_cast<char*>(ctx->scratch);
+  auto F = [&](size_t o) { return reinterpret_cast<float*>(sp + o); };
+  float* tl = a->token_loss ? a->token_loss : F(o_tl);
+  float2* part = reinterpret_cast<float2*>(sp + o_part);
+
+  // Advantages and per-sequence lengths.
+  const float* adv = a->advantages;
+  if (!adv) {
+    if ((e = launch_advantages(a->rewards, S, a->group_size, a->std_eps, F(o_adv), st)) != hipSuccess)
+      return hip_fail(ctx, e, "advantages launch");
+    adv = F(o_adv);
+  }
+  if (a->advantages_out && a->advantages_out != adv &&
+      (e = hipMemcpyAsync(a->advantages_out, adv, 4 * S, hipMemcpyDeviceToDevice, st)) != hipSuccess)
+    return hip_fail(ctx, e, "copying advantages");
+  const int mask_u8 = a->mask_dtype == PCP_BOOL;
+  if ((e = launch_seq_prep(a->mask, mask_u8, S, T, T, 0, loss_norm, F(o_len), F(o_scale), st)) != hipSuccess)
+    return hip_fail(ctx, e, "seq_prep launch");
+
+  // Forward, per model: tiles -> partials + target logit; merge -> lse2.
+  LmTileArgs ta;
+  std::memset(&ta, 0, sizeof(ta));
+  ta.A = a->hidden_states;
+  ta.N = static_cast<int>(N);
+  ta.V = static_cast<int>(V);
+  ta.H = static_cast<int>(H);
+  ta.vt0 = 0;
+  ta.nvt = nvt;
+  ta.ntt = ntt;
+  ta.ids = a->ids;
+  ta.ids_i64 = a->ids_dtype == PCP_I64;
+  ta.part = part;
+  ta.ldp = nvt;
+  LmReduceArgs rd{part, N, nvt, nvt, nullptr};
+  for (int m = 0; m < (ref ? 2 : 1); ++m) {
+    ta.B = m == 0 ? a->weight : a->ref_weight;
+    ta.tgt = F(m == 0 ? o_tgt : o_rtgt);
+    const bool timed = m == 0 && ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
+    if (timed && (e = hipEventRecord(ctx->prof_start[ctx->prof_used], st)) != hipSuccess)
+      return hip_fail(ctx, e, "hipEventRecord");
+    if ((e = launch_lm_tiles(kLmFwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head forward tiles");
+    if (timed && (e = hipEventRecord(ctx->prof_stop[ctx->prof_used++], st)) != hipSuccess)
+      return hip_fail(ctx, e, "hipEventRecord");
+    rd.lse2 = F(m == 0 ? o_l2 : o_rl2);
+    if ((e = launch_lm_reduce(rd, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head reduce");
+  }
+
+  // GRPO terms and the loss.
+  RowArgs ra;
+  std::memset(&ra, 0, sizeof(ra));
+  ra.ids = a->ids;
+  ra.mask = a->mask;
+  ra.old_logp = a->old_logp;
+  ra.adv = adv;
+  ra.seq_scale = F(o_scale);
+  ra.logp = a->logp;
+  ra.ref_logp = a->ref_logp;
+  ra.token_loss = tl;
+  ra.err = ctx->d_err;
+  ra.vocab = V;
+  ra.rows = T;
+  ra.logit_stride = T;
+  ra.tok_stride = T;
+  ra.tok_offset = 0;
+  ra.ids_i64 = ta.ids_i64;
+  ra.mask_u8 = mask_u8;
+  ra.loss_mode = a->loss_mode;
+  ra.clip_eps = a->clip_eps;
+  ra.kl_beta = a->kl_beta;
+  LmTermsArgs tma{N, F(o_tgt), F(o_l2), ref ? F(o_rtgt) : nullptr, ref ? F(o_rl2) : nullptr, F(o_coef)};
+  if ((e = launch_lm_terms(ra, tma, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head terms");
+  if ((e = launch_loss_reduce(tl, S, T, T, 0, F(o_len), adv, a->loss_mode == PCP_LOSS_REINFORCE, loss_norm,
+                              F(o_val), a->loss ? a->loss : F(o_loss), st)) != hipSuccess)
+    return hip_fail(ctx, e, "loss reduction");
+
+  // Backward per vocab chunk.
+  if (bwd) {
+    if (!ctx->blas) {
+      rocblas_handle h = nullptr;
+      if ((rc = blas_status(ctx, rocblas_create_handle(&h), "rocblas_create_handle")) != PCP_OK) return rc;
+      ctx->blas = h;
+    }
+    rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
+    if ((rc = blas_status(ctx, rocblas_set_stream(h, st), "rocblas_set_stream")) != PCP_OK) return rc;
+    ta.B = a->weight;
+    ta.lse2 = F(o_l2);
+    ta.coef = F(o_coef);
+    ta.dchunk = sp + o_chunk;
+    ta.ldd = static_cast<int>(chunk);
+    const float one = 1.f, zero = 0.f;
+    for (int64_t vc0 = 0; vc0 < V; vc0 += chunk) {
+      const int64_t w = (V - vc0 < chunk) ? V - vc0 : chunk;
+      ta.vc0 = static_cast<int>(vc0);
+      ta.vt0 = static_cast<int>(vc0 / kTile);
+      ta.nvt = static_cast<int>((w + kTile - 1) / kTile);
+      if ((e = launch_lm_tiles(kLmBwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head backward tiles");
+      const void* wc = static_cast<const char*>(a->weight) + vc0 * H * 2;
+      if (a->dhidden) {
+        // Column-major view: dhidden^T [H, N] (+)= W_c^T [H, w] * D^T [w, N].
+        rc = blas_status(ctx,
+                         rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_none, static_cast<int>(H),
+                                         static_cast<int>(N), static_cast<int>(w), &one, wc, rocblas_datatype_bf16_r,
+                                         static_cast<int>(H), ta.dchunk, rocblas_datatype_bf16_r,
+                                         static_cast<int>(chunk), vc0 == 0 ? &zero : &one, a->dhidden,
+                                         rocblas_datatype_f32_r, static_cast<int>(H), a->dhidden,
+                                         rocblas_datatype_f32_r, static_cast<int>(H), rocblas_datatype_f32_r,
+                                         rocblas_gemm_algo_standard, 0, 0),
+                         "dhidden GEMM");
+        if (rc != PCP_OK) return rc;
+      }
+      if (a->dweight) {
+        // Column-major view: dW_c^T [H, w] = hidden^T [H, N] * D [N, w].
+        float* dw = a->dweight + vc0 * H;
+        rc = blas_status(ctx,
+                         rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_transpose, static_cast<int>(H),
+                                         static_cast<int>(w), static_cast<int>(N), &one, a->hidden_states,
+                                         rocblas_datatype_bf16_r, static_cast<int>(H), ta.dchunk,
+                                         rocblas_datatype_bf16_r, static_cast<int>(chunk), &zero, dw,
+                                         rocblas_datatype_f32_r, static_cast<int>(H), dw, rocblas_datatype_f32_r,
+                                         static_cast<int>(H), rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
+                                         0),
+                         "dweight GEMM");
+        if (rc != PCP_OK) return rc;
+      }
+    }
+  }
+
+  if (a->flags & PCP_FLAG_ASYNC) {
+    ctx->pending.insert(st);
+    return PCP_OK;
+  }
+  if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+  return collect_device_errors(ctx);
+}
+
+}  // namespace
+
+void release_blas(pcp_ctx* ctx) {
+  if (ctx && ctx->blas) {
+    (void)rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
+    ctx->blas = nullptr;
+  }
+}
+
+}  // namespace pcp
+
+using namespace pcp;
+
+extern "C" {
+
+void pcp_lmhead_args_init(pcp_lmhead_args* a) {
+  if (!a) return;
+  std::memset(a, 0, sizeof(*a));
+  a->group_size = 1;
+  a->ids_dtype = PCP_I64;
+  a->mask_dtype = PCP_F32;
+  a->loss_mode = PCP_LOSS_REINFORCE;
+  a->clip_eps = 0.2f;
+  a->kl_beta = 0.04f;
+  a->std_eps = 1e-8f;
+}
+
+int pcp_grpo_lmhead_fwd_bwd(pcp_ctx* ctx, const pcp_lmhead_args* a) { return run_lm(ctx, a); }
+
+}  // extern "C"

@@ -198,3 +198,64 @@ def advantages(rewards: torch.Tensor, group_size: int, std_eps: float = 1e-8, *,
     check(lib().pcp_grpo_advantages(ctx.handle, _ptr(rewards), rewards.numel(), int(group_size),
                                     ctypes.c_float(std_eps), _ptr(out), _stream_handle(stream)), ctx.handle)
     return out
+
+
+@dataclass
+class LmheadOutputs:
+    loss: torch.Tensor          # f32 scalar
+    logp: torch.Tensor          # [S, T] f32
+    ref_logp: torch.Tensor | None
+    token_loss: torch.Tensor    # [S, T] f32
+    advantages: torch.Tensor    # [S] f32
+    dhidden: torch.Tensor | None  # [S*T, H] f32
+    dweight: torch.Tensor | None  # [V, H] f32
+
+
+def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor, mask: torch.Tensor | None = None,
+                   *, ref_weight: torch.Tensor | None = None, advantages: torch.Tensor | None = None,
+                   rewards: torch.Tensor | None = None, group_size: int = 1, old_logp: torch.Tensor | None = None,
+                   loss_mode: int = LossMode.REINFORCE, clip_eps: float = 0.2, kl_beta: float = 0.04,
+                   loss_norm: float = 0.0, std_eps: float = 1e-8, want_grads: bool = True, vocab_chunk: int = 0,
+                   outputs: LmheadOutputs | None = None, sync: bool = True, stream=None,
+                   ctx: Context | None = None) -> LmheadOutputs:
+    """Fused LM-head + GRPO loss (pcp_grpo_lmhead_fwd_bwd). hidden [S*T, H] bf16,
+    weight / ref_weight [V, H] bf16, ids / mask / old_logp [S, T]."""
+    ctx = ctx or default_context(hidden.device.index or 0)
+    if ids.dim() != 2:
+        raise PcpError(-1, "ids must be [S, T]")
+    S, T = ids.shape
+    N, H = hidden.shape
+    V = weight.shape[0]
+    if N != S * T or weight.shape[1] != H:
+        raise PcpError(-1, "hidden must be [S*T, H] and weight [V, H]")
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise PcpError(-2, "hidden and weight must be bf16")
+    dev = hidden.device
+    if outputs is None:
+        outputs = LmheadOutputs(
+            loss=torch.zeros((), dtype=torch.float32, device=dev),
+            logp=torch.zeros((S, T), dtype=torch.float32, device=dev),
+            ref_logp=torch.zeros((S, T), dtype=torch.float32, device=dev) if ref_weight is not None else None,
+            token_loss=torch.zeros((S, T), dtype=torch.float32, device=dev),
+            advantages=torch.zeros((S,), dtype=torch.float32, device=dev),
+            dhidden=torch.empty((N, H), dtype=torch.float32, device=dev) if want_grads else None,
+            dweight=torch.empty((V, H), dtype=torch.float32, device=dev) if want_grads else None)
+    a = _lib.LmheadArgs()
+    lib().pcp_lmhead_args_init(ctypes.byref(a))
+    a.n_seq, a.rows, a.hidden, a.vocab, a.group_size, a.vocab_chunk = S, T, H, V, int(group_size), int(vocab_chunk)
+    a.ids_dtype = dtype_code(ids)
+    a.hidden_states, a.weight, a.ref_weight = _ptr(hidden), _ptr(weight), _ptr(ref_weight)
+    a.ids = _ptr(ids)
+    if mask is not None:
+        a.mask = _ptr(mask)
+        a.mask_dtype = dtype_code(mask)
+    a.old_logp, a.advantages, a.rewards = _ptr(old_logp), _ptr(advantages), _ptr(rewards)
+    a.logp, a.ref_logp, a.token_loss = _ptr(outputs.logp), _ptr(outputs.ref_logp), _ptr(outputs.token_loss)
+    a.advantages_out, a.loss = _ptr(outputs.advantages), _ptr(outputs.loss)
+    a.dhidden, a.dweight = _ptr(outputs.dhidden), _ptr(outputs.dweight)
+    a.loss_mode = int(loss_mode)
+    a.clip_eps, a.kl_beta, a.std_eps, a.loss_norm = clip_eps, kl_beta, std_eps, loss_norm
+    a.flags = 0 if sync else _lib.FLAG_ASYNC
+    a.stream = _stream_handle(stream)
+    check(lib().pcp_grpo_lmhead_fwd_bwd(ctx.handle, ctypes.byref(a)), ctx.handle)
+    return outputs

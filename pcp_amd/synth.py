@@ -68,7 +68,66 @@ CONFIGS = {
 }
 
 
-def per_sequence(cfg: GrpoConfig) -> tuple[np.ndarray, np.ndarray]:
+@dataclass(frozen=True)
+class LmheadConfig:
+    """Configuration 5: fused LM-head + GRPO log-prob. hidden [N, H] ~ N(0, 1),
+    W [V, H] ~ N(0, 0.02^2), W_ref = W + N(0, 0.002^2), all bf16; tokens drawn from
+    softmax(hidden W^T) would need the logits, so targets are uniform in [0, V)
+    (the loss terms do not depend on how targets were drawn); lengths, rewards and
+    groups as configuration 2 (G=8, T=512)."""
+    key: int = 5
+    name: str = "fused-lm-head"
+    prompts: int = 4
+    group: int = 8
+    T: int = 512
+    H: int = 4096
+    V: int = 151936
+    std_h: float = 1.0
+    std_w: float = 0.02
+    std_r: float = 0.002
+    lengths: tuple = ("uniform", 64, 512)
+    rewards: tuple = ("binary",)
+    old_noise: float = 0.01
+    clip_eps: float = 0.2
+    kl_beta: float = 0.04
+    seed: int = 0
+
+    @property
+    def S(self) -> int:
+        return self.prompts * self.group
+
+    @property
+    def N(self) -> int:
+        return self.S * self.T
+
+
+LMHEAD = LmheadConfig()
+
+
+def make_lmhead_inputs(cfg: LmheadConfig, device="cuda"):
+    """Inputs of the fused LM-head configuration in HBM (hidden, weight, ref_weight,
+    ids, mask, rewards, old_logp offsets)."""
+    import torch
+
+    lengths, rewards = per_sequence(cfg)
+    S, T, H, V = cfg.S, cfg.T, cfg.H, cfg.V
+    stream = torch.cuda.current_stream().cuda_stream or None
+    hidden = torch.empty((S * T, H), dtype=torch.bfloat16, device=device)
+    check(lib().pcp_synth_logits(hidden.data_ptr(), None, hidden.numel(), int(DType.bf16), ctypes.c_float(cfg.std_h),
+                                 ctypes.c_float(0.0), cfg.seed + 10, stream))
+    weight = torch.empty((V, H), dtype=torch.bfloat16, device=device)
+    ref_weight = torch.empty_like(weight)
+    check(lib().pcp_synth_logits(weight.data_ptr(), ref_weight.data_ptr(), weight.numel(), int(DType.bf16),
+                                 ctypes.c_float(cfg.std_w), ctypes.c_float(cfg.std_r), cfg.seed + 11, stream))
+    rng = np.random.default_rng(cfg.seed + 12)
+    ids = torch.from_numpy(rng.integers(0, V, size=(S, T)).astype(np.int64)).to(device)
+    mask = torch.from_numpy(mask_from_lengths(lengths, T)).to(device)
+    old_shift = torch.from_numpy((rng.standard_normal((S, T)) * cfg.old_noise).astype(np.float32)).to(device)
+    return {"hidden": hidden, "weight": weight, "ref_weight": ref_weight, "ids": ids, "mask": mask,
+            "rewards": torch.from_numpy(rewards).to(device), "old_shift": old_shift, "lengths": lengths}
+
+
+def per_sequence(cfg) -> tuple[np.ndarray, np.ndarray]:
     """Response lengths (int64 [S]) and rewards (f32 [S]) from PCG64(seed)."""
     rng = np.random.default_rng(cfg.seed)
     S, T = cfg.S, cfg.T

@@ -41,20 +41,21 @@ def test_library_exports_every_declared_symbol():
     assert set(names) <= exported
 
 
-def test_struct_layout_matches_c(tmp_path):
-    fields = [f[0] for f in _lib.GrpoArgs._fields_]
+@pytest.mark.parametrize("cname,pyty", [("pcp_grpo_args", _lib.GrpoArgs), ("pcp_lmhead_args", _lib.LmheadArgs)])
+def test_struct_layout_matches_c(tmp_path, cname, pyty):
+    fields = [f[0] for f in pyty._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", '#include "pcp_grpo.h"', "int main(void){",
-           'printf("%zu\\n", sizeof(pcp_grpo_args));']
-    src += [f'printf("%zu\\n", offsetof(pcp_grpo_args, {f}));' for f in fields]
+           f'printf("%zu\\n", sizeof({cname}));']
+    src += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
     src += ["return 0;}"]
     c = tmp_path / "layout.c"
     c.write_text("\n".join(src))
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c99", "-I", INCLUDE, str(c), "-o", str(exe)], check=True)
     vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    assert vals[0] == ctypes.sizeof(_lib.GrpoArgs)
+    assert vals[0] == ctypes.sizeof(pyty)
     for f, off in zip(fields, vals[1:]):
-        assert getattr(_lib.GrpoArgs, f).offset == off, f
+        assert getattr(pyty, f).offset == off, f
 
 
 def test_c_host_links_against_the_library(tmp_path):
@@ -120,6 +121,41 @@ def test_argument_errors_without_device(mutate, code, text):
     rc = L.pcp_grpo_loss_fwd_bwd(None, ctypes.byref(a))
     assert rc == code
     assert text in L.pcp_last_error(None).decode()
+
+
+def _valid_lm_args():
+    a = _lib.LmheadArgs()
+    _lib.lib().pcp_lmhead_args_init(ctypes.byref(a))
+    a.n_seq, a.rows, a.hidden, a.vocab = 2, 4, 128, 1000
+    a.hidden_states, a.weight, a.ids, a.rewards = 0x1000, 0x2000, 0x3000, 0x4000
+    return a
+
+
+def test_lmhead_args_defaults():
+    a = _valid_lm_args()
+    assert a.group_size == 1 and a.ids_dtype == DType.i64 and a.mask_dtype == DType.f32 and a.vocab_chunk == 0
+    assert abs(a.clip_eps - 0.2) < 1e-7 and abs(a.kl_beta - 0.04) < 1e-8 and a.loss_mode == 0
+
+
+@pytest.mark.parametrize("mutate,code,text", [
+    (lambda a: setattr(a, "hidden", 96), -1, "multiple of 64"),
+    (lambda a: setattr(a, "vocab_chunk", 100), -1, "vocab_chunk"),
+    (lambda a: setattr(a, "weight", None), -1, "is NULL"),
+    (lambda a: setattr(a, "weight", 0x2008), -1, "16-byte aligned"),
+    (lambda a: setattr(a, "ids_dtype", int(DType.f32)), -2, "ids dtype"),
+    (lambda a: setattr(a, "loss_mode", 1), -1, "ref_weight"),
+    (lambda a: setattr(a, "rewards", None), -1, "both NULL"),
+    (lambda a: (setattr(a, "n_seq", 1 << 20), setattr(a, "rows", 1 << 10)), -9, "2^28"),
+])
+def test_lmhead_argument_errors_without_device(mutate, code, text):
+    L = _lib.lib()
+    a = _valid_lm_args()
+    mutate(a)
+    assert L.pcp_grpo_lmhead_fwd_bwd(None, ctypes.byref(a)) == code
+    assert text in L.pcp_last_error(None).decode()
+    b = _valid_lm_args()
+    assert L.pcp_grpo_lmhead_fwd_bwd(None, ctypes.byref(b)) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()
 
 
 def test_valid_args_then_null_context():

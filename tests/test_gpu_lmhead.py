@@ -1,0 +1,300 @@
+"""Parity of the fused LM-head + GRPO loss (pcp_grpo_lmhead_fwd_bwd) with the oracle.
+
+The oracle evaluates the logits hidden . W^T of the same bf16 operands exactly in
+float64 (oracle.lmhead_logits), runs the loss head on them (grpo_full on F64
+logits), and forms the float64 gradients D.W and D^T.hidden with
+D = c (onehot - softmax) (oracle.lmhead_grads). At the full configuration-5 size,
+where a float64 CPU evaluation would take minutes, the reference is torch fp32 on
+the GPU (token chunks of the same products), and the loss is checked against the
+reduction of the device's own token losses.
+
+Tolerances:
+  log-probs, token losses, loss: as the logits-input path (parity_tol). The tile
+    kernel sums products of bf16 values, each exact in f32, so its f32 accumulation
+    error is far below the 1e-5 * max(1, |lse|) bar.
+  dhidden, dW: the device rounds D to bf16 (2^-9 relative at most) before the two
+    GEMMs and c carries the coef_floor error, so elementwise
+    |dh - dh*| <= E . |W| and |dW - dW*| <= E^T . |hidden| with
+    E = (2^-8 + 1e-4) |D| + 2 floor_n (onehot + p).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from pcp_amd import grpo, synth
+from pcp_amd._lib import LossMode, PcpError
+from parity_tol import coef_floor, dev, loss_tolerance
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+ORC_MODE = {LossMode.REINFORCE: orc.REINFORCE, LossMode.GRPO_CLIP_KL: orc.CLIP_KL}
+
+
+def bf16_bits(rng, shape, std):
+    return orc.bf16_from_f32((rng.standard_normal(shape) * std).astype(np.float32))
+
+
+def make_case(S, T, H, V, G, seed, lengths=None, logit_std=2.0):
+    """hidden ~ N(0, 1), W ~ N(0, logit_std^2 / H) (logits ~ N(0, logit_std^2)),
+    W_ref = W + 5% noise, all rounded to bf16."""
+    rng = np.random.default_rng(seed)
+    N = S * T
+    w_std = logit_std / np.sqrt(H)
+    hb = bf16_bits(rng, (N, H), 1.0)
+    wb = bf16_bits(rng, (V, H), w_std)
+    rb = orc.bf16_from_f32(orc.bf16_to_f32(wb) + (rng.standard_normal((V, H)) * w_std * 0.05).astype(np.float32))
+    ids = rng.integers(0, V, size=(S, T)).astype(np.int64)
+    lengths = np.asarray(lengths if lengths is not None else rng.integers(1, T + 1, size=S))
+    mask = synth.mask_from_lengths(lengths, T)
+    rewards = rng.integers(0, 2, size=S).astype(np.float32)
+    noise = (rng.standard_normal((S, T)) * 0.01).astype(np.float32)
+    return dict(S=S, T=T, H=H, V=V, G=G, hb=hb, wb=wb, rb=rb, ids=ids, mask=mask, rewards=rewards, noise=noise)
+
+
+def oracle_case(c, mode, clip_eps=0.2, kl_beta=0.04):
+    S, T, V = c["S"], c["T"], c["V"]
+    L = orc.lmhead_logits(c["hb"], c["wb"])
+    R = orc.lmhead_logits(c["hb"], c["rb"])
+    idsf = c["ids"].reshape(-1)
+    lp0, lse = orc.logprob(L, np.clip(idsf, 0, V - 1), dtype=orc.F64)
+    _, rlse = orc.logprob(R, np.clip(idsf, 0, V - 1), dtype=orc.F64)
+    old = (lp0.reshape(S, T) + c["noise"]).astype(np.float32)
+    r = orc.grpo_full(L.reshape(S, T, V), c["ids"], c["mask"], rows=T, rewards=c["rewards"], group_size=c["G"],
+                      ref_logits=R.reshape(S, T, V), old_logp=old, loss_mode=ORC_MODE[mode], clip_eps=clip_eps,
+                      kl_beta=kl_beta, want_dlogits=False, dtype=orc.F64)
+    return L, lse, rlse, old, r
+
+
+def run_device(c, mode, old, *, vocab_chunk=0, want_grads=True, ids=None, mask=None, clip_eps=0.2, kl_beta=0.04):
+    return grpo.lmhead_fwd_bwd(dev(c["hb"]), dev(c["wb"]), dev(c["ids"]) if ids is None else ids,
+                               dev(c["mask"]) if mask is None else mask, ref_weight=dev(c["rb"]),
+                               rewards=dev(c["rewards"]), group_size=c["G"], old_logp=dev(old), loss_mode=mode,
+                               clip_eps=clip_eps, kl_beta=kl_beta, vocab_chunk=vocab_chunk, want_grads=want_grads)
+
+
+def grad_bounds(c, L, lse, r, mode, old, kl_beta=0.04, clip_eps=0.2):
+    """(want_dh, tol_dh, want_dw, tol_dw) in float64."""
+    S, T, V = c["S"], c["T"], c["V"]
+    ids = c["ids"].reshape(-1)
+    coef = r.coef.reshape(-1)
+    tscale = np.maximum(1.0, np.abs(lse)).reshape(S, T)
+    fl = coef_floor(r.coef, r.lp, r.lr, c["mask"].astype(np.float64), r.adv.astype(np.float64)[:, None],
+                    r.seq_len.astype(np.float64)[:, None], float(S), old.astype(np.float64),
+                    mode == LossMode.REINFORCE, kl_beta, clip_eps, tscale).reshape(-1)
+    dh, dw = orc.lmhead_grads(c["hb"], c["wb"], L, lse, coef, ids)
+    P = np.exp(L - lse[:, None])
+    D = -P * coef[:, None]
+    live = (coef != 0) & (ids >= 0) & (ids < V)
+    D[np.nonzero(live)[0], ids[live]] += coef[live]
+    onehot = np.zeros_like(P)
+    onehot[np.arange(len(ids)), np.clip(ids, 0, V - 1)] = 1.0
+    E = (2.0 ** -8 + 1e-4) * np.abs(D) + 2.0 * fl[:, None] * (onehot + P)
+    E[fl == 0] = (2.0 ** -8 + 1e-4) * np.abs(D[fl == 0])
+    W = np.abs(orc.bf16_to_f32(c["wb"]).astype(np.float64))
+    h = np.abs(orc.bf16_to_f32(c["hb"]).astype(np.float64))
+    return dh, E @ W + 1e-30, dw, E.T @ h + 1e-30
+
+
+def check_forward(c, out, L, lse, rlse, r, mode):
+    S, T = c["S"], c["T"]
+    sc = np.maximum(1.0, np.abs(lse)).reshape(S, T)
+    rsc = np.maximum(1.0, np.abs(rlse)).reshape(S, T)
+    lp = out.logp.cpu().numpy()
+    assert np.all(np.abs(lp - r.lp) <= 1e-5 * sc), np.abs(lp - r.lp).max()
+    assert np.all(lp[c["mask"] == 0] == 0)
+    if mode == LossMode.GRPO_CLIP_KL:
+        lr = out.ref_logp.cpu().numpy()
+        assert np.all(np.abs(lr - r.lr) <= 1e-5 * rsc), np.abs(lr - r.lr).max()
+    tl = out.token_loss.cpu().numpy()
+    assert np.all(np.abs(tl - r.token_loss) <= 1e-5 * sc), np.abs(tl - r.token_loss).max()
+    assert np.array_equal(out.advantages.cpu().numpy(), r.adv)
+    tol = loss_tolerance(r.token_loss, r.coef, r.lp, r.lr, c["mask"], r.adv, r.seq_len, float(S),
+                         mode == LossMode.REINFORCE, 0.04, np.maximum(sc, rsc))
+    assert abs(float(out.loss.cpu()) - r.loss) <= tol, (float(out.loss.cpu()), r.loss, tol)
+
+
+def check_grads(out, want_dh, tol_dh, want_dw, tol_dw):
+    dh = out.dhidden.cpu().numpy().astype(np.float64)
+    dw = out.dweight.cpu().numpy().astype(np.float64)
+    edh, edw = np.abs(dh - want_dh), np.abs(dw - want_dw)
+    assert not np.any(edh > tol_dh), f"dhidden: {(edh > tol_dh).sum()} out of tolerance, worst {edh.max():.3e}"
+    assert not np.any(edw > tol_dw), f"dW: {(edw > tol_dw).sum()} out of tolerance, worst {edw.max():.3e}"
+
+
+# ---- ragged small shapes against the float64 oracle -----------------------------------------
+
+SMALL = [
+    # S, T, H, V, G, chunk, lengths: 150 tokens (two token tiles, the second ragged),
+    # an odd number of K stages, a ragged last vocab tile and several vocab chunks.
+    (3, 50, 192, 1000, 3, 256, [50, 31, 7]),
+    (2, 64, 64, 129, 2, 0, [64, 1]),
+    (1, 7, 128, 4096, 1, 1024, [5]),
+]
+
+
+@pytest.mark.parametrize("mode", [LossMode.REINFORCE, LossMode.GRPO_CLIP_KL])
+@pytest.mark.parametrize("shape", SMALL, ids=lambda s: f"S{s[0]}T{s[1]}H{s[2]}V{s[3]}c{s[5]}")
+def test_lmhead_small_vs_oracle(shape, mode):
+    S, T, H, V, G, chunk, lengths = shape
+    c = make_case(S, T, H, V, G, seed=S * 1000 + V, lengths=lengths)
+    L, lse, rlse, old, r = oracle_case(c, mode)
+    print(f"lmhead small S={S} T={T} H={H} V={V} chunk={chunk} mode={int(mode)}", flush=True)
+    out = run_device(c, mode, old, vocab_chunk=chunk)
+    torch.cuda.synchronize()
+    check_forward(c, out, L, lse, rlse, r, mode)
+    check_grads(out, *grad_bounds(c, L, lse, r, mode, old))
+
+
+def test_lmhead_ignore_index_int32_bool_mask_and_no_grads():
+    c = make_case(2, 40, 128, 700, 2, seed=11, lengths=[40, 25])
+    c["ids"][0, 3] = -100          # live by mask, ignored by id: no loss, no gradient, no error
+    L, lse, rlse, old, r = oracle_case(c, LossMode.GRPO_CLIP_KL)
+    ids32 = dev(c["ids"].astype(np.int32))
+    maskb = dev(c["mask"].astype(bool))
+    out = run_device(c, LossMode.GRPO_CLIP_KL, old, ids=ids32, mask=maskb)
+    torch.cuda.synchronize()
+    check_forward(c, out, L, lse, rlse, r, LossMode.GRPO_CLIP_KL)
+    check_grads(out, *grad_bounds(c, L, lse, r, LossMode.GRPO_CLIP_KL, old))
+    fwd = run_device(c, LossMode.GRPO_CLIP_KL, old, want_grads=False)
+    torch.cuda.synchronize()
+    assert fwd.dhidden is None and fwd.dweight is None
+    assert torch.equal(fwd.logp, out.logp) and torch.equal(fwd.loss, out.loss)
+
+
+def test_lmhead_deterministic():
+    c = make_case(2, 70, 128, 900, 2, seed=5, lengths=[70, 33])
+    old = np.full((2, 70), -7.0, np.float32)
+    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=384)
+    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=384)
+    torch.cuda.synchronize()
+    for f in ("loss", "logp", "ref_logp", "token_loss", "dhidden", "dweight"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+
+
+def test_lmhead_errors():
+    c = make_case(1, 16, 64, 300, 1, seed=3, lengths=[16])
+    old = np.zeros((1, 16), np.float32)
+    bad = c["ids"].copy()
+    bad[0, 2] = 300
+    with pytest.raises(PcpError) as ei:
+        run_device(c, LossMode.REINFORCE, old, ids=dev(bad))
+    assert ei.value.code == -3
+    hb = c["hb"].copy()
+    hb[5] = orc.bf16_from_f32(np.full(64, np.nan, np.float32))
+    with pytest.raises(PcpError) as ei:
+        grpo.lmhead_fwd_bwd(dev(hb), dev(c["wb"]), dev(c["ids"]), dev(c["mask"]), rewards=dev(c["rewards"]))
+    assert ei.value.code == -4
+    # A NaN hidden row of a masked token is not an error (its loss weight is 0).
+    mask = c["mask"].copy()
+    mask[0, 5] = 0
+    out = grpo.lmhead_fwd_bwd(dev(hb), dev(c["wb"]), dev(c["ids"]), dev(mask), rewards=dev(c["rewards"]))
+    torch.cuda.synchronize()
+    assert np.isfinite(float(out.loss.cpu()))
+    with pytest.raises(PcpError) as ei:
+        grpo.lmhead_fwd_bwd(dev(c["hb"][:, :32].copy()), dev(c["wb"][:, :32].copy()), dev(c["ids"]),
+                            rewards=dev(c["rewards"]))
+    assert ei.value.code == -1   # hidden must be a multiple of 64
+
+
+# ---- real hidden and vocabulary sizes, few tokens, against the float64 oracle ---------------
+
+def test_lmhead_qwen_vocab_vs_oracle():
+    cfg = synth.LMHEAD
+    c = make_case(2, 128, cfg.H, cfg.V, 2, seed=17, lengths=[128, 77], logit_std=cfg.std_w * np.sqrt(cfg.H))
+    L, lse, rlse, old, r = oracle_case(c, LossMode.GRPO_CLIP_KL)
+    print("lmhead qwen-vocab N=256 H=4096 V=151936", flush=True)
+    out = run_device(c, LossMode.GRPO_CLIP_KL, old)
+    torch.cuda.synchronize()
+    check_forward(c, out, L, lse, rlse, r, LossMode.GRPO_CLIP_KL)
+    check_grads(out, *grad_bounds(c, L, lse, r, LossMode.GRPO_CLIP_KL, old))
+
+
+# ---- configuration 5 at full size against torch fp32 ------------------------------------------
+
+def _torch_reference(inp, coef=None, chunk=2048):
+    """fp32 logp / lse per token, and with coef the gradients and their bounds."""
+    h, W, ids = inp["hidden"], inp["weight"], inp["ids"].reshape(-1)
+    Wf = W.float()
+    N = h.shape[0]
+    lp = torch.empty(N, dtype=torch.float32, device=DEV)
+    lse = torch.empty_like(lp)
+    dh = tol_dh = dw = tol_dw = None
+    if coef is not None:
+        dh = torch.empty((N, Wf.shape[1]), dtype=torch.float32, device=DEV)
+        tol_dh = torch.empty_like(dh)
+        dw = torch.zeros_like(Wf)
+        tol_dw = torch.zeros_like(Wf)
+        Wa = Wf.abs()
+    for n0 in range(0, N, chunk):
+        hc = h[n0:n0 + chunk].float()
+        Lc = hc @ Wf.T
+        l = torch.logsumexp(Lc, dim=1)
+        lse[n0:n0 + chunk] = l
+        idc = ids[n0:n0 + chunk]
+        lp[n0:n0 + chunk] = Lc.gather(1, idc[:, None])[:, 0] - l
+        if coef is not None:
+            cc = coef[n0:n0 + chunk]
+            P = torch.exp(Lc - l[:, None])
+            del Lc
+            D = -P * cc[:, None]
+            D.scatter_add_(1, idc[:, None], cc[:, None])
+            E = (2.0 ** -8 + 1e-4) * D.abs()
+            # c is exact up to f32 rounding here (REINFORCE), so the softmax term carries
+            # only the log-prob error: |c| * 1e-5 * max(1, |lse|) * p.
+            E += (cc.abs() * 1e-5 * l.abs().clamp(min=1.0))[:, None] * P
+            del P
+            dh[n0:n0 + chunk] = D @ Wf
+            tol_dh[n0:n0 + chunk] = E @ Wa
+            dw += D.T @ hc
+            tol_dw += E.T @ hc.abs()
+            del D, E
+    return lp, lse, dh, tol_dh, dw, tol_dw
+
+
+def test_config5_full_size():
+    cfg = synth.LMHEAD
+    inp = synth.make_lmhead_inputs(cfg, DEV)
+    S, T = cfg.S, cfg.T
+    print("config 5 full size: reference log-probs", flush=True)
+    lp_ref, lse_ref, *_ = _torch_reference(inp)
+    old = (lp_ref.reshape(S, T) + inp["old_shift"]).contiguous()
+    for mode in (LossMode.REINFORCE, LossMode.GRPO_CLIP_KL):
+        print(f"config 5 full size: device mode={int(mode)}", flush=True)
+        out = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"],
+                                  ref_weight=inp["ref_weight"], rewards=inp["rewards"], group_size=cfg.group,
+                                  old_logp=old, loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta,
+                                  want_grads=mode == LossMode.REINFORCE)
+        torch.cuda.synchronize()
+        m = inp["mask"].reshape(-1) != 0
+        sc = lse_ref.abs().clamp(min=1.0)
+        err = (out.logp.reshape(-1) - lp_ref).abs()
+        assert bool((err[m] <= 1e-5 * sc[m]).all()), float(err[m].max())
+        assert bool((out.logp.reshape(-1)[~m] == 0).all())
+        # The loss is the masked sequence mean of the device's own token losses.
+        L = inp["mask"].double().sum(1).clamp(min=1.0)
+        tl = out.token_loss.double()
+        seq = tl.sum(1) / L
+        if mode == LossMode.REINFORCE:
+            seq = seq * out.advantages.double()
+        want = float(seq.sum() / S)
+        assert abs(float(out.loss) - want) <= 1e-5 * float((tl.abs().sum(1) / L).sum() / S) + 1e-12
+        adv = orc.advantages(inp["rewards"].cpu().numpy(), cfg.group)
+        assert np.array_equal(out.advantages.cpu().numpy(), adv)
+        if mode == LossMode.REINFORCE:
+            # REINFORCE: c = -A * w / (L * G) needs no log-prob, so the gradients have
+            # a reference independent of the device's forward.
+            coef = (-torch.from_numpy(adv).to(DEV).double()[:, None] * inp["mask"].double() / (L[:, None] * S))
+            print("config 5 full size: reference gradients", flush=True)
+            _, _, dh, tol_dh, dw, tol_dw = _torch_reference(inp, coef.float().reshape(-1))
+            bad_h = ((out.dhidden - dh).abs() > tol_dh + 1e-6 * tol_dh.max()).sum().item()
+            bad_w = ((out.dweight - dw).abs() > tol_dw + 1e-6 * tol_dw.max()).sum().item()
+            assert bad_h == 0 and bad_w == 0, (bad_h, bad_w)
+            del dh, tol_dh, dw, tol_dw
+        else:
+            lr_ref = _torch_reference({**inp, "weight": inp["ref_weight"]})[0]
+            err = (out.ref_logp.reshape(-1) - lr_ref).abs()
+            assert bool((err[m] <= 1e-5 * sc[m] + 1e-5).all()), float(err[m].max())
+        del out
+        torch.cuda.empty_cache()

@@ -24,6 +24,8 @@ from oracle import oracle as orc
 from pcp_amd import grpo, synth
 from pcp_amd._lib import DType, LossMode, PcpError
 from pcp_amd.backend import HipGrpoBackend
+from parity_tol import (assert_dlogits, coef_floor, dev, full_floor, full_loss_tol, host_bits, loss_tolerance,
+                        lse_scale, tok_to_rows, token_scale)
 
 pytestmark = pytest.mark.gpu
 
@@ -41,19 +43,6 @@ def load_cases():
 
 
 CASES = load_cases()
-
-
-def dev(a):
-    a = np.ascontiguousarray(a)
-    if a.dtype == np.uint16:
-        return torch.from_numpy(a.view(np.int16)).to(DEV).view(torch.bfloat16)
-    return torch.from_numpy(a).to(DEV)
-
-
-def host_bits(t):
-    if t.dtype == torch.bfloat16:
-        return t.view(torch.int16).cpu().numpy().view(np.uint16)
-    return t.cpu().numpy()
 
 
 def run_case(c, **kw):
@@ -74,33 +63,6 @@ def run_case(c, **kw):
     return out
 
 
-def token_scale(logits, ids, rows, off, dtype):
-    """max(1, |lse|) of every token-carrying row, placed at its token index: the
-    scale of the per-token log-prob tolerance (1e-5 * this)."""
-    S, LS, V = logits.shape
-    sel = np.ascontiguousarray(logits[:, :rows]).reshape(S * rows, V)
-    _, lse = orc.logprob(sel, np.clip(ids[:, off:off + rows].reshape(-1), 0, None), dtype=dtype)
-    out = np.zeros(ids.shape, np.float64)
-    out[:, off:off + rows] = np.maximum(1.0, np.abs(lse)).reshape(S, rows)
-    return out
-
-
-def loss_tolerance(token_loss, coef, lp, lr, mask, adv, seq_len, G, reinforce, beta, tscale):
-    """Forward-error bound of the loss given the per-token log-prob bar: each token's
-    logp / ref logp may be off by 1e-5*max(1,|lse|), which moves the loss by
-    |dloss/dlogp| + |dloss/dref| times that; the reduction adds 1e-5 of the sum of
-    |contributions| (the loss can be a near-cancellation of those terms)."""
-    L = np.asarray(seq_len, np.float64)[:, None]
-    per = np.abs(token_loss) / L
-    if reinforce:
-        per = per * np.abs(np.asarray(adv, np.float64))[:, None]
-        dref = 0.0
-    else:
-        dref = np.abs(beta * np.expm1(lr - lp)) * np.abs(mask) / (G * L)
-    delta = 1e-5 * tscale
-    return 1e-5 * per.sum() / G + ((np.abs(coef) + dref) * delta).sum() + 1e-12
-
-
 def golden_loss_tol(c):
     off, rows = int(c["tok_offset"]), int(c["rows"])
     dt = orc.BF16 if c["logits"].dtype == np.uint16 else orc.F32
@@ -109,46 +71,6 @@ def golden_loss_tol(c):
     return loss_tolerance(c["exp_token_loss"], c["exp_coef"], c["exp_lp"], c["exp_lr"], c["mask"], c["exp_adv"],
                           L, G, int(c["loss_mode"]) == 0, float(c["kl_beta"]),
                           token_scale(c["logits"], c["ids"], rows, off, dt))
-
-
-def full_loss_tol(r, logits, ids, mask, rows, off, dtype, reinforce, beta, G):
-    return loss_tolerance(r.token_loss, r.coef, r.lp, r.lr, mask, r.adv, r.seq_len, G, reinforce, beta,
-                          token_scale(logits, ids, rows, off, dtype))
-
-
-def lse_scale(logits_rows, ids_rows, dtype):
-    _, lse = orc.logprob(logits_rows, np.clip(ids_rows, 0, None), dtype=dtype)
-    return np.maximum(1.0, np.abs(lse))
-
-
-def coef_floor(coef, lp, lr, w, adv, seq_len, G, old, reinforce, beta, eps, tscale):
-    """Per-row absolute error allowed in dlogits = c*(onehot - softmax), from the f32
-    log-prob error delta = 1e-5*max(1,|lse|): c = scale*(-A*rho*[unclipped] - beta*expm1(d))
-    with rho = exp(logp - old), d = ref - logp moves by scale*(|A|*rho + 2*beta*e^d)*delta
-    (its terms can cancel, so this is not relative to c), and the softmax by |c|*delta."""
-    delta = 1e-5 * tscale
-    if reinforce:
-        return np.abs(coef) * (delta + 1e-5)
-    scale = np.abs(w) / (G * np.asarray(seq_len, np.float64))
-    rho = np.exp(lp - old)
-    unclipped = np.where(adv >= 0, rho <= 1 + eps, rho >= 1 - eps)
-    dc = scale * (np.abs(adv) * rho * unclipped + 2 * beta * np.exp(lr - lp)) * delta
-    return dc + np.abs(coef) * delta + 1e-5 * np.abs(coef)
-
-
-def full_floor(r, mask, old, G, reinforce, beta, eps, tscale):
-    """coef_floor over a FullResult ([S, TS] token arrays)."""
-    L = np.asarray(r.seq_len, np.float64)[:, None]
-    A = np.asarray(r.adv, np.float64)[:, None]
-    old = r.lp if old is None else np.asarray(old, np.float64)
-    return coef_floor(r.coef, r.lp, r.lr, np.asarray(mask, np.float64), A, L, G, old, reinforce, beta, eps, tscale)
-
-
-def tok_to_rows(a, rows, off, LS):
-    """[S, TS] token-indexed array -> [S, LS] logits-row-indexed (pad rows 0)."""
-    out = np.zeros((a.shape[0], LS), np.float64)
-    out[:, :rows] = a[:, off:off + rows]
-    return out
 
 
 def golden_floor_rows(c):
@@ -162,21 +84,6 @@ def golden_floor_rows(c):
                     c["exp_adv"].astype(np.float64)[:, None], L, G, old, int(c["loss_mode"]) == 0,
                     float(c["kl_beta"]), float(c["clip_eps"]), token_scale(c["logits"], c["ids"], rows, off, dt))
     return tok_to_rows(fl, rows, off, LS)
-
-
-def assert_dlogits(got, want, floor_rows, bf16_out):
-    """floor_rows: per-row absolute floor (coef_floor), broadcast over the vocabulary."""
-    got = got.astype(np.float64)
-    want = want.astype(np.float64)
-    fl = np.asarray(floor_rows, np.float64)[..., None]
-    err = np.abs(got - want)
-    if bf16_out:
-        tol = (2.0 ** -8 + 4e-6) * np.abs(want) + fl
-    else:
-        tol = 1e-5 * np.abs(want) + fl
-        assert err.max() <= 1e-4
-    bad = err > tol
-    assert not bad.any(), f"{bad.sum()} dlogits out of tolerance; worst {err.max():.3e}"
 
 
 # ---- golden fixtures through the device path ----------------------------------------
