@@ -186,10 +186,12 @@ def bench_lmhead(args) -> None:
     N, H, V = cfg.N, cfg.H, cfg.V
     live = int(inp["mask"].sum().item())
     ms_step = elapsed * 1e3 / args.steps
-    # Dense products per step: forward logits per model, recomputed logits, dhidden, dW.
+    # Dense products per step over the live (compacted) tokens: forward logits per
+    # model, recomputed logits, dhidden, dW. Masked tokens carry no loss weight and
+    # no gradient, so the algorithm needs 2*H*V flops per live token per product.
     products = (2 if clip else 1) + 3
-    step_flops = products * 2.0 * N * H * V
-    tile_flops = 2.0 * N * H * V
+    step_flops = products * 2.0 * live * H * V
+    tile_flops = 2.0 * live * H * V
     achieved = tile_flops / (kernel_ms / 1e3) / 1e12
     line = {
         "metric": "GRPO fused LM-head + loss fwd+bwd tokens/s, H=4096, V=151936 bf16",
@@ -208,6 +210,7 @@ def bench_lmhead(args) -> None:
                                f"hidden {H}, V={V}, bf16 hidden/weights, loss={args.mode}",
                    "tokens": N, "valid_tokens": live, "global_batch": cfg.S, "seq_len": cfg.T},
         "step_tflops": step_flops / (ms_step / 1e3) / 1e12,
+        "dense_equivalent_tflops": products * 2.0 * N * H * V / (ms_step / 1e3) / 1e12,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
                      "kernel": "lm_tile_kernel<kLmFwd> (policy logits tiles)", "kernel_ms": kernel_ms,

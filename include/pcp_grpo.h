@@ -185,8 +185,14 @@ int pcp_sync(pcp_ctx* ctx);
  *     out (logp f32[S,T]) or (logp, ref_logp)
  *  "grpo_advantages"
  *     in  (rewards f32[n], group_size i64[])   out (advantages f32[n])
+ *  "grpo_lmhead_fwd_bwd"  (the LM head + loss of export_qwen_forward.py:146-163)
+ *     in  (hidden bf16[S,T,H], weight bf16[V,H], ref_weight bf16[V,H], input_ids[S,T],
+ *          attention_mask[S,T], old_logp f32[S,T], rewards f32[S], hyper f32[5] =
+ *          {group_size, clip_eps, kl_beta, loss_norm (0 => S), loss_mode (0|1)})
+ *     out (loss f32[], dhidden f32[S,T,H], dweight f32[V,H], logp f32[S,T],
+ *          ref_logp f32[S,T], advantages f32[S]); ref_weight is read in mode 1 only
  *
- * All [.,T,V] functions use the reference's shift: logits row t scores token t+1,
+ * All [.,T,V] and [.,T,H] functions use the reference's shift: row t scores token t+1,
  * per-token outputs are indexed by token position (position 0 is 0).
  * dtypes == NULL selects each function's default dtypes (f32 floats, i64 ids).
  * On success *out_data[i] (malloc'd, *out_nbytes[i] bytes) belong to the caller;

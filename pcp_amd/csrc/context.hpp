@@ -24,6 +24,7 @@ struct pcp_ctx {
   int prof_used = 0;
   bool prof_on = false;
   void* blas = nullptr;           // rocblas_handle, created on first LM-head backward
+  int* h_count = nullptr;         // pinned host word: live-token count of the LM-head path
 };
 
 namespace pcp {

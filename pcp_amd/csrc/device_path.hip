@@ -338,6 +338,7 @@ void pcp_destroy(pcp_ctx* ctx) {
     (void)hipDeviceSynchronize();
     release_profile_events(ctx);
     release_blas(ctx);
+    if (ctx->h_count) (void)hipHostFree(ctx->h_count);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->d_err) (void)hipFree(ctx->d_err);
   }

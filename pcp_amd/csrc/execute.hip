@@ -169,13 +169,14 @@ int download(pcp_ctx* ctx, const Outputs& o, int* n_out, void*** out_data, size_
 
 // ---- functions ------------------------------------------------------------
 
-enum Fn { kLossFwdBwd, kClipKl, kLogprob, kAdvantages, kUnknown };
+enum Fn { kLossFwdBwd, kClipKl, kLogprob, kAdvantages, kLmhead, kUnknown };
 
 Fn lookup(const char* fn) {
   if (!std::strcmp(fn, "grpo_loss_fwd_bwd") || !std::strcmp(fn, "main")) return kLossFwdBwd;
   if (!std::strcmp(fn, "grpo_clip_kl_fwd_bwd")) return kClipKl;
   if (!std::strcmp(fn, "grpo_logprob_fwd")) return kLogprob;
   if (!std::strcmp(fn, "grpo_advantages")) return kAdvantages;
+  if (!std::strcmp(fn, "grpo_lmhead_fwd_bwd")) return kLmhead;
   return kUnknown;
 }
 
@@ -187,6 +188,125 @@ void shifted_layout(pcp_grpo_args* a, int64_t S, int64_t T, int64_t V) {
   a->logit_seq_stride = T;
   a->tok_seq_stride = T;
   a->tok_offset = T > 0 ? 1 : 0;
+}
+
+// Per-token outputs of the shifted layout: aligned value t belongs to position t+1.
+void shift_to_positions(float* v, int64_t S, int64_t T) {
+  for (int64_t s = 0; s < S; ++s) {
+    float* r = v + s * T;
+    if (T > 1) std::memmove(r + 1, r, sizeof(float) * (T - 1));
+    r[0] = 0.f;
+  }
+}
+
+// "grpo_lmhead_fwd_bwd": the LM head and loss of export_qwen_forward.py:146-163 on
+// hidden states, with the reference's shift (hidden row t scores token t+1). The
+// shift is applied to ids / mask / old_logp on the host; the last row of each
+// sequence has no target (mask 0), so its dhidden row is 0.
+int execute_lmhead(pcp_ctx* ctx, const std::vector<In>& in, int* n_out, void*** out_data, size_t** out_nbytes) {
+  int rc;
+  const In& Hs = in[0];
+  if ((rc = expect_dtype(Hs, 0, {PCP_BF16}, "hidden")) || (rc = expect_shape(Hs, 0, {-1, -1, -1}, "hidden")))
+    return rc;
+  const int64_t S = Hs.shape[0], T = Hs.shape[1], H = Hs.shape[2];
+  if (S < 1 || T < 2 || H < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden dims must be S >= 1, T >= 2, H >= 1");
+  if ((rc = expect_dtype(in[1], 1, {PCP_BF16}, "weight")) || (rc = expect_shape(in[1], 1, {-1, H}, "weight")))
+    return rc;
+  const int64_t V = in[1].shape[0];
+  if (V < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "weight must have >= 1 rows");
+  if ((rc = expect_dtype(in[2], 2, {PCP_BF16}, "ref_weight")) || (rc = expect_shape(in[2], 2, {V, H}, "ref_weight")) ||
+      (rc = expect_dtype(in[3], 3, {PCP_I64, PCP_I32}, "input_ids")) || (rc = expect_shape(in[3], 3, {S, T}, "input_ids")) ||
+      (rc = expect_dtype(in[4], 4, {PCP_F32, PCP_BOOL}, "attention_mask")) ||
+      (rc = expect_shape(in[4], 4, {S, T}, "attention_mask")) ||
+      (rc = expect_dtype(in[5], 5, {PCP_F32}, "old_logp")) || (rc = expect_shape(in[5], 5, {S, T}, "old_logp")) ||
+      (rc = expect_dtype(in[6], 6, {PCP_F32}, "rewards")) || (rc = expect_shape(in[6], 6, {S}, "rewards")) ||
+      (rc = expect_dtype(in[7], 7, {PCP_F32}, "hyper")) || (rc = expect_shape(in[7], 7, {5}, "hyper")))
+    return rc;
+  float hyper[5];
+  std::memcpy(hyper, in[7].data, sizeof(hyper));
+  if (!(hyper[0] >= 1.f) || hyper[0] != static_cast<float>(static_cast<int64_t>(hyper[0])))
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "hyper[0] (group_size) must be a positive integer");
+  if (hyper[4] != 0.f && hyper[4] != 1.f)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "hyper[4] (loss_mode) must be 0 (REINFORCE) or 1 (GRPO_CLIP_KL)");
+  if ((rc = check_ids(in[3], &in[4], S, T, V))) return rc;
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+
+  // Shifted token arrays (aligned: row t carries position t+1; row T-1 is dead).
+  const int64_t N = S * T;
+  std::vector<int64_t> ids(N, 0);
+  std::vector<float> mask(N, 0.f), old(N, 0.f);
+  const float* old_in = static_cast<const float*>(in[5].data);
+  for (int64_t s = 0; s < S; ++s)
+    for (int64_t t = 0; t + 1 < T; ++t) {
+      const int64_t src = s * T + t + 1, dst = s * T + t;
+      ids[dst] = id_at(in[3], src);
+      mask[dst] = in[4].dtype == PCP_F32 ? static_cast<const float*>(in[4].data)[src] : (mask_at(&in[4], src) ? 1.f : 0.f);
+      old[dst] = old_in[src];
+    }
+  DevArena arena;
+  pcp_lmhead_args a;
+  pcp_lmhead_args_init(&a);
+  a.n_seq = S;
+  a.rows = T;
+  a.hidden = H;
+  a.vocab = V;
+  a.group_size = static_cast<int64_t>(hyper[0]);
+  a.clip_eps = hyper[1];
+  a.kl_beta = hyper[2];
+  a.loss_norm = hyper[3];
+  a.loss_mode = hyper[4] == 1.f ? PCP_LOSS_GRPO_CLIP_KL : PCP_LOSS_REINFORCE;
+  a.ids_dtype = PCP_I64;
+  a.mask_dtype = PCP_F32;
+  void* p;
+  if ((rc = arena.upload(ctx, in[0], &p))) return rc;
+  a.hidden_states = p;
+  if ((rc = arena.upload(ctx, in[1], &p))) return rc;
+  a.weight = p;
+  if (a.loss_mode == PCP_LOSS_GRPO_CLIP_KL) {
+    if ((rc = arena.upload(ctx, in[2], &p))) return rc;
+    a.ref_weight = p;
+  }
+  auto put = [&](const void* src, size_t bytes, void** dst) {
+    int r = arena.alloc(ctx, bytes, dst);
+    if (r != PCP_OK) return r;
+    hipError_t e = hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice);
+    return e == hipSuccess ? PCP_OK : hip_fail(ctx, e, "host-to-device copy");
+  };
+  if ((rc = put(ids.data(), 8 * N, &p))) return rc;
+  a.ids = p;
+  if ((rc = put(mask.data(), 4 * N, &p))) return rc;
+  a.mask = p;
+  if ((rc = put(old.data(), 4 * N, &p))) return rc;
+  a.old_logp = static_cast<float*>(p);
+  if ((rc = arena.upload(ctx, in[6], &p))) return rc;
+  a.rewards = static_cast<float*>(p);
+
+  Outputs outs;
+  auto out = [&](size_t bytes, bool zero, void** dst) {
+    int r = zero ? arena.zeroed(ctx, bytes, dst) : arena.alloc(ctx, bytes, dst);
+    if (r == PCP_OK) {
+      outs.dev.push_back(*dst);
+      outs.bytes.push_back(bytes);
+    }
+    return r;
+  };
+  if ((rc = out(4, false, &p))) return rc;
+  a.loss = static_cast<float*>(p);
+  if ((rc = out(4 * static_cast<size_t>(N) * H, false, &p))) return rc;
+  a.dhidden = static_cast<float*>(p);
+  if ((rc = out(4 * static_cast<size_t>(V) * H, false, &p))) return rc;
+  a.dweight = static_cast<float*>(p);
+  if ((rc = out(4 * N, true, &p))) return rc;
+  a.logp = static_cast<float*>(p);
+  if ((rc = out(4 * N, true, &p))) return rc;
+  a.ref_logp = static_cast<float*>(p);
+  if ((rc = out(4 * S, false, &p))) return rc;
+  a.advantages_out = static_cast<float*>(p);
+  if ((rc = pcp_grpo_lmhead_fwd_bwd(ctx, &a))) return rc;
+  if ((rc = download(ctx, outs, n_out, out_data, out_nbytes))) return rc;
+  shift_to_positions(static_cast<float*>((*out_data)[3]), S, T);
+  shift_to_positions(static_cast<float*>((*out_data)[4]), S, T);
+  return PCP_OK;
 }
 
 }  // namespace
@@ -207,6 +327,7 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
   static const int kDefLp2[] = {PCP_F32, PCP_I64};
   static const int kDefLp3[] = {PCP_F32, PCP_F32, PCP_I64};
   static const int kDefAdv[] = {PCP_F32, PCP_I64};
+  static const int kDefLm[] = {PCP_BF16, PCP_BF16, PCP_BF16, PCP_I64, PCP_F32, PCP_F32, PCP_F32, PCP_F32};
   const int* defaults = nullptr;
   int want = 0;
   switch (f) {
@@ -214,6 +335,7 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
     case kClipKl: want = 7; defaults = kDefClip; break;
     case kLogprob: want = (n_in == 3) ? 3 : 2; defaults = (n_in == 3) ? kDefLp3 : kDefLp2; break;
     case kAdvantages: want = 2; defaults = kDefAdv; break;
+    case kLmhead: want = 8; defaults = kDefLm; break;
     default: break;
   }
   if (n_in != want) return fail(ctx, PCP_ERR_COUNT_MISMATCH, "'%s' takes %d inputs, got %d", fn, want, n_in);
@@ -221,6 +343,11 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
   std::vector<In> in;
   int rc = check_inputs(n_in, data, nbytes, shapes, ranks, dtypes, defaults, &in);
   if (rc != PCP_OK) goto arg_error;
+  if (f == kLmhead) {
+    rc = execute_lmhead(ctx, in, n_out, out_data, out_nbytes);
+    if (rc != PCP_OK && ctx) ctx->last_error = thread_error();
+    return rc;
+  }
 
   {
     pcp_grpo_args a;

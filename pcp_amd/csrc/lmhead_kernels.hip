@@ -251,19 +251,91 @@ __global__ void __launch_bounds__(256) lm_terms_kernel(RowArgs ra, LmTermsArgs a
   }
   float lp = 0.f, lr = 0.f;
   TokenTerms tt{0.f, 0.f};
-  if (r.live) {
+  // Live tokens are exactly those the compaction kept (same predicate).
+  const int c = a.cidx[n];
+  if (r.live && c >= 0) {
     // Non-finite logits of a live token poison its log-sum-exp (NaN propagates
     // through the partial merges); flag it like the logits-input path does.
-    const float l2 = a.lse2[n], rl2 = a.ref_tgt ? a.ref_lse2[n] : 0.f;
+    const float l2 = a.lse2[c], rl2 = a.ref_tgt ? a.ref_lse2[c] : 0.f;
     if (!(__builtin_isfinite(l2) && __builtin_isfinite(rl2))) atomicOr(ra.err, kErrNonFinite);
-    lp = a.tgt[n] - l2 * kLn2;
-    lr = a.ref_tgt ? a.ref_tgt[n] - rl2 * kLn2 : 0.f;
+    lp = a.tgt[c] - l2 * kLn2;
+    lr = a.ref_tgt ? a.ref_tgt[c] - rl2 * kLn2 : 0.f;
     tt = token_terms(ra, r, lp, lr);
+    a.coef[c] = tt.coef;
   }
   if (ra.logp) ra.logp[r.tix] = lp;
   if (ra.ref_logp) ra.ref_logp[r.tix] = lr;
   if (ra.token_loss) ra.token_loss[r.tix] = tt.loss;
-  a.coef[n] = tt.coef;
+}
+
+// Live-token compaction in one workgroup: each pass ranks 1024 tokens with a
+// ballot prefix per wave and a 16-entry wave scan in LDS, so the compact order is
+// the token order (deterministic).
+__global__ void __launch_bounds__(1024) lm_compact_kernel(LmCompactArgs a) {
+  __shared__ int wsum[16];
+  __shared__ int base_s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) base_s = 0;
+  __syncthreads();
+  for (int n0 = 0; n0 < a.N; n0 += 1024) {
+    const int n = n0 + tid;
+    bool live = false;
+    int64_t id = -1;
+    if (n < a.N) {
+      id = a.ids_i64 ? static_cast<const int64_t*>(a.ids)[n] : static_cast<int64_t>(static_cast<const int32_t*>(a.ids)[n]);
+      float w = 1.f;
+      if (a.mask) w = a.mask_u8 ? (static_cast<const uint8_t*>(a.mask)[n] ? 1.f : 0.f) : static_cast<const float*>(a.mask)[n];
+      live = w != 0.f && id >= 0 && id < a.V;
+    }
+    const uint64_t bal = __ballot(live);
+    const int before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0));
+    if (lane == 0) wsum[wave] = __popcll(bal);
+    __syncthreads();
+    int off = base_s;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    int total = 0;
+    for (int w = 0; w < 16; ++w) total += wsum[w];
+    if (n < a.N) {
+      const int c = live ? off + before : -1;
+      a.cidx[n] = c;
+      if (live) {
+        a.live[c] = n;
+        a.ids_c[c] = static_cast<int>(id);
+      }
+    }
+    __syncthreads();
+    if (tid == 0) base_s += total;
+    __syncthreads();
+  }
+  if (tid == 0) a.count[0] = base_s;
+}
+
+__global__ void __launch_bounds__(256) lm_gather_rows_kernel(const u32x4* src, u32x4* dst, const int* live, int H) {
+  const int c = blockIdx.x;
+  const int nv = H / 8;  // 16-byte vectors per bf16 row
+  const u32x4* s = src + static_cast<int64_t>(live[c]) * nv;
+  u32x4* d = dst + static_cast<int64_t>(c) * nv;
+  for (int i = threadIdx.x; i < nv; i += 256) d[i] = s[i];
+}
+
+__global__ void __launch_bounds__(256) lm_scatter_rows_kernel(const u32x4* src, u32x4* dst, const int* cidx, int H) {
+  const int t = blockIdx.x;
+  const int nv = H / 4;  // 16-byte vectors per f32 row
+  const int c = cidx[t];
+  u32x4* d = dst + static_cast<int64_t>(t) * nv;
+  if (c >= 0) {
+    const u32x4* s = src + static_cast<int64_t>(c) * nv;
+    for (int i = threadIdx.x; i < nv; i += 256) d[i] = s[i];
+  } else {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < nv; i += 256) d[i] = z;
+  }
+}
+
+__global__ void __launch_bounds__(256) lm_zero_kernel(float* dst, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    dst[i] = 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -290,6 +362,30 @@ hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st) {
 
 hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st) {
   lm_reduce_kernel<<<dim3(static_cast<unsigned>((a.N + 3) / 4)), dim3(256), 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_compact(const LmCompactArgs& a, hipStream_t st) {
+  lm_compact_kernel<<<dim3(1), dim3(1024), 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_gather_rows(const void* src, void* dst, const int* live, int n, int H, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  lm_gather_rows_kernel<<<dim3(n), dim3(256), 0, st>>>(static_cast<const u32x4*>(src), static_cast<u32x4*>(dst),
+                                                       live, H);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_scatter_rows(const float* src, float* dst, const int* cidx, int N, int H, hipStream_t st) {
+  lm_scatter_rows_kernel<<<dim3(N), dim3(256), 0, st>>>(reinterpret_cast<const u32x4*>(src),
+                                                        reinterpret_cast<u32x4*>(dst), cidx, H);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_zero(float* dst, int64_t n, hipStream_t st) {
+  const int64_t blocks = (n + 255) / 256;
+  lm_zero_kernel<<<dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st>>>(dst, n);
   return hipGetLastError();
 }
 

@@ -38,14 +38,34 @@ struct LmReduceArgs {
 
 struct LmTermsArgs {
   int64_t N;
-  const float* tgt;
+  const int* cidx;        // [N] token -> compact index (-1: not live)
+  const float* tgt;       // per compact index
   const float* lse2;
   const float* ref_tgt;   // nullptr: no reference model
   const float* ref_lse2;
-  float* coef;            // out
+  float* coef;            // out, per compact index
+};
+
+// Live-token compaction: live = mask != 0 and 0 <= id < V, in ascending token order.
+struct LmCompactArgs {
+  const void* ids;
+  int ids_i64;
+  const void* mask;       // nullptr: all live
+  int mask_u8;
+  int N, V;
+  int* live;              // [N] compact -> token
+  int* cidx;              // [N] token -> compact, -1 when not live
+  int* ids_c;             // [N] compact target ids (int32)
+  int* count;             // [1] number of live tokens
 };
 
 size_t lm_tile_smem_bytes();
+hipError_t launch_lm_compact(const LmCompactArgs& a, hipStream_t st);
+// dst[c, :] = src[live[c], :] for c < n (bf16 rows of H elements, H % 64 == 0).
+hipError_t launch_lm_gather_rows(const void* src, void* dst, const int* live, int n, int H, hipStream_t st);
+// dst[t, :] = cidx[t] >= 0 ? src[cidx[t], :] : 0 for t < N (f32 rows of H elements).
+hipError_t launch_lm_scatter_rows(const float* src, float* dst, const int* cidx, int N, int H, hipStream_t st);
+hipError_t launch_lm_zero(float* dst, int64_t n, hipStream_t st);
 hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st);
 hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st);
 hipError_t launch_lm_terms(const RowArgs& ra, const LmTermsArgs& a, hipStream_t st);

@@ -1,11 +1,16 @@
 // Device-pointer entry point of the fused LM-head + GRPO loss (pcp_grpo_lmhead_fwd_bwd).
 //
+// Live tokens (mask != 0, id in [0, V)) are compacted first: a masked or ignored
+// token has zero loss weight and zero gradient, so only live hidden rows enter the
+// products. The live count sizes the GEMMs, so the call reads it back once (one
+// stream synchronisation, also under PCP_FLAG_ASYNC).
 // Forward, per model (policy, then reference): MFMA logits tiles reduced in-tile to
 // per-(token, vocab tile) log-sum-exp partials and the target logit; one wave per
 // token merges the partials. Then the GRPO terms per token and the loss reduction
 // (the same kernels as the logits-input path). Backward, per vocab chunk: logits
 // tiles recomputed into bf16 dlogits, then two plain GEMMs on rocBLAS:
-//   dhidden (+)= dlogits_chunk * W_chunk,   dW_chunk = dlogits_chunk^T * hidden.
+//   dhidden (+)= dlogits_chunk * W_chunk,   dW_chunk = dlogits_chunk^T * hidden,
+// and the compact dhidden rows are scattered back (zero rows for dead tokens).
 // This mirrors the LM head's VJP (src/autodiff/vjp_rules.zig:426-497, matmulVJP).
 
 #include <hip/hip_runtime.h>
@@ -75,26 +80,45 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
 
   const int64_t S = a->n_seq, T = a->rows, N = S * T, H = a->hidden, V = a->vocab;
   const int nvt = static_cast<int>((V + kTile - 1) / kTile);
-  const int ntt = static_cast<int>((N + kTile - 1) / kTile);
   const bool ref = a->loss_mode == PCP_LOSS_GRPO_CLIP_KL;
   const bool bwd = a->dhidden || a->dweight;
   const int64_t chunk = a->vocab_chunk ? a->vocab_chunk : kDefaultChunk;
   const float loss_norm = a->loss_norm > 0.f ? a->loss_norm : static_cast<float>(S);
 
-  // Scratch layout.
+  // Scratch layout (token arrays sized for N; the live prefix is used).
   size_t off = 0;
   auto take = [&](size_t bytes) { const size_t o = off; off += r256(bytes); return o; };
   const size_t o_adv = take(4 * S), o_len = take(4 * S), o_scale = take(4 * S), o_val = take(4 * S), o_loss = take(4);
   const size_t o_tl = a->token_loss ? 0 : take(4 * N);
+  const size_t o_live = take(4 * N), o_cidx = take(4 * N), o_idsc = take(4 * N), o_cnt = take(4);
+  const size_t o_hid = take(2 * static_cast<size_t>(N) * H);
   const size_t o_part = take(8 * static_cast<size_t>(N) * nvt);
   const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
   const size_t o_chunk = bwd ? take(2 * static_cast<size_t>(N) * chunk) : 0;
+  const size_t o_dhc = a->dhidden ? take(4 * static_cast<size_t>(N) * H) : 0;
   rc = ensure_scratch(ctx, off);
   if (rc != PCP_OK) return rc;
+  if (!ctx->h_count && (e = hipHostMalloc(reinterpret_cast<void**>(&ctx->h_count), sizeof(int))) != hipSuccess)
+    return hip_fail(ctx, e, "hipHostMalloc");
   char* sp = static_cast<char*>(ctx->scratch);
   auto F = [&](size_t o) { return reinterpret_cast<float*>(sp + o); };
+  auto I = [&](size_t o) { return reinterpret_cast<int*>(sp + o); };
   float* tl = a->token_loss ? a->token_loss : F(o_tl);
   float2* part = reinterpret_cast<float2*>(sp + o_part);
+  const int mask_u8 = a->mask_dtype == PCP_BOOL;
+
+  // Live-token compaction; the count comes back to size the products.
+  LmCompactArgs ca{a->ids, a->ids_dtype == PCP_I64, a->mask, mask_u8, static_cast<int>(N), static_cast<int>(V),
+                   I(o_live), I(o_cidx), I(o_idsc), I(o_cnt)};
+  if ((e = launch_lm_compact(ca, st)) != hipSuccess) return hip_fail(ctx, e, "compaction launch");
+  if ((e = hipMemcpyAsync(ctx->h_count, I(o_cnt), sizeof(int), hipMemcpyDeviceToHost, st)) != hipSuccess)
+    return hip_fail(ctx, e, "reading the live-token count");
+  if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+  const int nl = *ctx->h_count;
+  if (nl < 0 || nl > N) return fail(ctx, PCP_ERR_DEVICE, "live-token count %d out of range", nl);
+  const int ntl = (nl + kTile - 1) / kTile;
+  if ((e = launch_lm_gather_rows(a->hidden_states, sp + o_hid, I(o_live), nl, static_cast<int>(H), st)) != hipSuccess)
+    return hip_fail(ctx, e, "gathering live hidden rows");
 
   // Advantages and per-sequence lengths.
   const float* adv = a->advantages;
@@ -106,26 +130,25 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   if (a->advantages_out && a->advantages_out != adv &&
       (e = hipMemcpyAsync(a->advantages_out, adv, 4 * S, hipMemcpyDeviceToDevice, st)) != hipSuccess)
     return hip_fail(ctx, e, "copying advantages");
-  const int mask_u8 = a->mask_dtype == PCP_BOOL;
   if ((e = launch_seq_prep(a->mask, mask_u8, S, T, T, 0, loss_norm, F(o_len), F(o_scale), st)) != hipSuccess)
     return hip_fail(ctx, e, "seq_prep launch");
 
   // Forward, per model: tiles -> partials + target logit; merge -> lse2.
   LmTileArgs ta;
   std::memset(&ta, 0, sizeof(ta));
-  ta.A = a->hidden_states;
-  ta.N = static_cast<int>(N);
+  ta.A = sp + o_hid;
+  ta.N = nl;
   ta.V = static_cast<int>(V);
   ta.H = static_cast<int>(H);
   ta.vt0 = 0;
   ta.nvt = nvt;
-  ta.ntt = ntt;
-  ta.ids = a->ids;
-  ta.ids_i64 = a->ids_dtype == PCP_I64;
+  ta.ntt = ntl;
+  ta.ids = I(o_idsc);
+  ta.ids_i64 = 0;
   ta.part = part;
   ta.ldp = nvt;
-  LmReduceArgs rd{part, N, nvt, nvt, nullptr};
-  for (int m = 0; m < (ref ? 2 : 1); ++m) {
+  LmReduceArgs rd{part, nl, nvt, nvt, nullptr};
+  for (int m = 0; m < (ref && nl > 0 ? 2 : nl > 0 ? 1 : 0); ++m) {
     ta.B = m == 0 ? a->weight : a->ref_weight;
     ta.tgt = F(m == 0 ? o_tgt : o_rtgt);
     const bool timed = m == 0 && ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
@@ -155,19 +178,23 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   ra.logit_stride = T;
   ra.tok_stride = T;
   ra.tok_offset = 0;
-  ra.ids_i64 = ta.ids_i64;
+  ra.ids_i64 = a->ids_dtype == PCP_I64;
   ra.mask_u8 = mask_u8;
   ra.loss_mode = a->loss_mode;
   ra.clip_eps = a->clip_eps;
   ra.kl_beta = a->kl_beta;
-  LmTermsArgs tma{N, F(o_tgt), F(o_l2), ref ? F(o_rtgt) : nullptr, ref ? F(o_rl2) : nullptr, F(o_coef)};
+  LmTermsArgs tma{N, I(o_cidx), F(o_tgt), F(o_l2), ref ? F(o_rtgt) : nullptr, ref ? F(o_rl2) : nullptr, F(o_coef)};
   if ((e = launch_lm_terms(ra, tma, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head terms");
   if ((e = launch_loss_reduce(tl, S, T, T, 0, F(o_len), adv, a->loss_mode == PCP_LOSS_REINFORCE, loss_norm,
                               F(o_val), a->loss ? a->loss : F(o_loss), st)) != hipSuccess)
     return hip_fail(ctx, e, "loss reduction");
 
-  // Backward per vocab chunk.
-  if (bwd) {
+  // Backward per vocab chunk over the live tokens; no live token: zero gradients.
+  if (bwd && nl == 0) {
+    if (a->dhidden && (e = launch_lm_zero(a->dhidden, N * H, st)) != hipSuccess) return hip_fail(ctx, e, "zero dhidden");
+    if (a->dweight && (e = launch_lm_zero(a->dweight, V * H, st)) != hipSuccess) return hip_fail(ctx, e, "zero dW");
+  }
+  if (bwd && nl > 0) {
     if (!ctx->blas) {
       rocblas_handle h = nullptr;
       if ((rc = blas_status(ctx, rocblas_create_handle(&h), "rocblas_create_handle")) != PCP_OK) return rc;
@@ -180,6 +207,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     ta.coef = F(o_coef);
     ta.dchunk = sp + o_chunk;
     ta.ldd = static_cast<int>(chunk);
+    float* dhc = a->dhidden ? F(o_dhc) : nullptr;
     const float one = 1.f, zero = 0.f;
     for (int64_t vc0 = 0; vc0 < V; vc0 += chunk) {
       const int64_t w = (V - vc0 < chunk) ? V - vc0 : chunk;
@@ -189,24 +217,24 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       if ((e = launch_lm_tiles(kLmBwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head backward tiles");
       const void* wc = static_cast<const char*>(a->weight) + vc0 * H * 2;
       if (a->dhidden) {
-        // Column-major view: dhidden^T [H, N] (+)= W_c^T [H, w] * D^T [w, N].
+        // Column-major view: dhidden_c^T [H, nl] (+)= W_c^T [H, w] * D^T [w, nl].
         rc = blas_status(ctx,
                          rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_none, static_cast<int>(H),
-                                         static_cast<int>(N), static_cast<int>(w), &one, wc, rocblas_datatype_bf16_r,
+                                         nl, static_cast<int>(w), &one, wc, rocblas_datatype_bf16_r,
                                          static_cast<int>(H), ta.dchunk, rocblas_datatype_bf16_r,
-                                         static_cast<int>(chunk), vc0 == 0 ? &zero : &one, a->dhidden,
-                                         rocblas_datatype_f32_r, static_cast<int>(H), a->dhidden,
+                                         static_cast<int>(chunk), vc0 == 0 ? &zero : &one, dhc,
+                                         rocblas_datatype_f32_r, static_cast<int>(H), dhc,
                                          rocblas_datatype_f32_r, static_cast<int>(H), rocblas_datatype_f32_r,
                                          rocblas_gemm_algo_standard, 0, 0),
                          "dhidden GEMM");
         if (rc != PCP_OK) return rc;
       }
       if (a->dweight) {
-        // Column-major view: dW_c^T [H, w] = hidden^T [H, N] * D [N, w].
+        // Column-major view: dW_c^T [H, w] = hidden_c^T [H, nl] * D [nl, w].
         float* dw = a->dweight + vc0 * H;
         rc = blas_status(ctx,
                          rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_transpose, static_cast<int>(H),
-                                         static_cast<int>(w), static_cast<int>(N), &one, a->hidden_states,
+                                         static_cast<int>(w), nl, &one, sp + o_hid,
                                          rocblas_datatype_bf16_r, static_cast<int>(H), ta.dchunk,
                                          rocblas_datatype_bf16_r, static_cast<int>(chunk), &zero, dw,
                                          rocblas_datatype_f32_r, static_cast<int>(H), dw, rocblas_datatype_f32_r,
@@ -216,6 +244,9 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         if (rc != PCP_OK) return rc;
       }
     }
+    if (a->dhidden && (e = launch_lm_scatter_rows(dhc, a->dhidden, I(o_cidx), static_cast<int>(N), static_cast<int>(H),
+                                                  st)) != hipSuccess)
+      return hip_fail(ctx, e, "scattering dhidden rows");
   }
 
   if (a->flags & PCP_FLAG_ASYNC) {

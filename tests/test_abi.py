@@ -218,6 +218,49 @@ def test_execute_argument_errors_without_device():
     assert "context is NULL" in str(e.value)
 
 
+def _lm_inputs(S=2, T=6, H=64, V=40):
+    rng = np.random.default_rng(1)
+    hidden = rng.integers(0, 1 << 16, (S, T, H)).astype(np.uint16)
+    w = rng.integers(0, 1 << 16, (V, H)).astype(np.uint16)
+    ids = rng.integers(0, V, (S, T)).astype(np.int64)
+    mask = np.ones((S, T), np.float32)
+    old = np.zeros((S, T), np.float32)
+    rewards = np.array([1.0, 0.0], np.float32)[:S]
+    hyper = np.array([S, 0.2, 0.04, 0, 1], np.float32)
+    data = [hidden, w, w, ids, mask, old, rewards, hyper]
+    dts = [DType.bf16, DType.bf16, DType.bf16, DType.i64, DType.f32, DType.f32, DType.f32, DType.f32]
+    return data, [x.shape for x in data], dts
+
+
+def test_execute_lmhead_argument_errors_without_device():
+    data, shapes, dts = _lm_inputs()
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data[:7], shapes[:7], dts[:7])
+    assert e.value.code == -8
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data, shapes, [DType.f16] + dts[1:])
+    assert e.value.code == -2 and "hidden" in str(e.value)
+    bad_w = data[1][:, :32].copy()
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", [data[0], bad_w] + data[2:], [shapes[0], bad_w.shape] + shapes[2:], dts)
+    assert e.value.code == -1 and "weight" in str(e.value)
+    hyper = data[7].copy()
+    hyper[4] = 3
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data[:7] + [hyper], shapes, dts)
+    assert e.value.code == -1 and "loss_mode" in str(e.value)
+    ids = data[3].copy()
+    ids[0, 0] = 999                 # position 0 is never a target under the shift: accepted
+    ids[1, 2] = 40                  # == V at a target position: rejected
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data[:3] + [ids] + data[4:], shapes, dts)
+    assert e.value.code == -3
+    ids[1, 2] = 0
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data[:3] + [ids] + data[4:], shapes, dts)
+    assert e.value.code == -1 and "context is NULL" in str(e.value)
+
+
 def test_philox_known_answers():
     # Random123 known-answer vectors for philox4x32-10.
     from pcp_amd.synth import philox

@@ -163,6 +163,71 @@ def test_lmhead_ignore_index_int32_bool_mask_and_no_grads():
     assert torch.equal(fwd.logp, out.logp) and torch.equal(fwd.loss, out.loss)
 
 
+def test_lmhead_all_masked_and_no_mask():
+    c = make_case(2, 20, 64, 500, 2, seed=9, lengths=[20, 20])
+    old = np.full((2, 20), -6.0, np.float32)
+    zero = torch.zeros((2, 20), dtype=torch.float32, device=DEV)
+    out = run_device(c, LossMode.GRPO_CLIP_KL, old, mask=zero)
+    torch.cuda.synchronize()
+    assert float(out.loss) == 0.0 and not out.logp.any() and not out.token_loss.any()
+    assert not out.dhidden.any() and not out.dweight.any()
+    # mask = NULL: every token with an in-range id is live (same result as an all-ones mask).
+    L, lse, rlse, old, r = oracle_case(c, LossMode.GRPO_CLIP_KL)
+    out = grpo.lmhead_fwd_bwd(dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), None, ref_weight=dev(c["rb"]),
+                              rewards=dev(c["rewards"]), group_size=2, old_logp=dev(old),
+                              loss_mode=LossMode.GRPO_CLIP_KL)
+    torch.cuda.synchronize()
+    check_forward(c, out, L, lse, rlse, r, LossMode.GRPO_CLIP_KL)
+    check_grads(out, *grad_bounds(c, L, lse, r, LossMode.GRPO_CLIP_KL, old))
+
+
+def test_execute_lmhead_shifted_vs_oracle():
+    """The host-bytes function: hidden row t scores token t+1 (the reference's shift)."""
+    from pcp_amd._lib import DType
+    from pcp_amd.backend import HipGrpoBackend
+
+    S, T, H, V, G = 2, 33, 128, 600, 2
+    c = make_case(S, T, H, V, G, seed=21, lengths=[33, 20])
+    L = orc.lmhead_logits(c["hb"], c["wb"]).reshape(S, T, V)
+    R = orc.lmhead_logits(c["hb"], c["rb"]).reshape(S, T, V)
+    old = np.full((S, T), -6.0, np.float32)
+    r = orc.grpo_full(L, c["ids"], c["mask"], rows=T - 1, tok_offset=1, rewards=c["rewards"], group_size=G,
+                      ref_logits=R, old_logp=old, loss_mode=orc.CLIP_KL, want_dlogits=False, dtype=orc.F64)
+    hyper = np.array([G, 0.2, 0.04, 0, 1], np.float32)
+    ins = [c["hb"].reshape(S, T, H), c["wb"], c["rb"], c["ids"], c["mask"], old, c["rewards"], hyper]
+    be = HipGrpoBackend.init()
+    outs = be.executeFunction(None, "grpo_lmhead_fwd_bwd", ins, [x.shape for x in ins],
+                              [DType.bf16, DType.bf16, DType.bf16, DType.i64, DType.f32, DType.f32, DType.f32,
+                               DType.f32])
+    be.deinit()
+    loss = np.frombuffer(outs[0], np.float32)[0]
+    dh = np.frombuffer(outs[1], np.float32).reshape(S, T, H)
+    dw = np.frombuffer(outs[2], np.float32).reshape(V, H)
+    lp = np.frombuffer(outs[3], np.float32).reshape(S, T)
+    lr = np.frombuffer(outs[4], np.float32).reshape(S, T)
+    _, lse = orc.logprob(L.reshape(-1, V), np.zeros(S * T, np.int64), dtype=orc.F64)
+    sc = np.maximum(1.0, np.abs(lse)).reshape(S, T)
+    sc_tok = np.ones((S, T))
+    sc_tok[:, 1:] = sc[:, :-1]
+    assert np.all(np.abs(lp - r.lp) <= 1e-5 * sc_tok) and np.all(lp[:, 0] == 0)
+    assert np.all(np.abs(lr - r.lr) <= 1e-5 * sc_tok + 1e-5)
+    tol = loss_tolerance(r.token_loss, r.coef, r.lp, r.lr, c["mask"], r.adv, r.seq_len, float(S), False, 0.04,
+                         sc_tok)
+    assert abs(loss - r.loss) <= tol
+    assert np.array_equal(np.frombuffer(outs[5], np.float32), r.adv)
+    # Gradients: rows t < T-1 carry token t+1's coefficient; the last row is 0.
+    crow = np.zeros((S, T))
+    crow[:, :-1] = r.coef[:, 1:]
+    irow = np.zeros((S, T), np.int64)
+    irow[:, :-1] = c["ids"][:, 1:]
+    want_dh, want_dw = orc.lmhead_grads(c["hb"], c["wb"], L.reshape(-1, V), lse, crow.reshape(-1), irow.reshape(-1))
+    assert not dh[:, -1].any()
+    scale_h = np.abs(want_dh).max()
+    scale_w = np.abs(want_dw).max()
+    assert np.abs(dh.reshape(-1, H) - want_dh).max() <= 2.0 ** -7 * scale_h
+    assert np.abs(dw - want_dw).max() <= 2.0 ** -7 * scale_w
+
+
 def test_lmhead_deterministic():
     c = make_case(2, 70, 128, 900, 2, seed=5, lengths=[70, 33])
     old = np.full((2, 70), -7.0, np.float32)
