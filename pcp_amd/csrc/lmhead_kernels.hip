@@ -26,19 +26,36 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace lm {
 
-constexpr int BM = 128;           // tokens per tile
-constexpr int BN = 128;           // vocab entries per tile
-constexpr int BK = 64;            // hidden (K) per LDS stage
-constexpr int LDK = BK + 8;       // padded LDS row (bf16): conflict-free 16-byte fragment reads
-constexpr int NTHR = 256;         // 4 waves: 2 (tokens) x 2 (vocab), 64 x 64 each
-constexpr int LDC = BN + 4;       // padded fp32 tile row in the epilogue
-constexpr int kStageElems = BM * LDK + BN * LDK;
-constexpr size_t kSmemGemm = 2 * kStageElems * sizeof(__bf16);
-constexpr size_t kSmemEpi = BM * LDC * sizeof(float);
+constexpr int BV = 256;           // vocab rows per tile (MFMA A operand: W rows)
+constexpr int BT = 256;           // tokens per tile (MFMA B operand: hidden rows)
+constexpr int BK = 32;            // hidden (K) per pipeline stage
+constexpr int NST = 4;            // LDS stages: up to 3 in flight while one is read
+constexpr int ROWB = BK * 2;      // bytes of one operand row in one stage
+constexpr int kOpBytes = BV * ROWB;             // 16 KB: one operand, one stage
+constexpr int kStageBytes = 2 * kOpBytes;       // 32 KB
+constexpr size_t kSmemGemm = NST * kStageBytes; // 128 KB
+constexpr int NTHR = 256;         // 4 waves: 2 (vocab) x 2 (tokens), 128 x 128 each
+constexpr int LDD = BV + 8;       // bf16 dlogits row in the backward epilogue (528 B, 16-B aligned)
+constexpr size_t kSmemEpi = (BT / 2) * LDD * sizeof(__bf16);   // half the token columns at a time
 constexpr size_t kSmem = kSmemGemm > kSmemEpi ? kSmemGemm : kSmemEpi;
 constexpr int kGroupM = 8;        // token tiles per group in the tile order
+constexpr int kPart = 128;        // vocab entries per log-sum-exp partial (one wave's rows)
+
+// s_waitcnt immediates (vmcnt only; expcnt and lgkmcnt left at their maxima).
+constexpr int kWaitVm0 = 0x0F70;
+constexpr int kWaitVm8 = 0x0F78;
+constexpr int kWaitVm16 = 0x4F70;
 
 }  // namespace lm
+
+#define LM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Slot of 16-byte chunk c of an operand row in LDS: c ^ lm_swz(row). Rows are 64
+// bytes (4 chunks) unpadded, as the direct-to-LDS loads write 1 KB per wave
+// contiguously; XOR with bits 2-3 of the row makes the MFMA fragment reads (32 rows,
+// one chunk) free of bank conflicts on gfx950 (measured with SQ_LDS_BANK_CONFLICT:
+// 0 per ds_read_b128, against 4 for bits 1-2 and 12 unswizzled).
+__device__ __forceinline__ int lm_swz(int row) { return (row >> 2) & 3; }
 
 // Tile order: work item p -> (token tile, vocab tile). Consecutive workgroup ids
 // are dealt round-robin to the 8 XCDs, so ids are first regrouped per XCD; within
@@ -59,148 +76,230 @@ __device__ __forceinline__ bool lm_tile_coords(int pid, int ntt, int nvt, int& t
   return true;
 }
 
+__device__ __forceinline__ int64_t lm_id(const LmTileArgs& a, int n) {
+  return a.ids_i64 ? static_cast<const int64_t*>(a.ids)[n] : static_cast<int64_t>(static_cast<const int32_t*>(a.ids)[n]);
+}
+
+// Workgroup barrier without a memory fence: LDS data of the pipeline is ordered by
+// the explicit s_waitcnt before it; the empty asm statements keep the compiler from
+// moving memory operations across it.
+__device__ __forceinline__ void lm_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One 256 (vocab) x 256 (token) logits tile C[v][t] = sum_h W[v][h] * hidden[t][h].
+// Wave (wv, wt) owns vocab rows wv*128 + [0,128) and token columns wt*128 + [0,128)
+// as 4 x 4 blocks of v_mfma_f32_32x32x16_bf16. Result layout of a 32 x 32 block:
+// lane l holds token column l%32 and vocab rows 8*(r/4) + 4*(l/32) + r%4, r < 16.
+// Operands stream global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging)
+// through NST stages of BK hidden columns.
 template <int MODE>
-__global__ void __launch_bounds__(lm::NTHR) lm_tile_kernel(LmTileArgs a) {
+__global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
+lm_tile_kernel(LmTileArgs a) {
   using namespace lm;
   extern __shared__ __align__(16) char smem[];
-  __bf16* sA = reinterpret_cast<__bf16*>(smem);             // [2][BM][LDK]
-  __bf16* sB = sA + 2 * BM * LDK;                            // [2][BN][LDK]
-  float* sC = reinterpret_cast<float*>(smem);                // [BM][LDC] after the K loop
 
   int tm, tn;
   if (!lm_tile_coords(blockIdx.x, a.ntt, a.nvt, tm, tn)) return;
-  const int m0 = tm * BM;
-  const int n0 = (a.vt0 + tn) * BN;
+  const int m0 = tm * BT;                  // first token
+  const int v0 = (a.vt0 + tn) * BV;        // first vocab entry
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wv = wave >> 1, wt = wave & 1;
 
-  // Operand row buffers: rows past N / V read 0 (range-checked lane offsets).
+  // Operand row buffers: rows past V / N read 0 (range-checked lane offsets).
   const uint32_t rowbytes = static_cast<uint32_t>(a.H) * 2u;
-  const int rows_a = min(BM, a.N - m0), rows_b = min(BN, a.V - n0);
-  const __amdgpu_buffer_rsrc_t ra =
-      row_rsrc(reinterpret_cast<const char*>(a.A) + static_cast<int64_t>(m0) * rowbytes, rows_a * rowbytes);
-  const __amdgpu_buffer_rsrc_t rb =
-      row_rsrc(reinterpret_cast<const char*>(a.B) + static_cast<int64_t>(n0) * rowbytes, rows_b * rowbytes);
+  const int rows_w = min(BV, a.V - v0), rows_h = min(BT, a.N - m0);
+  const __amdgpu_buffer_rsrc_t rw =
+      row_rsrc(reinterpret_cast<const char*>(a.B) + static_cast<int64_t>(v0) * rowbytes, rows_w * rowbytes);
+  const __amdgpu_buffer_rsrc_t rh =
+      row_rsrc(reinterpret_cast<const char*>(a.A) + static_cast<int64_t>(m0) * rowbytes, rows_h * rowbytes);
 
-  // Global -> LDS staging: thread t moves 16 bytes of rows t/8 + 32*i, k = (t%8)*8.
-  const int lr = tid >> 3, lk = (tid & 7) * 8;
-  u32x4 ga[4], gb[4];
-  auto gload = [&](int kb) {
+  // Direct-to-LDS loads: wave w fills rows 16*(4w+q) + lane/4, q < 4, of each operand;
+  // lane writes LDS slot lane%4 of its row, which holds chunk (lane%4) ^ swz(row).
+  uint32_t doff[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t off = static_cast<uint32_t>((lr + 32 * i)) * rowbytes + (kb * BK + lk) * 2u;
-      ga[i] = buf_ld16<false>(ra, off);
-      gb[i] = buf_ld16<false>(rb, off);
-    }
-  };
-  auto lstore = [&](int buf) {
-    __bf16* A = sA + buf * BM * LDK;
-    __bf16* B = sB + buf * BN * LDK;
+  for (int q = 0; q < 4; ++q) {
+    const int row = 16 * (4 * wave + q) + (lane >> 2);
+    doff[q] = static_cast<uint32_t>(row) * rowbytes + 16u * static_cast<uint32_t>((lane & 3) ^ lm_swz(row));
+  }
+  auto issue = [&](int st, int buf) {
+    char* base = smem + buf * kStageBytes;
+    const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u32x4*>(A + (lr + 32 * i) * LDK + lk) = ga[i];
-      *reinterpret_cast<u32x4*>(B + (lr + 32 * i) * LDK + lk) = gb[i];
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (4 * wave + q) * 1024), 16, doff[q] + koff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (4 * wave + q) * 1024), 16, doff[q] + koff,
+                                               0, 0, 0);
     }
   };
 
-  f32x16 acc[2][2];
+  // Fragment reads: row (lane%32) of each 32-row block, chunk 2*kk + lane/32. The
+  // swizzle depends on lane%32 only, so one offset per k-step serves every block.
+  const int sw = lm_swz(lane & 31);
+  const int fo0 = 16 * ((0 + (lane >> 5)) ^ sw), fo1 = 16 * ((2 + (lane >> 5)) ^ sw);
+  const int offA = (wv * 128 + (lane & 31)) * ROWB, offB = kOpBytes + (wt * 128 + (lane & 31)) * ROWB;
+  bf16x8 af[2][4], bfr[2][4];
+  auto fload = [&](int set, int st, int kk) {
+    const char* base = smem + (st % NST) * kStageBytes + (kk ? fo1 : fo0);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(base + offA + i * 32 * ROWB);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j) bfr[set][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 32 * ROWB);
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  auto mfmas = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], bfr[set][j], acc[i][j], 0, 0, 0);
+  };
 
+  // Pipeline: stage kb is read from LDS buffer kb % NST. Every iteration issues one
+  // stage (kb + 3, clamped to the last stage past the end: an L2 hit into a buffer
+  // nobody reads), so exactly one later stage (8 loads per wave) is in flight when
+  // a stage is waited for: vmcnt(8), then the barrier makes every wave's loads of
+  // it visible. Branch-free, so the compiler's LDS waits stay exact.
   const int nk = a.H / BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kb = 0; kb < nk; ++kb) {
-    const int buf = kb & 1;
-    if (kb + 1 < nk) gload(kb + 1);
-    const __bf16* A = sA + buf * BM * LDK;
-    const __bf16* B = sB + buf * BN * LDK;
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int ko = kk * 16 + (lane >> 5) * 8;
-      bf16x8 af[2], bfr[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(A + (wm * 64 + i * 32 + (lane & 31)) * LDK + ko);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(B + (wn * 64 + j * 32 + (lane & 31)) * LDK + ko);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (kb + 1 < nk) lstore(buf ^ 1);
-    __syncthreads();
+  for (int st = 0; st < NST - 1; ++st) issue(min(st, nk - 1), st);
+  __builtin_amdgcn_s_waitcnt(kWaitVm16);
+  lm_barrier();
+  fload(0, 0, 0);
+  for (int kb = 0; kb + 1 < nk; ++kb) {
+    fload(1, kb, 1);
+    mfmas(0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS reads of k-step 1
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // MFMAs of k-step 0
+    __builtin_amdgcn_s_waitcnt(kWaitVm8);                 // stage kb+1 landed
+    lm_barrier();
+    // Buffer (kb+3) % NST held stage kb-1, whose reads all completed before this barrier.
+    issue(min(kb + 3, nk - 1), (kb + 3) % NST);
+    fload(0, kb + 1, 0);
+    mfmas(1);
+    __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);    // the stage's loads
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS reads of the next k-step 0
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // MFMAs of k-step 1
   }
+  fload(1, nk - 1, 1);
+  mfmas(0);
+  mfmas(1);
+  // Drain the trailing loads before any LDS reuse (the backward epilogue).
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
-  // Accumulators -> LDS tile [BM][LDC]. MFMA 32x32 result layout: lane l holds
-  // column l%32 and rows 8*(r/4) + 4*(l/32) + r%4 of its 32 x 32 block.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        const int col = wn * 64 + j * 32 + (lane & 31);
-        sC[row * LDC + col] = acc[i][j][r];
-      }
-  __syncthreads();
+  const int vw = v0 + wv * 128;                 // first vocab row of this wave
+  const int half = lane >> 5;
+  const bool full_v = vw + 128 <= a.V;
+  // Vocab row of acc[i][*][r] relative to vw.
+  auto vrow = [&](int i, int r) { return 32 * i + 8 * (r >> 2) + 4 * half + (r & 3); };
 
-  // Epilogue: two lanes per token row, 64 vocab columns each.
-  const int row = tid >> 1, half = tid & 1;
-  const int n = m0 + row;
-  const int c0 = half * 64;
-  const int ncols = min(max(a.V - n0 - c0, 0), 64);   // valid columns of this half
-  const float* crow = sC + row * LDC + c0;
   if constexpr (MODE == kLmFwd) {
-    float mx = kNegInf;
-    for (int c = 0; c < ncols; ++c) mx = fmaxf(mx, crow[c]);
-    float m2 = mx * kLog2e;
-    const float ref = ms_ref(m2);
-    float s = 0.f;
-    for (int c = 0; c < ncols; ++c) s += hw_exp2(fmaf(crow[c], kLog2e, -ref));
-    const float om = __shfl_xor(m2, 1), os = __shfl_xor(s, 1);
-    ms_merge(m2, s, om, os);
-    if (n < a.N) {
-      if (half == 0) a.part[static_cast<int64_t>(n) * a.ldp + a.vt0 + tn] = make_float2(m2, s);
-      const int64_t id = a.ids_i64 ? static_cast<const int64_t*>(a.ids)[n]
-                                   : static_cast<int64_t>(static_cast<const int32_t*>(a.ids)[n]);
-      const int64_t c = id - n0 - c0;
-      if (c >= 0 && c < ncols) a.tgt[n] = crow[c];
+    // Per token column: (max * log2e, sum 2^(x*log2e - max*log2e)) over this wave's
+    // 128 vocab rows (64 in-lane + the partner lane l^32), and the target logit.
+    const bool any_v = vw < a.V;
+    // Vocab rows past V (last tile only) take no part: their logits become -inf,
+    // whose 2^(...) term is 0. Branch-free selects; full tiles skip them.
+    const int vlim = a.V - vw;
+    if (!full_v) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = vrow(i, r) < vlim ? acc[i][j][r] : kNegInf;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = m0 + wt * 128 + 32 * j + (lane & 31);
+      float mx = kNegInf;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[i][j][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m2 = mx * kLog2e;
+      const float ref = ms_ref(m2);
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += hw_exp2(fmaf(acc[i][j][r], kLog2e, -ref));
+      s += __shfl_xor(s, 32);
+      if (n < a.N && any_v) {
+        if (half == 0) a.part[static_cast<int64_t>(n) * a.ldp + vw / kPart] = make_float2(m2, s);
+        const int64_t rel = lm_id(a, n) - vw;
+        if (rel >= 0 && rel < 128) {
+          const int rr = static_cast<int>(rel) & 31, isel = static_cast<int>(rel) >> 5;
+          const int rsel = (rr >> 3) * 4 + (rr & 3);
+          float val = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) val = (i == isel && r == rsel) ? acc[i][j][r] : val;
+          if (((rr >> 2) & 1) == half) a.tgt[n] = val;
+        }
+      }
     }
   } else {
-    // dlogits[n, v] = coef_n * (onehot - 2^(x*log2e - lse2_n)), bf16, columns
-    // relative to the chunk start; columns past V are written as 0 (chunk padding).
-    if (n < a.N) {
-      const float cf = a.coef[n], l2 = a.lse2[n];
-      const int64_t id = a.ids_i64 ? static_cast<const int64_t*>(a.ids)[n]
-                                   : static_cast<int64_t>(static_cast<const int32_t*>(a.ids)[n]);
-      const int64_t rel = id - n0 - c0;
-      uint16_t* out = reinterpret_cast<uint16_t*>(a.dchunk) + static_cast<int64_t>(n) * a.ldd + (n0 - a.vc0) + c0;
+    // dlogits[t][v] = coef_t * (onehot - 2^(x*log2e - lse2_t)) in bf16, staged as a
+    // token-major tile in LDS (one half of the token columns at a time), then
+    // written with 16-byte row-contiguous stores. Columns are relative to the chunk
+    // start; vocab past V is written as 0.
+    uint16_t* Ds = reinterpret_cast<uint16_t*>(smem);      // [BT / 2][LDD]
+    const int vlim = a.V - vw;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        float v[8];
+    for (int h = 0; h < 2; ++h) {
+      __syncthreads();   // the pipeline's (or the previous half's) LDS reads are done
+      if (wt == h) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int c = q * 8 + e;
-          float d = 0.f;
-          if (c < ncols && cf != 0.f) {
-            d = -cf * hw_exp2(fmaf(crow[c], kLog2e, -l2));
-            if (c == rel) d += cf;
+        for (int j = 0; j < 4; ++j) {
+          const int tcol = 32 * j + (lane & 31);          // column within this half
+          const int n = m0 + h * 128 + tcol;
+          float cf = 0.f, l2 = 0.f;
+          int64_t rel = -1;
+          if (n < a.N) {
+            cf = a.coef[n];
+            l2 = a.lse2[n];
+            rel = lm_id(a, n) - vw;
           }
-          v[e] = d;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float d[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int vr = vrow(i, 4 * q + e);
+                const float x = -cf * hw_exp2(fmaf(acc[i][j][4 * q + e], kLog2e, -l2)) + (vr == rel ? cf : 0.f);
+                d[e] = (cf != 0.f && vr < vlim) ? x : 0.f;
+              }
+              const uint32_t lo = pack2<BF16T>(d[0], d[1]), hi = pack2<BF16T>(d[2], d[3]);
+              *reinterpret_cast<uint2*>(Ds + tcol * LDD + wv * 128 + vrow(i, 4 * q)) = make_uint2(lo, hi);
+            }
         }
-        u32x4 w = {pack2<BF16T>(v[0], v[1]), pack2<BF16T>(v[2], v[3]), pack2<BF16T>(v[4], v[5]),
-                   pack2<BF16T>(v[6], v[7])};
-        if (n0 - a.vc0 + c0 + q * 8 < a.ldd) *reinterpret_cast<u32x4*>(out + q * 8) = w;
+      }
+      __syncthreads();
+      // 32 lanes per token row (512 B), eight rows per step over the workgroup.
+      const int cidx = tid & 31;
+      const int col0 = v0 - a.vc0 + cidx * 8;
+#pragma unroll 4
+      for (int it = 0; it < BT / 2 / 8; ++it) {
+        const int t = it * 8 + (tid >> 5);
+        const int n = m0 + h * 128 + t;
+        if (n < a.N && col0 < a.ldd) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(Ds + t * LDD + cidx * 8);
+          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.dchunk) + static_cast<int64_t>(n) * a.ldd + col0) = w;
+        }
       }
     }
   }

@@ -10,7 +10,12 @@ struct RowArgs;
 
 enum { kLmFwd = 0, kLmBwd = 1 };
 
-// One launch covers token tiles [0, ntt) x vocab tiles [vt0, vt0 + nvt) of 128 x 128.
+constexpr int kLmTileV = 256;    // vocab entries per tile
+constexpr int kLmTileT = 256;    // tokens per tile
+constexpr int kLmPart = 128;     // vocab entries per log-sum-exp partial
+
+// One launch covers token tiles [0, ntt) x vocab tiles [vt0, vt0 + nvt) of
+// kLmTileT x kLmTileV.
 struct LmTileArgs {
   const void* A;        // hidden [N, H] bf16, row-major
   const void* B;        // weight [V, H] bf16, row-major
@@ -19,8 +24,8 @@ struct LmTileArgs {
   const void* ids;      // [N] target ids
   int ids_i64;
   // kLmFwd
-  float2* part;         // [N, ldp]: per vocab tile (max * log2e, sum 2^(x*log2e - max))
-  int ldp;
+  float2* part;         // [N, ldp]: per kLmPart vocab entries (max * log2e, sum 2^(x*log2e - max*log2e))
+  int ldp;              // ceil(V / kLmPart)
   float* tgt;           // [N] target logit
   // kLmBwd
   const float* lse2;    // [N] base-2 log-sum-exp

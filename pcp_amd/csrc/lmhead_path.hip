@@ -28,7 +28,6 @@
 namespace pcp {
 namespace {
 
-constexpr int kTile = 128;
 constexpr int64_t kDefaultChunk = 16384;
 
 inline size_t r256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
@@ -43,8 +42,8 @@ int validate_lm(const pcp_lmhead_args* a) {
   int64_t n;
   if (mul_overflows(a->n_seq, a->rows, &n) || n > (1 << 28))
     return fail(nullptr, PCP_ERR_OVERFLOW, "n_seq * rows exceeds 2^28 tokens");
-  if (a->vocab_chunk < 0 || a->vocab_chunk % kTile != 0)
-    return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab_chunk must be a multiple of 128");
+  if (a->vocab_chunk < 0 || a->vocab_chunk % kLmTileV != 0)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab_chunk must be a multiple of %d", kLmTileV);
   if (!a->hidden_states || !a->weight || !a->ids) return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden_states / weight / ids is NULL");
   if (a->ids_dtype != PCP_I64 && a->ids_dtype != PCP_I32) return fail(nullptr, PCP_ERR_DTYPE, "ids dtype must be i64 or i32");
   if (a->mask && a->mask_dtype != PCP_F32 && a->mask_dtype != PCP_BOOL)
@@ -79,7 +78,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   hipStream_t st = static_cast<hipStream_t>(a->stream);
 
   const int64_t S = a->n_seq, T = a->rows, N = S * T, H = a->hidden, V = a->vocab;
-  const int nvt = static_cast<int>((V + kTile - 1) / kTile);
+  const int nvt = static_cast<int>((V + kLmTileV - 1) / kLmTileV);     // vocab tiles
+  const int npart = static_cast<int>((V + kLmPart - 1) / kLmPart);    // log-sum-exp partials per token
   const bool ref = a->loss_mode == PCP_LOSS_GRPO_CLIP_KL;
   const bool bwd = a->dhidden || a->dweight;
   const int64_t chunk = a->vocab_chunk ? a->vocab_chunk : kDefaultChunk;
@@ -92,7 +92,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_tl = a->token_loss ? 0 : take(4 * N);
   const size_t o_live = take(4 * N), o_cidx = take(4 * N), o_idsc = take(4 * N), o_cnt = take(4);
   const size_t o_hid = take(2 * static_cast<size_t>(N) * H);
-  const size_t o_part = take(8 * static_cast<size_t>(N) * nvt);
+  const size_t o_part = take(8 * static_cast<size_t>(N) * npart);
   const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
   const size_t o_chunk = bwd ? take(2 * static_cast<size_t>(N) * chunk) : 0;
   const size_t o_dhc = a->dhidden ? take(4 * static_cast<size_t>(N) * H) : 0;
@@ -116,7 +116,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
   const int nl = *ctx->h_count;
   if (nl < 0 || nl > N) return fail(ctx, PCP_ERR_DEVICE, "live-token count %d out of range", nl);
-  const int ntl = (nl + kTile - 1) / kTile;
+  const int ntl = (nl + kLmTileT - 1) / kLmTileT;
   if ((e = launch_lm_gather_rows(a->hidden_states, sp + o_hid, I(o_live), nl, static_cast<int>(H), st)) != hipSuccess)
     return hip_fail(ctx, e, "gathering live hidden rows");
 
@@ -146,8 +146,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   ta.ids = I(o_idsc);
   ta.ids_i64 = 0;
   ta.part = part;
-  ta.ldp = nvt;
-  LmReduceArgs rd{part, nl, nvt, nvt, nullptr};
+  ta.ldp = npart;
+  LmReduceArgs rd{part, nl, npart, npart, nullptr};
   for (int m = 0; m < (ref && nl > 0 ? 2 : nl > 0 ? 1 : 0); ++m) {
     ta.B = m == 0 ? a->weight : a->ref_weight;
     ta.tgt = F(m == 0 ? o_tgt : o_rtgt);
@@ -212,8 +212,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     for (int64_t vc0 = 0; vc0 < V; vc0 += chunk) {
       const int64_t w = (V - vc0 < chunk) ? V - vc0 : chunk;
       ta.vc0 = static_cast<int>(vc0);
-      ta.vt0 = static_cast<int>(vc0 / kTile);
-      ta.nvt = static_cast<int>((w + kTile - 1) / kTile);
+      ta.vt0 = static_cast<int>(vc0 / kLmTileV);
+      ta.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
       if ((e = launch_lm_tiles(kLmBwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head backward tiles");
       const void* wc = static_cast<const char*>(a->weight) + vc0 * H * 2;
       if (a->dhidden) {

@@ -231,8 +231,8 @@ def test_execute_lmhead_shifted_vs_oracle():
 def test_lmhead_deterministic():
     c = make_case(2, 70, 128, 900, 2, seed=5, lengths=[70, 33])
     old = np.full((2, 70), -7.0, np.float32)
-    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=384)
-    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=384)
+    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=512)
+    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=512)
     torch.cuda.synchronize()
     for f in ("loss", "logp", "ref_logp", "token_loss", "dhidden", "dweight"):
         assert torch.equal(getattr(a, f), getattr(b, f)), f
