@@ -253,9 +253,6 @@ def main() -> None:
     from pcp_amd._lib import LossMode, check, lib
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    if args.config == 5:
-        bench_lmhead(args)
-        return
     dev = torch.device("cuda:0")
     if args.copy_calibration_gib > 0:
         n = int(args.copy_calibration_gib * (1 << 30)) // 2
@@ -263,6 +260,9 @@ def main() -> None:
         torch.empty_like(src).copy_(src)
         torch.cuda.synchronize()
         del src
+    if args.config == 5:
+        bench_lmhead(args)
+        return
     cfg = synth.CONFIGS[args.config]
     clip = args.mode == "clip_kl"
     mode = LossMode.GRPO_CLIP_KL if clip else LossMode.REINFORCE

@@ -271,3 +271,53 @@ def test_checks_catch_planted_mistakes(orc):
     transposed = np.transpose(r.dlogits, (1, 0, 2)).reshape(r.dlogits.shape) if S != LS else None
     if transposed is not None:
         assert not passes(transposed)
+
+
+# ---- a6: LM-head oracle -------------------------------------------------------------
+
+def test_lmhead_logits_brute_force_and_torch(orc):
+    """logits = hidden . W^T of the exact bf16 values: brute-force dot products on a tiny
+    case, torch float64 matmul on a larger one, and a transposed-operand mistake fails."""
+    rng = np.random.default_rng(3)
+    hb = orc.bf16_from_f32(rng.standard_normal((3, 5)).astype(np.float32))
+    wb = orc.bf16_from_f32(rng.standard_normal((4, 5)).astype(np.float32))
+    got = orc.lmhead_logits(hb, wb)
+    h, w = orc.bf16_to_f32(hb).astype(np.float64), orc.bf16_to_f32(wb).astype(np.float64)
+    brute = np.array([[sum(h[n, k] * w[v, k] for k in range(5)) for v in range(4)] for n in range(3)])
+    np.testing.assert_allclose(got, brute, rtol=1e-14, atol=1e-14)
+    hb = orc.bf16_from_f32(rng.standard_normal((17, 64)).astype(np.float32))
+    wb = orc.bf16_from_f32(rng.standard_normal((33, 64)).astype(np.float32))
+    ref = torch.from_numpy(orc.bf16_to_f32(hb).astype(np.float64)) @ torch.from_numpy(
+        orc.bf16_to_f32(wb).astype(np.float64)).T
+    np.testing.assert_allclose(orc.lmhead_logits(hb, wb), ref.numpy(), rtol=1e-13, atol=1e-13)
+    assert not np.allclose(orc.lmhead_logits(hb, wb)[:, :17], ref.numpy()[:17, :17].T, rtol=1e-3)
+
+
+def test_lmhead_grads_match_torch_autograd(orc):
+    """dhidden = D.W and dW = D^T.hidden with D = c (onehot - softmax) against torch float64
+    autograd of L = sum_n c_n * logp_n(hidden . W^T) (the LM head's VJP, matmulVJP,
+    src/autodiff/vjp_rules.zig:426-497). Masked tokens (c = 0) and an ignored id carry no gradient."""
+    rng = np.random.default_rng(4)
+    N, H, V = 9, 16, 23
+    hb = orc.bf16_from_f32(rng.standard_normal((N, H)).astype(np.float32))
+    wb = orc.bf16_from_f32((rng.standard_normal((V, H)) * 0.5).astype(np.float32))
+    ids = rng.integers(0, V, N)
+    ids[4] = -100
+    coef = rng.standard_normal(N)
+    coef[2] = 0.0
+    coef[4] = 0.0
+    h = torch.tensor(orc.bf16_to_f32(hb).astype(np.float64), requires_grad=True)
+    w = torch.tensor(orc.bf16_to_f32(wb).astype(np.float64), requires_grad=True)
+    logits = h @ w.T
+    lp = torch.log_softmax(logits, dim=1).gather(1, torch.from_numpy(np.clip(ids, 0, None))[:, None])[:, 0]
+    (torch.from_numpy(coef) * lp).sum().backward()
+    L = logits.detach().numpy()
+    lse = torch.logsumexp(logits, dim=1).detach().numpy()
+    dh, dw = orc.lmhead_grads(hb, wb, L, lse, coef, ids)
+    np.testing.assert_allclose(dh, h.grad.numpy(), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(dw, w.grad.numpy(), rtol=1e-12, atol=1e-13)
+    assert not np.any(dh[[2, 4]])
+    # planted mistakes: a flipped sign, a dropped onehot term
+    assert not np.allclose(-dh, h.grad.numpy(), rtol=1e-6)
+    D = -np.exp(L - lse[:, None]) * coef[:, None]
+    assert not np.allclose(D @ orc.bf16_to_f32(wb).astype(np.float64), h.grad.numpy(), rtol=1e-6)
