@@ -226,12 +226,77 @@ def bench_lmhead(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+QWEN05_PARAMS = 494_032_768   # Qwen2.5-0.5B, the RL model of the reference's runs (~494M f32 params)
+
+
+def bench_nesterov(args) -> None:
+    """The Nesterov update of RLShepherd's master weights (nesterov.zig:70-98) as one HBM
+    pass over a flat f32 parameter buffer, with the bf16 shadow copy for the next bf16
+    forward: reads p, v, g (12 B) and writes p, v, bf16 p (10 B) per parameter."""
+    import numpy as np
+    import torch
+
+    from pcp_amd import step
+
+    dev = torch.device("cuda:0")
+    P = QWEN05_PARAMS
+    gen = torch.Generator(device=dev).manual_seed(0)
+    p = torch.randn(P, device=dev, generator=gen)
+    g = torch.randn(P, device=dev, generator=gen) * 1e-3
+    shadow = torch.empty(P, dtype=torch.bfloat16, device=dev)
+    opt = step.Nesterov([P], 1e-5, 0.9)
+    for _ in range(args.warmup):
+        opt.update_flat(p, g, shadow)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record()
+    for _ in range(args.steps):
+        opt.update_flat(p, g, shadow)
+    b.record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kernel_ms = a.elapsed_time(b) / args.steps
+    ms_step = elapsed * 1e3 / args.steps
+    alg = 22 * P
+    line = {
+        "metric": "Nesterov update params/s and achieved HBM GB/s, 494M f32 params + bf16 shadow",
+        "value": P / (ms_step / 1e3), "unit": "params/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (torch normal init)",
+        "config": {"workload": f"Nesterov (Sutskever, nesterov.zig:86-97) over {P} f32 parameters, "
+                               "flat buffer, bf16 shadow", "params": P},
+        "roofline": {"bound": "hbm", "achieved": alg / (kernel_ms / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": alg / (kernel_ms / 1e3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "nesterov_kernel<0, true>", "kernel_ms": kernel_ms, "algorithmic_bytes": alg},
+    }
+    tfile = os.path.join(ROOT, "profiles", "traffic_nesterov.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+        n = P
+        ps, vs, gs = (np.random.default_rng(0).standard_normal(n).astype(np.float32) for _ in range(3))
+        t0 = time.perf_counter()
+        orc.nesterov(ps, vs, gs, 1e-5, 0.9)
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": n / dt, "unit": "params/s", "cores": 1, "kind": "port",
+                                "sample": f"{n} params in {dt:.2f} s: oracle f32 loop of nesterov.zig:86-97 "
+                                          "(step_oracle.cpp), one thread, as the reference's host loop"}
+    print(json.dumps(line), flush=True)
+    opt.close()
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--workload", choices=["loss", "nesterov"], default="loss",
+                    help="loss: the GRPO loss head of --config (the headline metric); nesterov: the "
+                         "optimizer step over Qwen2.5-0.5B's parameters")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -260,6 +325,9 @@ def main() -> None:
         torch.empty_like(src).copy_(src)
         torch.cuda.synchronize()
         del src
+    if args.workload == "nesterov":
+        bench_nesterov(args)
+        return
     if args.config == 5:
         bench_lmhead(args)
         return

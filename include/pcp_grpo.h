@@ -66,7 +66,10 @@ typedef enum pcp_status {
   PCP_ERR_COUNT_MISMATCH = -8,   /* pcp_execute: wrong number of inputs
                                     (rl_shepherd.zig:601-604 analogue)                */
   PCP_ERR_OVERFLOW = -9,         /* size computation overflows int64 / byte counts     */
-  PCP_ERR_UNSUPPORTED = -10      /* valid request this build does not implement        */
+  PCP_ERR_UNSUPPORTED = -10,     /* valid request this build does not implement        */
+  PCP_ERR_OUT_OF_BOUNDS = -11,   /* tensor index past the optimizer's tensors (nesterov.zig:72)  */
+  PCP_ERR_DIMENSION_MISMATCH = -12, /* element counts differ (nesterov.zig:73-76)        */
+  PCP_ERR_CORRUPT_STATE = -13    /* serialized state too short (nesterov.zig:124, CorruptSaveFile) */
 } pcp_status;
 
 /* Loss definitions for the per-token term l_t (aggregation is identical):

@@ -12,6 +12,10 @@ What each function restates (reference file:line):
                cited in grpo_oracle.cpp) and the clipped-ratio + k3-KL loss
   grpo_full    the whole loss head over [S, T, V] with the kernels' row layout
                (seq lengths = clamp(mask.sum(1), min=1), export_qwen_forward.py:160)
+  lmhead_*     export_qwen_forward.py:147 (lm_head) and matmulVJP, vjp_rules.zig:426-497
+  nesterov     src/optimizers/nesterov.zig:86-97 and nesterov_mlir.zig:93-99
+  grad_stats   src/nodes/controllers/rl_shepherd.zig:607-641
+  pack         src/nodes/controllers/rl_shepherd.zig:487-515
 
 Pinning: every function is checked in tests/test_oracle.py against the reference's
 known-answer tests (src/examples/isolated_vjp_tests.zig), closed forms, brute force
@@ -67,6 +71,13 @@ def lib() -> ctypes.CDLL:
         L.oracle_grpo_rows.argtypes = [ctypes.POINTER(_RowsArgs)]
         L.oracle_grpo_rows.restype = ctypes.c_int
         L.oracle_max_threads.restype = ctypes.c_int
+        _VP, _I64 = ctypes.c_void_p, ctypes.c_int64
+        L.oracle_nesterov.argtypes = [_VP, _VP, _VP, _I64, ctypes.c_float, ctypes.c_float, ctypes.c_int]
+        L.oracle_nesterov.restype = None
+        L.oracle_grad_stats.argtypes = [_VP, _I64, _VP, _VP, _VP, _VP]
+        L.oracle_grad_stats.restype = None
+        L.oracle_pack.argtypes = [_VP, _I64, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP]
+        L.oracle_pack.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -256,3 +267,41 @@ def grpo_full(logits: np.ndarray, ids: np.ndarray, mask: np.ndarray | None, *, r
         dl = np.zeros((S, LS, V), np.float32)
         dl[:, :rows, :] = r.dlogits.reshape(S, rows, V)
     return FullResult(loss, place(r.lp), place(r.lr), place(r.token_loss), place(r.coef), adv, L, dl)
+
+
+# ---- the work around the loss head in one step (step_oracle.cpp) ---------------------
+
+def nesterov(p: np.ndarray, v: np.ndarray, g: np.ndarray, lr: float, mu: float, mode: int = 0):
+    """One update, f32 op by op: mode 0 = nesterov.zig:86-97 (v = mu*v + g;
+    p = p - lr*(g + mu*v)), mode 1 = nesterov_mlir.zig:93-99 (v = mu*v + lr*g; p = p - v).
+    Returns new (p, v) arrays."""
+    p = np.array(p, dtype=np.float32, copy=True)
+    v = np.array(v, dtype=np.float32, copy=True)
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    lib().oracle_nesterov(_ptr(p), _ptr(v), _ptr(g), p.size, ctypes.c_float(lr), ctypes.c_float(mu), int(mode))
+    return p, v
+
+
+def grad_stats(g: np.ndarray) -> dict:
+    """rl_shepherd.zig:607-641: f64 sum of squares and max |g| over the finite values,
+    NaN and Inf counts (sequential, as the reference)."""
+    g = np.ascontiguousarray(g, dtype=np.float32).reshape(-1)
+    s, m = ctypes.c_double(), ctypes.c_float()
+    nn, ni = ctypes.c_int64(), ctypes.c_int64()
+    lib().oracle_grad_stats(_ptr(g), g.size, ctypes.byref(s), ctypes.byref(m), ctypes.byref(nn), ctypes.byref(ni))
+    return {"sumsq": s.value, "l2_norm": float(np.sqrt(s.value)), "max_abs": m.value, "nan_count": nn.value,
+            "inf_count": ni.value, "elements": g.size}
+
+
+def pack(prompt_tokens, prompt_offsets, completion_tokens, completion_offsets, n_rows: int, seq_len: int):
+    """rl_shepherd.zig:487-515 packing. Returns (ids int64 [n_rows, T], mask f32, ok)."""
+    pt = np.ascontiguousarray(prompt_tokens, dtype=np.int64)
+    po = np.ascontiguousarray(prompt_offsets, dtype=np.int64)
+    ct = np.ascontiguousarray(completion_tokens, dtype=np.int64)
+    co = np.ascontiguousarray(completion_offsets, dtype=np.int64)
+    R = po.size - 1
+    ids = np.empty((n_rows, seq_len), np.int64)
+    mask = np.empty((n_rows, seq_len), np.float32)
+    rc = lib().oracle_pack(_ptr(pt), pt.size, _ptr(po), _ptr(ct), ct.size, _ptr(co), R, n_rows, seq_len,
+                           _ptr(ids), _ptr(mask))
+    return ids, mask, rc == 0

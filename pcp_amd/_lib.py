@@ -59,6 +59,9 @@ STATUS = {
     -8: "PCP_ERR_COUNT_MISMATCH",
     -9: "PCP_ERR_OVERFLOW",
     -10: "PCP_ERR_UNSUPPORTED",
+    -11: "PCP_ERR_OUT_OF_BOUNDS",
+    -12: "PCP_ERR_DIMENSION_MISMATCH",
+    -13: "PCP_ERR_CORRUPT_STATE",
 }
 
 
@@ -108,6 +111,19 @@ class LmheadArgs(ctypes.Structure):
     ]
 
 
+class GradStats(ctypes.Structure):
+    """pcp_grad_stats (include/pcp_step.h)."""
+    _fields_ = [
+        ("sumsq", ctypes.c_double), ("l2_norm", ctypes.c_double), ("max_abs", ctypes.c_float),
+        ("nan_count", ctypes.c_int64), ("inf_count", ctypes.c_int64), ("elements", ctypes.c_int64),
+    ]
+
+
+class NesterovMode(enum.IntEnum):
+    sutskever = 0   # nesterov.zig:86-97 (RLShepherd's optimizer)
+    mlir = 1        # nesterov_mlir.zig:93-99
+
+
 # Every symbol the headers in include/ declare, with its ctypes signature.
 _VP, _I, _I64, _F, _U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint64
 SIGNATURES = {
@@ -134,6 +150,16 @@ SIGNATURES = {
                                        ctypes.POINTER(ctypes.c_uint32)]),
     "pcp_synth_logits": (_I, [_VP, _VP, _I64, _I, _F, _F, _U64, _VP]),
     "pcp_synth_sample_tokens": (_I, [_VP, _I, _I64, _I64, _U64, _VP, _VP]),
+    "pcp_pack_rollouts": (_I, [_VP, _VP, _I64, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP]),
+    "pcp_grad_stats_compute": (_I, [_VP, _VP, _I64, _I, ctypes.POINTER(GradStats), _VP]),
+    "pcp_nesterov_create": (_I, [_VP, _F, _F, _I, _I, ctypes.POINTER(_I64), ctypes.POINTER(_VP)]),
+    "pcp_nesterov_destroy": (None, [_VP]),
+    "pcp_nesterov_reset": (_I, [_VP, _VP]),
+    "pcp_nesterov_update": (_I, [_VP, _I, _VP, _VP, _I64, _VP]),
+    "pcp_nesterov_update_flat": (_I, [_VP, _VP, _VP, _VP, _VP]),
+    "pcp_nesterov_total": (_I64, [_VP]),
+    "pcp_nesterov_serialize": (_I, [_VP, _VP, ctypes.c_size_t]),
+    "pcp_nesterov_deserialize": (_I, [_VP, _VP, ctypes.c_size_t]),
 }
 
 _lib = None

@@ -53,6 +53,8 @@ int collect_device_errors(pcp_ctx* ctx) {
   if (e != hipSuccess) return hip_fail(ctx, e, "clearing the device error word");
   if (h & kErrTokenRange)
     return fail(ctx, PCP_ERR_TOKEN_RANGE, "a live token id is outside [0, vocab) and is not -100");
+  if (h & kErrBadRagged)
+    return fail(ctx, PCP_ERR_INVALID_ARG, "rollout offsets decrease or run past the token array");
   return fail(ctx, PCP_ERR_NONFINITE, "a live row has a non-finite log-sum-exp (NaN/Inf logits)");
 }
 

@@ -268,3 +268,49 @@ def test_philox_known_answers():
     assert philox([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2) == [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]
     assert philox([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0]) == \
         [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]
+
+
+def test_step_api_argument_errors_without_device():
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    counts = (ctypes.c_int64 * 3)(4, 5, 6)
+    assert L.pcp_nesterov_create(None, 0.1, 0.9, 7, 3, counts, ctypes.byref(h)) == -1
+    assert "mode" in L.pcp_last_error(None).decode()
+    assert L.pcp_nesterov_create(None, 0.1, 0.9, 0, 0, counts, ctypes.byref(h)) == -1
+    neg = (ctypes.c_int64 * 2)(3, -1)
+    assert L.pcp_nesterov_create(None, 0.1, 0.9, 0, 2, neg, ctypes.byref(h)) == -1
+    assert L.pcp_nesterov_create(None, float("nan"), 0.9, 0, 3, counts, ctypes.byref(h)) == -1
+    assert L.pcp_nesterov_create(None, 0.1, 0.9, 0, 3, counts, ctypes.byref(h)) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode() and not h.value
+    assert L.pcp_nesterov_update(None, 0, None, None, 0, None) == -1
+    assert L.pcp_nesterov_update_flat(None, None, None, None, None) == -1
+    assert L.pcp_nesterov_reset(None, None) == -1
+    assert L.pcp_nesterov_total(None) == -1
+    assert L.pcp_nesterov_serialize(None, None, 0) == -1
+    assert L.pcp_nesterov_deserialize(None, None, 0) == -1
+    L.pcp_nesterov_destroy(None)
+    st = _lib.GradStats()
+    assert L.pcp_grad_stats_compute(None, None, 5, 0, ctypes.byref(st), None) == -1
+    assert L.pcp_grad_stats_compute(None, None, 0, 0, ctypes.byref(st), None) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()
+    assert L.pcp_pack_rollouts(None, None, 0, None, None, 0, None, 3, 2, 8, 0x10, 0x20, None) == -1
+    assert "n_rollouts <= n_rows" in L.pcp_last_error(None).decode()
+    assert L.pcp_pack_rollouts(None, None, 0, 0x10, None, 0, 0x20, 1, 2, 8, 0x10, 0x20, None) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()
+    assert L.pcp_pack_rollouts(None, None, 0, 0x10, None, 0, 0x20, 1, 1 << 40, 1 << 30, 0x10, 0x20, None) == -9
+
+
+def test_grad_stats_struct_layout(tmp_path):
+    fields = [f[0] for f in _lib.GradStats._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "pcp_step.h"', "int main(void){",
+           'printf("%zu\\n", sizeof(pcp_grad_stats));']
+    src += [f'printf("%zu\\n", offsetof(pcp_grad_stats, {f}));' for f in fields]
+    src += ["return 0;}"]
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", INCLUDE, str(c), "-o", str(exe)], check=True)
+    vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(_lib.GradStats)
+    for f, off in zip(fields, vals[1:]):
+        assert getattr(_lib.GradStats, f).offset == off, f

@@ -1,0 +1,184 @@
+"""Parity of the step around the loss head (include/pcp_step.h) with the CPU oracle:
+Nesterov update (both formulations), gradient statistics and rollout packing.
+
+Bars: the update, the bf16 shadow copy, packing and the statistics' counts and max are
+bit-exact; the f64 sum of squares runs in a different (fixed) order than the
+reference's sequential loop, so it is checked to 1e-12 relative.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from pcp_amd import step
+from pcp_amd._lib import NesterovMode, PcpError
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("mode", [NesterovMode.sutskever, NesterovMode.mlir])
+def test_nesterov_flat_bit_exact(mode):
+    rng = np.random.default_rng(11)
+    counts = [3, 1000, 5, 65537, 7, 4096]           # ragged: tensor offsets are not 16-byte aligned
+    n = sum(counts)
+    p = rng.standard_normal(n).astype(np.float32)
+    lr, mu = 0.01, 0.9
+    opt = step.Nesterov(counts, lr, mu, mode)
+    pd = t(p)
+    shadow = torch.empty(n, dtype=torch.bfloat16, device=DEV)
+    v = np.zeros(n, np.float32)
+    for k in range(3):
+        g = rng.standard_normal(n).astype(np.float32)
+        opt.update_flat(pd, t(g), shadow)
+        p, v = orc.nesterov(p, v, g, lr, mu, int(mode))
+        assert np.array_equal(bits(pd.cpu().numpy()), bits(p)), f"step {k}"
+        assert np.array_equal(shadow.view(torch.int16).cpu().numpy().view(np.uint16), orc.bf16_from_f32(p))
+    assert np.array_equal(bits(np.frombuffer(opt.serialize(), np.float32)), bits(v))
+    opt.close()
+
+
+def test_nesterov_per_tensor_matches_flat_and_errors():
+    rng = np.random.default_rng(12)
+    counts = [5, 17, 1024, 3, 333]
+    n = sum(counts)
+    offs = np.concatenate([[0], np.cumsum(counts)])
+    p0 = rng.standard_normal(n).astype(np.float32)
+    g = rng.standard_normal(n).astype(np.float32)
+    opt = step.Nesterov(counts, 0.05, 0.8)
+    flat = t(p0)                                     # per-tensor views of one flat buffer
+    gd = t(g)
+    for i in range(len(counts)):
+        opt.update(i, flat[offs[i]:offs[i + 1]], gd[offs[i]:offs[i + 1]])
+    want, v = orc.nesterov(p0, np.zeros(n, np.float32), g, 0.05, 0.8)
+    assert np.array_equal(bits(flat.cpu().numpy()), bits(want))
+    assert np.array_equal(bits(np.frombuffer(opt.serialize(), np.float32)), bits(v))
+    # standalone (separately allocated, aligned) tensors give the same values
+    opt2 = step.Nesterov(counts, 0.05, 0.8)
+    parts = [t(p0[offs[i]:offs[i + 1]]) for i in range(len(counts))]
+    for i, pt in enumerate(parts):
+        opt2.update(i, pt, gd[offs[i]:offs[i + 1]].clone())
+    assert np.array_equal(bits(torch.cat(parts).cpu().numpy()), bits(want))
+    with pytest.raises(PcpError) as e:
+        opt.update(len(counts), parts[0], parts[0])
+    assert e.value.code == -11
+    with pytest.raises(PcpError) as e:
+        opt.update(1, parts[0], parts[0])
+    assert e.value.code == -12
+    opt.close()
+    opt2.close()
+
+
+def test_nesterov_state_round_trip_and_reset():
+    rng = np.random.default_rng(13)
+    counts = [100, 28]
+    n = sum(counts)
+    opt = step.Nesterov(counts, 0.1, 0.9)
+    pd = t(rng.standard_normal(n).astype(np.float32))
+    opt.update_flat(pd, t(rng.standard_normal(n).astype(np.float32)))
+    state = opt.serialize()
+    assert len(state) == 4 * n and np.any(np.frombuffer(state, np.float32))
+    opt.reset()
+    assert not np.any(np.frombuffer(opt.serialize(), np.float32))
+    opt.deserialize(state + b"extra bytes are ignored")
+    assert opt.serialize() == state
+    with pytest.raises(PcpError) as e:
+        opt.deserialize(state[:-4])
+    assert e.value.code == -13
+    assert opt.serialize() == state                 # a rejected state changes nothing
+    opt.close()
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+def test_grad_stats_match_oracle(offset):
+    rng = np.random.default_rng(14)
+    g = (rng.standard_normal(1 << 20) * 2).astype(np.float32)
+    g[[3, 77777]] = np.nan
+    g[[10, 500000]] = np.inf
+    g[99] = -np.inf
+    gd = t(g)[offset:]                              # offset 1: a pointer that is not 16-byte aligned
+    got = step.grad_stats(gd)
+    want = orc.grad_stats(g[offset:])
+    for k in ("nan_count", "inf_count", "elements"):
+        assert got[k] == want[k], k
+    assert got["max_abs"] == want["max_abs"]
+    assert abs(got["sumsq"] - want["sumsq"]) <= 1e-12 * want["sumsq"]
+    # two tensors accumulate like the reference's loop over gradients
+    both = step.grad_stats([gd[:1000], gd[1000:]])
+    assert both["nan_count"] == want["nan_count"] and both["max_abs"] == want["max_abs"]
+    assert abs(both["sumsq"] - want["sumsq"]) <= 1e-12 * want["sumsq"]
+    assert both["elements"] == want["elements"]
+
+
+def test_grad_stats_sum_of_squares_in_f64():
+    x = np.array([1e20, 3.0, -1e20], np.float32)                         # squares overflow f32
+    got = step.grad_stats(t(x))
+    big = float(x[0]) ** 2
+    assert got["sumsq"] == (big + 9.0) + big and np.isfinite(got["l2_norm"]) and got["max_abs"] == x[0]
+
+
+def test_grad_stats_deterministic():
+    g = t(np.random.default_rng(15).standard_normal(3_000_001).astype(np.float32))
+    a, b = step.grad_stats(g), step.grad_stats(g)
+    assert a == b
+
+
+def test_pack_rollouts_match_oracle():
+    rng = np.random.default_rng(16)
+    R, n_rows, T = 13, 16, 512
+    lp = rng.integers(0, 300, R)
+    lc = rng.integers(0, 400, R)
+    lp[0], lc[1] = 0, 0
+    lp[4], lc[4] = 500, 100                         # truncated at T
+    pt = rng.integers(0, 151936, lp.sum())
+    ct = rng.integers(0, 151936, lc.sum())
+    po = np.concatenate([[0], np.cumsum(lp)])
+    co = np.concatenate([[0], np.cumsum(lc)])
+    ids, mask = step.pack_rollouts(t(pt), t(po), t(ct), t(co), n_rows, T)
+    want_ids, want_mask, ok = orc.pack(pt, po, ct, co, n_rows, T)
+    assert ok
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    assert np.array_equal(mask.cpu().numpy(), want_mask)
+
+
+def test_pack_rollouts_bad_offsets_are_reported():
+    po = np.array([0, 5, 3, 6], np.int64)            # rollout 1 ends before it starts
+    co = np.array([0, 2, 4, 100], np.int64)          # rollout 2 runs past the completion tokens
+    pt = np.arange(1, 7, dtype=np.int64)
+    ct = np.arange(11, 17, dtype=np.int64)
+    with pytest.raises(PcpError) as e:
+        step.pack_rollouts(t(pt), t(po), t(ct), t(co), 3, 8)
+    assert e.value.code == -1
+    ids, mask = step.pack_rollouts(t(pt), t(np.array([0, 5, 6, 6])), t(ct), t(np.array([0, 2, 4, 6])), 3, 8)
+    want_ids, want_mask, ok = orc.pack(pt, [0, 5, 6, 6], ct, [0, 2, 4, 6], 3, 8)
+    assert ok and np.array_equal(ids.cpu().numpy(), want_ids) and np.array_equal(mask.cpu().numpy(), want_mask)
+
+
+def test_nesterov_full_model_size_sampled():
+    """494,032,768 parameters (Qwen2.5-0.5B): the update is elementwise, so the oracle
+    checks a random sample of 2^20 elements bit for bit."""
+    P = 494_032_768
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    p = torch.randn(P, device=DEV, generator=gen)
+    g = torch.randn(P, device=DEV, generator=gen)
+    idx = torch.from_numpy(np.random.default_rng(17).integers(0, P, 1 << 20)).to(DEV)
+    p_s, g_s = p[idx].cpu().numpy(), g[idx].cpu().numpy()
+    opt = step.Nesterov([P], 1e-5, 0.9)
+    shadow = torch.empty(P, dtype=torch.bfloat16, device=DEV)
+    opt.update_flat(p, g, shadow)
+    opt.update_flat(p, g, shadow)
+    torch.cuda.synchronize()
+    want, _ = orc.nesterov(p_s, np.zeros_like(p_s), g_s, 1e-5, 0.9)
+    want, _ = orc.nesterov(want, orc.nesterov(p_s, np.zeros_like(p_s), g_s, 1e-5, 0.9)[1], g_s, 1e-5, 0.9)
+    assert np.array_equal(bits(p[idx].cpu().numpy()), bits(want))
+    assert np.array_equal(shadow[idx].view(torch.int16).cpu().numpy().view(np.uint16), orc.bf16_from_f32(want))
+    opt.close()

@@ -321,3 +321,96 @@ def test_lmhead_grads_match_torch_autograd(orc):
     assert not np.allclose(-dh, h.grad.numpy(), rtol=1e-6)
     D = -np.exp(L - lse[:, None]) * coef[:, None]
     assert not np.allclose(D @ orc.bf16_to_f32(wb).astype(np.float64), h.grad.numpy(), rtol=1e-6)
+
+
+# ---- the step around the loss head: Nesterov, gradient statistics, packing ----------------
+
+def test_nesterov_mlir_reference_kat(orc):
+    """The reference's known answer (src/examples/mlir_optimizer_test.zig:176-256):
+    p=0.5, v=0, g=0.2, lr=0.1, mu=0.9 -> p=0.48, v=0.02 (within 1e-6)."""
+    p, v = orc.nesterov([0.5], [0.0], [0.2], 0.1, 0.9, mode=1)
+    assert abs(p[0] - 0.48) <= 1e-6 and abs(v[0] - 0.02) <= 1e-6
+    p, v = orc.nesterov([0.5], [0.0], [0.2], 0.1, 0.9, mode=0)   # the other formulation differs
+    assert abs(p[0] - 0.48) > 1e-3
+
+
+def test_nesterov_matches_torch_sgd(orc):
+    """nesterov.zig's update is torch.optim.SGD(momentum=mu, nesterov=True, dampening=0):
+    buf = mu*buf + g; p -= lr*(g + mu*buf). torch may fuse into FMAs, so a few ulp."""
+    rng = np.random.default_rng(5)
+    n, lr, mu = 4099, 0.03, 0.9
+    p0 = rng.standard_normal(n).astype(np.float32)
+    pt = torch.tensor(p0.copy(), requires_grad=True)
+    opt = torch.optim.SGD([pt], lr=lr, momentum=mu, nesterov=True, dampening=0.0)
+    p, v = p0.copy(), np.zeros(n, np.float32)
+    pb, vb = p0.copy(), np.zeros(n, np.float32)     # planted mistake: lookahead on the old velocity
+    tol = dict(rtol=4e-7, atol=4e-7 * np.abs(p0).max())
+    for step in range(5):
+        g = rng.standard_normal(n).astype(np.float32)
+        pt.grad = torch.from_numpy(g.copy())
+        opt.step()
+        p, v = orc.nesterov(p, v, g, lr, mu, mode=0)
+        np.testing.assert_allclose(p, pt.detach().numpy(), **tol)
+        np.testing.assert_allclose(v, opt.state[pt]["momentum_buffer"].numpy(), rtol=4e-7, atol=1e-6)
+        pb = (pb - np.float32(lr) * (g + np.float32(mu) * vb)).astype(np.float32)
+        vb = (np.float32(mu) * vb + g).astype(np.float32)
+    assert not np.allclose(pb, pt.detach().numpy(), **tol)
+
+
+def test_nesterov_closed_forms(orc):
+    """Constant gradient from v0 = 0: v_k = g (1 - mu^k) / (1 - mu) and
+    p_k = p0 - lr * sum_j (g + mu v_j) (float64); mu = 0 is plain SGD bit for bit."""
+    g = np.array([0.25, -1.5, 3.0], np.float32)
+    p0 = np.array([1.0, 2.0, -0.5], np.float32)
+    lr, mu, k = 0.05, 0.8, 7
+    p, v = p0.copy(), np.zeros(3, np.float32)
+    for _ in range(k):
+        p, v = orc.nesterov(p, v, g, lr, mu, mode=0)
+    gd, vs = g.astype(np.float64), [g.astype(np.float64) * (1 - mu ** j) / (1 - mu) for j in range(1, k + 1)]
+    want_p = p0 - lr * sum(gd + mu * vj for vj in vs)
+    np.testing.assert_allclose(v, vs[-1], rtol=2e-6)
+    np.testing.assert_allclose(p, want_p, rtol=2e-6)
+    p1, v1 = orc.nesterov(p0, np.zeros(3, np.float32), g, lr, 0.0, mode=0)
+    assert np.array_equal(p1, (p0 - np.float32(lr) * g).astype(np.float32)) and np.array_equal(v1, g)
+    p2, _ = orc.nesterov(p0, np.ones(3, np.float32), g, 0.0, mu, mode=0)
+    assert np.array_equal(p2, p0)
+
+
+def test_grad_stats_against_numpy(orc):
+    rng = np.random.default_rng(6)
+    g = (rng.standard_normal(100003) * 3).astype(np.float32)
+    g[[5, 77, 901]] = np.nan
+    g[[13, 4000]] = np.inf
+    g[20] = -np.inf
+    s = orc.grad_stats(g)
+    fin = g[np.isfinite(g)].astype(np.float64)
+    assert s["nan_count"] == 3 and s["inf_count"] == 3 and s["elements"] == g.size
+    assert s["max_abs"] == np.float32(np.abs(fin).max())
+    assert abs(s["sumsq"] - float(np.sum(fin * fin))) <= 1e-12 * float(np.sum(fin * fin))
+    assert abs(s["l2_norm"] - float(np.linalg.norm(fin))) <= 1e-12 * float(np.linalg.norm(fin))
+    z = orc.grad_stats(np.zeros(0, np.float32))
+    assert z["max_abs"] == 0 and z["sumsq"] == 0
+
+
+def test_pack_against_numpy(orc):
+    """Row k = concat(prompt_k, completion_k)[:T] with mask 1 there; missing rollouts
+    give zero rows; bad offsets are reported and their rows stay zero."""
+    rng = np.random.default_rng(7)
+    R, n_rows, T = 5, 7, 12
+    lp = rng.integers(0, 8, R)
+    lc = rng.integers(0, 9, R)
+    lp[2], lc[3] = 0, 0
+    prompts = [rng.integers(1, 1000, n) for n in lp]
+    comps = [rng.integers(1, 1000, n) for n in lc]
+    po = np.concatenate([[0], np.cumsum(lp)])
+    co = np.concatenate([[0], np.cumsum(lc)])
+    ids, mask, ok = orc.pack(np.concatenate(prompts), po, np.concatenate(comps), co, n_rows, T)
+    assert ok
+    for k in range(n_rows):
+        row = np.concatenate([prompts[k], comps[k]])[:T] if k < R else np.zeros(0, np.int64)
+        assert np.array_equal(ids[k, :len(row)], row) and not ids[k, len(row):].any()
+        assert mask[k].sum() == len(row) and np.all(mask[k, :len(row)] == 1)
+    bad = po.copy()
+    bad[2] = bad[3] + 1                           # decreasing pair for rollout 2
+    ids2, mask2, ok2 = orc.pack(np.concatenate(prompts), bad, np.concatenate(comps), co, n_rows, T)
+    assert not ok2 and not mask2[2].any()
