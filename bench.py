@@ -226,6 +226,27 @@ def bench_lmhead(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def _timed_calls(ctx, steps: int, call):
+    """Run call() steps times between pcp_profile_start/stop: returns (mean kernel ms
+    from the library's HIP events on the launch stream, wall seconds)."""
+    import ctypes
+
+    import torch
+
+    from pcp_amd._lib import check, lib
+
+    check(lib().pcp_profile_start(ctx.handle, steps), ctx.handle)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    n_l, tot = ctypes.c_int(0), ctypes.c_double(0)
+    check(lib().pcp_profile_stop(ctx.handle, ctypes.byref(n_l), ctypes.byref(tot)), ctx.handle)
+    return tot.value / max(n_l.value, 1), elapsed
+
+
 QWEN05_PARAMS = 494_032_768   # Qwen2.5-0.5B, the RL model of the reference's runs (~494M f32 params)
 
 
@@ -248,15 +269,7 @@ def bench_nesterov(args) -> None:
     for _ in range(args.warmup):
         opt.update_flat(p, g, shadow)
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    a.record()
-    for _ in range(args.steps):
-        opt.update_flat(p, g, shadow)
-    b.record()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    kernel_ms = a.elapsed_time(b) / args.steps
+    kernel_ms, elapsed = _timed_calls(opt.ctx, args.steps, lambda: opt.update_flat(p, g, shadow))
     ms_step = elapsed * 1e3 / args.steps
     alg = 22 * P
     line = {
@@ -288,15 +301,61 @@ def bench_nesterov(args) -> None:
     opt.close()
 
 
+def bench_sample(args) -> None:
+    """The rollout sampler: one decoding step of the 64 rollouts of configuration 2
+    (8 prompts x G=8) over f32 logits [64, 151936] in HBM (Sampler.sample,
+    math.zig:21-58, at temperature 0.7, the reference's default, generation_engine.zig:163)."""
+    import numpy as np
+    import torch
+
+    from pcp_amd import step
+
+    dev = torch.device("cuda:0")
+    R, V, T = 64, 151936, 0.7
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((R, V), device=dev, generator=gen) * 3
+    u = torch.rand(R, device=dev, generator=gen)
+    ids = torch.empty(R, dtype=torch.int64, device=dev)
+    from pcp_amd.grpo import default_context
+    for _ in range(args.warmup):
+        step.sample_tokens(x, T, u, ids=ids)
+    torch.cuda.synchronize()
+    kernel_ms, elapsed = _timed_calls(default_context(0), args.steps, lambda: step.sample_tokens(x, T, u, ids=ids))
+    ms_step = elapsed * 1e3 / args.steps
+    alg = R * V * 4 + R * 4 + R * 8
+    line = {
+        "metric": "rollout sampler tokens/s and achieved HBM GB/s, 64 rows x V=151936 f32",
+        "value": R / (ms_step / 1e3), "unit": "sampled tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (torch normal logits, uniform draws)",
+        "config": {"workload": f"Sampler.sample at T={T} over {R} rows of {V} f32 logits", "rows": R, "vocab": V},
+        "roofline": {"bound": "hbm", "achieved": alg / (kernel_ms / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": alg / (kernel_ms / 1e3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "sample_part_kernel<F32T> + sample_select_kernel<F32T>", "kernel_ms": kernel_ms,
+                     "algorithmic_bytes": alg},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+        xh, uh = x.cpu().numpy(), u.cpu().numpy()
+        t0 = time.perf_counter()
+        for r in range(R):
+            orc.sample(xh[r], T, float(uh[r]))
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": R / dt, "unit": "sampled tokens/s", "cores": 1, "kind": "port",
+                                "sample": f"{R} rows in {dt:.2f} s: oracle f32 loop of math.zig:21-58 "
+                                          "(step_oracle.cpp), one thread, logits already in host memory"}
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--workload", choices=["loss", "nesterov"], default="loss",
+    ap.add_argument("--workload", choices=["loss", "nesterov", "sample"], default="loss",
                     help="loss: the GRPO loss head of --config (the headline metric); nesterov: the "
-                         "optimizer step over Qwen2.5-0.5B's parameters")
+                         "optimizer step over Qwen2.5-0.5B's parameters; sample: the rollout sampler")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -327,6 +386,9 @@ def main() -> None:
         del src
     if args.workload == "nesterov":
         bench_nesterov(args)
+        return
+    if args.workload == "sample":
+        bench_sample(args)
         return
     if args.config == 5:
         bench_lmhead(args)

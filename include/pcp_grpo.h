@@ -274,8 +274,10 @@ int pcp_grpo_lmhead_fwd_bwd(pcp_ctx* ctx, const pcp_lmhead_args* a);
 /*
  * Kernel timing (no reference counterpart: the reference never times its step).
  * Between pcp_profile_start and pcp_profile_stop, every row-kernel launch of
- * pcp_grpo_loss_fwd_bwd / pcp_grpo_logprob_fwd is bracketed by HIP events recorded
- * on the launch stream (at most max_launches launches are recorded). Stop
+ * pcp_grpo_loss_fwd_bwd / pcp_grpo_logprob_fwd, the policy forward-tile launch of
+ * pcp_grpo_lmhead_fwd_bwd, the kernels of pcp_sample_tokens and the launch of
+ * pcp_nesterov_update_flat are bracketed by HIP events recorded on the launch stream
+ * (at most max_launches launches are recorded). Stop
  * synchronises those events and returns the count and the summed kernel time.
  */
 int pcp_profile_start(pcp_ctx* ctx, int max_launches);

@@ -16,6 +16,7 @@ What each function restates (reference file:line):
   nesterov     src/optimizers/nesterov.zig:86-97 and nesterov_mlir.zig:93-99
   grad_stats   src/nodes/controllers/rl_shepherd.zig:607-641
   pack         src/nodes/controllers/rl_shepherd.zig:487-515
+  sample       src/core/math.zig:21-73 (Sampler.sample with the uniform draw given)
 
 Pinning: every function is checked in tests/test_oracle.py against the reference's
 known-answer tests (src/examples/isolated_vjp_tests.zig), closed forms, brute force
@@ -78,6 +79,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_grad_stats.restype = None
         L.oracle_pack.argtypes = [_VP, _I64, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP]
         L.oracle_pack.restype = ctypes.c_int
+        L.oracle_sample.argtypes = [_VP, _I64, ctypes.c_float, ctypes.c_float]
+        L.oracle_sample.restype = _I64
         _lib = L
     return _lib
 
@@ -305,3 +308,10 @@ def pack(prompt_tokens, prompt_offsets, completion_tokens, completion_offsets, n
     rc = lib().oracle_pack(_ptr(pt), pt.size, _ptr(po), _ptr(ct), ct.size, _ptr(co), R, n_rows, seq_len,
                            _ptr(ids), _ptr(mask))
     return ids, mask, rc == 0
+
+
+def sample(logits: np.ndarray, temperature: float, u: float = 0.0) -> int:
+    """math.zig:21-73 Sampler.sample on one f32 row with the uniform draw u given
+    (the reference draws it with prng.random().float(f32))."""
+    x = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+    return int(lib().oracle_sample(_ptr(x), x.size, ctypes.c_float(temperature), ctypes.c_float(u)))

@@ -82,3 +82,36 @@ int oracle_pack(const int64_t* pt, int64_t npt, const int64_t* po, const int64_t
 }
 
 }  // extern "C"
+
+extern "C" {
+
+// src/core/math.zig:21-73, Sampler.sample with the uniform draw given: greedy
+// (strict '>' argmax from index 0) for temperature < 1e-6, else the sequential f32
+// max, sum of expf((l - max) / T), threshold u * sum and first crossing; falls back
+// to n - 1 (:56).
+int64_t oracle_sample(const float* logits, int64_t n, float temperature, float u) {
+  if (temperature < 1e-6f) {
+    float max_val = -INFINITY;
+    int64_t max_idx = 0;
+    for (int64_t i = 0; i < n; ++i)
+      if (logits[i] > max_val) {
+        max_val = logits[i];
+        max_idx = i;
+      }
+    return max_idx;
+  }
+  float max_logit = -INFINITY;
+  for (int64_t i = 0; i < n; ++i)
+    if (logits[i] > max_logit) max_logit = logits[i];
+  float sum_exp = 0.f;
+  for (int64_t i = 0; i < n; ++i) sum_exp += std::exp((logits[i] - max_logit) / temperature);
+  const float threshold = u * sum_exp;
+  float cumulative = 0.f;
+  for (int64_t i = 0; i < n; ++i) {
+    cumulative += std::exp((logits[i] - max_logit) / temperature);
+    if (cumulative >= threshold) return i;
+  }
+  return n - 1;
+}
+
+}  // extern "C"

@@ -160,6 +160,7 @@ SIGNATURES = {
     "pcp_nesterov_total": (_I64, [_VP]),
     "pcp_nesterov_serialize": (_I, [_VP, _VP, ctypes.c_size_t]),
     "pcp_nesterov_deserialize": (_I, [_VP, _VP, ctypes.c_size_t]),
+    "pcp_sample_tokens": (_I, [_VP, _VP, _I, _I64, _I64, _I64, _F, _VP, _VP, _VP]),
 }
 
 _lib = None

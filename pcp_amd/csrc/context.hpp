@@ -74,4 +74,15 @@ int collect_device_errors(pcp_ctx* ctx);
 // Release the context's BLAS handle (defined with the LM-head path).
 void release_blas(pcp_ctx* ctx);
 
+// pcp_profile_start/stop: HIP events around a timed launch on its stream. prof_begin
+// returns whether this launch is timed (profiling on and an event pair left).
+inline bool prof_begin(pcp_ctx* ctx, hipStream_t st) {
+  const bool timed = ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
+  if (timed && hipEventRecord(ctx->prof_start[ctx->prof_used], st) != hipSuccess) return false;
+  return timed;
+}
+inline void prof_end(pcp_ctx* ctx, hipStream_t st, bool timed) {
+  if (timed && hipEventRecord(ctx->prof_stop[ctx->prof_used], st) == hipSuccess) ++ctx->prof_used;
+}
+
 }  // namespace pcp

@@ -455,9 +455,10 @@ int pcp_nesterov_update_flat(pcp_nesterov* opt, float* params, const float* grad
   if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (opt->total == 0) return PCP_OK;
-  if ((e = launch_nesterov(opt, params, opt->vel, grads, static_cast<uint16_t*>(param_bf16), opt->total, st)) !=
-      hipSuccess)
-    return hip_fail(ctx, e, "Nesterov launch");
+  const bool timed = prof_begin(ctx, st);
+  e = launch_nesterov(opt, params, opt->vel, grads, static_cast<uint16_t*>(param_bf16), opt->total, st);
+  prof_end(ctx, st, timed);
+  if (e != hipSuccess) return hip_fail(ctx, e, "Nesterov launch");
   return sync_only(ctx, st);
 }
 

@@ -117,3 +117,28 @@ def _f32(*ts):
     for t in ts:
         if t.dtype != torch.float32:
             raise PcpError(-2, "parameters and gradients must be f32")
+
+
+def sample_tokens(logits: torch.Tensor, temperature: float, uniforms: torch.Tensor | None = None, *,
+                  ids: torch.Tensor | None = None, stream=None, ctx: Context | None = None) -> torch.Tensor:
+    """Sampler.sample (src/core/math.zig:21-58) on every row of logits [R, V] (f32 or
+    bf16, HBM): greedy when temperature < 1e-6, else inverse-transform sampling with
+    the caller's uniform draws (f32 [R] in [0, 1)). Returns int64 [R] token ids."""
+    from ._lib import DType
+    if logits.dim() != 2:
+        raise PcpError(-1, "logits must be [rows, vocab]")
+    code = {torch.float32: DType.f32, torch.bfloat16: DType.bf16}.get(logits.dtype)
+    if code is None:
+        raise PcpError(-2, "logits must be f32 or bf16")
+    if logits.stride(1) != 1:
+        raise PcpError(-1, "logits rows must be contiguous")
+    R, V = logits.shape
+    ctx = ctx or default_context(logits.device.index or 0)
+    if ids is None:
+        ids = torch.empty(R, dtype=torch.int64, device=logits.device)
+    if uniforms is not None and (uniforms.dtype != torch.float32 or uniforms.numel() != R):
+        raise PcpError(-1, "uniforms must be f32 with one value per row")
+    check(lib().pcp_sample_tokens(ctx.handle, logits.data_ptr(), int(code), R, V, logits.stride(0),
+                                  float(temperature), _ptr(uniforms), _ptr(ids), _stream_handle(stream)),
+          ctx.handle)
+    return ids

@@ -314,3 +314,17 @@ def test_grad_stats_struct_layout(tmp_path):
     assert vals[0] == ctypes.sizeof(_lib.GradStats)
     for f, off in zip(fields, vals[1:]):
         assert getattr(_lib.GradStats, f).offset == off, f
+
+
+def test_sampler_argument_errors_without_device():
+    L = _lib.lib()
+    assert L.pcp_sample_tokens(None, 0x1000, int(DType.f16), 4, 100, 100, 1.0, 0x2000, 0x3000, None) == -2
+    assert L.pcp_sample_tokens(None, 0x1000, int(DType.f32), 4, 100, 50, 1.0, 0x2000, 0x3000, None) == -1
+    assert L.pcp_sample_tokens(None, 0x1000, int(DType.f32), 4, (1 << 20) + 1, (1 << 20) + 4, 1.0, 0x2000,
+                               0x3000, None) == -1
+    assert L.pcp_sample_tokens(None, 0x1008, int(DType.f32), 4, 100, 100, 1.0, 0x2000, 0x3000, None) == -1
+    assert "16-byte" in L.pcp_last_error(None).decode()
+    assert L.pcp_sample_tokens(None, 0x1000, int(DType.f32), 4, 100, 100, 1.0, None, 0x3000, None) == -1
+    assert "uniforms" in L.pcp_last_error(None).decode()
+    assert L.pcp_sample_tokens(None, 0x1000, int(DType.f32), 4, 100, 100, 0.0, None, 0x3000, None) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()     # greedy needs no uniforms

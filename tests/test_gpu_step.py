@@ -182,3 +182,87 @@ def test_nesterov_full_model_size_sampled():
     assert np.array_equal(bits(p[idx].cpu().numpy()), bits(want))
     assert np.array_equal(shadow[idx].view(torch.int16).cpu().numpy().view(np.uint16), orc.bf16_from_f32(want))
     opt.close()
+
+
+# ---- the rollout sampler (math.zig:21-58) -------------------------------------------------
+
+def _exact_cdf(x, T):
+    x64 = x.astype(np.float64)
+    m = x64.max()
+    return np.cumsum(np.exp((x64 - m) / T))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sampler_greedy_bit_exact(dtype):
+    rng = np.random.default_rng(21)
+    R, V = 40, 151936
+    x = (rng.standard_normal((R, V)) * 3).astype(np.float32)
+    x[1, [5, 90000, 151935]] = 50.0                   # ties: the first maximum wins
+    x[2, :] = -np.inf                                 # nothing above -inf: index 0
+    x[3, [0, 7]] = np.nan
+    x[3, 100] = 40.0                                  # NaN never wins
+    x[4, 151935] = 60.0                               # maximum in the ragged last block
+    xd = torch.from_numpy(x).to(DEV).to(dtype)
+    got = step.sample_tokens(xd, 0.0).cpu().numpy()
+    xh = xd.float().cpu().numpy()
+    want = np.array([orc.sample(xh[r], 0.0) for r in range(R)])
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("T", [0.7, 1.0, 1.6])
+def test_sampler_exact_cdf_and_reference_drift(T):
+    """The GPU sums f32 terms in float64, so its index is the exact inverse CDF to 1e-6
+    of the sum. The reference adds 151936 f32 terms one by one, which absorbs small
+    terms: its cumulative drifts from the exact one (by ~2e-4 of the sum here), and a
+    draw whose threshold falls in that gap picks another token. Every disagreement with
+    the reference restatement must lie inside the reference's own drift, measured per
+    row with numpy's sequential float32 cumsum."""
+    rng = np.random.default_rng(22)
+    R, V = 256, 151936
+    x = (rng.standard_normal((R, V)) * 2.5).astype(np.float32)
+    u = rng.random(R).astype(np.float32)
+    got = step.sample_tokens(t(x), T, t(u)).cpu().numpy()
+    for r in range(R):
+        c = _exact_cdf(x[r], T)
+        thr = float(u[r]) * c[-1]
+        g = got[r]
+        assert c[g] >= thr - 1e-6 * c[-1] and (g == 0 or c[g - 1] <= thr + 1e-6 * c[-1]), (r, g)
+        if r % 4 == 0:                                # the sequential oracle is slow: every 4th row
+            want = orc.sample(x[r], T, float(u[r]))
+            if g != want:
+                e32 = np.exp(((x[r] - x[r].max()) / np.float32(T)).astype(np.float32))
+                drift = np.abs(np.cumsum(e32, dtype=np.float32).astype(np.float64) - c).max()
+                lo, hi = min(g, want), max(g, want)
+                assert c[hi - 1] - drift <= thr <= c[lo] + drift + 1e-6 * c[-1], (r, g, want)
+
+
+def test_sampler_closed_forms_and_specials():
+    V = 151936
+    x = np.zeros((6, V), np.float32)                  # uniform rows: index = ceil(u V) - 1
+    u = np.array([0.25, 0.5, 0.999, 1e-7, 0.0, 0.33333334], np.float32)
+    got = step.sample_tokens(t(x), 1.0, t(u)).cpu().numpy()
+    want = np.maximum(np.ceil(u.astype(np.float64) * V) - 1, 0).astype(np.int64)
+    assert np.array_equal(got, want), (got, want)
+    y = np.full((4, 1000), -30.0, np.float32)
+    y[0, 417] = 30.0                                  # one dominant logit
+    y[1, 3] = np.nan                                  # NaN: the reference's sum is NaN -> n - 1
+    y[2, :] = -np.inf                                 # -inf row: NaN sum -> n - 1
+    y[3, 9] = np.inf                                  # +inf: inf - inf -> n - 1
+    got = step.sample_tokens(t(y), 1.0, t(np.full(4, 0.5, np.float32))).cpu().numpy()
+    assert list(got) == [417, 999, 999, 999]
+    assert [orc.sample(y[r], 1.0, 0.5) for r in range(4)] == [417, 999, 999, 999]
+
+
+def test_sampler_bf16_and_strided_rows():
+    rng = np.random.default_rng(23)
+    R, V, LD = 16, 5000, 5120                         # rows inside a wider buffer
+    full = (rng.standard_normal((R, LD)) * 2).astype(np.float32)
+    xd = torch.from_numpy(full).to(DEV).to(torch.bfloat16)[:, :V]
+    u = rng.random(R).astype(np.float32)
+    got = step.sample_tokens(xd, 0.8, t(u)).cpu().numpy()
+    xh = xd.float().cpu().numpy()
+    for r in range(R):
+        c = _exact_cdf(xh[r], 0.8)
+        thr = float(u[r]) * c[-1]
+        g = got[r]
+        assert c[g] >= thr - 1e-6 * c[-1] and (g == 0 or c[g - 1] <= thr + 1e-6 * c[-1])

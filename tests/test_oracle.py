@@ -414,3 +414,59 @@ def test_pack_against_numpy(orc):
     bad[2] = bad[3] + 1                           # decreasing pair for rollout 2
     ids2, mask2, ok2 = orc.pack(np.concatenate(prompts), bad, np.concatenate(comps), co, n_rows, T)
     assert not ok2 and not mask2[2].any()
+
+
+# ---- the rollout sampler (math.zig:21-73) -------------------------------------------------
+
+def test_sampler_reference_kat(orc):
+    """math.zig:76-89: greedy [1, 5, 2] -> 1; [1, 10, 1] at T = 1 -> 1 for the draws in
+    [p0, p0 + p1) = [1.2e-4, 0.99988) (p1 = 0.99975), 0 below, 2 above."""
+    assert orc.sample([1.0, 5.0, 2.0], 0.0) == 1
+    for u in (0.001, 0.3, 0.9998):
+        assert orc.sample([1.0, 10.0, 1.0], 1.0, u) == 1
+    assert orc.sample([1.0, 10.0, 1.0], 1.0, 0.0) == 0
+    assert orc.sample([1.0, 10.0, 1.0], 1.0, 0.00005) == 0
+    assert orc.sample([1.0, 10.0, 1.0], 1.0, 0.99999) == 2
+
+
+def test_sampler_against_inverse_cdf(orc):
+    """Inverse-transform sampling: index = first i with cumsum(p)_i >= u (numpy float64
+    searchsorted on the exact CDF), up to the f32 sum's rounding near a boundary."""
+    rng = np.random.default_rng(8)
+    for T in (0.7, 1.0, 2.5):
+        x = (rng.standard_normal(3000) * 2).astype(np.float32)
+        p = np.exp((x.astype(np.float64) - x.max()) / T)
+        c = np.cumsum(p)
+        for u in rng.random(200).astype(np.float32):
+            got = orc.sample(x, T, float(u))
+            want = int(np.searchsorted(c, float(u) * c[-1], side="left"))
+            if got != want:                              # only at a rounding boundary
+                assert abs(c[min(got, want)] - float(u) * c[-1]) <= 1e-5 * c[-1]
+
+
+def test_sampler_closed_forms(orc):
+    V = 1000
+    assert orc.sample(np.zeros(V, np.float32), 1.0, 0.25) == 249      # uniform: ceil(u V) - 1
+    assert orc.sample(np.zeros(V, np.float32), 1.0, 0.0) == 0
+    x = np.full(V, -30.0, np.float32)
+    x[417] = 30.0
+    assert orc.sample(x, 1.0, 0.5) == 417                              # one dominant logit
+    ties = np.array([3.0, 7.0, 7.0, 1.0], np.float32)
+    assert orc.sample(ties, 0.0) == 1                                  # first maximum
+    assert orc.sample(np.array([np.nan, 2.0, np.nan, 5.0], np.float32), 0.0) == 3   # NaN never wins
+    assert orc.sample(np.full(4, -np.inf, np.float32), 0.0) == 0
+    assert orc.sample(np.array([1.0, np.nan, 2.0], np.float32), 1.0, 0.5) == 2       # NaN sum: n - 1
+
+
+def test_sampler_is_the_sequential_f32_cumsum_rule(orc):
+    """The restatement picks the first index where numpy's sequential float32 cumsum of
+    the f32 terms reaches float32(u) * total (math.zig:35-53's loop)."""
+    rng = np.random.default_rng(9)
+    for T in (0.7, 1.3):
+        for _ in range(12):
+            x = (rng.standard_normal(20000) * 2.5).astype(np.float32)
+            u = np.float32(rng.random())
+            e32 = np.exp(((x - x.max()) / np.float32(T)).astype(np.float32))
+            c32 = np.cumsum(e32, dtype=np.float32)
+            want = int(np.argmax(c32 >= u * c32[-1])) if np.any(c32 >= u * c32[-1]) else x.size - 1
+            assert orc.sample(x, T, float(u)) == want
