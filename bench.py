@@ -347,15 +347,76 @@ def bench_sample(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def bench_b64(args) -> None:
+    """The UPDATE_WEIGHTS payload (rl_shepherd.zig:691-711 encodes, worker.zig:2631-2667
+    decodes): base64 of Qwen2.5-0.5B's flat f32 weights (1.98 GB) on the device. A step
+    is one encode and one decode; the roofline entry is the encode kernel (reads the
+    weight bytes, writes 4/3 as many characters)."""
+    import base64
+
+    import torch
+
+    from pcp_amd import formats
+    from pcp_amd.grpo import default_context
+
+    dev = torch.device("cuda:0")
+    P = QWEN05_PARAMS
+    w = torch.randn(P, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
+    raw = w.view(torch.uint8)
+    nb = raw.numel()
+    enc = torch.empty(nb // 3 * 4 + 4, dtype=torch.uint8, device=dev)
+    dec = torch.empty(nb + 3, dtype=torch.uint8, device=dev)   # len / 4 * 3 >= nb: room for the padded quad
+    text = formats.b64encode(raw, out=enc)
+    nc = text.numel()
+    for _ in range(args.warmup):
+        formats.b64encode(raw, out=enc)
+        formats.b64decode(text, out=dec)
+    torch.cuda.synchronize()
+    ctx = default_context(0)
+    enc_ms, t_enc = _timed_calls(ctx, args.steps, lambda: formats.b64encode(raw, out=enc))
+    dec_ms, t_dec = _timed_calls(ctx, args.steps, lambda: formats.b64decode(text, out=dec))
+    if not torch.equal(dec[:nb], raw):
+        raise SystemExit("base64 round trip differs")
+    ms_step = (t_enc + t_dec) * 1e3 / args.steps
+    alg = nb + nc   # encode: read the weight bytes, write the characters (decode: the reverse)
+    line = {
+        "metric": "UPDATE_WEIGHTS payload base64 encode + decode, bytes of weights/s, 494M f32 weights",
+        "value": 2 * nb / (ms_step / 1e3), "unit": "bytes/s (weights, encode + decode)", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic (torch normal weights)",
+        "config": {"workload": f"base64 of {nb} weight bytes ({P} f32) -> {nc} characters, then back", "bytes": nb},
+        "roofline": {"bound": "hbm", "achieved": alg / (enc_ms / 1e3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": alg / (enc_ms / 1e3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "b64_encode_kernel", "kernel_ms": enc_ms, "algorithmic_bytes": alg,
+                     "decode_kernel_ms": dec_ms, "decode_gbs": alg / (dec_ms / 1e3) / 1e9},
+    }
+    tfile = os.path.join(ROOT, "profiles", "traffic_b64.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    if not args.no_cpu_baseline:
+        host = raw[:3 << 28].cpu().numpy().tobytes()
+        t0 = time.perf_counter()
+        base64.b64encode(host)
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": len(host) / dt, "unit": "bytes/s (weights, encode)", "cores": 1,
+                                "kind": "port", "sample": f"{len(host)} weight bytes encoded in {dt:.2f} s by "
+                                                          "Python's base64 (C, one thread), standing for the "
+                                                          "reference's host std.base64 encoder"}
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--workload", choices=["loss", "nesterov", "sample"], default="loss",
+    ap.add_argument("--workload", choices=["loss", "nesterov", "sample", "b64"], default="loss",
                     help="loss: the GRPO loss head of --config (the headline metric); nesterov: the "
-                         "optimizer step over Qwen2.5-0.5B's parameters; sample: the rollout sampler")
+                         "optimizer step over Qwen2.5-0.5B's parameters; sample: the rollout sampler; "
+                         "b64: the UPDATE_WEIGHTS payload codec")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -389,6 +450,9 @@ def main() -> None:
         return
     if args.workload == "sample":
         bench_sample(args)
+        return
+    if args.workload == "b64":
+        bench_b64(args)
         return
     if args.config == 5:
         bench_lmhead(args)

@@ -69,7 +69,9 @@ typedef enum pcp_status {
   PCP_ERR_UNSUPPORTED = -10,     /* valid request this build does not implement        */
   PCP_ERR_OUT_OF_BOUNDS = -11,   /* tensor index past the optimizer's tensors (nesterov.zig:72)  */
   PCP_ERR_DIMENSION_MISMATCH = -12, /* element counts differ (nesterov.zig:73-76)        */
-  PCP_ERR_CORRUPT_STATE = -13    /* serialized state too short (nesterov.zig:124, CorruptSaveFile) */
+  PCP_ERR_CORRUPT_STATE = -13,   /* serialized state or file too short (nesterov.zig:124,
+                                    rl_shepherd.zig:199 WeightFileTooSmall, EndOfStream)  */
+  PCP_ERR_IO = -14               /* a file could not be opened, read or written        */
 } pcp_status;
 
 /* Loss definitions for the per-token term l_t (aggregation is identical):

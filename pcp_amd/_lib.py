@@ -62,6 +62,7 @@ STATUS = {
     -11: "PCP_ERR_OUT_OF_BOUNDS",
     -12: "PCP_ERR_DIMENSION_MISMATCH",
     -13: "PCP_ERR_CORRUPT_STATE",
+    -14: "PCP_ERR_IO",
 }
 
 
@@ -161,6 +162,13 @@ SIGNATURES = {
     "pcp_nesterov_serialize": (_I, [_VP, _VP, ctypes.c_size_t]),
     "pcp_nesterov_deserialize": (_I, [_VP, _VP, ctypes.c_size_t]),
     "pcp_sample_tokens": (_I, [_VP, _VP, _I, _I64, _I64, _I64, _F, _VP, _VP, _VP]),
+    "pcp_prompts_load": (_I, [_VP, ctypes.c_char_p, _VP, _I64, _VP, _I64, ctypes.POINTER(_I64),
+                              ctypes.POINTER(_I64)]),
+    "pcp_weights_load": (_I, [_VP, ctypes.c_char_p, _I, ctypes.POINTER(_I64), _VP, _VP]),
+    "pcp_weights_save": (_I, [_VP, ctypes.c_char_p, _VP, _I64]),
+    "pcp_base64_encoded_len": (_I64, [_I64]),
+    "pcp_base64_encode": (_I, [_VP, _VP, _I64, _VP, _VP]),
+    "pcp_base64_decode": (_I, [_VP, _VP, _I64, _VP, ctypes.POINTER(_I64), _VP]),
 }
 
 _lib = None

@@ -55,6 +55,9 @@ int collect_device_errors(pcp_ctx* ctx) {
     return fail(ctx, PCP_ERR_TOKEN_RANGE, "a live token id is outside [0, vocab) and is not -100");
   if (h & kErrBadRagged)
     return fail(ctx, PCP_ERR_INVALID_ARG, "rollout offsets decrease or run past the token array");
+  if (h & kErrBadBase64)
+    return fail(ctx, PCP_ERR_INVALID_ARG, "base64 text has a character outside the alphabet or misplaced padding "
+                                          "(InvalidCharacter / InvalidPadding)");
   return fail(ctx, PCP_ERR_NONFINITE, "a live row has a non-finite log-sum-exp (NaN/Inf logits)");
 }
 

@@ -328,3 +328,51 @@ def test_sampler_argument_errors_without_device():
     assert "uniforms" in L.pcp_last_error(None).decode()
     assert L.pcp_sample_tokens(None, 0x1000, int(DType.f32), 4, 100, 100, 0.0, None, 0x3000, None) == -1
     assert "context is NULL" in L.pcp_last_error(None).decode()     # greedy needs no uniforms
+
+
+def _write_prompts(path, prompts):
+    import struct
+    with open(path, "wb") as f:
+        f.write(struct.pack("<I", len(prompts)))
+        for p in prompts:
+            f.write(struct.pack("<I", len(p)))
+            for t in p:
+                f.write(struct.pack("<Q", t))
+
+
+def test_prompt_file_counts_and_errors_without_device(tmp_path):
+    """The .bin of tools/prepare_rl_dataset.py:28-40, written here with struct as that
+    script does, read back by the library (counting pass, no device)."""
+    from pcp_amd import formats
+    p = tmp_path / "prompts.bin"
+    _write_prompts(p, [[1, 2, 3], [], [151935, 7]])
+    assert formats.prompt_counts(str(p)) == (3, 5)
+    raw = p.read_bytes()
+    (tmp_path / "cut.bin").write_bytes(raw[:-3])                # ends inside the last prompt
+    with pytest.raises(PcpError) as e:
+        formats.prompt_counts(str(tmp_path / "cut.bin"))
+    assert e.value.code == -13
+    with pytest.raises(PcpError) as e:
+        formats.prompt_counts(str(tmp_path / "missing.bin"))
+    assert e.value.code == -14
+    _write_prompts(tmp_path / "big.bin", [[1 << 63]])           # the reference's @intCast to i64 fails
+    with pytest.raises(PcpError) as e:
+        formats.prompt_counts(str(tmp_path / "big.bin"))
+    assert e.value.code == -9
+
+
+def test_weights_and_base64_errors_without_device(tmp_path):
+    L = _lib.lib()
+    w = tmp_path / "w.bin"
+    w.write_bytes(np.arange(10, dtype=np.float32).tobytes())
+    counts = (ctypes.c_int64 * 2)(6, 5)                         # 11 floats > 10 in the file
+    assert L.pcp_weights_load(None, str(w).encode(), 2, counts, 0x1000, None) == -13
+    assert "WeightFileTooSmall" in L.pcp_last_error(None).decode()
+    assert L.pcp_weights_load(None, str(tmp_path / "no.bin").encode(), 2, counts, 0x1000, None) == -14
+    ok = (ctypes.c_int64 * 2)(6, 4)
+    assert L.pcp_weights_load(None, str(w).encode(), 2, ok, 0x1000, None) == -1   # valid: needs a context
+    assert "context is NULL" in L.pcp_last_error(None).decode()
+    assert [L.pcp_base64_encoded_len(n) for n in (0, 1, 2, 3, 4, 5, 6)] == [0, 4, 4, 4, 8, 8, 8]
+    n = ctypes.c_int64()
+    assert L.pcp_base64_decode(None, 0x1000, 6, 0x2000, ctypes.byref(n), None) == -1
+    assert "multiple of 4" in L.pcp_last_error(None).decode()
