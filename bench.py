@@ -165,6 +165,11 @@ def bench_lmhead(args) -> None:
     t_setup = time.perf_counter() - t_setup
     kw = dict(ref_weight=inp["ref_weight"] if clip else None, rewards=inp["rewards"], group_size=cfg.group,
               old_logp=inp["old_logp"], loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, ctx=ctx)
+    if args.final_norm:
+        # The decoder's final RMSNorm fused in: hidden is the last layer's output before it.
+        g = torch.Generator(device=dev).manual_seed(5)
+        kw["norm_weight"] = (1 + 0.1 * torch.randn(cfg.H, device=dev, generator=g)).bfloat16().float()
+        kw["norm_eps"] = 1e-6
     out = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], **kw)
     for _ in range(args.warmup):
         grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], outputs=out, sync=False, **kw)
@@ -207,7 +212,8 @@ def bench_lmhead(args) -> None:
         "dtype": "bf16",
         "data": "synthetic (seeded Philox/PCG64 inputs of the configuration)",
         "config": {"workload": f"config5 {cfg.name}: {cfg.prompts} prompts x G={cfg.group}, T={cfg.T}, "
-                               f"hidden {H}, V={V}, bf16 hidden/weights, loss={args.mode}",
+                               f"hidden {H}, V={V}, bf16 hidden/weights, loss={args.mode}"
+                               + (", final RMSNorm fused" if args.final_norm else ""),
                    "tokens": N, "valid_tokens": live, "global_batch": cfg.S, "seq_len": cfg.T},
         "step_tflops": step_flops / (ms_step / 1e3) / 1e12,
         "dense_equivalent_tflops": products * 2.0 * N * H * V / (ms_step / 1e3) / 1e12,
@@ -419,6 +425,8 @@ def main() -> None:
                          "b64: the UPDATE_WEIGHTS payload codec")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
+    ap.add_argument("--final-norm", action="store_true",
+                    help="config 5: fuse the decoder's final RMSNorm (hidden = the last layer's output)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--copy-calibration-gib", type=float, default=0.0,

@@ -195,7 +195,11 @@ int pcp_sync(pcp_ctx* ctx);
  *          attention_mask[S,T], old_logp f32[S,T], rewards f32[S], hyper f32[5] =
  *          {group_size, clip_eps, kl_beta, loss_norm (0 => S), loss_mode (0|1)})
  *     out (loss f32[], dhidden f32[S,T,H], dweight f32[V,H], logp f32[S,T],
- *          ref_logp f32[S,T], advantages f32[S]); ref_weight is read in mode 1 only
+ *          ref_logp f32[S,T], advantages f32[S]); ref_weight is read in mode 1 only.
+ *     A ninth input norm_weight f32[H] fuses the decoder's final RMSNorm
+ *     (pcp_lmhead_args.norm_weight; hyper may then be f32[6] with norm_eps last,
+ *     1e-6 otherwise): hidden is the last layer's output, dhidden the gradient there,
+ *     and a seventh output is dnorm_weight f32[H].
  *
  * All [.,T,V] and [.,T,H] functions use the reference's shift: row t scores token t+1,
  * per-token outputs are indexed by token position (position 0 is 0).
@@ -265,9 +269,19 @@ typedef struct pcp_lmhead_args {
   float loss_norm;            /* 0 => n_seq                                               */
   uint32_t flags;             /* PCP_FLAG_ASYNC                                           */
   void* stream;
+  /* The decoder's final RMSNorm (Qwen2RMSNorm: the model.norm that
+   * tools/export_qwen_forward.py:112 applies before lm_head), fused at both ends. With
+   * norm_weight set, hidden_states are the last decoder layer's output h (bf16), the
+   * LM head's operand is bf16(norm_weight * bf16(h * rsqrt(mean(h^2) + norm_eps))) and
+   * dhidden receives dL/dh, the gradient the last block's VJP takes. hidden <= 8192;
+   * norm_weight and dhidden 16-byte aligned. */
+  const float* norm_weight;   /* [H] f32, or NULL (hidden_states are the LM-head input)   */
+  float* dnorm_weight;        /* [H] f32 gradient of norm_weight, or NULL                 */
+  float norm_eps;             /* Qwen2: 1e-6                                              */
 } pcp_lmhead_args;
 
-/* Defaults as pcp_grpo_args_init (ids i64, mask f32, eps 0.2, beta 0.04, std_eps 1e-8). */
+/* Defaults as pcp_grpo_args_init (ids i64, mask f32, eps 0.2, beta 0.04, std_eps 1e-8;
+ * norm_eps 1e-6). */
 void pcp_lmhead_args_init(pcp_lmhead_args* a);
 /* Forward loss (+ logp / ref logp / token losses) and, when dhidden / dweight are
  * given, their gradients. */

@@ -13,6 +13,8 @@ What each function restates (reference file:line):
   grpo_full    the whole loss head over [S, T, V] with the kernels' row layout
                (seq lengths = clamp(mask.sum(1), min=1), export_qwen_forward.py:160)
   lmhead_*     export_qwen_forward.py:147 (lm_head) and matmulVJP, vjp_rules.zig:426-497
+  rmsnorm_*    the final norm before lm_head (export_qwen_forward.py:112, model.norm =
+               Qwen2RMSNorm of transformers' modeling_qwen2) and its VJP
   nesterov     src/optimizers/nesterov.zig:86-97 and nesterov_mlir.zig:93-99
   grad_stats   src/nodes/controllers/rl_shepherd.zig:607-641
   pack         src/nodes/controllers/rl_shepherd.zig:487-515
@@ -124,6 +126,54 @@ def lmhead_grads(hidden_bits: np.ndarray, weight_bits: np.ndarray, logits: np.nd
     h = bf16_to_f32(hidden_bits).astype(np.float64)
     W = bf16_to_f32(weight_bits).astype(np.float64)
     return D @ W, D.T @ h
+
+
+def rmsnorm_operand(h_bits: np.ndarray, gamma: np.ndarray, eps: float) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Qwen2RMSNorm of bf16 rows h [N, H] as the LM head's bf16 operand, in f32 with a
+    stated summation order, so the result is a function of the inputs alone:
+      ss = sum_k h_k^2: each of 256 lanes adds columns lane, lane + 256, ... in turn;
+           lanes 64w..64w+63 reduce by halving (a[i] + a[i + 32], then + 16, ..., + 1);
+           the four wave sums add as ((w0 + w1) + w2) + w3
+      r  = 1 / sqrt(ss / H + eps)           (correctly rounded f32)
+      x  = bf16(h * r)                      (Qwen2RMSNorm's .to(input_dtype))
+      y  = bf16(gamma * x)                  (the bf16 operand of lm_head)
+    Returns (y bits uint16 [N, H], r f32 [N], x bits uint16 [N, H])."""
+    h = bf16_to_f32(h_bits)
+    N, H = h.shape
+    per = -(-H // 256)
+    hp = np.zeros((N, per * 256), np.float32)
+    hp[:, :H] = h
+    hp = hp.reshape(N, per, 256)
+    acc = np.zeros((N, 256), np.float32)
+    for i in range(per):
+        acc = acc + hp[:, i, :] * hp[:, i, :]
+    w = acc.reshape(N, 4, 64)
+    half = 32
+    while half >= 1:
+        w = w[..., :half] + w[..., half:2 * half]
+        half //= 2
+    w = w[..., 0]
+    ss = ((w[:, 0] + w[:, 1]) + w[:, 2]) + w[:, 3]
+    r = np.float32(1) / np.sqrt(ss / np.float32(H) + np.float32(eps))
+    x_bits = bf16_from_f32(h * r[:, None])
+    y_bits = bf16_from_f32(np.asarray(gamma, np.float32)[None, :] * bf16_to_f32(x_bits))
+    return y_bits, r.astype(np.float32), x_bits
+
+
+def rmsnorm_vjp(h_bits: np.ndarray, gamma: np.ndarray, eps: float, x_bits: np.ndarray,
+                dy: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """float64 (dh, dgamma) of y = gamma * x, x = h / sqrt(mean(h^2) + eps), given dL/dy;
+    the bf16 roundings of x and y pass gradients through (a dtype cast under autograd),
+    and dgamma multiplies dy by the rounded x that the forward used:
+      g = dy * gamma,  dh = r g - h r^3 (sum_k g_k h_k) / H,  dgamma = sum_n dy_n * x_n."""
+    h = bf16_to_f32(h_bits).astype(np.float64)
+    H = h.shape[1]
+    r = 1.0 / np.sqrt((h * h).mean(axis=1) + eps)
+    g = dy * np.asarray(gamma, np.float64)[None, :]
+    dot = (g * h).sum(axis=1)
+    dh = r[:, None] * g - h * (r ** 3 * dot / H)[:, None]
+    dgamma = (dy * bf16_to_f32(x_bits).astype(np.float64)).sum(axis=0)
+    return dh, dgamma
 
 
 def widen(x: np.ndarray, dtype: int) -> np.ndarray:

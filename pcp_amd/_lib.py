@@ -109,6 +109,7 @@ class LmheadArgs(ctypes.Structure):
         ("loss_mode", ctypes.c_int32), ("clip_eps", ctypes.c_float), ("kl_beta", ctypes.c_float),
         ("std_eps", ctypes.c_float), ("loss_norm", ctypes.c_float), ("flags", ctypes.c_uint32),
         ("stream", ctypes.c_void_p),
+        ("norm_weight", ctypes.c_void_p), ("dnorm_weight", ctypes.c_void_p), ("norm_eps", ctypes.c_float),
     ]
 
 

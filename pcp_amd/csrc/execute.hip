@@ -202,7 +202,10 @@ void shift_to_positions(float* v, int64_t S, int64_t T) {
 // "grpo_lmhead_fwd_bwd": the LM head and loss of export_qwen_forward.py:146-163 on
 // hidden states, with the reference's shift (hidden row t scores token t+1). The
 // shift is applied to ids / mask / old_logp on the host; the last row of each
-// sequence has no target (mask 0), so its dhidden row is 0.
+// sequence has no target (mask 0), so its dhidden row is 0. An optional ninth input,
+// norm_weight f32[H], fuses the decoder's final RMSNorm (hyper[5], when given, is its
+// eps; 1e-6 otherwise): hidden is then the last layer's output and a seventh output
+// carries dnorm_weight.
 int execute_lmhead(pcp_ctx* ctx, const std::vector<In>& in, int* n_out, void*** out_data, size_t** out_nbytes) {
   int rc;
   const In& Hs = in[0];
@@ -220,10 +223,14 @@ int execute_lmhead(pcp_ctx* ctx, const std::vector<In>& in, int* n_out, void*** 
       (rc = expect_shape(in[4], 4, {S, T}, "attention_mask")) ||
       (rc = expect_dtype(in[5], 5, {PCP_F32}, "old_logp")) || (rc = expect_shape(in[5], 5, {S, T}, "old_logp")) ||
       (rc = expect_dtype(in[6], 6, {PCP_F32}, "rewards")) || (rc = expect_shape(in[6], 6, {S}, "rewards")) ||
-      (rc = expect_dtype(in[7], 7, {PCP_F32}, "hyper")) || (rc = expect_shape(in[7], 7, {5}, "hyper")))
+      (rc = expect_dtype(in[7], 7, {PCP_F32}, "hyper")))
     return rc;
-  float hyper[5];
-  std::memcpy(hyper, in[7].data, sizeof(hyper));
+  const bool norm = in.size() == 9;
+  if ((rc = expect_shape(in[7], 7, {norm && in[7].numel == 6 ? 6 : 5}, "hyper"))) return rc;
+  if (norm && ((rc = expect_dtype(in[8], 8, {PCP_F32}, "norm_weight")) || (rc = expect_shape(in[8], 8, {H}, "norm_weight"))))
+    return rc;
+  float hyper[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 1e-6f};
+  std::memcpy(hyper, in[7].data, sizeof(float) * static_cast<size_t>(in[7].numel));
   if (!(hyper[0] >= 1.f) || hyper[0] != static_cast<float>(static_cast<int64_t>(hyper[0])))
     return fail(nullptr, PCP_ERR_INVALID_ARG, "hyper[0] (group_size) must be a positive integer");
   if (hyper[4] != 0.f && hyper[4] != 1.f)
@@ -280,6 +287,11 @@ int execute_lmhead(pcp_ctx* ctx, const std::vector<In>& in, int* n_out, void*** 
   a.old_logp = static_cast<float*>(p);
   if ((rc = arena.upload(ctx, in[6], &p))) return rc;
   a.rewards = static_cast<float*>(p);
+  if (norm) {
+    if ((rc = arena.upload(ctx, in[8], &p))) return rc;
+    a.norm_weight = static_cast<float*>(p);
+    a.norm_eps = hyper[5];
+  }
 
   Outputs outs;
   auto out = [&](size_t bytes, bool zero, void** dst) {
@@ -302,6 +314,10 @@ int execute_lmhead(pcp_ctx* ctx, const std::vector<In>& in, int* n_out, void*** 
   a.ref_logp = static_cast<float*>(p);
   if ((rc = out(4 * S, false, &p))) return rc;
   a.advantages_out = static_cast<float*>(p);
+  if (norm) {
+    if ((rc = out(4 * static_cast<size_t>(H), false, &p))) return rc;
+    a.dnorm_weight = static_cast<float*>(p);
+  }
   if ((rc = pcp_grpo_lmhead_fwd_bwd(ctx, &a))) return rc;
   if ((rc = download(ctx, outs, n_out, out_data, out_nbytes))) return rc;
   shift_to_positions(static_cast<float*>((*out_data)[3]), S, T);
@@ -327,7 +343,7 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
   static const int kDefLp2[] = {PCP_F32, PCP_I64};
   static const int kDefLp3[] = {PCP_F32, PCP_F32, PCP_I64};
   static const int kDefAdv[] = {PCP_F32, PCP_I64};
-  static const int kDefLm[] = {PCP_BF16, PCP_BF16, PCP_BF16, PCP_I64, PCP_F32, PCP_F32, PCP_F32, PCP_F32};
+  static const int kDefLm[] = {PCP_BF16, PCP_BF16, PCP_BF16, PCP_I64, PCP_F32, PCP_F32, PCP_F32, PCP_F32, PCP_F32};
   const int* defaults = nullptr;
   int want = 0;
   switch (f) {
@@ -335,7 +351,7 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
     case kClipKl: want = 7; defaults = kDefClip; break;
     case kLogprob: want = (n_in == 3) ? 3 : 2; defaults = (n_in == 3) ? kDefLp3 : kDefLp2; break;
     case kAdvantages: want = 2; defaults = kDefAdv; break;
-    case kLmhead: want = 8; defaults = kDefLm; break;
+    case kLmhead: want = (n_in == 9) ? 9 : 8; defaults = kDefLm; break;
     default: break;
   }
   if (n_in != want) return fail(ctx, PCP_ERR_COUNT_MISMATCH, "'%s' takes %d inputs, got %d", fn, want, n_in);

@@ -65,6 +65,31 @@ struct LmCompactArgs {
 };
 
 size_t lm_tile_smem_bytes();
+// Final RMSNorm around the LM head (norm_kernels.hip).
+constexpr int kLmNormMaxHidden = 8192;   // the forward holds 32 columns per thread
+constexpr int kLmNormSlices = 64;        // dgamma partials (slices of the live rows)
+
+struct LmNormBwdArgs {
+  const float* dyc;       // [n_live, H] f32 gradient of the normed operand, compact rows
+  const uint16_t* h;      // [N, H] bf16 pre-norm hidden states (token order)
+  const float* gamma;     // [H]
+  const float* rstd;      // [n_live] from the forward
+  const int* cidx;        // [N] token -> compact index (-1: not live)
+  const int* live;        // [n_live] compact index -> token
+  int64_t N;
+  int H;
+  int n_live;
+  int nslice;             // lm_norm_slices(n_live)
+  float* dh;              // [N, H] or nullptr
+  float* gpart;           // [nslice, H] dgamma partials, or nullptr
+  float* dgamma;          // [H] or nullptr
+};
+
+int lm_norm_slices(int n_live);
+hipError_t launch_lm_norm_rows(const void* h, const float* gamma, float eps, const int* live, int n, int H, void* y,
+                               float* rstd, hipStream_t st);
+hipError_t launch_lm_norm_bwd(const LmNormBwdArgs& a, hipStream_t st);
+
 hipError_t launch_lm_compact(const LmCompactArgs& a, hipStream_t st);
 // dst[c, :] = src[live[c], :] for c < n (bf16 rows of H elements, H % 64 == 0).
 hipError_t launch_lm_gather_rows(const void* src, void* dst, const int* live, int n, int H, hipStream_t st);

@@ -55,6 +55,14 @@ int validate_lm(const pcp_lmhead_args* a) {
   if (!a->advantages && !a->rewards) return fail(nullptr, PCP_ERR_INVALID_ARG, "advantages and rewards are both NULL");
   if (!(a->clip_eps >= 0.f && a->clip_eps < 1.f)) return fail(nullptr, PCP_ERR_INVALID_ARG, "clip_eps must be in [0, 1)");
   if (!(a->loss_norm >= 0.f)) return fail(nullptr, PCP_ERR_INVALID_ARG, "loss_norm must be >= 0");
+  if (a->dnorm_weight && !a->norm_weight) return fail(nullptr, PCP_ERR_INVALID_ARG, "dnorm_weight needs norm_weight");
+  if (a->norm_weight && a->hidden > kLmNormMaxHidden)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "the fused final norm takes hidden <= %d (got %lld)", kLmNormMaxHidden,
+                (long long)a->hidden);
+  if (a->norm_weight && !(a->norm_eps >= 0.f && a->norm_eps < 1e30f))
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "norm_eps must be finite and >= 0");
+  if (a->norm_weight && ((reinterpret_cast<uintptr_t>(a->norm_weight) | reinterpret_cast<uintptr_t>(a->dhidden)) & 15u))
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "norm_weight / dhidden must be 16-byte aligned");
   const uintptr_t al = reinterpret_cast<uintptr_t>(a->hidden_states) | reinterpret_cast<uintptr_t>(a->weight) |
                        reinterpret_cast<uintptr_t>(a->ref_weight);
   if (al & 15u) return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden_states / weights must be 16-byte aligned");
@@ -81,7 +89,9 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const int nvt = static_cast<int>((V + kLmTileV - 1) / kLmTileV);     // vocab tiles
   const int npart = static_cast<int>((V + kLmPart - 1) / kLmPart);    // log-sum-exp partials per token
   const bool ref = a->loss_mode == PCP_LOSS_GRPO_CLIP_KL;
-  const bool bwd = a->dhidden || a->dweight;
+  const bool norm = a->norm_weight != nullptr;
+  const bool bwd = a->dhidden || a->dweight || a->dnorm_weight;
+  const bool want_dy = a->dhidden || a->dnorm_weight;   // compact gradient of the LM head's operand
   const int64_t chunk = a->vocab_chunk ? a->vocab_chunk : kDefaultChunk;
   const float loss_norm = a->loss_norm > 0.f ? a->loss_norm : static_cast<float>(S);
 
@@ -95,7 +105,9 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_part = take(8 * static_cast<size_t>(N) * npart);
   const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
   const size_t o_chunk = bwd ? take(2 * static_cast<size_t>(N) * chunk) : 0;
-  const size_t o_dhc = a->dhidden ? take(4 * static_cast<size_t>(N) * H) : 0;
+  const size_t o_dhc = want_dy ? take(4 * static_cast<size_t>(N) * H) : 0;
+  const size_t o_rstd = norm ? take(4 * N) : 0;
+  const size_t o_gpart = a->dnorm_weight ? take(4 * static_cast<size_t>(kLmNormSlices) * H) : 0;
   rc = ensure_scratch(ctx, off);
   if (rc != PCP_OK) return rc;
   if (!ctx->h_count && (e = hipHostMalloc(reinterpret_cast<void**>(&ctx->h_count), sizeof(int))) != hipSuccess)
@@ -117,8 +129,14 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const int nl = *ctx->h_count;
   if (nl < 0 || nl > N) return fail(ctx, PCP_ERR_DEVICE, "live-token count %d out of range", nl);
   const int ntl = (nl + kLmTileT - 1) / kLmTileT;
-  if ((e = launch_lm_gather_rows(a->hidden_states, sp + o_hid, I(o_live), nl, static_cast<int>(H), st)) != hipSuccess)
+  if (norm) {
+    if ((e = launch_lm_norm_rows(a->hidden_states, a->norm_weight, a->norm_eps, I(o_live), nl, static_cast<int>(H),
+                                 sp + o_hid, F(o_rstd), st)) != hipSuccess)
+      return hip_fail(ctx, e, "final norm of live hidden rows");
+  } else if ((e = launch_lm_gather_rows(a->hidden_states, sp + o_hid, I(o_live), nl, static_cast<int>(H), st)) !=
+             hipSuccess) {
     return hip_fail(ctx, e, "gathering live hidden rows");
+  }
 
   // Advantages and per-sequence lengths.
   const float* adv = a->advantages;
@@ -193,6 +211,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   if (bwd && nl == 0) {
     if (a->dhidden && (e = launch_lm_zero(a->dhidden, N * H, st)) != hipSuccess) return hip_fail(ctx, e, "zero dhidden");
     if (a->dweight && (e = launch_lm_zero(a->dweight, V * H, st)) != hipSuccess) return hip_fail(ctx, e, "zero dW");
+    if (a->dnorm_weight && (e = launch_lm_zero(a->dnorm_weight, H, st)) != hipSuccess)
+      return hip_fail(ctx, e, "zero dnorm_weight");
   }
   if (bwd && nl > 0) {
     if (!ctx->blas) {
@@ -207,7 +227,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     ta.coef = F(o_coef);
     ta.dchunk = sp + o_chunk;
     ta.ldd = static_cast<int>(chunk);
-    float* dhc = a->dhidden ? F(o_dhc) : nullptr;
+    float* dhc = want_dy ? F(o_dhc) : nullptr;
     const float one = 1.f, zero = 0.f;
     for (int64_t vc0 = 0; vc0 < V; vc0 += chunk) {
       const int64_t w = (V - vc0 < chunk) ? V - vc0 : chunk;
@@ -216,7 +236,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       ta.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
       if ((e = launch_lm_tiles(kLmBwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head backward tiles");
       const void* wc = static_cast<const char*>(a->weight) + vc0 * H * 2;
-      if (a->dhidden) {
+      if (want_dy) {
         // Column-major view: dhidden_c^T [H, nl] (+)= W_c^T [H, w] * D^T [w, nl].
         rc = blas_status(ctx,
                          rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_none, static_cast<int>(H),
@@ -244,9 +264,15 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         if (rc != PCP_OK) return rc;
       }
     }
-    if (a->dhidden && (e = launch_lm_scatter_rows(dhc, a->dhidden, I(o_cidx), static_cast<int>(N), static_cast<int>(H),
-                                                  st)) != hipSuccess)
+    if (norm && want_dy) {
+      const LmNormBwdArgs nb{dhc, static_cast<const uint16_t*>(a->hidden_states), a->norm_weight, F(o_rstd),
+                             I(o_cidx), I(o_live), N, static_cast<int>(H), nl, lm_norm_slices(nl), a->dhidden,
+                             a->dnorm_weight ? F(o_gpart) : nullptr, a->dnorm_weight};
+      if ((e = launch_lm_norm_bwd(nb, st)) != hipSuccess) return hip_fail(ctx, e, "final norm backward");
+    } else if (!norm && a->dhidden && (e = launch_lm_scatter_rows(dhc, a->dhidden, I(o_cidx), static_cast<int>(N),
+                                                         static_cast<int>(H), st)) != hipSuccess) {
       return hip_fail(ctx, e, "scattering dhidden rows");
+    }
   }
 
   if (a->flags & PCP_FLAG_ASYNC) {
@@ -282,6 +308,7 @@ void pcp_lmhead_args_init(pcp_lmhead_args* a) {
   a->clip_eps = 0.2f;
   a->kl_beta = 0.04f;
   a->std_eps = 1e-8f;
+  a->norm_eps = 1e-6f;
 }
 
 int pcp_grpo_lmhead_fwd_bwd(pcp_ctx* ctx, const pcp_lmhead_args* a) { return run_lm(ctx, a); }

@@ -207,8 +207,9 @@ class LmheadOutputs:
     ref_logp: torch.Tensor | None
     token_loss: torch.Tensor    # [S, T] f32
     advantages: torch.Tensor    # [S] f32
-    dhidden: torch.Tensor | None  # [S*T, H] f32
+    dhidden: torch.Tensor | None  # [S*T, H] f32 (dL/dh before the final norm when it is fused)
     dweight: torch.Tensor | None  # [V, H] f32
+    dnorm_weight: torch.Tensor | None = None  # [H] f32, with the fused final norm
 
 
 def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor, mask: torch.Tensor | None = None,
@@ -216,10 +217,13 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
                    rewards: torch.Tensor | None = None, group_size: int = 1, old_logp: torch.Tensor | None = None,
                    loss_mode: int = LossMode.REINFORCE, clip_eps: float = 0.2, kl_beta: float = 0.04,
                    loss_norm: float = 0.0, std_eps: float = 1e-8, want_grads: bool = True, vocab_chunk: int = 0,
+                   norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6,
                    outputs: LmheadOutputs | None = None, sync: bool = True, stream=None,
                    ctx: Context | None = None) -> LmheadOutputs:
     """Fused LM-head + GRPO loss (pcp_grpo_lmhead_fwd_bwd). hidden [S*T, H] bf16,
-    weight / ref_weight [V, H] bf16, ids / mask / old_logp [S, T]."""
+    weight / ref_weight [V, H] bf16, ids / mask / old_logp [S, T]. With norm_weight
+    (f32 [H]) the decoder's final RMSNorm is fused in: hidden is the last layer's
+    output before the norm, and dhidden / dnorm_weight are the gradients there."""
     ctx = ctx or default_context(hidden.device.index or 0)
     if ids.dim() != 2:
         raise PcpError(-1, "ids must be [S, T]")
@@ -239,7 +243,12 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
             token_loss=torch.zeros((S, T), dtype=torch.float32, device=dev),
             advantages=torch.zeros((S,), dtype=torch.float32, device=dev),
             dhidden=torch.empty((N, H), dtype=torch.float32, device=dev) if want_grads else None,
-            dweight=torch.empty((V, H), dtype=torch.float32, device=dev) if want_grads else None)
+            dweight=torch.empty((V, H), dtype=torch.float32, device=dev) if want_grads else None,
+            dnorm_weight=torch.empty(H, dtype=torch.float32, device=dev)
+            if want_grads and norm_weight is not None else None)
+    if norm_weight is not None and (norm_weight.dtype != torch.float32 or norm_weight.numel() != H
+                                    or not norm_weight.is_contiguous()):
+        raise PcpError(-2, "norm_weight must be a contiguous f32 tensor of H elements")
     a = _lib.LmheadArgs()
     lib().pcp_lmhead_args_init(ctypes.byref(a))
     a.n_seq, a.rows, a.hidden, a.vocab, a.group_size, a.vocab_chunk = S, T, H, V, int(group_size), int(vocab_chunk)
@@ -253,6 +262,7 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
     a.logp, a.ref_logp, a.token_loss = _ptr(outputs.logp), _ptr(outputs.ref_logp), _ptr(outputs.token_loss)
     a.advantages_out, a.loss = _ptr(outputs.advantages), _ptr(outputs.loss)
     a.dhidden, a.dweight = _ptr(outputs.dhidden), _ptr(outputs.dweight)
+    a.norm_weight, a.dnorm_weight, a.norm_eps = _ptr(norm_weight), _ptr(outputs.dnorm_weight), norm_eps
     a.loss_mode = int(loss_mode)
     a.clip_eps, a.kl_beta, a.std_eps, a.loss_norm = clip_eps, kl_beta, std_eps, loss_norm
     a.flags = 0 if sync else _lib.FLAG_ASYNC

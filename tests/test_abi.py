@@ -135,6 +135,7 @@ def test_lmhead_args_defaults():
     a = _valid_lm_args()
     assert a.group_size == 1 and a.ids_dtype == DType.i64 and a.mask_dtype == DType.f32 and a.vocab_chunk == 0
     assert abs(a.clip_eps - 0.2) < 1e-7 and abs(a.kl_beta - 0.04) < 1e-8 and a.loss_mode == 0
+    assert abs(a.norm_eps - 1e-6) < 1e-12 and not a.norm_weight and not a.dnorm_weight
 
 
 @pytest.mark.parametrize("mutate,code,text", [
@@ -146,6 +147,9 @@ def test_lmhead_args_defaults():
     (lambda a: setattr(a, "loss_mode", 1), -1, "ref_weight"),
     (lambda a: setattr(a, "rewards", None), -1, "both NULL"),
     (lambda a: (setattr(a, "n_seq", 1 << 20), setattr(a, "rows", 1 << 10)), -9, "2^28"),
+    (lambda a: setattr(a, "dnorm_weight", 0x5000), -1, "needs norm_weight"),
+    (lambda a: (setattr(a, "norm_weight", 0x5000), setattr(a, "hidden", 8256)), -1, "hidden <= 8192"),
+    (lambda a: (setattr(a, "norm_weight", 0x5000), setattr(a, "norm_eps", float("nan"))), -1, "norm_eps"),
 ])
 def test_lmhead_argument_errors_without_device(mutate, code, text):
     L = _lib.lib()
@@ -258,6 +262,22 @@ def test_execute_lmhead_argument_errors_without_device():
     ids[1, 2] = 0
     with pytest.raises(PcpError) as e:
         execute_raw(None, "grpo_lmhead_fwd_bwd", data[:3] + [ids] + data[4:], shapes, dts)
+    assert e.value.code == -1 and "context is NULL" in str(e.value)
+    # the optional ninth input (final norm weight): its shape, its dtype, hyper of 6
+    gamma = np.ones(64, np.float32)
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data + [gamma[:32]], shapes + [(32,)], dts + [DType.f32])
+    assert e.value.code == -1 and "norm_weight" in str(e.value)
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data + [gamma.view(np.int32)], shapes + [(64,)], dts + [DType.i32])
+    assert e.value.code == -2 and "norm_weight" in str(e.value)
+    hyper6 = np.append(data[7], np.float32(1e-5))
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data[:7] + [hyper6], shapes[:7] + [(6,)], dts)
+    assert e.value.code == -1 and "hyper" in str(e.value)     # six entries only with the norm
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "grpo_lmhead_fwd_bwd", data[:7] + [hyper6, gamma], shapes[:7] + [(6,), (64,)],
+                    dts + [DType.f32])
     assert e.value.code == -1 and "context is NULL" in str(e.value)
 
 

@@ -228,6 +228,44 @@ def test_execute_lmhead_shifted_vs_oracle():
     assert np.abs(dw - want_dw).max() <= 2.0 ** -7 * scale_w
 
 
+def test_execute_lmhead_final_norm_shifted():
+    """The host-bytes function with the ninth input (final norm weight, eps in hyper[5]):
+    the same outputs as the device-pointer call on the shifted token arrays, plus
+    dnorm_weight as the seventh output."""
+    from pcp_amd._lib import DType
+    from pcp_amd.backend import HipGrpoBackend
+
+    S, T, H, V, G = 2, 33, 192, 500, 2
+    c = make_norm_case(S, T, H, V, G, seed=23, lengths=[33, 21])
+    c["eps"] = 1e-5
+    old = np.full((S, T), -6.0, np.float32)
+    hyper = np.array([G, 0.2, 0.04, 0, 1, c["eps"]], np.float32)
+    ins = [c["h"].reshape(S, T, H), c["wb"], c["rb"], c["ids"], c["mask"], old, c["rewards"], hyper, c["gamma"]]
+    be = HipGrpoBackend.init()
+    outs = be.executeFunction(None, "grpo_lmhead_fwd_bwd", ins, [x.shape for x in ins],
+                              [DType.bf16, DType.bf16, DType.bf16, DType.i64, DType.f32, DType.f32, DType.f32,
+                               DType.f32, DType.f32])
+    be.deinit()
+    assert len(outs) == 7
+    # The device-pointer call on the shifted arrays (row t scores token t + 1).
+    sid = np.zeros_like(c["ids"])
+    sid[:, :-1] = c["ids"][:, 1:]
+    smask = np.zeros_like(c["mask"])
+    smask[:, :-1] = c["mask"][:, 1:]
+    sold = np.zeros_like(old)
+    sold[:, :-1] = old[:, 1:]
+    ref = grpo.lmhead_fwd_bwd(dev(c["h"]), dev(c["wb"]), dev(sid), dev(smask), ref_weight=dev(c["rb"]),
+                              rewards=dev(c["rewards"]), group_size=G, old_logp=dev(sold),
+                              loss_mode=LossMode.GRPO_CLIP_KL, norm_weight=dev(c["gamma"]), norm_eps=c["eps"])
+    torch.cuda.synchronize()
+    assert np.frombuffer(outs[0], np.float32)[0] == float(ref.loss.cpu())
+    assert np.array_equal(np.frombuffer(outs[1], np.float32), ref.dhidden.cpu().numpy().reshape(-1))
+    assert np.array_equal(np.frombuffer(outs[2], np.float32), ref.dweight.cpu().numpy().reshape(-1))
+    lp = np.frombuffer(outs[3], np.float32).reshape(S, T)
+    assert np.array_equal(lp[:, 1:], ref.logp.cpu().numpy()[:, :-1]) and not lp[:, 0].any()
+    assert np.array_equal(np.frombuffer(outs[6], np.float32), ref.dnorm_weight.cpu().numpy())
+
+
 def test_lmhead_deterministic():
     c = make_case(2, 70, 128, 900, 2, seed=5, lengths=[70, 33])
     old = np.full((2, 70), -7.0, np.float32)
@@ -261,6 +299,137 @@ def test_lmhead_errors():
         grpo.lmhead_fwd_bwd(dev(c["hb"][:, :32].copy()), dev(c["wb"][:, :32].copy()), dev(c["ids"]),
                             rewards=dev(c["rewards"]))
     assert ei.value.code == -1   # hidden must be a multiple of 64
+
+
+# ---- the decoder's final RMSNorm fused at both ends ------------------------------------------
+
+def make_norm_case(S, T, H, V, G, seed, lengths, logit_std=2.0):
+    """make_case plus the pre-norm hidden states h (rows of scales e^-2 .. e^3), a norm
+    weight near 1 (bf16 values) and eps 1e-6. The oracle's LM-head operand hb is the
+    norm's bf16 output, reproduced bit for bit by oracle.rmsnorm_operand."""
+    c = make_case(S, T, H, V, G, seed, lengths, logit_std)
+    rng = np.random.default_rng(seed + 7)
+    scale = np.exp(rng.uniform(-2, 3, size=(S * T, 1)))
+    c["h"] = orc.bf16_from_f32((rng.standard_normal((S * T, H)) * scale).astype(np.float32))
+    c["gamma"] = orc.bf16_to_f32(orc.bf16_from_f32((1 + 0.2 * rng.standard_normal(H)).astype(np.float32)))
+    c["eps"] = 1e-6
+    c["hb"], c["rstd"], c["xb"] = orc.rmsnorm_operand(c["h"], c["gamma"], c["eps"])
+    return c
+
+
+def run_device_norm(c, mode, old, *, vocab_chunk=0, outputs=None):
+    return grpo.lmhead_fwd_bwd(dev(c["h"]), dev(c["wb"]), dev(c["ids"]), dev(c["mask"]), ref_weight=dev(c["rb"]),
+                               rewards=dev(c["rewards"]), group_size=c["G"], old_logp=dev(old), loss_mode=mode,
+                               vocab_chunk=vocab_chunk, norm_weight=dev(c["gamma"]), norm_eps=c["eps"],
+                               outputs=outputs)
+
+
+def norm_grad_bounds(c, want_dy, tol_dy, n_live):
+    """float64 (dh, tol_dh, dgamma, tol_dgamma) through the norm's VJP. The bound on the
+    LM head's dy propagates as |d(dh)| <= r (tg + |x| sum_k tg_k |x_k| / H) with
+    tg = tol_dy |gamma| and x = h r; f32 slack covers the device's dot products and its
+    f32 r; dgamma adds its f32 sum over live rows (block partials, then blocks)."""
+    h = orc.bf16_to_f32(c["h"]).astype(np.float64)
+    H = h.shape[1]
+    r = 1.0 / np.sqrt((h * h).mean(1) + c["eps"])
+    x = h * r[:, None]
+    gam = np.abs(c["gamma"].astype(np.float64))
+    dh, dg = orc.rmsnorm_vjp(c["h"], c["gamma"], c["eps"], c["xb"], want_dy)
+    tg = tol_dy * gam[None, :]
+    g = np.abs(want_dy) * gam[None, :]
+    tol_dh = r[:, None] * (tg + np.abs(x) * ((tg * np.abs(x)).sum(1) / H)[:, None])
+    tol_dh += 8e-6 * r[:, None] * (g + np.abs(x) * ((g * np.abs(x)).sum(1) / H)[:, None])
+    xr = np.abs(orc.bf16_to_f32(c["xb"]).astype(np.float64))
+    tol_dg = (tol_dy * xr).sum(0) + (n_live + 600) * 2.0 ** -24 * (np.abs(want_dy) * xr).sum(0)
+    return dh, tol_dh + 1e-30, dg, tol_dg + 1e-30
+
+
+NORM_SHAPES = [
+    # S, T, H, V, G, chunk, lengths: H = 192 (one column per thread, ragged), Qwen2.5-0.5B's
+    # H = 896 (four columns per thread, the last ragged), H = 4096 (sixteen).
+    (3, 50, 192, 1000, 3, 256, [50, 31, 7]),
+    (2, 64, 896, 2048, 2, 0, [64, 20]),
+    (1, 40, 4096, 1024, 1, 512, [33]),
+]
+
+
+@pytest.mark.parametrize("mode", [LossMode.REINFORCE, LossMode.GRPO_CLIP_KL])
+@pytest.mark.parametrize("shape", NORM_SHAPES, ids=lambda s: f"S{s[0]}T{s[1]}H{s[2]}V{s[3]}")
+def test_lmhead_final_norm_vs_oracle(shape, mode):
+    S, T, H, V, G, chunk, lengths = shape
+    c = make_norm_case(S, T, H, V, G, seed=S * 100 + H, lengths=lengths)
+    L, lse, rlse, old, r = oracle_case(c, mode)
+    print(f"lmhead final norm S={S} T={T} H={H} V={V} mode={int(mode)}", flush=True)
+    out = run_device_norm(c, mode, old, vocab_chunk=chunk)
+    torch.cuda.synchronize()
+    check_forward(c, out, L, lse, rlse, r, mode)
+    want_dy, tol_dy, want_dw, tol_dw = grad_bounds(c, L, lse, r, mode, old)
+    dw = out.dweight.cpu().numpy().astype(np.float64)
+    assert not np.any(np.abs(dw - want_dw) > tol_dw), np.abs(dw - want_dw).max()
+    n_live = int((c["mask"] != 0).sum())
+    want_dh, tol_dh, want_dg, tol_dg = norm_grad_bounds(c, want_dy, tol_dy, n_live)
+    dh = out.dhidden.cpu().numpy().astype(np.float64)
+    edh = np.abs(dh - want_dh)
+    assert not np.any(edh > tol_dh), f"dh: {(edh > tol_dh).sum()} out of tolerance, worst {edh.max():.3e}"
+    assert np.all(dh[c["mask"].reshape(-1) == 0] == 0)
+    dg = out.dnorm_weight.cpu().numpy().astype(np.float64)
+    edg = np.abs(dg - want_dg)
+    assert not np.any(edg > tol_dg), f"dgamma: {(edg > tol_dg).sum()} out of tolerance, worst {edg.max():.3e}"
+
+
+def test_lmhead_final_norm_operand_bit_exact():
+    """The norm's bf16 output, the LM head's operand, equals oracle.rmsnorm_operand bit
+    for bit. With one live token the dW GEMM has K = 1, so dW[v, k] = D_v * y_k exactly
+    (a product of two bf16 values is exact in f32), and y = y* holds iff
+    dW[v, k] * y*_k0 == dW[v, k0] * y*_k for every k, exactly in float64."""
+    T, H, V = 64, 896, 300
+    c = make_norm_case(1, T, H, V, 1, seed=21, lengths=[T])
+    ypos = orc.bf16_to_f32(c["hb"]).astype(np.float64)
+    rng = np.random.default_rng(22)
+    for t in rng.choice(T, 8, replace=False):
+        mask = np.zeros((1, T), np.float32)
+        mask[0, t] = 1.0
+        print(f"final norm operand: live token {t}", flush=True)
+        out = grpo.lmhead_fwd_bwd(dev(c["h"]), dev(c["wb"]), dev(c["ids"]), dev(mask), rewards=dev(np.ones(1, np.float32)),
+                                  advantages=dev(np.full(1, 0.75, np.float32)), norm_weight=dev(c["gamma"]),
+                                  norm_eps=c["eps"])
+        torch.cuda.synchronize()
+        dw = out.dweight.cpu().numpy().astype(np.float64)
+        y = ypos[t]
+        v = int(np.argmax(np.abs(dw).sum(1)))
+        k0 = int(np.argmax(np.abs(y)))
+        assert dw[v, k0] != 0 and y[k0] != 0
+        assert np.array_equal(dw[v] * y[k0], dw[v, k0] * y), np.nonzero(dw[v] * y[k0] != dw[v, k0] * y)[0][:8]
+        assert np.all(np.isfinite(dw))
+
+
+def test_lmhead_final_norm_partial_gradients_and_errors():
+    """dW alone (no gradient through the norm is formed), dgamma alone, the same values as
+    with every gradient; dnorm_weight without norm_weight and hidden > 8192 are rejected."""
+    c = make_norm_case(2, 32, 256, 700, 2, seed=9, lengths=[32, 9])
+    mode = LossMode.REINFORCE
+    old = np.zeros((2, 32), np.float32)
+    full = run_device_norm(c, mode, old)
+    mk = lambda **kw: grpo.LmheadOutputs(
+        loss=torch.zeros((), device=DEV), logp=torch.zeros((2, 32), device=DEV), ref_logp=None,
+        token_loss=torch.zeros((2, 32), device=DEV), advantages=torch.zeros(2, device=DEV), **kw)
+    only_w = run_device_norm(c, mode, old, outputs=mk(dhidden=None, dweight=torch.empty((700, 256), device=DEV)))
+    only_g = run_device_norm(c, mode, old, outputs=mk(dhidden=None, dweight=None,
+                                                      dnorm_weight=torch.empty(256, device=DEV)))
+    torch.cuda.synchronize()
+    assert torch.equal(only_w.dweight, full.dweight)
+    assert torch.equal(only_g.dnorm_weight, full.dnorm_weight)
+    assert torch.equal(only_w.loss, full.loss)
+    with pytest.raises(PcpError) as ei:
+        grpo.lmhead_fwd_bwd(dev(c["h"]), dev(c["wb"]), dev(c["ids"]), dev(c["mask"]), rewards=dev(c["rewards"]),
+                            outputs=mk(dhidden=None, dweight=None, dnorm_weight=torch.empty(256, device=DEV)))
+    assert ei.value.code == -1
+    hb = torch.zeros((64, 8256), dtype=torch.bfloat16, device=DEV)
+    wb = torch.zeros((8, 8256), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(PcpError) as ei:
+        grpo.lmhead_fwd_bwd(hb, wb, torch.zeros((1, 64), dtype=torch.int64, device=DEV),
+                            rewards=torch.zeros(1, device=DEV), norm_weight=torch.ones(8256, device=DEV))
+    assert ei.value.code == -1
 
 
 # ---- real hidden and vocabulary sizes, few tokens, against the float64 oracle ---------------

@@ -323,6 +323,105 @@ def test_lmhead_grads_match_torch_autograd(orc):
     assert not np.allclose(D @ orc.bf16_to_f32(wb).astype(np.float64), h.grad.numpy(), rtol=1e-6)
 
 
+# ---- the final RMSNorm before the LM head -------------------------------------------------
+
+def test_rmsnorm_operand_closed_forms_order_and_torch(orc):
+    """Qwen2RMSNorm as the LM head's bf16 operand (oracle.rmsnorm_operand):
+    closed forms (constant rows, a one-hot row), the stated f32 summation order against
+    a scalar loop over the same order, and the transformers formula in torch f32."""
+    H = 320
+    gamma = orc.bf16_to_f32(orc.bf16_from_f32(np.linspace(0.5, 1.5, H).astype(np.float32)))
+    # constant 2.0 rows, eps = 0: r = 1/2 exactly, x = 1, y = gamma
+    hb = orc.bf16_from_f32(np.full((2, H), 2.0, np.float32))
+    y, r, x = orc.rmsnorm_operand(hb, gamma, 0.0)
+    assert np.all(r == 0.5) and np.all(orc.bf16_to_f32(x) == 1.0)
+    assert np.array_equal(y, np.broadcast_to(orc.bf16_from_f32(gamma), (2, H)))
+    # one-hot row a = 3 at k = 7: r = sqrt(H) / 3 (eps = 0), x_k = sqrt(H)
+    h = np.zeros((1, H), np.float32)
+    h[0, 7] = 3.0
+    y, r, x = orc.rmsnorm_operand(orc.bf16_from_f32(h), gamma, 0.0)
+    assert abs(float(r[0]) - np.sqrt(H) / 3) <= 2e-7 * np.sqrt(H) / 3
+    xv = orc.bf16_to_f32(x)[0]
+    assert xv[7] == orc.bf16_to_f32(orc.bf16_from_f32(np.float32([np.sqrt(H)])))[0] and not np.any(np.delete(xv, 7))
+    # the summation order, scalar by scalar
+    rng = np.random.default_rng(5)
+    hb = orc.bf16_from_f32((rng.standard_normal((3, H)) * 3).astype(np.float32))
+    eps = np.float32(1e-6)
+    y, r, x = orc.rmsnorm_operand(hb, gamma, eps)
+    hf = orc.bf16_to_f32(hb)
+    for n in range(3):
+        lanes = []
+        for t in range(256):
+            a = np.float32(0)
+            for k in range(t, H, 256):
+                a = np.float32(a + np.float32(hf[n, k] * hf[n, k]))
+            lanes.append(a)
+        waves = []
+        for w in range(4):
+            v = lanes[64 * w:64 * w + 64]
+            while len(v) > 1:
+                v = [np.float32(v[i] + v[i + len(v) // 2]) for i in range(len(v) // 2)]
+            waves.append(v[0])
+        ss = np.float32(np.float32(np.float32(waves[0] + waves[1]) + waves[2]) + waves[3])
+        want = np.float32(1) / np.sqrt(np.float32(ss / np.float32(H)) + eps)
+        assert r[n] == want
+    # transformers' Qwen2RMSNorm in torch f32 (another summation order): y equal but for
+    # rare one-ulp flips at bf16 rounding boundaries
+    N = 64
+    hb = orc.bf16_from_f32((rng.standard_normal((N, 896)) * 2).astype(np.float32))
+    g2 = orc.bf16_to_f32(orc.bf16_from_f32((1 + 0.1 * rng.standard_normal(896)).astype(np.float32)))
+    y, r, x = orc.rmsnorm_operand(hb, g2, 1e-6)
+    ht = torch.from_numpy(orc.bf16_to_f32(hb)).to(torch.bfloat16)
+    hs = ht.float()
+    var = hs.pow(2).mean(-1, keepdim=True)
+    xt = (hs * torch.rsqrt(var + 1e-6)).to(torch.bfloat16)
+    yt = (torch.from_numpy(g2).to(torch.bfloat16) * xt).view(torch.int16).numpy().view(np.uint16)
+    d = np.abs(y.astype(np.int32) - yt.astype(np.int32))
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3
+    r64 = 1 / np.sqrt((orc.bf16_to_f32(hb).astype(np.float64) ** 2).mean(1) + 1e-6)
+    assert np.all(np.abs(r - r64) <= 1e-6 * r64)
+
+
+def test_rmsnorm_vjp_matches_torch_autograd(orc):
+    """dh and dgamma (oracle.rmsnorm_vjp) against torch float64 autograd of
+    L = sum(dy * gamma * x) with the bf16 rounding of x passing gradients through;
+    central differences; scale invariance (eps = 0: sum_k dh_k h_k = 0); and two planted
+    mistakes (a flipped sign, a dropped r^3 term) fail."""
+    rng = np.random.default_rng(6)
+    N, H, eps = 5, 192, 1e-6
+    hb = orc.bf16_from_f32((rng.standard_normal((N, H)) * 2).astype(np.float32))
+    gamma = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    dy = rng.standard_normal((N, H))
+    _, _, xb = orc.rmsnorm_operand(hb, gamma, eps)
+    dh, dg = orc.rmsnorm_vjp(hb, gamma, eps, xb, dy)
+    h = torch.tensor(orc.bf16_to_f32(hb).astype(np.float64), requires_grad=True)
+    g = torch.tensor(gamma.astype(np.float64), requires_grad=True)
+    x = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
+    xr = x + (torch.from_numpy(orc.bf16_to_f32(xb).astype(np.float64)) - x).detach()
+    (torch.from_numpy(dy) * (g * xr)).sum().backward()
+    np.testing.assert_allclose(dh, h.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dg, g.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+    def F(hh):
+        return float((dy * gamma.astype(np.float64) * hh / np.sqrt((hh * hh).mean(1, keepdims=True) + eps)).sum())
+    h0 = orc.bf16_to_f32(hb).astype(np.float64)
+    for (n, k) in [(0, 0), (2, 17), (4, 191)]:
+        e = np.zeros_like(h0)
+        e[n, k] = 1e-6
+        fd = (F(h0 + e) - F(h0 - e)) / 2e-6
+        assert abs(fd - dh[n, k]) <= 1e-6 * max(1.0, abs(dh[n, k]))
+    dh0, _ = orc.rmsnorm_vjp(hb, gamma, 0.0, xb, dy)
+    assert np.all(np.abs((dh0 * h0).sum(1)) <= 1e-12 * (np.abs(dh0 * h0)).sum(1))
+    # planted mistakes
+    r = 1 / np.sqrt((h0 * h0).mean(1) + eps)
+    gg = dy * gamma[None, :]
+    dot = (gg * h0).sum(1)
+    flipped = r[:, None] * gg + h0 * (r ** 3 * dot / H)[:, None]
+    no_r3 = r[:, None] * gg - h0 * (r * dot / H)[:, None]
+    for bad in (flipped, no_r3):
+        assert not np.allclose(bad, h.grad.numpy(), rtol=1e-6)
+
+
 # ---- the step around the loss head: Nesterov, gradient statistics, packing ----------------
 
 def test_nesterov_mlir_reference_kat(orc):
