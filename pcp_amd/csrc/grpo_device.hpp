@@ -38,6 +38,7 @@ __device__ __forceinline__ float hw_exp2(float x) { return __builtin_amdgcn_exp2
 // ---------------------------------------------------------------------------
 struct F32T {
   static constexpr int kBytes = 4;
+  static constexpr uint32_t kNegInfWord = 0xff800000u;   // a word of -inf elements
   __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
     return __uint_as_float(w[j]);
   }
@@ -48,6 +49,7 @@ struct F32T {
 
 struct BF16T {
   static constexpr int kBytes = 2;
+  static constexpr uint32_t kNegInfWord = 0xff80ff80u;
   __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
     const uint32_t x = w[j >> 1];
     return __uint_as_float((j & 1) ? (x & 0xffff0000u) : (x << 16));
@@ -59,6 +61,7 @@ struct BF16T {
 
 struct F16T {
   static constexpr int kBytes = 2;
+  static constexpr uint32_t kNegInfWord = 0xfc00fc00u;
   __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
     const uint32_t x = w[j >> 1];
     const uint16_t h = (j & 1) ? static_cast<uint16_t>(x >> 16) : static_cast<uint16_t>(x & 0xffffu);
@@ -120,6 +123,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, uint32
                                            static_cast<int>(nbytes), 0x00020000);
 }
 
+// Byte offset base + add, formed at the point of use by an opaque v_add_u32. Left to
+// itself the compiler computes the NCH chunk offsets of a row once and keeps them
+// live from the first load to the last store (19 VGPRs at V = 151936), which pushes
+// the resident kernel past its 128-VGPR budget.
+__device__ __forceinline__ uint32_t fresh_off(uint32_t base, uint32_t add) {
+  uint32_t r;
+  asm volatile("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(add), "v"(base));
+  return r;
+}
+
 // Cache-policy bits of buffer accesses: 2 = NT (streaming, not retained).
 constexpr int kBufNT = 2;
 
@@ -133,6 +146,17 @@ template <bool NT>
 __device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, u32x4 v, uint32_t off) {
   typedef int i32x4 __attribute__((ext_vector_type(4)));
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, off, 0, NT ? kBufNT : 0);
+}
+
+// Store one output element at byte offset `off` of a row buffer (range-checked).
+template <typename TO, bool NT>
+__device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  if constexpr (TO::kBytes == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, NT ? kBufNT : 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(pack2<TO>(v, 0.f) & 0xffffu), r, off, 0,
+                                          NT ? kBufNT : 0);
+  }
 }
 
 // Pack N floats into N output elements (N * kBytes = 16 or 32 bytes) and store them

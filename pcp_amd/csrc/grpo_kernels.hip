@@ -11,8 +11,9 @@
 //   3. one workgroup merge of both (m, s) pairs: xor-butterfly in the wave, then a
 //      fixed-order combine of the 16 wave results through LDS;
 //   4. token math (logp, ref logp, ratio, clip, k3-KL, coefficient c);
-//   5. dlogits = c * (onehot - 2^(x*log2e - lse2)) straight from the registers,
-//      packed to bf16 with v_cvt_pk_bf16_f32, stored 16 B per lane.
+//   5. dlogits = c * (onehot - softmax) straight from the registers, packed to
+//      bf16 with v_cvt_pk_bf16_f32, stored 16 B per lane. For bf16 -> bf16 the
+//      softmax terms come from the sum pass, cached as f16 in place of the row.
 // Rows whose token is masked, ignored or a pad row only zero-fill dlogits.
 //
 // Reference semantics: tools/export_qwen_forward.py:150-163 (loss),
@@ -24,6 +25,10 @@
 
 #include "grpo_device.hpp"
 #include "grpo_launch.hpp"
+
+#ifndef PCP_RES_PREFETCH
+#define PCP_RES_PREFETCH 1
+#endif
 
 namespace pcp {
 
@@ -61,6 +66,10 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   constexpr int EPV = 16 / TI::kBytes;
   constexpr uint32_t kChunkBytes = BLOCK * 16;          // one chunk: 16 bytes per lane
   constexpr uint32_t kOutVec = EPV * TO::kBytes;        // output bytes per input vector
+  // bf16 logits -> bf16 dlogits: the sum pass's softmax terms are cached (f16) and
+  // scaled into dlogits, one exponential per element fewer. Other pairs recompute.
+  constexpr bool kCache = __is_same(TI, BF16T) && __is_same(TO, BF16T);
+  constexpr int kPrefetch = PCP_RES_PREFETCH;   // reference batches in flight ahead of the math
   __shared__ float lds[4 * (BLOCK / 64)];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
@@ -93,54 +102,98 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   const float ry = has_ref ? TI::load1(rrow, r.id) : 0.f;
 
   // 1. Policy row -> registers: all NCH loads back to back through one row
-  //    descriptor (lanes past the row end read 0 and are skipped below).
+  //    descriptor. Lanes past the row end read 0; the chunks that hold such lanes
+  //    (a uniform test) get -inf there, so no pass below needs a per-lane branch.
   const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xrow, in_bytes);
   const uint32_t voff = tid * 16u;
   u32x4 xv[NCH];
 #pragma unroll
-  for (int k = 0; k < NCH; ++k) xv[k] = buf_ld16<true>(xbuf, voff + k * kChunkBytes);
+  for (int k = 0; k < NCH; ++k) xv[k] = buf_ld16<true>(xbuf, fresh_off(voff, k * kChunkBytes));
 
-  // 2a. Per-lane (max, sum) of the resident policy values.
-  float pm, ps;
+  // 2. Per-lane (max, sum) of the resident policy values and online (max, sum) of
+  //    the reference row, streamed in batches of RB chunks PD batches ahead. The
+  //    policy sum for chunks [kb, kb + RB) runs in the same step as reference batch
+  //    kb, so its exponentials overlap reference loads in flight instead of leaving
+  //    the CU's memory idle. For bf16 -> bf16 the policy terms e = 2^(x*log2e - m2)
+  //    are also kept, as f16 in place of the row (e <= 1: 2^-12 relative, 2^-25
+  //    absolute below the f16 normal range), and dlogits become a multiple of them.
+  constexpr int NB = (NCH + RB - 1) / RB;
+  constexpr int PD = kPrefetch;
+  const __amdgpu_buffer_rsrc_t rbuf = has_ref ? row_rsrc(rrow, in_bytes) : xbuf;
+  u32x4 rv[PD + 1][RB];
+  if (has_ref) {
+#pragma unroll
+    for (int b = 0; b < PD; ++b)
+#pragma unroll
+      for (int q = 0; q < RB; ++q)
+        if (b < NB && b * RB + q < NCH) rv[b][q] = buf_ld16<true>(rbuf, fresh_off(voff, (b * RB + q) * kChunkBytes));
+  }
+  float pm;
   {
     float mx = kNegInf;
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
       if (k * BLOCK + tid < nv) {
         const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
+        if constexpr (kCache) {
+          // bf16 halves by byte permutes: the same values as unpack(), but not
+          // merged with the sum pass's unpacks, which would keep 152 f32 values
+          // live from here to the sum of the last chunk.
 #pragma unroll
-        for (int j = 0; j < EPV; ++j) mx = fmaxf(mx, TI::unpack(w, j));
+          for (int h = 0; h < 4; ++h)
+            mx = fmaxf(fmaxf(mx, __uint_as_float(__builtin_amdgcn_perm(w[h], 0u, 0x05040c0cu))),
+                       __uint_as_float(__builtin_amdgcn_perm(w[h], 0u, 0x07060c0cu)));
+        } else {
+#pragma unroll
+          for (int j = 0; j < EPV; ++j) mx = fmaxf(mx, TI::unpack(w, j));
+        }
       }
     }
     pm = mx * kLog2e;
-    const float m2 = ms_ref(pm);
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < NCH; ++k) {
-      if (k * BLOCK + tid < nv) {
-        const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
-#pragma unroll
-        for (int j = 0; j < EPV; ++j) s += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -m2));
-      }
-    }
-    ps = s;
   }
-
-  // 2b. Reference row: online (max, sum) over batches of RB chunks.
-  float rm = kNegInf, rs = 0.f;
-  if (has_ref) {
-    const __amdgpu_buffer_rsrc_t rbuf = row_rsrc(rrow, in_bytes);
+  const float m2 = ms_ref(pm);   // this lane's shift (kept for the cached terms)
+  float ps = 0.f, rm = kNegInf, rs = 0.f;
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int kb = 0; kb < NCH; kb += RB) {
-      u32x4 rv[RB];
+  for (int b = 0; b < NB; ++b) {
+    const int kb = b * RB;
+    if (has_ref) {
 #pragma unroll
       for (int q = 0; q < RB; ++q)
-        if (kb + q < NCH) rv[q] = buf_ld16<true>(rbuf, voff + (kb + q) * kChunkBytes);
+        if (b + PD < NB && kb + PD * RB + q < NCH)
+          rv[(b + PD) % (PD + 1)][q] = buf_ld16<true>(rbuf, fresh_off(voff, (kb + PD * RB + q) * kChunkBytes));
+    }
+    // policy sum over chunks [kb, kb + RB)
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int k = kb + q;
+      if (k >= NCH || k * BLOCK + tid >= nv) continue;
+      uint32_t* w = reinterpret_cast<uint32_t*>(&xv[k]);
+      if constexpr (kCache) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const float e0 = hw_exp2(fmaf(TI::unpack(w, 2 * h), kLog2e, -m2));
+          const float e1 = hw_exp2(fmaf(TI::unpack(w, 2 * h + 1), kLog2e, -m2));
+          ps += e0;
+          ps += e1;
+          w[h] = pack2<F16T>(e0, e1);
+          // Pin the pack here: left to itself the compiler sinks the packs into the
+          // dlogits loop and keeps 152 f32 terms live across the merge.
+          asm volatile("" ::"v"(w[h]));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < EPV; ++j) ps += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -m2));
+      }
+    }
+    // reference batch b
+    if (has_ref) {
+      u32x4* cur = rv[b % (PD + 1)];
       float bm = kNegInf;
 #pragma unroll
       for (int q = 0; q < RB; ++q) {
         if (kb + q < NCH && (kb + q) * BLOCK + tid < nv) {
-          const uint32_t* w = reinterpret_cast<const uint32_t*>(&rv[q]);
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(&cur[q]);
 #pragma unroll
           for (int j = 0; j < EPV; ++j) bm = fmaxf(bm, TI::unpack(w, j));
         }
@@ -151,7 +204,7 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
 #pragma unroll
       for (int q = 0; q < RB; ++q) {
         if (kb + q < NCH && (kb + q) * BLOCK + tid < nv) {
-          const uint32_t* w = reinterpret_cast<const uint32_t*>(&rv[q]);
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(&cur[q]);
 #pragma unroll
           for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -ref));
         }
@@ -162,6 +215,7 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   }
 
   // 3. Workgroup merge.
+  __builtin_amdgcn_sched_barrier(0);
   block_merge2<BLOCK>(pm, ps, rm, rs, lds);
   const float lse2 = pm + log2f(ps);
   const float lse = lse2 * kLn2;
@@ -175,22 +229,31 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   write_token_outputs(a, r, lp, lr, tt.loss);
 
   // 5. dlogits = c * (onehot - softmax) from the resident row; stores past the
-  //    row end are dropped by the buffer range check.
+  //    row end are dropped by the buffer range check. The target element,
+  //    c * (1 - p_y) from the target logit itself, is then rewritten by the lane
+  //    that stored it (one store; a lane's stores to one address land in order).
   const float c = tt.coef, nc = -tt.coef;
-  const int vid = static_cast<int>(r.id / EPV);
-  const int kid = vid / BLOCK, tid_id = vid - kid * BLOCK, jid = static_cast<int>(r.id) - vid * EPV;
+  const float f = nc * hw_exp2(m2 - lse2);   // softmax = e * 2^(m2 - lse2)
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
     const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
     float o[EPV];
+    if constexpr (kCache) {
 #pragma unroll
-    for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -lse2));
-    if (k == kid && tid == tid_id) {
+      for (int q = 0; q < 4; ++q) {
+        const f16x2 h = __builtin_bit_cast(f16x2, w[q]);
+        o[2 * q] = f * static_cast<float>(h[0]);
+        o[2 * q + 1] = f * static_cast<float>(h[1]);
+      }
+    } else {
 #pragma unroll
-      for (int j = 0; j < EPV; ++j)
-        if (j == jid) o[j] += c;
+      for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -lse2));
     }
-    buf_store_vals<TO, EPV, true>(drow, (k * BLOCK + tid) * kOutVec, o);
+    buf_store_vals<TO, EPV, true>(drow, fresh_off(tid * kOutVec, k * BLOCK * kOutVec), o);
+  }
+  if (tid == static_cast<int>((r.id / EPV) % BLOCK)) {
+    const float dy = c - c * hw_exp2(fmaf(xy, kLog2e, -lse2));
+    buf_store1<TO, true>(drow, static_cast<uint32_t>(r.id) * TO::kBytes, dy);
   }
 }
 
