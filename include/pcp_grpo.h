@@ -20,7 +20,9 @@
  *
  * Every function returns PCP_OK (0) or a negative pcp_status; none aborts.
  * pcp_last_error() returns the message of the most recent failure on a context.
- * A context is not thread-safe (same contract as iree.zig:7).
+ * A context is not thread-safe (same contract as iree.zig:7). Calls on one context
+ * run in stream order; calls that may overlap on different streams need separate
+ * contexts (they share the context's work buffers and row counter).
  */
 #ifndef PCP_GRPO_H
 #define PCP_GRPO_H

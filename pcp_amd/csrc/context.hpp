@@ -16,6 +16,7 @@ struct pcp_ctx {
   int backend = PCP_BACKEND_ROCM;
   std::string last_error;
   int* d_err = nullptr;          // device error word (kErr* bits)
+  int* d_next_row = nullptr;     // row counter of the persistent row kernel (same allocation)
   void* scratch = nullptr;       // per-call work buffers, grown on demand
   size_t scratch_bytes = 0;
   std::set<hipStream_t> pending;  // streams holding PCP_FLAG_ASYNC work

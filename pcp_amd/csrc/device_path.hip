@@ -168,6 +168,8 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op) {
   ra.ids = a->ids;
   ra.mask = a->mask;
   ra.err = ctx->d_err;
+  ra.next_row = ctx->d_next_row;
+  ra.nrows = g.nrows;
   ra.vocab = g.vocab;
   ra.rows = g.rows;
   ra.logit_stride = g.lstride;
@@ -272,12 +274,14 @@ int pcp_init(int backend, int device_ordinal, pcp_ctx** out) {
   pcp_ctx* c = new (std::nothrow) pcp_ctx();
   if (!c) return fail(nullptr, PCP_ERR_OOM, "allocating the context");
   c->device = device_ordinal;
-  e = hipMalloc(&c->d_err, sizeof(int));
+  // Error word at 0, the row kernel's counter 64 bytes on (its own cache line).
+  e = hipMalloc(&c->d_err, 128);
   if (e != hipSuccess) {
     delete c;
     return fail(nullptr, PCP_ERR_OOM, "hipMalloc(error word): %s", hipGetErrorString(e));
   }
-  e = hipMemset(c->d_err, 0, sizeof(int));
+  c->d_next_row = c->d_err + 16;
+  e = hipMemset(c->d_err, 0, 128);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     (void)hipFree(c->d_err);

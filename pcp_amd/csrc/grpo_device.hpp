@@ -38,7 +38,6 @@ __device__ __forceinline__ float hw_exp2(float x) { return __builtin_amdgcn_exp2
 // ---------------------------------------------------------------------------
 struct F32T {
   static constexpr int kBytes = 4;
-  static constexpr uint32_t kNegInfWord = 0xff800000u;   // a word of -inf elements
   __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
     return __uint_as_float(w[j]);
   }
@@ -49,7 +48,6 @@ struct F32T {
 
 struct BF16T {
   static constexpr int kBytes = 2;
-  static constexpr uint32_t kNegInfWord = 0xff80ff80u;
   __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
     const uint32_t x = w[j >> 1];
     return __uint_as_float((j & 1) ? (x & 0xffff0000u) : (x << 16));
@@ -61,7 +59,6 @@ struct BF16T {
 
 struct F16T {
   static constexpr int kBytes = 2;
-  static constexpr uint32_t kNegInfWord = 0xfc00fc00u;
   __device__ static __forceinline__ float unpack(const uint32_t* w, int j) {
     const uint32_t x = w[j >> 1];
     const uint16_t h = (j & 1) ? static_cast<uint16_t>(x >> 16) : static_cast<uint16_t>(x & 0xffffu);
@@ -295,6 +292,8 @@ struct RowArgs {
   float* ref_logp;
   float* token_loss;
   int* err;
+  int* next_row;           // persistent row kernel: rows handed out past the first grid
+  int64_t nrows;           // logits rows of the launch
   int64_t vocab;
   int64_t rows;
   int64_t logit_stride;

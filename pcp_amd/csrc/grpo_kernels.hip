@@ -1,9 +1,10 @@
 // GRPO loss-head kernels for MI355X (gfx950).
 //
-// One workgroup owns one logits row. The hot kernel (grpo_resident_kernel) keeps
-// the policy row in VGPRs as packed 16-bit words (V=151936 bf16 = 19 x 16 B per
-// lane at 1024 lanes), so a live row costs exactly one read of the policy row,
-// one read of the reference row and one write of dlogits:
+// One workgroup owns one logits row at a time. The hot kernel (grpo_resident_kernel)
+// is persistent: one workgroup per CU takes rows from a counter. It keeps the policy
+// row in VGPRs as packed 16-bit words (V=151936 bf16 = 19 x 16 B per lane at 1024
+// lanes), so a live row costs exactly one read of the policy row, one read of the
+// reference row and one write of dlogits:
 //   1. issue every 16-byte load of the policy row (coalesced, 1 KiB per wave per
 //      chunk), then stream the reference row in batches;
 //   2. per-lane max and sum of 2^(x*log2e - m) over the resident values, online
@@ -62,7 +63,7 @@ __device__ __forceinline__ void flag_nonfinite(const RowArgs& a, float lse, floa
 // V <= BLOCK*NCH*EPV, dlogits != nullptr.
 // ---------------------------------------------------------------------------
 template <typename TI, typename TO, int BLOCK, int NCH, int RB>
-__global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
+__device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row, float* lds) {
   constexpr int EPV = 16 / TI::kBytes;
   constexpr uint32_t kChunkBytes = BLOCK * 16;          // one chunk: 16 bytes per lane
   constexpr uint32_t kOutVec = EPV * TO::kBytes;        // output bytes per input vector
@@ -70,9 +71,7 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   // scaled into dlogits, one exponential per element fewer. Other pairs recompute.
   constexpr bool kCache = __is_same(TI, BF16T) && __is_same(TO, BF16T);
   constexpr int kPrefetch = PCP_RES_PREFETCH;   // reference batches in flight ahead of the math
-  __shared__ float lds[4 * (BLOCK / 64)];
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
   const RowMeta r = row_meta(a, row);
   const int nv = static_cast<int>(a.vocab / EPV);
   const int64_t row_elem = row * a.vocab;
@@ -102,8 +101,7 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   const float ry = has_ref ? TI::load1(rrow, r.id) : 0.f;
 
   // 1. Policy row -> registers: all NCH loads back to back through one row
-  //    descriptor. Lanes past the row end read 0; the chunks that hold such lanes
-  //    (a uniform test) get -inf there, so no pass below needs a per-lane branch.
+  //    descriptor (lanes past the row end read 0 and are skipped below).
   const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xrow, in_bytes);
   const uint32_t voff = tid * 16u;
   u32x4 xv[NCH];
@@ -256,6 +254,37 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
     buf_store1<TO, true>(drow, static_cast<uint32_t>(r.id) * TO::kBytes, dy);
   }
 }
+
+// Persistent: a workgroup takes row blockIdx.x, then rows from the launch's counter
+// (zeroed before the launch) until none are left, so the CU starts its next row
+// without a workgroup launch and the counter's latency hides under the current row.
+// Every wave reads the same row index from LDS, so all of them leave the loop
+// together. The index is double-buffered: thread 0 writes slot i & 1 at the top of
+// step i, while slot (i - 1) & 1 may still be read; the barrier at the end of step i
+// orders the reads of slot i & 1 before its next write, in step i + 2.
+// bf16 logits with f32 dlogits keep one row per workgroup: in the loop that pair
+// runs past 128 VGPRs (86 spilled at 19 chunks).
+template <typename TI, typename TO>
+constexpr bool kPersistentRows = !(__is_same(TI, BF16T) && __is_same(TO, F32T));
+
+template <typename TI, typename TO, int BLOCK, int NCH, int RB>
+__global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
+  __shared__ float lds[4 * (BLOCK / 64)];
+  __shared__ int s_next[2];
+  if constexpr (!kPersistentRows<TI, TO>) {
+    resident_row<TI, TO, BLOCK, NCH, RB>(a, blockIdx.x, lds);
+    return;
+  }
+  int64_t row = blockIdx.x;
+  for (int i = 0; row < a.nrows; ++i) {
+    if (threadIdx.x == 0) s_next[i & 1] = atomicAdd(a.next_row, 1) + static_cast<int>(gridDim.x);
+    resident_row<TI, TO, BLOCK, NCH, RB>(a, row, lds);
+    __syncthreads();   // s_next visible; this row's LDS reads done before the next row writes
+    row = s_next[i & 1];
+  }
+}
+
+__global__ void reset_counter_kernel(int* c) { *c = 0; }
 
 // ---------------------------------------------------------------------------
 // Streaming kernel: any V, any alignment (VEC = false uses element loads).
@@ -514,8 +543,23 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
   // RB = 2: the largest reference batch that needs no register spill next to a
   // 19-chunk resident row at 128 VGPRs (4 spills 9 VGPRs and measured ~1% slower).
   constexpr int RB = 2;
-  grpo_resident_kernel<TI, TO, BLOCK, NCH, RB>
-      <<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
+  // One workgroup per resident slot of the device (the kernel's occupancy times the
+  // CU count), at most one per row.
+  static const int slots = [] {
+    int dev = 0, cus = 0, occ = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &occ, reinterpret_cast<const void*>(&grpo_resident_kernel<TI, TO, BLOCK, NCH, RB>), BLOCK, 0) !=
+            hipSuccess)
+      return 0;
+    return cus * (occ > 0 ? occ : 1);
+  }();
+  if (slots <= 0) return hipErrorInvalidDeviceFunction;
+  const int64_t grid = kPersistentRows<TI, TO> ? (nrows < slots ? nrows : slots) : nrows;
+  if (grid <= 0) return hipSuccess;
+  if (kPersistentRows<TI, TO>) reset_counter_kernel<<<1, 1, 0, st>>>(a.next_row);
+  grpo_resident_kernel<TI, TO, BLOCK, NCH, RB><<<dim3(static_cast<unsigned>(grid)), dim3(BLOCK), 0, st>>>(a);
   return hipGetLastError();
 }
 
