@@ -29,11 +29,14 @@ namespace lm {
 constexpr int BV = 256;           // vocab rows per tile (MFMA A operand: W rows)
 constexpr int BT = 256;           // tokens per tile (MFMA B operand: hidden rows)
 constexpr int BK = 32;            // hidden (K) per pipeline stage
-constexpr int NST = 4;            // LDS stages: up to 3 in flight while one is read
+#ifndef PCP_LM_NST
+#define PCP_LM_NST 4
+#endif
+constexpr int NST = PCP_LM_NST;   // LDS stages: up to NST - 1 in flight while one is read
 constexpr int ROWB = BK * 2;      // bytes of one operand row in one stage
 constexpr int kOpBytes = BV * ROWB;             // 16 KB: one operand, one stage
 constexpr int kStageBytes = 2 * kOpBytes;       // 32 KB
-constexpr size_t kSmemGemm = NST * kStageBytes; // 128 KB
+constexpr size_t kSmemGemm = NST * kStageBytes; // 32 KB per stage
 constexpr int NTHR = 256;         // 4 waves: 2 (vocab) x 2 (tokens), 128 x 128 each
 constexpr int LDD = BV + 8;       // bf16 dlogits row in the backward epilogue (528 B, 16-B aligned)
 constexpr size_t kSmemEpi = (BT / 2) * LDD * sizeof(__bf16);   // half the token columns at a time
@@ -41,10 +44,14 @@ constexpr size_t kSmem = kSmemGemm > kSmemEpi ? kSmemGemm : kSmemEpi;
 constexpr int kGroupM = 8;        // token tiles per group in the tile order
 constexpr int kPart = 128;        // vocab entries per log-sum-exp partial (one wave's rows)
 
-// s_waitcnt immediates (vmcnt only; expcnt and lgkmcnt left at their maxima).
-constexpr int kWaitVm0 = 0x0F70;
-constexpr int kWaitVm8 = 0x0F78;
-constexpr int kWaitVm16 = 0x4F70;
+// s_waitcnt immediate for vmcnt(n), expcnt and lgkmcnt left at their maxima: vmcnt
+// bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+constexpr int kWaitVm0 = wait_vm(0);
+constexpr int kWaitPrologue = wait_vm(8 * (NST - 2));   // stage 0 landed, NST - 2 later ones in flight
+constexpr int kWaitLoop = wait_vm(8 * (NST - 3));       // stage kb + 1 landed, NST - 3 later ones in flight
+static_assert(wait_vm(0) == 0x0F70 && wait_vm(8) == 0x0F78 && wait_vm(16) == 0x4F70 && wait_vm(24) == 0x4F78,
+              "vmcnt encoding");
 
 }  // namespace lm
 
@@ -166,14 +173,15 @@ lm_tile_kernel(LmTileArgs a) {
   };
 
   // Pipeline: stage kb is read from LDS buffer kb % NST. Every iteration issues one
-  // stage (kb + 3, clamped to the last stage past the end: an L2 hit into a buffer
-  // nobody reads), so exactly one later stage (8 loads per wave) is in flight when
-  // a stage is waited for: vmcnt(8), then the barrier makes every wave's loads of
-  // it visible. Branch-free, so the compiler's LDS waits stay exact.
+  // stage (kb + NST - 1, clamped to the last stage past the end: an L2 hit into a
+  // buffer nobody reads), so NST - 3 later stages (8 loads per wave each) are in
+  // flight when a stage is waited for: vmcnt(8 (NST - 3)), then the barrier makes
+  // every wave's loads of it visible. Branch-free, so the compiler's LDS waits stay
+  // exact.
   const int nk = a.H / BK;
 #pragma unroll
   for (int st = 0; st < NST - 1; ++st) issue(min(st, nk - 1), st);
-  __builtin_amdgcn_s_waitcnt(kWaitVm16);
+  __builtin_amdgcn_s_waitcnt(kWaitPrologue);
   lm_barrier();
   fload(0, 0, 0);
   for (int kb = 0; kb + 1 < nk; ++kb) {
@@ -181,10 +189,11 @@ lm_tile_kernel(LmTileArgs a) {
     mfmas(0);
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS reads of k-step 1
     __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // MFMAs of k-step 0
-    __builtin_amdgcn_s_waitcnt(kWaitVm8);                 // stage kb+1 landed
+    __builtin_amdgcn_s_waitcnt(kWaitLoop);                // stage kb+1 landed
     lm_barrier();
-    // Buffer (kb+3) % NST held stage kb-1, whose reads all completed before this barrier.
-    issue(min(kb + 3, nk - 1), (kb + 3) % NST);
+    // Buffer (kb + NST - 1) % NST held stage kb - 1, whose reads all completed before
+    // this barrier.
+    issue(min(kb + NST - 1, nk - 1), (kb + NST - 1) % NST);
     fload(0, kb + 1, 0);
     mfmas(1);
     __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);    // the stage's loads
