@@ -60,7 +60,7 @@ __device__ __forceinline__ void flag_nonfinite(const RowArgs& a, float lse, floa
 //   TI/TO: input / output codecs; BLOCK lanes; NCH 16-byte chunks per lane
 //   (row capacity BLOCK*NCH*16 bytes); RB reference chunks per batch.
 // Requirements (checked on the host): V % EPV == 0, 16-byte aligned rows,
-// V <= BLOCK*NCH*EPV, dlogits != nullptr.
+// V <= BLOCK*NCH*EPV. dlogits == nullptr: forward only (log-probs).
 // ---------------------------------------------------------------------------
 template <typename TI, typename TO, int BLOCK, int NCH, int RB>
 __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row, float* lds) {
@@ -81,7 +81,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
 
   if (!r.live) {
     write_token_outputs(a, r, 0.f, 0.f, 0.f);
-    if (a.zero_fill) {
+    if (a.dlogits && a.zero_fill) {
       float z[EPV];
 #pragma unroll
       for (int j = 0; j < EPV; ++j) z[j] = 0.f;
@@ -225,6 +225,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   const float lr = ry - rlse;
   const TokenTerms tt = token_terms(a, r, lp, lr);
   write_token_outputs(a, r, lp, lr, tt.loss);
+  if (a.dlogits == nullptr) return;   // forward only (log-probs)
 
   // 5. dlogits = c * (onehot - softmax) from the resident row; stores past the
   //    row end are dropped by the buffer range check. The target element,
@@ -613,14 +614,17 @@ hipError_t dispatch_rows(const RowPlan& p, const RowArgs& a, int64_t nrows, hipS
 
 }  // namespace
 
-RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool want_bwd, bool force_stream) {
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool force_stream) {
   RowPlan p;
   const int epv = 16 / in_bytes;
   const bool vec = aligned16 && (vocab % epv == 0);
   p.kind = vec ? RowPlan::kStreamVec : RowPlan::kStreamScalar;
   p.cfg = -1;
   p.block = 1024;
-  if (!vec || !want_bwd || force_stream) return p;
+  // Forward-only calls take the resident kernel too: its whole-row load keeps 19
+  // loads in flight per lane, where the streaming kernel (79 VGPRs, one workgroup
+  // per CU) waits out one latency per 4-chunk batch.
+  if (!vec || force_stream) return p;
   const int64_t nv = vocab / epv;
   for (int i = 0; i < static_cast<int>(sizeof(kResCfgs) / sizeof(kResCfgs[0])); ++i) {
     if (static_cast<int64_t>(kResCfgs[i].block) * kResCfgs[i].nch >= nv) {

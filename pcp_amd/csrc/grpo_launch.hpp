@@ -18,7 +18,7 @@ struct RowPlan {
 };
 
 // in_bytes: logits element size; aligned16: every row base is 16-byte aligned.
-RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool want_bwd, bool force_stream);
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool force_stream);
 
 hipError_t launch_rows(const RowPlan& p, int in_dtype, int out_dtype, const RowArgs& a,
                        int64_t nrows, hipStream_t st);

@@ -170,7 +170,7 @@ def grpo_loss_fwd_bwd(logits: torch.Tensor, ids: torch.Tensor, mask: torch.Tenso
 
 def logprob_fwd(logits: torch.Tensor, ids: torch.Tensor, ref_logits: torch.Tensor | None = None, *,
                 rows: int | None = None, tok_offset: int = 0, mask: torch.Tensor | None = None,
-                sync: bool = True, stream=None, ctx: Context | None = None):
+                force_streaming: bool = False, sync: bool = True, stream=None, ctx: Context | None = None):
     """Per-token log-probs of ids under logits (and ref_logits): pcp_grpo_logprob_fwd.
     Returns (logp, ref_logp or None), each [S, TS] f32."""
     ctx = ctx or default_context(logits.device.index or 0)
@@ -182,7 +182,7 @@ def logprob_fwd(logits: torch.Tensor, ids: torch.Tensor, ref_logits: torch.Tenso
     a.ref_logits = _ptr(ref_logits)
     a.logp = _ptr(logp)
     a.ref_logp = _ptr(ref_logp)
-    a.flags = 0 if sync else _lib.FLAG_ASYNC
+    a.flags = (0 if sync else _lib.FLAG_ASYNC) | (_lib.FLAG_FORCE_STREAMING if force_streaming else 0)
     a.stream = _stream_handle(stream)
     check(lib().pcp_grpo_logprob_fwd(ctx.handle, ctypes.byref(a)), ctx.handle)
     return logp, ref_logp

@@ -192,6 +192,39 @@ def test_logprob_fwd_matches_oracle():
     assert np.all(np.abs(lr.cpu().numpy().reshape(-1) - want_r) <= 1e-5 * np.maximum(1, np.abs(lse_r)))
 
 
+def test_logprob_fwd_config2_resident_and_streaming():
+    """Forward-only log-probs at config 2 (bf16, V = 151936): the resident kernel gives
+    the loss path's log-probs bit for bit on live tokens (the same row body), the
+    streaming kernel agrees within 1e-5 * max(1, |lse|), and sampled rows match the
+    float64 oracle."""
+    cfg = synth.CONFIGS[2]
+    inp = synth.make_device_inputs(cfg, DEV)
+    print("config 2 forward-only log-probs: resident, streaming, loss path", flush=True)
+    lp, lr = grpo.logprob_fwd(inp["logits"], inp["ids"], inp["ref_logits"], mask=inp["mask"])
+    lps, lrs = grpo.logprob_fwd(inp["logits"], inp["ids"], inp["ref_logits"], mask=inp["mask"], force_streaming=True)
+    out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], rewards=inp["rewards"], group_size=cfg.group,
+                                 ref_logits=inp["ref_logits"], old_logp=inp["old_logp"],
+                                 loss_mode=LossMode.GRPO_CLIP_KL)
+    torch.cuda.synchronize()
+    m = inp["mask"] != 0
+    assert torch.equal(lp[m], out.logp[m]) and torch.equal(lr[m], out.ref_logp[m])
+    rng = np.random.default_rng(7)
+    rows = rng.choice(np.nonzero(m.cpu().numpy().reshape(-1))[0], 24, replace=False)
+    L = inp["logits"].reshape(-1, cfg.V)[torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
+    R = inp["ref_logits"].reshape(-1, cfg.V)[torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
+    ids = inp["ids"].reshape(-1).cpu().numpy()[rows]
+    want, lse = orc.logprob(L.astype(np.float64), ids, dtype=orc.F64)
+    want_r, lse_r = orc.logprob(R.astype(np.float64), ids, dtype=orc.F64)
+    idt = inp["ids"].reshape(-1, 1)
+    for got, got_s, logits, w, l in ((lp, lps, inp["logits"], want, lse), (lr, lrs, inp["ref_logits"], want_r, lse_r)):
+        g = got.reshape(-1).cpu().numpy()[rows]
+        assert np.all(np.abs(g - w) <= 1e-5 * np.maximum(1, np.abs(l))), np.abs(g - w).max()
+        # Both kernels are within 1e-5 * max(1, |lse|) of the truth, lse = x_y - logp per token.
+        xy = logits.reshape(-1, cfg.V).gather(1, idt).float().reshape(got.shape)
+        tol = 2e-5 * torch.clamp((xy - got).abs(), min=1.0)
+        assert bool(((got - got_s).abs()[m] <= tol[m]).all()), float((got - got_s).abs()[m].max())
+
+
 # ---- host-bytes path (the WorkerBackend face) ------------------------------------------------
 
 def test_execute_reference_signature():
