@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "grpo_device.hpp"
 #include "grpo_launch.hpp"
 
@@ -545,18 +547,20 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
   // 19-chunk resident row at 128 VGPRs (4 spills 9 VGPRs and measured ~1% slower).
   constexpr int RB = 2;
   // One workgroup per resident slot of the device (the kernel's occupancy times the
-  // CU count), at most one per row.
-  static const int slots = [] {
+  // CU count), at most one per row. Only a successful query is cached.
+  static std::atomic<int> cached{0};
+  int slots = cached.load(std::memory_order_relaxed);
+  if (slots <= 0) {
     int dev = 0, cus = 0, occ = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &occ, reinterpret_cast<const void*>(&grpo_resident_kernel<TI, TO, BLOCK, NCH, RB>), BLOCK, 0) !=
-            hipSuccess)
-      return 0;
-    return cus * (occ > 0 ? occ : 1);
-  }();
-  if (slots <= 0) return hipErrorInvalidDeviceFunction;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &occ, reinterpret_cast<const void*>(&grpo_resident_kernel<TI, TO, BLOCK, NCH, RB>), BLOCK, 0);
+    if (e != hipSuccess) return e;
+    slots = cus * (occ > 0 ? occ : 1);
+    cached.store(slots, std::memory_order_relaxed);
+  }
   const int64_t grid = kPersistentRows<TI, TO> ? (nrows < slots ? nrows : slots) : nrows;
   if (grid <= 0) return hipSuccess;
   if (kPersistentRows<TI, TO>) reset_counter_kernel<<<1, 1, 0, st>>>(a.next_row);

@@ -189,6 +189,7 @@ lm_tile_kernel(LmTileArgs a) {
     mfmas(0);
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS reads of k-step 1
     __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // MFMAs of k-step 0
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitLoop);                // stage kb+1 landed
     lm_barrier();
     // Buffer (kb + NST - 1) % NST held stage kb - 1, whose reads all completed before
