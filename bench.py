@@ -413,18 +413,99 @@ def bench_b64(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def bench_logprob(args) -> None:
+    """Forward-only log-probs (pcp_grpo_logprob_fwd: log-softmax + sampled-token gather
+    of the policy rows, and of the reference rows unless --policy-only) over the
+    configuration's rows; masked tokens give 0 without reading their rows. The roofline
+    entry is grpo_fwd_kernel: its algorithmic bytes are one read of each live row and
+    the token scalars (id 8, mask 4, one 4-byte log-prob per model) of every row."""
+    import numpy as np
+    import torch
+
+    from pcp_amd import grpo, synth
+
+    dev = torch.device("cuda:0")
+    cfg = synth.CONFIGS[args.config]
+    inp = synth.make_device_inputs(cfg, dev)
+    ref = None if args.policy_only else inp["ref_logits"]
+    ctx = grpo.default_context(0)
+
+    def call():
+        return grpo.logprob_fwd(inp["logits"], inp["ids"], ref, mask=inp["mask"], sync=False, ctx=ctx)
+
+    for _ in range(args.warmup):
+        call()
+    ctx.sync()
+    torch.cuda.synchronize()
+    kernel_ms, elapsed = _timed_calls(ctx, args.steps, call)
+    ctx.sync()
+    nmod = 1 if args.policy_only else 2
+    s_in = 2 if cfg.dtype == "bf16" else 4
+    live = int((inp["mask"] != 0).sum())
+    rows = cfg.S * cfg.T
+    alg = live * nmod * cfg.V * s_in + rows * (12 + 4 * nmod)
+    ms_step = elapsed * 1e3 / args.steps
+    achieved = alg / (kernel_ms / 1e3) / 1e9
+    what = "policy" if args.policy_only else "policy + reference"
+    line = {
+        "metric": f"GRPO forward-only log-probs ({what}), valid tokens/s, V={cfg.V} {cfg.dtype}",
+        "value": live / (ms_step / 1e3), "unit": "valid tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": cfg.dtype, "data": "synthetic (seeded Philox/PCG64 inputs of the configuration)",
+        "config": {"workload": f"config{cfg.key} {cfg.name}: log-probs of {what} rows, {cfg.prompts} prompts x "
+                               f"G={cfg.group}, T={cfg.T}, V={cfg.V}, {cfg.dtype} logits",
+                   "rows": rows, "valid_rows": live},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "grpo_fwd_kernel",
+                     "kernel_ms": kernel_ms, "algorithmic_bytes": alg},
+    }
+    tfile = os.path.join(ROOT, "profiles", f"traffic_logprob_config{cfg.key}_{'policy' if args.policy_only else 'ref'}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+
+        threads = min(os.cpu_count() or 1, 16)
+        flat = inp["logits"].view(-1, cfg.V)
+        ids = inp["ids"].view(-1).cpu().numpy()
+        livei = np.nonzero(inp["mask"].view(-1).cpu().numpy() != 0)[0]
+        order = np.random.default_rng(0).permutation(livei)
+        spent, done, chunk = 0.0, 0, 256
+        while spent < args.cpu_budget and done < len(order):
+            idx = np.sort(order[done:done + chunk])
+            ti = torch.as_tensor(idx, device=dev)
+            for src in ([flat] if args.policy_only else [flat, inp["ref_logits"].view(-1, cfg.V)]):
+                blk = src.index_select(0, ti)
+                if blk.dtype == torch.bfloat16:
+                    host, dt = blk.view(torch.int16).cpu().numpy().view(np.uint16), orc.BF16
+                else:
+                    host, dt = blk.cpu().numpy(), orc.F32
+                t0 = time.perf_counter()
+                orc.logprob(host, ids[idx], dtype=dt, precision=orc.REF_F32, nthreads=threads)
+                spent += time.perf_counter() - t0
+            done += len(idx)
+        line["cpu_baseline"] = {"value": done / spent, "unit": "valid tokens/s", "cores": threads, "kind": "port",
+                                "sample": f"{done} of {live} valid rows in {spent:.1f} s: oracle fp32 "
+                                          f"reference-op-order log-softmax + gather of the {what} rows "
+                                          f"(grpo_oracle.cpp, OpenMP {threads} threads)"}
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--workload", choices=["loss", "nesterov", "sample", "b64"], default="loss",
-                    help="loss: the GRPO loss head of --config (the headline metric); nesterov: the "
+    ap.add_argument("--workload", choices=["loss", "logprob", "nesterov", "sample", "b64"], default="loss",
+                    help="loss: the GRPO loss head of --config (the headline metric); logprob: forward-only "
+                         "log-probs of --config's rows; nesterov: the "
                          "optimizer step over Qwen2.5-0.5B's parameters; sample: the rollout sampler; "
                          "b64: the UPDATE_WEIGHTS payload codec")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
+    ap.add_argument("--policy-only", action="store_true", help="logprob workload: the policy rows only")
     ap.add_argument("--final-norm", action="store_true",
                     help="config 5: fuse the decoder's final RMSNorm (hidden = the last layer's output)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -461,6 +542,9 @@ def main() -> None:
         return
     if args.workload == "b64":
         bench_b64(args)
+        return
+    if args.workload == "logprob":
+        bench_logprob(args)
         return
     if args.config == 5:
         bench_lmhead(args)

@@ -16,6 +16,8 @@
 //      bf16 with v_cvt_pk_bf16_f32, stored 16 B per lane. For bf16 -> bf16 the
 //      softmax terms come from the sum pass, cached as f16 in place of the row.
 // Rows whose token is masked, ignored or a pad row only zero-fill dlogits.
+// Forward-only calls (no dlogits) take grpo_fwd_kernel instead: one online pass per
+// row at 256 lanes, several workgroups per CU.
 //
 // Reference semantics: tools/export_qwen_forward.py:150-163 (loss),
 // models/tests/qwen_test.mlir:257-286 (cross-entropy lowering),
@@ -288,6 +290,122 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
 }
 
 __global__ void reset_counter_kernel(int* c) { *c = 0; }
+
+// ---------------------------------------------------------------------------
+// Forward-only rows (dlogits == nullptr: log-probs, or the loss without its
+// gradient). One online (max, sum) pass over the row in batches of U 16-byte vectors
+// per lane, through the row's buffer descriptor (lanes past the row end read 0 and
+// are skipped). REF adds the reference row in the same batches. The small register
+// footprint lets several workgroups share a CU, so one workgroup's exponentials run
+// while the others' loads are in flight; the resident kernel holds one row per CU and
+// leaves the CU's memory idle while it sums.
+// Requirements (checked on the host): V % EPV == 0, 16-byte aligned rows.
+// ---------------------------------------------------------------------------
+#ifndef PCP_FWD_BLOCK
+#define PCP_FWD_BLOCK 256
+#endif
+#ifndef PCP_FWD_U
+#define PCP_FWD_U 8
+#endif
+
+// max(m, the EPV values of one 16-byte vector). bf16 halves come from byte permutes:
+// the same values as unpack(), but the compiler does not merge them with the sum
+// pass's unpacks, which would keep every unpacked value of the batch live.
+template <typename TI>
+__device__ __forceinline__ float vec_max(float m, const u32x4& v) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(&v);
+  if constexpr (__is_same(TI, BF16T)) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      m = fmaxf(fmaxf(m, __uint_as_float(__builtin_amdgcn_perm(w[h], 0u, 0x05040c0cu))),
+                __uint_as_float(__builtin_amdgcn_perm(w[h], 0u, 0x07060c0cu)));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16 / TI::kBytes; ++j) m = fmaxf(m, TI::unpack(w, j));
+  }
+  return m;
+}
+
+template <typename TI, int BLOCK, int U, bool REF>
+__global__ void __launch_bounds__(BLOCK) grpo_fwd_kernel(RowArgs a) {
+  constexpr int EPV = 16 / TI::kBytes;
+  constexpr uint32_t kStep = BLOCK * 16u;   // bytes between a lane's vectors in one batch
+  __shared__ float lds[4 * (BLOCK / 64)];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const RowMeta r = row_meta(a, row);
+  if (!r.live) {
+    write_token_outputs(a, r, 0.f, 0.f, 0.f);
+    return;
+  }
+  const int nv = static_cast<int>(a.vocab / EPV);
+  const int64_t row_elem = row * a.vocab;
+  const uint32_t in_bytes = static_cast<uint32_t>(a.vocab) * TI::kBytes;
+  const void* xrow = static_cast<const char*>(a.logits) + row_elem * TI::kBytes;
+  const void* rrow = REF ? static_cast<const char*>(a.ref_logits) + row_elem * TI::kBytes : nullptr;
+  const float xy = TI::load1(xrow, r.id);
+  const float ry = REF ? TI::load1(rrow, r.id) : 0.f;
+  const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xrow, in_bytes);
+  const __amdgpu_buffer_rsrc_t rbuf = REF ? row_rsrc(rrow, in_bytes) : xbuf;
+
+  float pm = kNegInf, ps = 0.f, rm = kNegInf, rs = 0.f;
+  for (int base = 0; base < nv; base += BLOCK * U) {
+    const uint32_t off = static_cast<uint32_t>(base + tid) * 16u;
+    u32x4 xb[U], rb[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q) xb[q] = buf_ld16<true>(xbuf, off + q * kStep);
+    if constexpr (REF) {
+#pragma unroll
+      for (int q = 0; q < U; ++q) rb[q] = buf_ld16<true>(rbuf, off + q * kStep);
+    }
+    float bx = kNegInf, br = kNegInf;
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      if (base + q * BLOCK + tid < nv) {
+        bx = vec_max<TI>(bx, xb[q]);
+        if constexpr (REF) br = vec_max<TI>(br, rb[q]);
+      }
+    }
+    {
+      const float nm = fmaxf(pm, bx * kLog2e);
+      const float ref = ms_ref(nm);
+      float acc = ms_rescale(ps, pm, nm);
+#pragma unroll
+      for (int q = 0; q < U; ++q)
+        if (base + q * BLOCK + tid < nv) {
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(&xb[q]);
+#pragma unroll
+          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -ref));
+        }
+      pm = nm;
+      ps = acc;
+    }
+    if constexpr (REF) {
+      const float nm = fmaxf(rm, br * kLog2e);
+      const float ref = ms_ref(nm);
+      float acc = ms_rescale(rs, rm, nm);
+#pragma unroll
+      for (int q = 0; q < U; ++q)
+        if (base + q * BLOCK + tid < nv) {
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(&rb[q]);
+#pragma unroll
+          for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -ref));
+        }
+      rm = nm;
+      rs = acc;
+    }
+  }
+
+  block_merge2<BLOCK>(pm, ps, rm, rs, lds);
+  const float lse2 = pm + log2f(ps);
+  const float lse = lse2 * kLn2;
+  const float rlse = REF ? ms_lse(rm, rs) : 0.f;
+  flag_nonfinite(a, lse, rlse);
+  const float lp = xy - lse;
+  const float lr = ry - rlse;
+  const TokenTerms tt = token_terms(a, r, lp, lr);
+  write_token_outputs(a, r, lp, lr, tt.loss);
+}
 
 // ---------------------------------------------------------------------------
 // Streaming kernel: any V, any alignment (VEC = false uses element loads).
@@ -582,6 +700,17 @@ hipError_t launch_stream(const RowArgs& a, int64_t nrows, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename TI>
+hipError_t launch_fwd(const RowArgs& a, int64_t nrows, hipStream_t st) {
+  constexpr int BLOCK = PCP_FWD_BLOCK, U = PCP_FWD_U;
+  if (nrows <= 0) return hipSuccess;
+  if (a.ref_logits)
+    grpo_fwd_kernel<TI, BLOCK, U, true><<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
+  else
+    grpo_fwd_kernel<TI, BLOCK, U, false><<<dim3(static_cast<unsigned>(nrows)), dim3(BLOCK), 0, st>>>(a);
+  return hipGetLastError();
+}
+
 // Resident configurations: (BLOCK, NCH). A row of NV 16-byte vectors fits the
 // first configuration with BLOCK*NCH >= NV.
 struct ResCfg {
@@ -612,23 +741,27 @@ hipError_t dispatch_resident(int cfg, const RowArgs& a, int64_t nrows, hipStream
 template <typename TI, typename TO>
 hipError_t dispatch_rows(const RowPlan& p, const RowArgs& a, int64_t nrows, hipStream_t st) {
   if (p.kind == RowPlan::kResident) return dispatch_resident<TI, TO>(p.cfg, a, nrows, st);
+  if (p.kind == RowPlan::kForward) return launch_fwd<TI>(a, nrows, st);
   if (p.kind == RowPlan::kStreamVec) return launch_stream<TI, TO, true>(a, nrows, st);
   return launch_stream<TI, TO, false>(a, nrows, st);
 }
 
 }  // namespace
 
-RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool force_stream) {
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool forward_only, bool force_stream) {
   RowPlan p;
   const int epv = 16 / in_bytes;
   const bool vec = aligned16 && (vocab % epv == 0);
   p.kind = vec ? RowPlan::kStreamVec : RowPlan::kStreamScalar;
   p.cfg = -1;
   p.block = 1024;
-  // Forward-only calls take the resident kernel too: its whole-row load keeps 19
-  // loads in flight per lane, where the streaming kernel (79 VGPRs, one workgroup
-  // per CU) waits out one latency per 4-chunk batch.
+  p.nch = 0;
   if (!vec || force_stream) return p;
+  if (forward_only) {
+    p.kind = RowPlan::kForward;
+    p.block = PCP_FWD_BLOCK;
+    return p;
+  }
   const int64_t nv = vocab / epv;
   for (int i = 0; i < static_cast<int>(sizeof(kResCfgs) / sizeof(kResCfgs[0])); ++i) {
     if (static_cast<int64_t>(kResCfgs[i].block) * kResCfgs[i].nch >= nv) {

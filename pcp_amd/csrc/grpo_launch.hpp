@@ -10,15 +10,16 @@ struct RowArgs;
 
 // Which row kernel serves a request.
 struct RowPlan {
-  enum Kind { kResident = 0, kStreamVec = 1, kStreamScalar = 2 };
+  enum Kind { kResident = 0, kStreamVec = 1, kStreamScalar = 2, kForward = 3 };
   int kind;
   int cfg;    // resident configuration index
   int block;  // lanes per workgroup
   int nch;    // resident 16-byte chunks per lane
 };
 
-// in_bytes: logits element size; aligned16: every row base is 16-byte aligned.
-RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool force_stream);
+// in_bytes: logits element size; aligned16: every row base is 16-byte aligned;
+// forward_only: no dlogits are written.
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool forward_only, bool force_stream);
 
 hipError_t launch_rows(const RowPlan& p, int in_dtype, int out_dtype, const RowArgs& a,
                        int64_t nrows, hipStream_t st);

@@ -192,14 +192,14 @@ def test_logprob_fwd_matches_oracle():
     assert np.all(np.abs(lr.cpu().numpy().reshape(-1) - want_r) <= 1e-5 * np.maximum(1, np.abs(lse_r)))
 
 
-def test_logprob_fwd_config2_resident_and_streaming():
-    """Forward-only log-probs at config 2 (bf16, V = 151936): the resident kernel gives
-    the loss path's log-probs bit for bit on live tokens (the same row body), the
-    streaming kernel agrees within 1e-5 * max(1, |lse|), and sampled rows match the
-    float64 oracle."""
+def test_logprob_fwd_config2_forward_streaming_and_loss_path():
+    """Forward-only log-probs at config 2 (bf16, V = 151936): the forward kernel, the
+    streaming kernel and the loss path (resident kernel) agree within
+    2e-5 * max(1, |lse|) on live tokens, masked tokens read exactly 0, and sampled rows
+    match the float64 oracle within 1e-5 * max(1, |lse|)."""
     cfg = synth.CONFIGS[2]
     inp = synth.make_device_inputs(cfg, DEV)
-    print("config 2 forward-only log-probs: resident, streaming, loss path", flush=True)
+    print("config 2 forward-only log-probs: forward kernel, streaming, loss path", flush=True)
     lp, lr = grpo.logprob_fwd(inp["logits"], inp["ids"], inp["ref_logits"], mask=inp["mask"])
     lps, lrs = grpo.logprob_fwd(inp["logits"], inp["ids"], inp["ref_logits"], mask=inp["mask"], force_streaming=True)
     out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], rewards=inp["rewards"], group_size=cfg.group,
@@ -207,7 +207,8 @@ def test_logprob_fwd_config2_resident_and_streaming():
                                  loss_mode=LossMode.GRPO_CLIP_KL)
     torch.cuda.synchronize()
     m = inp["mask"] != 0
-    assert torch.equal(lp[m], out.logp[m]) and torch.equal(lr[m], out.ref_logp[m])
+    for t in (lp, lr, lps, lrs):
+        assert not bool(t[~m].any())
     rng = np.random.default_rng(7)
     rows = rng.choice(np.nonzero(m.cpu().numpy().reshape(-1))[0], 24, replace=False)
     L = inp["logits"].reshape(-1, cfg.V)[torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
@@ -216,13 +217,72 @@ def test_logprob_fwd_config2_resident_and_streaming():
     want, lse = orc.logprob(L.astype(np.float64), ids, dtype=orc.F64)
     want_r, lse_r = orc.logprob(R.astype(np.float64), ids, dtype=orc.F64)
     idt = inp["ids"].reshape(-1, 1)
-    for got, got_s, logits, w, l in ((lp, lps, inp["logits"], want, lse), (lr, lrs, inp["ref_logits"], want_r, lse_r)):
-        g = got.reshape(-1).cpu().numpy()[rows]
-        assert np.all(np.abs(g - w) <= 1e-5 * np.maximum(1, np.abs(l))), np.abs(g - w).max()
-        # Both kernels are within 1e-5 * max(1, |lse|) of the truth, lse = x_y - logp per token.
+    for got, got_s, got_l, logits, w, l in ((lp, lps, out.logp, inp["logits"], want, lse),
+                                            (lr, lrs, out.ref_logp, inp["ref_logits"], want_r, lse_r)):
+        for g in (got, got_s, got_l):
+            g = g.reshape(-1).cpu().numpy()[rows]
+            assert np.all(np.abs(g - w) <= 1e-5 * np.maximum(1, np.abs(l))), np.abs(g - w).max()
+        # All three are within 1e-5 * max(1, |lse|) of the truth, lse = x_y - logp per token.
         xy = logits.reshape(-1, cfg.V).gather(1, idt).float().reshape(got.shape)
         tol = 2e-5 * torch.clamp((xy - got).abs(), min=1.0)
-        assert bool(((got - got_s).abs()[m] <= tol[m]).all()), float((got - got_s).abs()[m].max())
+        for other in (got_s, got_l):
+            assert bool(((got - other).abs()[m] <= tol[m]).all()), float((got - other).abs()[m].max())
+
+
+def _fwd_logits(rng, n, V, dtype, neg_inf):
+    x = (rng.standard_normal((n, V)) * 3.0).astype(np.float32)
+    x[:, rng.integers(0, V, 3)] += 12.0                   # a few dominant columns
+    if neg_inf:
+        x[::2, rng.integers(0, V, max(1, V // 5))] = -np.inf  # masked-out vocabulary entries
+    if dtype == "bf16":
+        bits = orc.bf16_from_f32(x)
+        return bits, orc.bf16_to_f32(bits).astype(np.float64)
+    if dtype == "f16":
+        h = x.astype(np.float16)
+        return h, h.astype(np.float64)
+    return x, x.astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype,V", [("bf16", 8), ("bf16", 136), ("bf16", 16408), ("bf16", 151936),
+                                     ("f16", 24), ("f16", 32776), ("f32", 4), ("f32", 8196), ("f32", 50000)])
+@pytest.mark.parametrize("with_ref", [False, True])
+def test_logprob_fwd_kernel_shapes(dtype, V, with_ref):
+    """The forward-only kernel (V a multiple of the 16-byte vector, aligned rows) over
+    one-vector rows, a ragged last batch, multi-batch rows and the config-2 width, with
+    -inf vocabulary entries: log-probs within 1e-5 * max(1, |lse|) of the float64 oracle,
+    the streaming kernel within 2e-5 * max(1, |lse|), masked and ignored tokens 0."""
+    rng = np.random.default_rng(V * 3 + with_ref)
+    S, T = 3, 5
+    n = S * T
+    x, x64 = _fwd_logits(rng, n, V, dtype, neg_inf=True)
+    r, r64 = _fwd_logits(rng, n, V, dtype, neg_inf=False)
+    ids = rng.integers(0, V, n).astype(np.int64)
+    ids[x64[np.arange(n), ids] == -np.inf] = int(np.argmax(x64[0]))   # keep targets finite
+    ids = ids.reshape(S, T)
+    ids[1, 2] = -100
+    mask = np.ones((S, T), np.float32)
+    mask[0, 4] = 0.0
+    print(f"forward kernel {dtype} V={V} ref={with_ref}", flush=True)
+    sh = (S, T, V)
+    lt, rt = dev(x.reshape(sh)), dev(r.reshape(sh))
+    args = dict(mask=dev(mask))
+    lp, lr = grpo.logprob_fwd(lt, dev(ids), rt if with_ref else None, **args)
+    lps, lrs = grpo.logprob_fwd(lt, dev(ids), rt if with_ref else None, force_streaming=True, **args)
+    torch.cuda.synchronize()
+    live = (mask != 0) & (ids != -100)
+    fid = np.where(ids.reshape(-1) < 0, 0, ids.reshape(-1))
+    pairs = [(lp, lps, x64)] + ([(lr, lrs, r64)] if with_ref else [])
+    for got, got_s, ref64 in pairs:
+        want, lse = orc.logprob(ref64, fid, dtype=orc.F64)
+        g = got.cpu().numpy().reshape(-1)
+        gs = got_s.cpu().numpy().reshape(-1)
+        lv = live.reshape(-1)
+        tol = 1e-5 * np.maximum(1, np.abs(lse))
+        assert np.all(np.abs(g - want)[lv] <= tol[lv]), np.abs(g - want)[lv].max()
+        assert np.all(np.abs(g - gs)[lv] <= 2 * tol[lv])
+        assert np.all(g[~lv] == 0) and np.all(gs[~lv] == 0)
+    if not with_ref:
+        assert lr is None
 
 
 # ---- host-bytes path (the WorkerBackend face) ------------------------------------------------
@@ -377,7 +437,7 @@ def _full_config(key, mode, n_seq=None):
     scale = (np.abs(tl).sum(1) / Ls * (np.abs(out.advantages.double().cpu().numpy())
                                         if mode == LossMode.REINFORCE else 1.0)).sum() / S
     assert abs(float(out.loss.cpu()) - seqv.sum() / S) <= 1e-5 * scale
-    # log-probs of every row agree with the forward-only streaming kernel
+    # log-probs of every row agree with the forward-only kernel
     lp2, _ = grpo.logprob_fwd(inp["logits"], inp["ids"])
     m = inp["mask"] != 0
     assert float((out.logp - lp2).abs()[m].max()) <= 2e-5 * 20
