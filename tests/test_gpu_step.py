@@ -266,3 +266,29 @@ def test_sampler_bf16_and_strided_rows():
         thr = float(u[r]) * c[-1]
         g = got[r]
         assert c[g] >= thr - 1e-6 * c[-1] and (g == 0 or c[g - 1] <= thr + 1e-6 * c[-1])
+
+
+def test_sampler_successive_calls_reuse_counters_and_partials():
+    """Successive calls on the same logits buffer and the context's scratch partials,
+    alternating greedy and sampled rows, changing row counts and single-workgroup rows:
+    each call selects from its own data."""
+    rng = np.random.default_rng(24)
+    V = 151936
+    buf = torch.empty((64, V), dtype=torch.float32, device=DEV)
+    for call, (R, T) in enumerate([(64, 0.9), (64, 0.0), (17, 1.3), (64, 0.9), (1, 0.0), (33, 0.7)]):
+        x = (rng.standard_normal((R, V)) * 2.0).astype(np.float32)
+        x[:, rng.integers(0, V, R)] += 8.0 * (call + 1)   # the mass moves between calls
+        buf[:R].copy_(t(x))
+        u = rng.random(R).astype(np.float32)
+        got = step.sample_tokens(buf[:R], T, t(u) if T > 0 else None).cpu().numpy()
+        for r in range(R):
+            if T == 0.0:
+                assert got[r] == int(np.argmax(x[r])), (call, r)
+                continue
+            c = _exact_cdf(x[r], T)
+            thr = float(u[r]) * c[-1]
+            g = got[r]
+            assert c[g] >= thr - 1e-6 * c[-1] and (g == 0 or c[g - 1] <= thr + 1e-6 * c[-1]), (call, r, g)
+    small = torch.tensor([[0.5, 2.0, -1.0, -3.0]], device=DEV)   # one block, one workgroup
+    assert int(step.sample_tokens(small, 0.0)[0]) == 1
+    assert int(step.sample_tokens(small, 1.0, t(np.array([0.0], np.float32)))[0]) == 0
