@@ -757,7 +757,10 @@ RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool forward_only
   p.block = 1024;
   p.nch = 0;
   if (!vec || force_stream) return p;
-  if (forward_only) {
+  // The forward kernel addresses a row through a 32-bit buffer offset that runs up to
+  // one batch past the row end: rows up to 2 GiB take it, longer rows stream (64-bit
+  // addressing).
+  if (forward_only && vocab * in_bytes <= (int64_t{1} << 31)) {
     p.kind = RowPlan::kForward;
     p.block = PCP_FWD_BLOCK;
     return p;

@@ -455,3 +455,29 @@ def test_config3_full_size():
 
 def test_config4_full_size():
     _full_config(4, LossMode.GRPO_CLIP_KL)
+
+
+@pytest.mark.parametrize("V", [(1 << 29) - 4, (1 << 29) + 4])
+def test_logprob_fwd_two_gib_rows(V):
+    """f32 rows just under 2 GiB (the forward kernel, 32-bit buffer offsets) and just
+    over (the streaming kernel): log-probs within 1e-5 * max(1, |lse|) of a float64
+    log-sum-exp on the host. The target, three elements before the row end where the
+    offsets are largest, holds e^8 times the rest of the row's mass: a kernel that
+    missed or misplaced it would be off by ~8. (With no dominant term, each lane's f32
+    sum of ~2M small terms drops those below half an ulp, ~0.3% of the sum here.)"""
+    print(f"forward-only f32 row of V={V}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(V & 0xFFFF)
+    x = torch.randn((1, 1, V), device=DEV, generator=g) * 2.0
+    ids = torch.tensor([[V - 3]], device=DEV)
+    x[0, 0, V - 3] = 30.0
+    lp, _ = grpo.logprob_fwd(x, ids)
+    torch.cuda.synchronize()
+    h = x.view(-1).cpu().numpy()
+    del x
+    m = float(h.max())
+    s = 0.0
+    for i in range(0, V, 1 << 26):
+        s += float(np.exp(h[i:i + (1 << 26)].astype(np.float64) - m).sum())
+    lse = m + np.log(s)
+    want = 30.0 - lse
+    assert abs(float(lp[0, 0]) - want) <= 1e-5 * max(1.0, abs(lse)), (float(lp[0, 0]), want)
