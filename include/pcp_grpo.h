@@ -100,6 +100,9 @@ typedef enum pcp_loss_mode {
 /* The token id that contributes nothing (F.cross_entropy ignore_index; the
  * "compare NE -100" select in models/tests/qwen_test.mlir:267-280). */
 #define PCP_IGNORE_INDEX (-100)
+/* Largest vocab of the logits entry points: 2^31 - 2^20, so every per-row index, one
+ * batch past the row end, stays a 32-bit integer. */
+#define PCP_GRPO_MAX_VOCAB ((int64_t)2147483648 - 1048576)
 
 typedef struct pcp_ctx pcp_ctx;
 
@@ -122,7 +125,7 @@ typedef struct pcp_ctx pcp_ctx;
 typedef struct pcp_grpo_args {
   int64_t n_seq;            /* S = prompts * group_size                                 */
   int64_t rows;             /* token-carrying rows per sequence                          */
-  int64_t vocab;            /* V                                                         */
+  int64_t vocab;            /* V, 1 .. PCP_GRPO_MAX_VOCAB                                */
   int64_t group_size;       /* consecutive sequences per group (advantages); >= 1        */
   int64_t logit_seq_stride; /* rows between sequences in logits/dlogits; 0 => rows       */
   int64_t tok_seq_stride;   /* elements between sequences in ids/mask/...; 0 => rows     */

@@ -75,8 +75,8 @@ int validate(const pcp_grpo_args* a, Op op, Geo* g) {
   if (!a) return fail(nullptr, PCP_ERR_INVALID_ARG, "args is NULL");
   if (a->n_seq < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "n_seq must be >= 1 (got %lld)", (long long)a->n_seq);
   if (a->rows < 0) return fail(nullptr, PCP_ERR_INVALID_ARG, "rows must be >= 0");
-  if (a->vocab < 1 || a->vocab > INT32_MAX)
-    return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab must be in [1, 2^31) (got %lld)", (long long)a->vocab);
+  if (a->vocab < 1 || a->vocab > PCP_GRPO_MAX_VOCAB)
+    return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab must be in [1, 2^31 - 2^20] (got %lld)", (long long)a->vocab);
   if (a->group_size < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "group_size must be >= 1");
   g->n_seq = a->n_seq;
   g->rows = a->rows;

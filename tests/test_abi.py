@@ -99,6 +99,7 @@ def _valid_args():
 @pytest.mark.parametrize("mutate,code,text", [
     (lambda a: setattr(a, "n_seq", 0), -1, "n_seq"),
     (lambda a: setattr(a, "vocab", 0), -1, "vocab"),
+    (lambda a: setattr(a, "vocab", (1 << 31) - (1 << 20) + 1), -1, "2^31 - 2^20"),
     (lambda a: setattr(a, "group_size", 0), -1, "group_size"),
     (lambda a: setattr(a, "logit_seq_stride", 3), -1, "logit_seq_stride"),
     (lambda a: setattr(a, "tok_offset", 1), -1, "tok_offset"),
