@@ -492,15 +492,87 @@ def bench_logprob(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def bench_execute(args) -> None:
+    """The host-bytes boundary: pcp_execute("grpo_clip_kl_fwd_bwd") (the mirror of
+    IreeBackend.execute, iree.zig:336-442) on the configuration's inputs held in
+    ordinary (pageable) host memory, as the reference's caller passes them. A step is
+    one call: upload, the loss head on the device, download of every output. Reported
+    for the record of the PCIe-inclusive rate; the device-resident path is the
+    headline."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from pcp_amd import synth
+    from pcp_amd._lib import DType, check, lib
+    from pcp_amd.backend import HipGrpoBackend, marshal_inputs
+
+    dev = torch.device("cuda:0")
+    cfg = synth.CONFIGS[args.config]
+    inp = synth.make_device_inputs(cfg, dev)
+
+    def host(t):
+        if t.dtype == torch.bfloat16:
+            return t.view(torch.int16).cpu().numpy().view(np.uint16)
+        return t.cpu().numpy()
+
+    ins = [host(inp["logits"]), host(inp["ref_logits"]), inp["ids"].to(torch.int64).cpu().numpy(),
+           inp["mask"].float().cpu().numpy(), inp["old_logp"].cpu().numpy(), inp["rewards"].cpu().numpy(),
+           np.array([cfg.group, cfg.clip_eps, cfg.kl_beta, 0.0], np.float32)]
+    del inp
+    torch.cuda.empty_cache()
+    ldt = DType.bf16 if cfg.dtype == "bf16" else DType.f32
+    dts = [ldt, ldt, DType.i64, DType.f32, DType.f32, DType.f32, DType.f32]
+    m = marshal_inputs(ins, [x.shape for x in ins], dts)
+    be = HipGrpoBackend.init()
+    h = be._h
+    in_bytes = sum(x.nbytes for x in ins)
+
+    def call():
+        n_out = ctypes.c_int(0)
+        od = ctypes.POINTER(ctypes.c_void_p)()
+        ob = ctypes.POINTER(ctypes.c_size_t)()
+        t0 = time.perf_counter()
+        check(lib().pcp_execute(h, b"grpo_clip_kl_fwd_bwd", m.n, m.ptrs, m.nbytes, m.shapes, m.ranks, m.dtypes,
+                                ctypes.byref(n_out), ctypes.byref(od), ctypes.byref(ob)), h)
+        dt = time.perf_counter() - t0
+        out_bytes = sum(ob[i] for i in range(n_out.value))
+        lib().pcp_free(h, n_out.value, od, ob)
+        return dt, out_bytes
+
+    for _ in range(args.warmup):
+        call()
+    times, out_bytes = [], 0
+    for _ in range(args.steps):
+        dt, out_bytes = call()
+        times.append(dt)
+    be.deinit()
+    ms_step = 1e3 * sum(times) / len(times)
+    live = int((ins[3][:, 1:] != 0).sum())   # the shifted layout: row t predicts ids[t + 1]
+    line = {
+        "metric": f"GRPO loss fwd+bwd through the host-bytes execute boundary (PCIe-inclusive), valid tokens/s, "
+                  f"V={cfg.V} {cfg.dtype}",
+        "value": live / (ms_step / 1e3), "unit": "valid tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": cfg.dtype, "data": "synthetic (seeded Philox/PCG64 inputs, pageable host memory)",
+        "config": {"workload": f"config{cfg.key} {cfg.name} via pcp_execute(grpo_clip_kl_fwd_bwd)", "valid_rows": live},
+        "host_bytes_in": in_bytes, "host_bytes_out": out_bytes,
+        "host_GBs": (in_bytes + out_bytes) / (ms_step / 1e3) / 1e9,
+        "step_ms_min": 1e3 * min(times),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--workload", choices=["loss", "logprob", "nesterov", "sample", "b64"], default="loss",
+    ap.add_argument("--workload", choices=["loss", "logprob", "execute", "nesterov", "sample", "b64"], default="loss",
                     help="loss: the GRPO loss head of --config (the headline metric); logprob: forward-only "
-                         "log-probs of --config's rows; nesterov: the "
+                         "log-probs of --config's rows; execute: the host-bytes boundary (PCIe-inclusive); nesterov: the "
                          "optimizer step over Qwen2.5-0.5B's parameters; sample: the rollout sampler; "
                          "b64: the UPDATE_WEIGHTS payload codec")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
@@ -545,6 +617,9 @@ def main() -> None:
         return
     if args.workload == "logprob":
         bench_logprob(args)
+        return
+    if args.workload == "execute":
+        bench_execute(args)
         return
     if args.config == 5:
         bench_lmhead(args)

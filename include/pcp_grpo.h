@@ -209,8 +209,11 @@ int pcp_sync(pcp_ctx* ctx);
  * All [.,T,V] and [.,T,H] functions use the reference's shift: row t scores token t+1,
  * per-token outputs are indexed by token position (position 0 is 0).
  * dtypes == NULL selects each function's default dtypes (f32 floats, i64 ids).
- * On success *out_data[i] (malloc'd, *out_nbytes[i] bytes) belong to the caller;
- * release everything with pcp_free.
+ * On success *out_data[i] (*out_nbytes[i] bytes of host memory) belong to the caller
+ * until pcp_free, which releases everything: outputs of 4 MiB and more are pinned
+ * buffers that pcp_free returns to a process-wide pool for later calls (up to 64 GiB
+ * kept), smaller ones are malloc'd. Inputs of 4 MiB and more are staged to the device
+ * through a pinned ring of the context, filled by up to 8 host threads.
  */
 int pcp_execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data,
                 const size_t* nbytes, const int64_t* const* shapes, const int* ranks,

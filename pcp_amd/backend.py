@@ -111,6 +111,33 @@ def execute_raw(handle, function_name: str, inputs_data: Sequence, input_shapes:
     """pcp_execute over host buffers; ``handle`` may be None to exercise argument
     checking without a device (the call then fails with PCP_ERR_INVALID_ARG after
     the checks pass)."""
+    m = marshal_inputs(inputs_data, input_shapes, input_dtypes)
+    n_out = ctypes.c_int(0)
+    out_data = ctypes.POINTER(ctypes.c_void_p)()
+    out_nbytes = ctypes.POINTER(ctypes.c_size_t)()
+    rc = lib().pcp_execute(handle, function_name.encode(), m.n, m.ptrs, m.nbytes, m.shapes, m.ranks, m.dtypes,
+                           ctypes.byref(n_out), ctypes.byref(out_data), ctypes.byref(out_nbytes))
+    check(rc, handle)
+    try:
+        return [ctypes.string_at(out_data[i], out_nbytes[i]) for i in range(n_out.value)]
+    finally:
+        lib().pcp_free(handle, n_out.value, out_data, out_nbytes)
+
+
+@dataclass
+class MarshalledInputs:
+    """pcp_execute's input arrays over borrowed host buffers (``keep`` holds them alive)."""
+    n: int
+    ptrs: object
+    nbytes: object
+    shapes: object
+    ranks: object
+    dtypes: object
+    keep: list
+
+
+def marshal_inputs(inputs_data: Sequence, input_shapes: Sequence[Sequence[int]],
+                   input_dtypes: Sequence[DType | int] | None) -> MarshalledInputs:
     n = len(inputs_data)
     if len(input_shapes) != n or (input_dtypes is not None and len(input_dtypes) != n):
         raise PcpError(-8, "inputs, shapes and dtypes differ in length")
@@ -131,13 +158,4 @@ def execute_raw(handle, function_name: str, inputs_data: Sequence, input_shapes:
     dts = None
     if input_dtypes is not None:
         dts = (ctypes.c_int * max(n, 1))(*[int(t) for t in input_dtypes])
-    n_out = ctypes.c_int(0)
-    out_data = ctypes.POINTER(ctypes.c_void_p)()
-    out_nbytes = ctypes.POINTER(ctypes.c_size_t)()
-    rc = lib().pcp_execute(handle, function_name.encode(), n, ptrs, nbytes, shapes, ranks, dts,
-                           ctypes.byref(n_out), ctypes.byref(out_data), ctypes.byref(out_nbytes))
-    check(rc, handle)
-    try:
-        return [ctypes.string_at(out_data[i], out_nbytes[i]) for i in range(n_out.value)]
-    finally:
-        lib().pcp_free(handle, n_out.value, out_data, out_nbytes)
+    return MarshalledInputs(n, ptrs, nbytes, shapes, ranks, dts, keep)

@@ -11,6 +11,10 @@
 
 #include "pcp_grpo.h"
 
+namespace pcp {
+struct HostStager;
+}
+
 struct pcp_ctx {
   int device = 0;
   int backend = PCP_BACKEND_ROCM;
@@ -26,6 +30,7 @@ struct pcp_ctx {
   bool prof_on = false;
   void* blas = nullptr;           // rocblas_handle, created on first LM-head backward
   int* h_count = nullptr;         // pinned host word: live-token count of the LM-head path
+  pcp::HostStager* stager = nullptr;  // pinned staging ring of the host-bytes path
 };
 
 namespace pcp {

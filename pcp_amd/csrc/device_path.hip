@@ -11,6 +11,7 @@
 #include <cstring>
 
 #include "context.hpp"
+#include "host_transfer.hpp"
 #include "grpo_device.hpp"
 #include "grpo_launch.hpp"
 #include "pcp_grpo.h"
@@ -349,6 +350,7 @@ void pcp_destroy(pcp_ctx* ctx) {
     release_blas(ctx);
     if (ctx->h_count) (void)hipHostFree(ctx->h_count);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    destroy_stager(ctx);
     if (ctx->d_err) (void)hipFree(ctx->d_err);
   }
   delete ctx;

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "context.hpp"
+#include "host_transfer.hpp"
 #include "pcp_grpo.h"
 
 namespace pcp {
@@ -124,7 +125,7 @@ struct DevArena {
     int rc = alloc(ctx, t.nbytes, out);
     if (rc != PCP_OK) return rc;
     if (t.nbytes == 0) return PCP_OK;
-    hipError_t e = hipMemcpy(*out, t.data, t.nbytes, hipMemcpyHostToDevice);
+    hipError_t e = upload_pageable(ctx, *out, t.data, t.nbytes, nullptr);
     return e == hipSuccess ? PCP_OK : hip_fail(ctx, e, "host-to-device copy");
   }
   int zeroed(pcp_ctx* ctx, size_t bytes, void** out) {
@@ -150,11 +151,11 @@ int download(pcp_ctx* ctx, const Outputs& o, int* n_out, void*** out_data, size_
     return fail(ctx, PCP_ERR_OOM, "allocating the output list");
   }
   for (int i = 0; i < n; ++i) {
-    od[i] = std::malloc(o.bytes[i] ? o.bytes[i] : 1);
+    od[i] = host_out_alloc(o.bytes[i]);
     ob[i] = o.bytes[i];
     hipError_t e = od[i] ? hipMemcpy(od[i], o.dev[i], o.bytes[i], hipMemcpyDeviceToHost) : hipErrorOutOfMemory;
     if (e != hipSuccess) {
-      for (int k = 0; k <= i; ++k) std::free(od[k]);
+      for (int k = 0; k <= i; ++k) host_out_free(od[k]);
       std::free(od);
       std::free(ob);
       return e == hipErrorOutOfMemory ? fail(ctx, PCP_ERR_OOM, "allocating output %d", i)
@@ -532,7 +533,7 @@ int pcp_execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data,
 void pcp_free(pcp_ctx* ctx, int n_out, void** out_data, size_t* out_nbytes) {
   (void)ctx;
   if (out_data) {
-    for (int i = 0; i < n_out; ++i) std::free(out_data[i]);
+    for (int i = 0; i < n_out; ++i) pcp::host_out_free(out_data[i]);
     std::free(out_data);
   }
   std::free(out_nbytes);

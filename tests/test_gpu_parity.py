@@ -339,6 +339,42 @@ def test_execute_clip_kl_and_logprob():
     be.deinit()
 
 
+def test_execute_large_inputs_staged_and_pinned_outputs():
+    """Inputs of 4 MiB and more go to the device through the context's pinned staging
+    ring (three 64 MiB slots: a 158 MB logits tensor spans it and the reference tensor
+    wraps it), outputs of 4 MiB and more come back in pooled pinned buffers. Two
+    successive host-bytes calls on fresh data each equal the device-pointer call on the
+    same data bit for bit (loss, dlogits, log-probs, advantages)."""
+    rng = np.random.default_rng(31)
+    S, T, V, G = 4, 130, 151936, 2
+    be = HipGrpoBackend.init()
+    for call in range(2):
+        print(f"host-bytes call {call}: [{S}, {T}, {V}] bf16", flush=True)
+        x = (rng.standard_normal((S, T, V)) * 3).astype(np.float32)
+        logits = orc.bf16_from_f32(x)
+        ref = orc.bf16_from_f32(x + (rng.standard_normal((S, T, V)) * 0.1).astype(np.float32))
+        del x
+        ids = rng.integers(0, V, (S, T)).astype(np.int64)
+        mask = (rng.random((S, T)) < 0.8).astype(np.float32)
+        old = (rng.standard_normal((S, T)) * 0.05 - 12).astype(np.float32)
+        rewards = rng.random(S).astype(np.float32)
+        hyper = np.array([G, 0.2, 0.04, 0], np.float32)
+        ins = [logits, ref, ids, mask, old, rewards, hyper]
+        outs = be.executeFunction(None, "grpo_clip_kl_fwd_bwd", ins, [a.shape for a in ins],
+                                  [DType.bf16, DType.bf16, DType.i64, DType.f32, DType.f32, DType.f32, DType.f32])
+        out = grpo.grpo_loss_fwd_bwd(dev(logits), dev(ids), dev(mask), rows=T - 1, tok_offset=1,
+                                     rewards=dev(rewards), group_size=G, ref_logits=dev(ref), old_logp=dev(old),
+                                     loss_mode=LossMode.GRPO_CLIP_KL, clip_eps=0.2, kl_beta=0.04)
+        torch.cuda.synchronize()
+        assert np.frombuffer(outs[0], np.float32)[0] == float(out.loss.cpu())
+        assert np.array_equal(np.frombuffer(outs[1], np.uint16).reshape(S, T, V), host_bits(out.dlogits))
+        assert np.array_equal(np.frombuffer(outs[2], np.float32).reshape(S, T)[:, 1:],
+                              out.logp.cpu().numpy()[:, 1:])
+        assert np.array_equal(np.frombuffer(outs[4], np.float32), out.advantages.cpu().numpy())
+        del outs, out
+    be.deinit()
+
+
 # ---- device error reporting ---------------------------------------------------------------
 
 def test_device_errors_are_reported_and_cleared():
