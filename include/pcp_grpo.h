@@ -213,7 +213,11 @@ int pcp_sync(pcp_ctx* ctx);
  * until pcp_free, which releases everything: outputs of 4 MiB and more are pinned
  * buffers that pcp_free returns to a process-wide pool for later calls (up to 64 GiB
  * kept), smaller ones are malloc'd. Inputs of 4 MiB and more are staged to the device
- * through a pinned ring of the context, filled by up to 8 host threads.
+ * through a pinned ring of the context, filled by up to 8 host threads. The loss
+ * functions on logits of two groups or more (PCP_EXECUTE_GROUP_MIB of policy logits
+ * per group, default 1024) run group by group, with the upload of later groups, the
+ * kernels and the download of earlier groups' dlogits overlapping; the results are
+ * those of one call.
  */
 int pcp_execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data,
                 const size_t* nbytes, const int64_t* const* shapes, const int* ranks,

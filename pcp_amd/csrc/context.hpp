@@ -31,6 +31,7 @@ struct pcp_ctx {
   void* blas = nullptr;           // rocblas_handle, created on first LM-head backward
   int* h_count = nullptr;         // pinned host word: live-token count of the LM-head path
   pcp::HostStager* stager = nullptr;  // pinned staging ring of the host-bytes path
+  hipStream_t xs[3] = {};         // host-bytes path: upload, compute and download streams
 };
 
 namespace pcp {

@@ -351,6 +351,8 @@ void pcp_destroy(pcp_ctx* ctx) {
     if (ctx->h_count) (void)hipHostFree(ctx->h_count);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     destroy_stager(ctx);
+    for (hipStream_t x : ctx->xs)
+      if (x) (void)hipStreamDestroy(x);
     if (ctx->d_err) (void)hipFree(ctx->d_err);
   }
   delete ctx;

@@ -10,11 +10,13 @@
 
 #include <cstdint>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
 
 #include "context.hpp"
+#include "grpo_launch.hpp"
 #include "host_transfer.hpp"
 #include "pcp_grpo.h"
 
@@ -139,9 +141,13 @@ struct DevArena {
 struct Outputs {
   std::vector<void*> dev;
   std::vector<size_t> bytes;
+  std::vector<void*> host;   // optional: outputs already copied into their host buffer
+  ~Outputs() {
+    for (void* h : host) host_out_free(h);   // still owned here: not handed to the caller
+  }
 };
 
-int download(pcp_ctx* ctx, const Outputs& o, int* n_out, void*** out_data, size_t** out_nbytes) {
+int download(pcp_ctx* ctx, Outputs& o, int* n_out, void*** out_data, size_t** out_nbytes) {
   const int n = static_cast<int>(o.dev.size());
   void** od = static_cast<void**>(std::calloc(n, sizeof(void*)));
   size_t* ob = static_cast<size_t*>(std::calloc(n, sizeof(size_t)));
@@ -151,11 +157,15 @@ int download(pcp_ctx* ctx, const Outputs& o, int* n_out, void*** out_data, size_
     return fail(ctx, PCP_ERR_OOM, "allocating the output list");
   }
   for (int i = 0; i < n; ++i) {
-    od[i] = host_out_alloc(o.bytes[i]);
+    void* pre = i < static_cast<int>(o.host.size()) ? o.host[i] : nullptr;
+    od[i] = pre ? pre : host_out_alloc(o.bytes[i]);
     ob[i] = o.bytes[i];
-    hipError_t e = od[i] ? hipMemcpy(od[i], o.dev[i], o.bytes[i], hipMemcpyDeviceToHost) : hipErrorOutOfMemory;
+    hipError_t e = pre ? hipSuccess
+                 : od[i] ? hipMemcpy(od[i], o.dev[i], o.bytes[i], hipMemcpyDeviceToHost)
+                         : hipErrorOutOfMemory;
     if (e != hipSuccess) {
-      for (int k = 0; k <= i; ++k) host_out_free(od[k]);
+      for (int k = 0; k <= i; ++k)
+        if (!(k < static_cast<int>(o.host.size()) && o.host[k])) host_out_free(od[k]);   // others: o's
       std::free(od);
       std::free(ob);
       return e == hipErrorOutOfMemory ? fail(ctx, PCP_ERR_OOM, "allocating output %d", i)
@@ -165,7 +175,127 @@ int download(pcp_ctx* ctx, const Outputs& o, int* n_out, void*** out_data, size_
   *n_out = n;
   *out_data = od;
   *out_nbytes = ob;
+  o.host.clear();   // the caller owns them now
   return PCP_OK;
+}
+
+// ---- the loss functions over sequence groups ---------------------------------
+// A host-bytes loss call on large logits is moved and computed in groups of whole
+// sequences: the upload stream stages group k's policy (and reference) rows while the
+// compute stream runs the loss head on earlier groups and the download stream copies
+// their dlogits into the pinned output, so both PCIe directions carry data at once.
+// The advantages are computed once over all sequences before the groups, and the
+// sequence lengths and the loss reduction once over all token losses after them, with
+// the same kernels and arguments as one call over every sequence: every output is
+// bit-identical to it.
+// Policy-logit bytes per group: PCP_EXECUTE_GROUP_MIB (MiB, default 1024). Calls with
+// fewer than two groups' worth of logits run as one call.
+size_t group_bytes() {
+  const char* v = std::getenv("PCP_EXECUTE_GROUP_MIB");
+  const long long mib = v ? std::atoll(v) : 0;
+  return (mib > 0 && mib < (1LL << 30) ? static_cast<size_t>(mib) : size_t{1024}) << 20;
+}
+
+int64_t seqs_per_group(size_t seq_bytes, size_t gbytes) {
+  return std::max<int64_t>(1, static_cast<int64_t>(gbytes / std::max<size_t>(seq_bytes, 1)));
+}
+
+int ensure_xs(pcp_ctx* ctx) {
+  for (hipStream_t& x : ctx->xs) {
+    if (x) continue;
+    const hipError_t e = hipStreamCreateWithFlags(&x, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      x = nullptr;
+      return hip_fail(ctx, e, "hipStreamCreateWithFlags");
+    }
+  }
+  return PCP_OK;
+}
+
+// Waits for the call's streams and releases its events on every exit path, before
+// the device buffers they use are freed.
+struct GroupDrain {
+  pcp_ctx* ctx;
+  std::vector<hipEvent_t> ev;
+  ~GroupDrain() {
+    for (hipStream_t x : ctx->xs)
+      if (x) (void)hipStreamSynchronize(x);
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+  }
+  hipError_t mark(hipStream_t after, hipStream_t waiter) {
+    hipEvent_t e = nullptr;
+    hipError_t r = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+    if (r != hipSuccess) return r;
+    ev.push_back(e);
+    if ((r = hipEventRecord(e, after)) != hipSuccess) return r;
+    return hipStreamWaitEvent(waiter, e, 0);
+  }
+};
+
+// full: the call over all S sequences with every device buffer allocated and the
+// small inputs uploaded; its logits / ref_logits / dlogits are filled or drained here.
+// tl, slen, sscale, sval: device f32 [S*T], [S], [S], [S]. host_dl: the dlogits output.
+int run_loss_groups(pcp_ctx* ctx, const pcp_grpo_args& full, const In& L, const In* R, int64_t S, int64_t T,
+                    int64_t gs, float* tl, float* slen, float* sscale, float* sval, void* host_dl) {
+  int rc = ensure_xs(ctx);
+  if (rc != PCP_OK) return rc;
+  hipError_t e = hipDeviceSynchronize();   // allocations, clears and small uploads of the call
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipDeviceSynchronize");
+  const hipStream_t up = ctx->xs[0], run = ctx->xs[1], down = ctx->xs[2];
+  GroupDrain drain{ctx, {}};
+  const size_t seq_bytes = L.nbytes / static_cast<size_t>(S);
+  const float gtot = full.loss_norm > 0.f ? full.loss_norm : static_cast<float>(S);
+  const size_t id_b = dtype_bytes(full.ids_dtype), m_b = full.mask_dtype == PCP_BOOL ? 1 : 4;
+  const float* adv = full.advantages ? full.advantages : full.advantages_out;
+  if (!full.advantages) {
+    e = launch_advantages(full.rewards, S, full.group_size, full.std_eps, full.advantages_out, run);
+    if (e != hipSuccess) return hip_fail(ctx, e, "advantages launch");
+  }
+  for (int64_t s0 = 0; s0 < S; s0 += gs) {
+    const int64_t n = std::min(gs, S - s0);
+    const size_t off = static_cast<size_t>(s0) * seq_bytes, len = static_cast<size_t>(n) * seq_bytes;
+    e = upload_pageable(ctx, static_cast<char*>(const_cast<void*>(full.logits)) + off,
+                        static_cast<const char*>(L.data) + off, len, up);
+    if (e == hipSuccess && R)
+      e = upload_pageable(ctx, static_cast<char*>(const_cast<void*>(full.ref_logits)) + off,
+                          static_cast<const char*>(R->data) + off, len, up);
+    if (e == hipSuccess) e = drain.mark(up, run);
+    if (e != hipSuccess) return hip_fail(ctx, e, "host-to-device copy");
+    pcp_grpo_args g = full;
+    const int64_t t0 = s0 * T;
+    g.n_seq = n;
+    g.logits = static_cast<const char*>(full.logits) + off;
+    g.ref_logits = full.ref_logits ? static_cast<const char*>(full.ref_logits) + off : nullptr;
+    g.dlogits = static_cast<char*>(full.dlogits) + off;
+    g.ids = static_cast<const char*>(full.ids) + t0 * id_b;
+    g.mask = static_cast<const char*>(full.mask) + t0 * m_b;
+    g.old_logp = full.old_logp ? full.old_logp + t0 : nullptr;
+    g.advantages = adv + s0;
+    g.rewards = nullptr;
+    g.logp = full.logp ? full.logp + t0 : nullptr;
+    g.ref_logp = full.ref_logp ? full.ref_logp + t0 : nullptr;
+    g.token_loss = tl + t0;
+    g.advantages_out = nullptr;
+    g.loss = nullptr;
+    g.loss_norm = gtot;
+    g.flags = PCP_FLAG_ASYNC;
+    g.stream = run;
+    if ((rc = pcp_grpo_loss_fwd_bwd(ctx, &g)) != PCP_OK) return rc;
+    e = drain.mark(run, down);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(static_cast<char*>(host_dl) + off, static_cast<char*>(full.dlogits) + off, len,
+                         hipMemcpyDeviceToHost, down);
+    if (e != hipSuccess) return hip_fail(ctx, e, "device-to-host copy");
+  }
+  e = launch_seq_prep(full.mask, full.mask_dtype == PCP_BOOL, S, full.rows, T, full.tok_offset, gtot, slen, sscale,
+                      run);
+  if (e == hipSuccess)
+    e = launch_loss_reduce(tl, S, full.rows, T, full.tok_offset, slen, adv, full.loss_mode == PCP_LOSS_REINFORCE,
+                           gtot, sval, full.loss, run);
+  if (e != hipSuccess) return hip_fail(ctx, e, "loss reduction launch");
+  if ((rc = pcp_sync(ctx)) != PCP_OK) return rc;   // the compute stream and the device error word
+  e = hipStreamSynchronize(down);
+  return e == hipSuccess ? PCP_OK : hip_fail(ctx, e, "device-to-host copy");
 }
 
 // ---- functions ------------------------------------------------------------
@@ -444,10 +574,13 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
     a.dlogits_dtype = L.dtype;
     a.ids_dtype = ids.dtype;
     void* p;
-    if ((rc = arena.upload(ctx, L, &p))) return rc;
+    const size_t gbytes = group_bytes();
+    const int64_t gs = seqs_per_group(L.nbytes / S, gbytes);
+    const bool grouped = f != kLogprob && L.nbytes >= 2 * gbytes && gs < S;
+    if ((rc = grouped ? arena.alloc(ctx, L.nbytes, &p) : arena.upload(ctx, L, &p))) return rc;
     a.logits = p;
     if (has_ref) {
-      if ((rc = arena.upload(ctx, in[1], &p))) return rc;
+      if ((rc = grouped ? arena.alloc(ctx, in[1].nbytes, &p) : arena.upload(ctx, in[1], &p))) return rc;
       a.ref_logits = p;
     }
     if ((rc = arena.upload(ctx, ids, &p))) return rc;
@@ -507,7 +640,21 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
       outs.dev.push_back(p);
       outs.bytes.push_back(sizeof(float) * S);
     }
-    if ((rc = pcp_grpo_loss_fwd_bwd(ctx, &a))) return rc;
+    if (grouped) {
+      void *tl, *slen, *sscale, *sval;
+      if ((rc = arena.alloc(ctx, tok_bytes, &tl)) || (rc = arena.alloc(ctx, sizeof(float) * S, &slen)) ||
+          (rc = arena.alloc(ctx, sizeof(float) * S, &sscale)) || (rc = arena.alloc(ctx, sizeof(float) * S, &sval)))
+        return rc;
+      outs.host.assign(outs.dev.size(), nullptr);
+      outs.host[1] = host_out_alloc(L.nbytes);   // dlogits, filled group by group
+      if (!outs.host[1]) return fail(ctx, PCP_ERR_OOM, "allocating the dlogits output");
+      if ((rc = run_loss_groups(ctx, a, L, has_ref ? &in[1] : nullptr, S, T, gs, static_cast<float*>(tl),
+                                static_cast<float*>(slen), static_cast<float*>(sscale), static_cast<float*>(sval),
+                                outs.host[1])))
+        return rc;
+    } else if ((rc = pcp_grpo_loss_fwd_bwd(ctx, &a))) {
+      return rc;
+    }
     return download(ctx, outs, n_out, out_data, out_nbytes);
   }
 

@@ -339,17 +339,22 @@ def test_execute_clip_kl_and_logprob():
     be.deinit()
 
 
-def test_execute_large_inputs_staged_and_pinned_outputs():
+@pytest.mark.parametrize("group_mib", [None, 48])
+def test_execute_large_inputs_staged_and_pinned_outputs(group_mib, monkeypatch):
     """Inputs of 4 MiB and more go to the device through the context's pinned staging
     ring (three 64 MiB slots: a 158 MB logits tensor spans it and the reference tensor
-    wraps it), outputs of 4 MiB and more come back in pooled pinned buffers. Two
-    successive host-bytes calls on fresh data each equal the device-pointer call on the
-    same data bit for bit (loss, dlogits, log-probs, advantages)."""
+    wraps it), outputs of 4 MiB and more come back in pooled pinned buffers. With
+    PCP_EXECUTE_GROUP_MIB=48 the loss runs over groups of one sequence (40 MB of
+    logits), uploads, kernels and downloads overlapping on three streams. Two successive
+    host-bytes calls on fresh data each equal the device-pointer call on the same data
+    bit for bit (loss, dlogits, log-probs, advantages)."""
+    if group_mib:
+        monkeypatch.setenv("PCP_EXECUTE_GROUP_MIB", str(group_mib))
     rng = np.random.default_rng(31)
     S, T, V, G = 4, 130, 151936, 2
     be = HipGrpoBackend.init()
     for call in range(2):
-        print(f"host-bytes call {call}: [{S}, {T}, {V}] bf16", flush=True)
+        print(f"host-bytes call {call}: [{S}, {T}, {V}] bf16, group MiB {group_mib}", flush=True)
         x = (rng.standard_normal((S, T, V)) * 3).astype(np.float32)
         logits = orc.bf16_from_f32(x)
         ref = orc.bf16_from_f32(x + (rng.standard_normal((S, T, V)) * 0.1).astype(np.float32))
