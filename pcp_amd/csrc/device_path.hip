@@ -105,6 +105,14 @@ int validate(const pcp_grpo_args* a, Op op, Geo* g) {
     return fail(nullptr, PCP_ERR_DTYPE, "mask dtype must be f32 or bool (got %d)", a->mask_dtype);
   if (!a->logits) return fail(nullptr, PCP_ERR_INVALID_ARG, "logits is NULL");
   if (!a->ids && g->rows > 0) return fail(nullptr, PCP_ERR_INVALID_ARG, "ids is NULL");
+  {
+    // Rows may start anywhere, but each element on its own size.
+    const uintptr_t m = static_cast<uintptr_t>(dtype_bytes(a->logits_dtype)) - 1;
+    const uintptr_t md = a->dlogits && op == kLoss ? static_cast<uintptr_t>(dtype_bytes(a->dlogits_dtype)) - 1 : 0;
+    if ((reinterpret_cast<uintptr_t>(a->logits) & m) || (reinterpret_cast<uintptr_t>(a->ref_logits) & m) ||
+        (op == kLoss && (reinterpret_cast<uintptr_t>(a->dlogits) & md)))
+      return fail(nullptr, PCP_ERR_INVALID_ARG, "logits / ref_logits / dlogits must be aligned to their element size");
+  }
   if (op == kLoss) {
     if (a->dlogits) {
       if (a->dlogits_dtype != a->logits_dtype && a->dlogits_dtype != PCP_F32)

@@ -326,6 +326,39 @@ __device__ __forceinline__ float vec_max(float m, const u32x4& v) {
   return m;
 }
 
+// A row of the forward kernel: its 16-byte-aligned interior of nv vectors, and the
+// head (before it) and tail (after it) of fewer than EPV elements each.
+struct RowSpan {
+  const void* vec;
+  int head, nv, tail;
+};
+
+template <typename TI>
+__device__ __forceinline__ RowSpan row_span(const void* p, int64_t vocab) {
+  constexpr int EPV = 16 / TI::kBytes;
+  RowSpan s;
+  const int mis = static_cast<int>(reinterpret_cast<uintptr_t>(p) & 15u);
+  s.head = static_cast<int>(min<int64_t>(((16 - mis) & 15) / TI::kBytes, vocab));
+  s.nv = static_cast<int>((vocab - s.head) / EPV);
+  s.tail = static_cast<int>(vocab - s.head - static_cast<int64_t>(s.nv) * EPV);
+  s.vec = static_cast<const char*>(p) + s.head * TI::kBytes;
+  return s;
+}
+
+// Thread tid's head or tail element of the row as a one-element online state (m, s):
+// threads [0, head) take the head, [head, head + tail) the tail, the rest nothing.
+template <typename TI>
+__device__ __forceinline__ void edge_state(const void* p, const RowSpan& sp, int tid, float& m, float& s) {
+  constexpr int EPV = 16 / TI::kBytes;
+  const int k = tid < sp.head ? tid : (tid - sp.head < sp.tail ? sp.head + sp.nv * EPV + (tid - sp.head) : -1);
+  m = kNegInf;
+  s = 0.f;
+  if (k < 0) return;
+  const float x = TI::load1(p, k) * kLog2e;
+  m = fmaxf(m, x);
+  s = hw_exp2(x - ms_ref(m));
+}
+
 template <typename TI, int BLOCK, int U, bool REF>
 __global__ void __launch_bounds__(BLOCK) grpo_fwd_kernel(RowArgs a) {
   constexpr int EPV = 16 / TI::kBytes;
@@ -338,17 +371,23 @@ __global__ void __launch_bounds__(BLOCK) grpo_fwd_kernel(RowArgs a) {
     write_token_outputs(a, r, 0.f, 0.f, 0.f);
     return;
   }
-  const int nv = static_cast<int>(a.vocab / EPV);
   const int64_t row_elem = row * a.vocab;
-  const uint32_t in_bytes = static_cast<uint32_t>(a.vocab) * TI::kBytes;
   const void* xrow = static_cast<const char*>(a.logits) + row_elem * TI::kBytes;
   const void* rrow = REF ? static_cast<const char*>(a.ref_logits) + row_elem * TI::kBytes : nullptr;
   const float xy = TI::load1(xrow, r.id);
   const float ry = REF ? TI::load1(rrow, r.id) : 0.f;
-  const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xrow, in_bytes);
-  const __amdgpu_buffer_rsrc_t rbuf = REF ? row_rsrc(rrow, in_bytes) : xbuf;
+  // Rows may start off 16 bytes (V * element size not a multiple of 16, or an offset
+  // view): the aligned interior goes through the descriptor as 16-byte vectors, the
+  // head and tail element by element, so no load leaves the row.
+  const RowSpan xsp = row_span<TI>(xrow, a.vocab);
+  const RowSpan rsp = REF ? row_span<TI>(rrow, a.vocab) : xsp;
+  const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xsp.vec, static_cast<uint32_t>(xsp.nv) * 16u);
+  const __amdgpu_buffer_rsrc_t rbuf = REF ? row_rsrc(rsp.vec, static_cast<uint32_t>(rsp.nv) * 16u) : xbuf;
+  const int nv = REF ? max(xsp.nv, rsp.nv) : xsp.nv;
 
-  float pm = kNegInf, ps = 0.f, rm = kNegInf, rs = 0.f;
+  float pm, ps, rm = kNegInf, rs = 0.f;
+  edge_state<TI>(xrow, xsp, tid, pm, ps);
+  if constexpr (REF) edge_state<TI>(rrow, rsp, tid, rm, rs);
   for (int base = 0; base < nv; base += BLOCK * U) {
     const uint32_t off = static_cast<uint32_t>(base + tid) * 16u;
     u32x4 xb[U], rb[U];
@@ -361,10 +400,9 @@ __global__ void __launch_bounds__(BLOCK) grpo_fwd_kernel(RowArgs a) {
     float bx = kNegInf, br = kNegInf;
 #pragma unroll
     for (int q = 0; q < U; ++q) {
-      if (base + q * BLOCK + tid < nv) {
-        bx = vec_max<TI>(bx, xb[q]);
-        if constexpr (REF) br = vec_max<TI>(br, rb[q]);
-      }
+      if (base + q * BLOCK + tid < xsp.nv) bx = vec_max<TI>(bx, xb[q]);
+      if constexpr (REF)
+        if (base + q * BLOCK + tid < rsp.nv) br = vec_max<TI>(br, rb[q]);
     }
     {
       const float nm = fmaxf(pm, bx * kLog2e);
@@ -372,7 +410,7 @@ __global__ void __launch_bounds__(BLOCK) grpo_fwd_kernel(RowArgs a) {
       float acc = ms_rescale(ps, pm, nm);
 #pragma unroll
       for (int q = 0; q < U; ++q)
-        if (base + q * BLOCK + tid < nv) {
+        if (base + q * BLOCK + tid < xsp.nv) {
           const uint32_t* w = reinterpret_cast<const uint32_t*>(&xb[q]);
 #pragma unroll
           for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -ref));
@@ -386,7 +424,7 @@ __global__ void __launch_bounds__(BLOCK) grpo_fwd_kernel(RowArgs a) {
       float acc = ms_rescale(rs, rm, nm);
 #pragma unroll
       for (int q = 0; q < U; ++q)
-        if (base + q * BLOCK + tid < nv) {
+        if (base + q * BLOCK + tid < rsp.nv) {
           const uint32_t* w = reinterpret_cast<const uint32_t*>(&rb[q]);
 #pragma unroll
           for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -ref));
@@ -756,15 +794,16 @@ RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool forward_only
   p.cfg = -1;
   p.block = 1024;
   p.nch = 0;
-  if (!vec || force_stream) return p;
-  // The forward kernel addresses a row through a 32-bit buffer offset that runs up to
-  // one batch past the row end: rows up to 2 GiB take it, longer rows stream (64-bit
-  // addressing).
+  if (force_stream) return p;
+  // The forward kernel takes rows of any alignment. It addresses a row through a
+  // 32-bit buffer offset that runs up to one batch past the row end: rows up to 2 GiB
+  // take it, longer rows stream (64-bit addressing).
   if (forward_only && vocab * in_bytes <= (int64_t{1} << 31)) {
     p.kind = RowPlan::kForward;
     p.block = PCP_FWD_BLOCK;
     return p;
   }
+  if (!vec) return p;
   const int64_t nv = vocab / epv;
   for (int i = 0; i < static_cast<int>(sizeof(kResCfgs) / sizeof(kResCfgs[0])); ++i) {
     if (static_cast<int64_t>(kResCfgs[i].block) * kResCfgs[i].nch >= nv) {

@@ -108,6 +108,10 @@ def _valid_args():
     (lambda a: (setattr(a, "mask", 0x10), setattr(a, "mask_dtype", int(DType.i64))), -2, "mask dtype"),
     (lambda a: setattr(a, "logits", None), -1, "logits is NULL"),
     (lambda a: setattr(a, "ids", None), -1, "ids is NULL"),
+    (lambda a: setattr(a, "logits", 0x1001), -1, "element size"),
+    (lambda a: (setattr(a, "logits_dtype", int(DType.f32)), setattr(a, "logits", 0x1002)), -1, "element size"),
+    (lambda a: (setattr(a, "ref_logits", 0x4001), setattr(a, "loss_mode", 1)), -1, "element size"),
+    (lambda a: (setattr(a, "dlogits", 0x5002), setattr(a, "dlogits_dtype", int(DType.f32))), -1, "element size"),
     (lambda a: setattr(a, "loss_mode", 7), -1, "loss_mode"),
     (lambda a: setattr(a, "loss_mode", 1), -1, "ref_logits"),
     (lambda a: setattr(a, "advantages", None), -1, "both NULL"),

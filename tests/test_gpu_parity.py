@@ -243,15 +243,19 @@ def _fwd_logits(rng, n, V, dtype, neg_inf):
     return x, x.astype(np.float64)
 
 
-@pytest.mark.parametrize("dtype,V", [("bf16", 8), ("bf16", 136), ("bf16", 16408), ("bf16", 151936),
-                                     ("f16", 24), ("f16", 32776), ("f32", 4), ("f32", 8196), ("f32", 50000)])
+@pytest.mark.parametrize("dtype,V,lead", [("bf16", 8, 0), ("bf16", 136, 0), ("bf16", 16408, 0), ("bf16", 151936, 0),
+                                          ("f16", 24, 0), ("f16", 32776, 0), ("f32", 4, 0), ("f32", 8196, 0),
+                                          ("f32", 50000, 0), ("bf16", 3, 0), ("bf16", 50257, 0), ("bf16", 151936, 5),
+                                          ("f16", 130, 3), ("f32", 1027, 1), ("f32", 7, 3)])
 @pytest.mark.parametrize("with_ref", [False, True])
-def test_logprob_fwd_kernel_shapes(dtype, V, with_ref):
-    """The forward-only kernel (V a multiple of the 16-byte vector, aligned rows) over
-    one-vector rows, a ragged last batch, multi-batch rows and the config-2 width, with
-    -inf vocabulary entries: log-probs within 1e-5 * max(1, |lse|) of the float64 oracle,
-    the streaming kernel within 2e-5 * max(1, |lse|), masked and ignored tokens 0."""
-    rng = np.random.default_rng(V * 3 + with_ref)
+def test_logprob_fwd_kernel_shapes(dtype, V, lead, with_ref):
+    """The forward-only kernel over one-vector rows, a ragged last batch, multi-batch
+    rows and the config-2 width, and rows off 16 bytes: V not a multiple of the 16-byte
+    vector (every row starts at a different offset) and logits viewed `lead` elements
+    into their allocation (so even row 0 has a head). -inf vocabulary entries included.
+    Log-probs within 1e-5 * max(1, |lse|) of the float64 oracle, the streaming kernel
+    within 2e-5 * max(1, |lse|), masked and ignored tokens 0."""
+    rng = np.random.default_rng(V * 3 + with_ref + 7 * lead)
     S, T = 3, 5
     n = S * T
     x, x64 = _fwd_logits(rng, n, V, dtype, neg_inf=True)
@@ -262,9 +266,14 @@ def test_logprob_fwd_kernel_shapes(dtype, V, with_ref):
     ids[1, 2] = -100
     mask = np.ones((S, T), np.float32)
     mask[0, 4] = 0.0
-    print(f"forward kernel {dtype} V={V} ref={with_ref}", flush=True)
+    print(f"forward kernel {dtype} V={V} lead={lead} ref={with_ref}", flush=True)
     sh = (S, T, V)
-    lt, rt = dev(x.reshape(sh)), dev(r.reshape(sh))
+
+    def placed(a):
+        flat = dev(np.concatenate([a.reshape(-1)[:lead] if lead else a.reshape(-1)[:0], a.reshape(-1)]))
+        return flat[lead:].view(sh)
+
+    lt, rt = placed(x), placed(r)
     args = dict(mask=dev(mask))
     lp, lr = grpo.logprob_fwd(lt, dev(ids), rt if with_ref else None, **args)
     lps, lrs = grpo.logprob_fwd(lt, dev(ids), rt if with_ref else None, force_streaming=True, **args)
