@@ -59,14 +59,56 @@ __device__ __forceinline__ void flag_nonfinite(const RowArgs& a, float lse, floa
     atomicOr(a.err, kErrNonFinite);
 }
 
+// A row that may start off 16 bytes: its 16-byte-aligned interior of nv vectors, and
+// the head (before it) and tail (after it) of fewer than EPV elements each.
+struct RowSpan {
+  const void* vec;
+  int head, nv, tail;
+};
+
+template <typename TI>
+__device__ __forceinline__ RowSpan row_span(const void* p, int64_t vocab) {
+  constexpr int EPV = 16 / TI::kBytes;
+  RowSpan s;
+  const int mis = static_cast<int>(reinterpret_cast<uintptr_t>(p) & 15u);
+  s.head = static_cast<int>(min<int64_t>(((16 - mis) & 15) / TI::kBytes, vocab));
+  s.nv = static_cast<int>((vocab - s.head) / EPV);
+  s.tail = static_cast<int>(vocab - s.head - static_cast<int64_t>(s.nv) * EPV);
+  s.vec = static_cast<const char*>(p) + s.head * TI::kBytes;
+  return s;
+}
+
+// The head or tail element that thread tid handles: threads [0, head) take the head,
+// [head, head + tail) the tail; -1 for the rest.
+template <typename TI>
+__device__ __forceinline__ int edge_index(const RowSpan& sp, int tid) {
+  constexpr int EPV = 16 / TI::kBytes;
+  return tid < sp.head ? tid : (tid - sp.head < sp.tail ? sp.head + sp.nv * EPV + (tid - sp.head) : -1);
+}
+
+// Thread tid's head or tail element of the row as a one-element online state (m, s).
+template <typename TI>
+__device__ __forceinline__ void edge_state(const void* p, const RowSpan& sp, int tid, float& m, float& s) {
+  const int k = edge_index<TI>(sp, tid);
+  m = kNegInf;
+  s = 0.f;
+  if (k < 0) return;
+  const float x = TI::load1(p, k) * kLog2e;
+  m = fmaxf(m, x);
+  s = hw_exp2(x - ms_ref(m));
+}
+
 // ---------------------------------------------------------------------------
 // Register-resident fused forward+backward.
 //   TI/TO: input / output codecs; BLOCK lanes; NCH 16-byte chunks per lane
 //   (row capacity BLOCK*NCH*16 bytes); RB reference chunks per batch.
-// Requirements (checked on the host): V % EPV == 0, 16-byte aligned rows,
-// V <= BLOCK*NCH*EPV. dlogits == nullptr: forward only (log-probs).
+// Requirements (checked on the host): V <= BLOCK*NCH*EPV; without EDGE, V % EPV == 0
+// and 16-byte aligned rows. EDGE: rows may start off 16 bytes, and dlogits rows have
+// the logits rows' element type and offset mod 16: the aligned interior is held and
+// stored as vectors, the head and tail (under EPV elements each) by threads 0..13 one
+// element each. dlogits == nullptr: forward only (log-probs).
 // ---------------------------------------------------------------------------
-template <typename TI, typename TO, int BLOCK, int NCH, int RB>
+template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE>
 __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row, float* lds) {
   constexpr int EPV = 16 / TI::kBytes;
   constexpr uint32_t kChunkBytes = BLOCK * 16;          // one chunk: 16 bytes per lane
@@ -77,11 +119,15 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   constexpr int kPrefetch = PCP_RES_PREFETCH;   // reference batches in flight ahead of the math
   const int tid = threadIdx.x;
   const RowMeta r = row_meta(a, row);
-  const int nv = static_cast<int>(a.vocab / EPV);
   const int64_t row_elem = row * a.vocab;
-  const uint32_t in_bytes = static_cast<uint32_t>(a.vocab) * TI::kBytes;
-  const uint32_t out_bytes = static_cast<uint32_t>(a.vocab) * TO::kBytes;
-  const __amdgpu_buffer_rsrc_t drow = row_rsrc(static_cast<char*>(a.dlogits) + row_elem * TO::kBytes, out_bytes);
+  const void* xrow = static_cast<const char*>(a.logits) + row_elem * TI::kBytes;
+  const RowSpan xsp = EDGE ? row_span<TI>(xrow, a.vocab) : RowSpan{xrow, 0, static_cast<int>(a.vocab / EPV), 0};
+  const int nv = xsp.nv;
+  const int ek = EDGE ? edge_index<TI>(xsp, tid) : -1;   // this thread's head / tail element
+  const uint32_t in_bytes = static_cast<uint32_t>(nv) * 16u;
+  const uint32_t out_bytes = static_cast<uint32_t>(nv) * kOutVec;
+  const __amdgpu_buffer_rsrc_t drow =
+      row_rsrc(static_cast<char*>(a.dlogits) + (row_elem + xsp.head) * TO::kBytes, out_bytes);
 
   if (!r.live) {
     write_token_outputs(a, r, 0.f, 0.f, 0.f);
@@ -91,11 +137,11 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
       for (int j = 0; j < EPV; ++j) z[j] = 0.f;
 #pragma unroll
       for (int k = 0; k < NCH; ++k) buf_store_vals<TO, EPV, true>(drow, (k * BLOCK + tid) * kOutVec, z);
+      if (EDGE && ek >= 0) store1<TO>(a.dlogits, row_elem + ek, 0.f);
     }
     return;
   }
 
-  const void* xrow = static_cast<const char*>(a.logits) + row_elem * TI::kBytes;
   const bool has_ref = a.ref_logits != nullptr;
   const void* rrow =
       has_ref ? static_cast<const char*>(a.ref_logits) + row_elem * TI::kBytes : nullptr;
@@ -106,11 +152,12 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
 
   // 1. Policy row -> registers: all NCH loads back to back through one row
   //    descriptor (lanes past the row end read 0 and are skipped below).
-  const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xrow, in_bytes);
+  const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xsp.vec, in_bytes);
   const uint32_t voff = tid * 16u;
   u32x4 xv[NCH];
 #pragma unroll
   for (int k = 0; k < NCH; ++k) xv[k] = buf_ld16<true>(xbuf, fresh_off(voff, k * kChunkBytes));
+  const float xe = (EDGE && ek >= 0) ? TI::load1(xrow, ek) : kNegInf;
 
   // 2. Per-lane (max, sum) of the resident policy values and online (max, sum) of
   //    the reference row, streamed in batches of RB chunks PD batches ahead. The
@@ -121,7 +168,10 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   //    absolute below the f16 normal range), and dlogits become a multiple of them.
   constexpr int NB = (NCH + RB - 1) / RB;
   constexpr int PD = kPrefetch;
-  const __amdgpu_buffer_rsrc_t rbuf = has_ref ? row_rsrc(rrow, in_bytes) : xbuf;
+  // The reference row's own split (its offset may differ from the policy row's).
+  const RowSpan rsp = (EDGE && has_ref) ? row_span<TI>(rrow, a.vocab) : RowSpan{rrow, 0, nv, 0};
+  const int nvr = rsp.nv;
+  const __amdgpu_buffer_rsrc_t rbuf = has_ref ? row_rsrc(rsp.vec, static_cast<uint32_t>(nvr) * 16u) : xbuf;
   u32x4 rv[PD + 1][RB];
   if (has_ref) {
 #pragma unroll
@@ -151,10 +201,12 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
         }
       }
     }
+    if constexpr (EDGE) mx = fmaxf(mx, xe);
     pm = mx * kLog2e;
   }
   const float m2 = ms_ref(pm);   // this lane's shift (kept for the cached terms)
   float ps = 0.f, rm = kNegInf, rs = 0.f;
+  if (EDGE && has_ref) edge_state<TI>(rrow, rsp, tid, rm, rs);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
@@ -194,7 +246,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
       float bm = kNegInf;
 #pragma unroll
       for (int q = 0; q < RB; ++q) {
-        if (kb + q < NCH && (kb + q) * BLOCK + tid < nv) {
+        if (kb + q < NCH && (kb + q) * BLOCK + tid < nvr) {
           const uint32_t* w = reinterpret_cast<const uint32_t*>(&cur[q]);
 #pragma unroll
           for (int j = 0; j < EPV; ++j) bm = fmaxf(bm, TI::unpack(w, j));
@@ -205,7 +257,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
       float acc = ms_rescale(rs, rm, nm);
 #pragma unroll
       for (int q = 0; q < RB; ++q) {
-        if (kb + q < NCH && (kb + q) * BLOCK + tid < nv) {
+        if (kb + q < NCH && (kb + q) * BLOCK + tid < nvr) {
           const uint32_t* w = reinterpret_cast<const uint32_t*>(&cur[q]);
 #pragma unroll
           for (int j = 0; j < EPV; ++j) acc += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -ref));
@@ -215,6 +267,8 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
       rs = acc;
     }
   }
+
+  if constexpr (EDGE) ps += hw_exp2(fmaf(xe, kLog2e, -m2));   // 0 for threads without one
 
   // 3. Workgroup merge.
   __builtin_amdgcn_sched_barrier(0);
@@ -254,9 +308,17 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
     }
     buf_store_vals<TO, EPV, true>(drow, fresh_off(tid * kOutVec, k * BLOCK * kOutVec), o);
   }
-  if (tid == static_cast<int>((r.id / EPV) % BLOCK)) {
+  const int64_t it = r.id - xsp.head;   // the target's index in the interior
+  if (it >= 0 && it < static_cast<int64_t>(nv) * EPV && tid == static_cast<int>((it / EPV) % BLOCK)) {
     const float dy = c - c * hw_exp2(fmaf(xy, kLog2e, -lse2));
-    buf_store1<TO, true>(drow, static_cast<uint32_t>(r.id) * TO::kBytes, dy);
+    buf_store1<TO, true>(drow, static_cast<uint32_t>(it) * TO::kBytes, dy);
+  }
+  if constexpr (EDGE) {
+    if (ek >= 0) {
+      const float o = (ek == r.id) ? c - c * hw_exp2(fmaf(xy, kLog2e, -lse2))
+                                   : nc * hw_exp2(fmaf(xe, kLog2e, -lse2));
+      store1<TO>(a.dlogits, row_elem + ek, o);
+    }
   }
 }
 
@@ -272,18 +334,18 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
 template <typename TI, typename TO>
 constexpr bool kPersistentRows = !(__is_same(TI, BF16T) && __is_same(TO, F32T));
 
-template <typename TI, typename TO, int BLOCK, int NCH, int RB>
+template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE>
 __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   __shared__ float lds[4 * (BLOCK / 64)];
   __shared__ int s_next[2];
   if constexpr (!kPersistentRows<TI, TO>) {
-    resident_row<TI, TO, BLOCK, NCH, RB>(a, blockIdx.x, lds);
+    resident_row<TI, TO, BLOCK, NCH, RB, EDGE>(a, blockIdx.x, lds);
     return;
   }
   int64_t row = blockIdx.x;
   for (int i = 0; row < a.nrows; ++i) {
     if (threadIdx.x == 0) s_next[i & 1] = atomicAdd(a.next_row, 1) + static_cast<int>(gridDim.x);
-    resident_row<TI, TO, BLOCK, NCH, RB>(a, row, lds);
+    resident_row<TI, TO, BLOCK, NCH, RB, EDGE>(a, row, lds);
     __syncthreads();   // s_next visible; this row's LDS reads done before the next row writes
     row = s_next[i & 1];
   }
@@ -324,39 +386,6 @@ __device__ __forceinline__ float vec_max(float m, const u32x4& v) {
     for (int j = 0; j < 16 / TI::kBytes; ++j) m = fmaxf(m, TI::unpack(w, j));
   }
   return m;
-}
-
-// A row of the forward kernel: its 16-byte-aligned interior of nv vectors, and the
-// head (before it) and tail (after it) of fewer than EPV elements each.
-struct RowSpan {
-  const void* vec;
-  int head, nv, tail;
-};
-
-template <typename TI>
-__device__ __forceinline__ RowSpan row_span(const void* p, int64_t vocab) {
-  constexpr int EPV = 16 / TI::kBytes;
-  RowSpan s;
-  const int mis = static_cast<int>(reinterpret_cast<uintptr_t>(p) & 15u);
-  s.head = static_cast<int>(min<int64_t>(((16 - mis) & 15) / TI::kBytes, vocab));
-  s.nv = static_cast<int>((vocab - s.head) / EPV);
-  s.tail = static_cast<int>(vocab - s.head - static_cast<int64_t>(s.nv) * EPV);
-  s.vec = static_cast<const char*>(p) + s.head * TI::kBytes;
-  return s;
-}
-
-// Thread tid's head or tail element of the row as a one-element online state (m, s):
-// threads [0, head) take the head, [head, head + tail) the tail, the rest nothing.
-template <typename TI>
-__device__ __forceinline__ void edge_state(const void* p, const RowSpan& sp, int tid, float& m, float& s) {
-  constexpr int EPV = 16 / TI::kBytes;
-  const int k = tid < sp.head ? tid : (tid - sp.head < sp.tail ? sp.head + sp.nv * EPV + (tid - sp.head) : -1);
-  m = kNegInf;
-  s = 0.f;
-  if (k < 0) return;
-  const float x = TI::load1(p, k) * kLog2e;
-  m = fmaxf(m, x);
-  s = hw_exp2(x - ms_ref(m));
 }
 
 template <typename TI, int BLOCK, int U, bool REF>
@@ -697,7 +726,7 @@ loss_final_kernel(const float* seq_val, int64_t n_seq, float loss_norm, float* l
 // ---------------------------------------------------------------------------
 namespace {
 
-template <typename TI, typename TO, int BLOCK, int NCH>
+template <typename TI, typename TO, int BLOCK, int NCH, bool EDGE>
 hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
   // RB = 2: the largest reference batch that needs no register spill next to a
   // 19-chunk resident row at 128 VGPRs (4 spills 9 VGPRs and measured ~1% slower).
@@ -712,7 +741,7 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e == hipSuccess)
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &occ, reinterpret_cast<const void*>(&grpo_resident_kernel<TI, TO, BLOCK, NCH, RB>), BLOCK, 0);
+          &occ, reinterpret_cast<const void*>(&grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE>), BLOCK, 0);
     if (e != hipSuccess) return e;
     slots = cus * (occ > 0 ? occ : 1);
     cached.store(slots, std::memory_order_relaxed);
@@ -720,7 +749,7 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
   const int64_t grid = kPersistentRows<TI, TO> ? (nrows < slots ? nrows : slots) : nrows;
   if (grid <= 0) return hipSuccess;
   if (kPersistentRows<TI, TO>) reset_counter_kernel<<<1, 1, 0, st>>>(a.next_row);
-  grpo_resident_kernel<TI, TO, BLOCK, NCH, RB><<<dim3(static_cast<unsigned>(grid)), dim3(BLOCK), 0, st>>>(a);
+  grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE><<<dim3(static_cast<unsigned>(grid)), dim3(BLOCK), 0, st>>>(a);
   return hipGetLastError();
 }
 
@@ -759,26 +788,37 @@ struct ResCfg {
 constexpr ResCfg kResCfgs[] = {{256, 1},   {256, 2},   {256, 4},   {1024, 2}, {1024, 4},
                                {1024, 8},  {1024, 12}, {1024, 16}, {1024, 19}, {1024, 20}};
 
+// Rows off 16 bytes (EDGE) need dlogits of the logits' element type.
+template <typename TI, typename TO, int BLOCK, int NCH>
+hipError_t launch_resident_cfg(bool edge, const RowArgs& a, int64_t nrows, hipStream_t st) {
+  if constexpr (__is_same(TI, TO)) {
+    if (edge) return launch_resident<TI, TO, BLOCK, NCH, true>(a, nrows, st);
+  } else {
+    if (edge) return hipErrorInvalidValue;
+  }
+  return launch_resident<TI, TO, BLOCK, NCH, false>(a, nrows, st);
+}
+
 template <typename TI, typename TO>
-hipError_t dispatch_resident(int cfg, const RowArgs& a, int64_t nrows, hipStream_t st) {
+hipError_t dispatch_resident(int cfg, bool edge, const RowArgs& a, int64_t nrows, hipStream_t st) {
   switch (cfg) {
-    case 0: return launch_resident<TI, TO, 256, 1>(a, nrows, st);
-    case 1: return launch_resident<TI, TO, 256, 2>(a, nrows, st);
-    case 2: return launch_resident<TI, TO, 256, 4>(a, nrows, st);
-    case 3: return launch_resident<TI, TO, 1024, 2>(a, nrows, st);
-    case 4: return launch_resident<TI, TO, 1024, 4>(a, nrows, st);
-    case 5: return launch_resident<TI, TO, 1024, 8>(a, nrows, st);
-    case 6: return launch_resident<TI, TO, 1024, 12>(a, nrows, st);
-    case 7: return launch_resident<TI, TO, 1024, 16>(a, nrows, st);
-    case 8: return launch_resident<TI, TO, 1024, 19>(a, nrows, st);
-    case 9: return launch_resident<TI, TO, 1024, 20>(a, nrows, st);
+    case 0: return launch_resident_cfg<TI, TO, 256, 1>(edge, a, nrows, st);
+    case 1: return launch_resident_cfg<TI, TO, 256, 2>(edge, a, nrows, st);
+    case 2: return launch_resident_cfg<TI, TO, 256, 4>(edge, a, nrows, st);
+    case 3: return launch_resident_cfg<TI, TO, 1024, 2>(edge, a, nrows, st);
+    case 4: return launch_resident_cfg<TI, TO, 1024, 4>(edge, a, nrows, st);
+    case 5: return launch_resident_cfg<TI, TO, 1024, 8>(edge, a, nrows, st);
+    case 6: return launch_resident_cfg<TI, TO, 1024, 12>(edge, a, nrows, st);
+    case 7: return launch_resident_cfg<TI, TO, 1024, 16>(edge, a, nrows, st);
+    case 8: return launch_resident_cfg<TI, TO, 1024, 19>(edge, a, nrows, st);
+    case 9: return launch_resident_cfg<TI, TO, 1024, 20>(edge, a, nrows, st);
   }
   return hipErrorInvalidValue;
 }
 
 template <typename TI, typename TO>
 hipError_t dispatch_rows(const RowPlan& p, const RowArgs& a, int64_t nrows, hipStream_t st) {
-  if (p.kind == RowPlan::kResident) return dispatch_resident<TI, TO>(p.cfg, a, nrows, st);
+  if (p.kind == RowPlan::kResident) return dispatch_resident<TI, TO>(p.cfg, p.edge != 0, a, nrows, st);
   if (p.kind == RowPlan::kForward) return launch_fwd<TI>(a, nrows, st);
   if (p.kind == RowPlan::kStreamVec) return launch_stream<TI, TO, true>(a, nrows, st);
   return launch_stream<TI, TO, false>(a, nrows, st);
@@ -786,7 +826,7 @@ hipError_t dispatch_rows(const RowPlan& p, const RowArgs& a, int64_t nrows, hipS
 
 }  // namespace
 
-RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool forward_only, bool force_stream) {
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool edge_ok, bool forward_only, bool force_stream) {
   RowPlan p;
   const int epv = 16 / in_bytes;
   const bool vec = aligned16 && (vocab % epv == 0);
@@ -794,6 +834,7 @@ RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool forward_only
   p.cfg = -1;
   p.block = 1024;
   p.nch = 0;
+  p.edge = 0;
   if (force_stream) return p;
   // The forward kernel takes rows of any alignment. It addresses a row through a
   // 32-bit buffer offset that runs up to one batch past the row end: rows up to 2 GiB
@@ -803,14 +844,17 @@ RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool forward_only
     p.block = PCP_FWD_BLOCK;
     return p;
   }
-  if (!vec) return p;
-  const int64_t nv = vocab / epv;
+  // Rows off 16 bytes stay resident when dlogits rows share the logits rows' element
+  // type and offset (the head and tail then line up); otherwise they stream.
+  if (!vec && !edge_ok) return p;
+  const int64_t nv = vocab / epv;   // the interior of a row off 16 bytes has at most as many
   for (int i = 0; i < static_cast<int>(sizeof(kResCfgs) / sizeof(kResCfgs[0])); ++i) {
     if (static_cast<int64_t>(kResCfgs[i].block) * kResCfgs[i].nch >= nv) {
       p.kind = RowPlan::kResident;
       p.cfg = i;
       p.block = kResCfgs[i].block;
       p.nch = kResCfgs[i].nch;
+      p.edge = vec ? 0 : 1;
       return p;
     }
   }

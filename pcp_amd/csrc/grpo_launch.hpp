@@ -15,11 +15,13 @@ struct RowPlan {
   int cfg;    // resident configuration index
   int block;  // lanes per workgroup
   int nch;    // resident 16-byte chunks per lane
+  int edge;   // resident rows off 16 bytes (head / tail element-wise)
 };
 
 // in_bytes: logits element size; aligned16: every row base is 16-byte aligned;
-// forward_only: no dlogits are written.
-RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool forward_only, bool force_stream);
+// edge_ok: dlogits (if any) have the logits' element type and the same address mod 16,
+// so rows off 16 bytes split alike; forward_only: no dlogits are written.
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool edge_ok, bool forward_only, bool force_stream);
 
 hipError_t launch_rows(const RowPlan& p, int in_dtype, int out_dtype, const RowArgs& a,
                        int64_t nrows, hipStream_t st);

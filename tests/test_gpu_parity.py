@@ -294,6 +294,53 @@ def test_logprob_fwd_kernel_shapes(dtype, V, lead, with_ref):
         assert lr is None
 
 
+@pytest.mark.parametrize("dtype,V,lead,dlead", [("bf16", 50257, 0, 0), ("bf16", 130, 3, 3), ("bf16", 130, 3, 4),
+                                               ("f16", 24, 5, 5), ("f32", 1027, 1, 1), ("f32", 7, 3, 0),
+                                               ("bf16", 151937, 0, 0)])
+def test_loss_rows_off_16_bytes(dtype, V, lead, dlead):
+    """The loss path (fwd + bwd) on rows that start off 16 bytes: V not a multiple of the
+    16-byte vector, and logits / dlogits viewed lead / dlead elements into their
+    allocations. When dlogits share the logits' offset mod 16 the rows stay resident
+    (aligned interior as vectors, head and tail element-wise); otherwise they stream.
+    Log-probs, dlogits and the loss against the float64 oracle at the golden bars; the
+    dlogits before and after the viewed rows are untouched."""
+    rng = np.random.default_rng(V + 13 * lead + dlead)
+    S, T, G = 4, 5, 2
+    x, x64 = _fwd_logits(rng, S * T, V, dtype, neg_inf=False)
+    noisy = (x64 + rng.standard_normal(x64.shape) * 0.1).astype(np.float32)   # ref = policy + N(0, 0.1^2)
+    rr = {"bf16": orc.bf16_from_f32, "f16": lambda v: v.astype(np.float16), "f32": lambda v: v}[dtype](noisy)
+    ids = rng.integers(0, V, (S, T)).astype(np.int64)
+    mask = (rng.random((S, T)) < 0.8).astype(np.float32)
+    old = (rng.standard_normal((S, T)) * 0.05 - np.log(V)).astype(np.float32)
+    rewards = np.array([1, 0, 0.5, 0.25], np.float32)
+    sh = (S, T, V)
+    print(f"loss rows off 16 bytes: {dtype} V={V} lead={lead} dlead={dlead}", flush=True)
+
+    def placed(a, k):
+        flat = dev(np.concatenate([a.reshape(-1)[:k], a.reshape(-1)]))
+        return flat[k:].view(sh)
+
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    guard = 11
+    dl_alloc = torch.full((dlead + S * T * V + guard,), 7.0, dtype=tdt, device=DEV)
+    dl = dl_alloc[dlead:dlead + S * T * V].view(sh)
+    out = grpo.grpo_loss_fwd_bwd(placed(x, lead), dev(ids), dev(mask), rewards=dev(rewards), group_size=G,
+                                 ref_logits=placed(rr, 2 * lead), old_logp=dev(old),
+                                 loss_mode=LossMode.GRPO_CLIP_KL, dlogits=dl)
+    torch.cuda.synchronize()
+    assert bool((dl_alloc[:dlead] == 7.0).all()) and bool((dl_alloc[dlead + S * T * V:] == 7.0).all())
+    odt = {"bf16": orc.BF16, "f16": orc.F16, "f32": orc.F32}[dtype]
+    want = orc.grpo_full(x.reshape(sh), ids, mask, rows=T, tok_offset=0, rewards=rewards, group_size=G,
+                         ref_logits=rr.reshape(sh), old_logp=old, loss_mode=orc.CLIP_KL, dtype=odt)
+    xs = x.reshape(sh)
+    ts = token_scale(xs, ids, T, 0, odt)
+    assert np.all(np.abs(out.logp.cpu().numpy() - want.lp) <= 1e-5 * ts)
+    fl = full_floor(want, mask, old, S, False, 0.04, 0.2, ts)
+    got = out.dlogits.float().cpu().numpy()
+    assert_dlogits(got, want.dlogits, tok_to_rows(fl, T, 0, T), dtype != "f32")
+    assert abs(float(out.loss.cpu()) - want.loss) <= full_loss_tol(want, xs, ids, mask, T, 0, odt, False, 0.04, S)
+
+
 # ---- host-bytes path (the WorkerBackend face) ------------------------------------------------
 
 def test_execute_reference_signature():
