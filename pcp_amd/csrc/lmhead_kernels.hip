@@ -178,6 +178,11 @@ lm_tile_kernel(LmTileArgs a) {
   // flight when a stage is waited for: vmcnt(8 (NST - 3)), then the barrier makes
   // every wave's loads of it visible. Branch-free, so the compiler's LDS waits stay
   // exact.
+  // Issue order: one memory instruction per MFMA. The wave issues in order, so a
+  // burst of the stage's 8 direct-to-LDS loads right after the barrier held the
+  // MFMAs behind it whenever the memory pipeline pushed back; one load (or
+  // fragment read) between consecutive MFMAs measured 6% faster on config 5
+  // (11.72 -> 11.04 ms per forward launch).
   const int nk = a.H / BK;
 #pragma unroll
   for (int st = 0; st < NST - 1; ++st) issue(min(st, nk - 1), st);
@@ -187,8 +192,12 @@ lm_tile_kernel(LmTileArgs a) {
   for (int kb = 0; kb + 1 < nk; ++kb) {
     fload(1, kb, 1);
     mfmas(0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS reads of k-step 1
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // MFMAs of k-step 0
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a DS read of k-step 1
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 0
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);    // the rest of k-step 0
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitLoop);                // stage kb+1 landed
     lm_barrier();
@@ -197,9 +206,16 @@ lm_tile_kernel(LmTileArgs a) {
     issue(min(kb + NST - 1, nk - 1), (kb + NST - 1) % NST);
     fload(0, kb + 1, 0);
     mfmas(1);
-    __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);    // the stage's loads
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS reads of the next k-step 0
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // MFMAs of k-step 1
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a load of the stage
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 1
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a DS read of the next k-step 0
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 1
+    }
   }
   fload(1, nk - 1, 1);
   mfmas(0);
