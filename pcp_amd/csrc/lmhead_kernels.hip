@@ -41,7 +41,6 @@ constexpr int NTHR = 256;         // 4 waves: 2 (vocab) x 2 (tokens), 128 x 128 
 constexpr int LDD = BV + 8;       // bf16 dlogits row in the backward epilogue (528 B, 16-B aligned)
 constexpr size_t kSmemEpi = (BT / 2) * LDD * sizeof(__bf16);   // half the token columns at a time
 constexpr size_t kSmem = kSmemGemm > kSmemEpi ? kSmemGemm : kSmemEpi;
-constexpr int kGroupM = 8;        // token tiles per group in the tile order
 constexpr int kPart = 128;        // vocab entries per log-sum-exp partial (one wave's rows)
 
 // s_waitcnt immediate for vmcnt(n), expcnt and lgkmcnt left at their maxima: vmcnt
@@ -66,17 +65,18 @@ __device__ __forceinline__ int lm_swz(int row) { return (row >> 2) & 3; }
 
 // Tile order: work item p -> (token tile, vocab tile). Consecutive workgroup ids
 // are dealt round-robin to the 8 XCDs, so ids are first regrouped per XCD; within
-// an XCD, groups of kGroupM token tiles sweep the vocab tiles together, so the
-// workgroups resident on one XCD read the same operand K-slabs from its L2.
-__device__ __forceinline__ bool lm_tile_coords(int pid, int ntt, int nvt, int& tm, int& tn) {
+// an XCD, groups of group_m token tiles sweep the vocab tiles together, so the
+// workgroups resident on one XCD read the same operand K-slabs from its L2, and W
+// comes from HBM once per group.
+__device__ __forceinline__ bool lm_tile_coords(int pid, int ntt, int nvt, int group_m, int& tm, int& tn) {
   const int total = ntt * nvt;
   const int per_xcd = (total + 7) / 8;
   const int p = (pid % 8) * per_xcd + pid / 8;
   if (p >= total) return false;
-  const int group = lm::kGroupM * nvt;
+  const int group = group_m * nvt;
   const int g = p / group;
-  const int first_m = g * lm::kGroupM;
-  const int gm = min(ntt - first_m, lm::kGroupM);
+  const int first_m = g * group_m;
+  const int gm = min(ntt - first_m, group_m);
   const int q = p - g * group;
   tm = first_m + q % gm;
   tn = q / gm;
@@ -109,7 +109,7 @@ lm_tile_kernel(LmTileArgs a) {
   extern __shared__ __align__(16) char smem[];
 
   int tm, tn;
-  if (!lm_tile_coords(blockIdx.x, a.ntt, a.nvt, tm, tn)) return;
+  if (!lm_tile_coords(blockIdx.x, a.ntt, a.nvt, a.group_m, tm, tn)) return;
   const int m0 = tm * BT;                  // first token
   const int v0 = (a.vt0 + tn) * BV;        // first vocab entry
   const int tid = threadIdx.x;
@@ -468,7 +468,25 @@ __global__ void __launch_bounds__(256) lm_zero_kernel(float* dst, int64_t n) {
 // ---------------------------------------------------------------------------
 size_t lm_tile_smem_bytes() { return lm::kSmem; }
 
-hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st) {
+// Token tiles per group in the tile order. Measured on config 5 (38 token tiles,
+// interleaved on one box): the forward launch takes 11.05 ms with groups of 8, 10.2
+// with 2 equal groups of 19, 10.4 with one group of 38, 10.5 with 4 groups of
+// about 10, and 11.5 with groups of 32 and 6; so the forward splits the token
+// tiles into equal groups of at most kLmFwdGroupMax. The backward's chunks (64
+// vocab tiles) measured best with groups of 4 (step 55.3 ms against 55.6 with 8).
+constexpr int kLmFwdGroupMax = 20;
+constexpr int kLmBwdGroup = 4;
+
+int lm_group_m(int mode, int ntt) {
+  if (ntt < 1) return 1;
+  if (mode != kLmFwd) return ntt < kLmBwdGroup ? ntt : kLmBwdGroup;
+  const int ng = (ntt + kLmFwdGroupMax - 1) / kLmFwdGroupMax;
+  return (ntt + ng - 1) / ng;
+}
+
+hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {
+  LmTileArgs a = args;
+  a.group_m = lm_group_m(mode, a.ntt);
   const int total = a.ntt * a.nvt;
   const int grid = ((total + 7) / 8) * 8;
   if (mode == kLmFwd) {

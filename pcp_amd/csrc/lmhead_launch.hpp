@@ -21,6 +21,7 @@ struct LmTileArgs {
   const void* B;        // weight [V, H] bf16, row-major
   int N, V, H;          // H % 64 == 0
   int vt0, nvt, ntt;
+  int group_m;          // token tiles per group in the tile order (set by launch_lm_tiles)
   const void* ids;      // [N] target ids
   int ids_i64;
   // kLmFwd
