@@ -468,20 +468,28 @@ __global__ void __launch_bounds__(256) lm_zero_kernel(float* dst, int64_t n) {
 // ---------------------------------------------------------------------------
 size_t lm_tile_smem_bytes() { return lm::kSmem; }
 
-// Token tiles per group in the tile order. Measured on config 5 (38 token tiles,
-// interleaved on one box): the forward launch takes 11.05 ms with groups of 8, 10.2
-// with 2 equal groups of 19, 10.4 with one group of 38, 10.5 with 4 groups of
-// about 10, and 11.5 with groups of 32 and 6; so the forward splits the token
-// tiles into equal groups of at most kLmFwdGroupMax. The backward's chunks (64
-// vocab tiles) measured best with groups of 4 (step 55.3 ms against 55.6 with 8).
-constexpr int kLmFwdGroupMax = 20;
+// Token tiles per group in the tile order. lm_tile_coords gives each XCD a
+// contiguous eighth of the work items; the forward measured fastest with the
+// smallest group (at least 8 token tiles) whose boundaries fall on those eighths:
+// 8 * group a multiple of the token tiles, or the token tiles a multiple of
+// 8 * group. Forward launch, H = 4096, V = 151936, all tokens live, interleaved on
+// one box (ms):
+//   token tiles 10:  groups of 10  2.70 | 8 (misaligned)   2.85
+//   token tiles 20:  groups of 10  5.39 | 20 5.43-5.46
+//   token tiles 32:  groups of 8   8.73-8.82 | 16 8.91-8.99 | 32 9.45-9.50
+//   token tiles 38:  groups of 19  10.28 | 13 10.70-10.81 | 10 11.02-11.09 | 8 11.05 (config 5)
+//   token tiles 64:  groups of 8   17.46-17.53 | 16 17.88-17.94 | 32 18.59-18.61 | 64 18.26-18.28
+//   token tiles 128: groups of 8   34.86-34.93 | 16 36.87-36.91 | 32 38.25-38.28
+// The backward's chunks (64 vocab tiles) measured best with groups of 4 at config 5
+// (step 55.3 ms against 55.6 with 8; 2 matched 4, 1 and 38 were slower).
 constexpr int kLmBwdGroup = 4;
 
 int lm_group_m(int mode, int ntt) {
   if (ntt < 1) return 1;
   if (mode != kLmFwd) return ntt < kLmBwdGroup ? ntt : kLmBwdGroup;
-  const int ng = (ntt + kLmFwdGroupMax - 1) / kLmFwdGroupMax;
-  return (ntt + ng - 1) / ng;
+  for (int g = ntt < 8 ? ntt : 8; g < ntt; ++g)
+    if ((8 * g) % ntt == 0 || ntt % (8 * g) == 0) return g;
+  return ntt;
 }
 
 hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {

@@ -131,8 +131,9 @@ SMALL = [
     (3, 50, 192, 1000, 3, 256, [50, 31, 7]),
     (2, 64, 64, 129, 2, 0, [64, 1]),
     (1, 7, 128, 4096, 1, 1024, [5]),
-    # 10,900 live tokens = 43 token tiles: the forward tile order splits them into
-    # groups of 15, 15 and 13, the backward into groups of 4 with a last group of 3.
+    # 6,000 live tokens = 24 token tiles: forward tile groups of 9, 9 and 6;
+    # 10,900 = 43 token tiles: one forward group, backward groups of 4 and a last of 3.
+    (2, 3000, 64, 300, 2, 256, [3000, 3000]),
     (4, 3000, 64, 300, 2, 256, [3000, 3000, 3000, 1900]),
 ]
 
