@@ -23,7 +23,8 @@ def declared_functions():
     for h in sorted(os.listdir(INCLUDE)):
         if not h.endswith(".h"):
             continue
-        text = open(os.path.join(INCLUDE, h)).read()
+        with open(os.path.join(INCLUDE, h)) as f:
+            text = f.read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"^[A-Za-z_][\w \*]*?\b(pcp_\w+)\s*\(", text, flags=re.M)
     return sorted(set(names))

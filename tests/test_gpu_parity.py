@@ -128,7 +128,8 @@ def test_golden_bf16_in_f32_out():
 # ---- advantages -----------------------------------------------------------------------
 
 def test_advantages_bit_exact():
-    d = json.load(open(os.path.join(GOLD, "advantages.json")))
+    with open(os.path.join(GOLD, "advantages.json")) as f:
+        d = json.load(f)
     for c in d["cases"]:
         r = np.array(c["rewards_bits"], np.uint32).view(np.float32)
         got = grpo.advantages(dev(r), c["group"], d["eps"]).cpu().numpy().view(np.uint32)

@@ -63,7 +63,8 @@ def test_bf16_rne_matches_torch(orc):
 # ---- a3 advantages -----------------------------------------------------------------
 
 def test_advantages_bit_exact_against_fixture(orc):
-    d = json.load(open(os.path.join(GOLD, "advantages.json")))
+    with open(os.path.join(GOLD, "advantages.json")) as f:
+        d = json.load(f)
     assert len(d["cases"]) >= 9
     for c in d["cases"]:
         r = np.array(c["rewards_bits"], np.uint32).view(np.float32)
@@ -123,7 +124,8 @@ def test_logprob_brute_force_and_torch(orc):
 
 
 def test_reference_kat_cross_entropy_stability(orc):
-    kat = json.load(open(os.path.join(GOLD, "reference_kats.json")))["cross_entropy_stability"]
+    with open(os.path.join(GOLD, "reference_kats.json")) as f:
+        kat = json.load(f)["cross_entropy_stability"]
     x = np.array([kat["logits"]], np.float32)
     ids = np.array([kat["target"]])
     for prec in (orc.EXACT, orc.REF_F32, orc.FAITHFUL):
@@ -137,7 +139,8 @@ def test_reference_kat_reduce_max_routes_to_the_max(orc):
     # reduceMaxVJP sends the upstream gradient to the element equal to the max
     # ([1,5,3] -> [0,1,0]); in the faithful backward that is the only place the
     # 1e-4 leak of the log guard appears.
-    kat = json.load(open(os.path.join(GOLD, "reference_kats.json")))["reduce_max_grad"]
+    with open(os.path.join(GOLD, "reference_kats.json")) as f:
+        kat = json.load(f)["reduce_max_grad"]
     x = np.array([kat["x"]], np.float32)
     ex = orc.grpo_rows(x, np.array([2]), [1.0], [1.0], [1.0], 1.0, precision=orc.EXACT)
     fa = orc.grpo_rows(x, np.array([2]), [1.0], [1.0], [1.0], 1.0, precision=orc.FAITHFUL)
