@@ -256,7 +256,7 @@ typedef struct pcp_lmhead_args {
   int64_t hidden;             /* H; multiple of 64                                        */
   int64_t vocab;              /* V                                                        */
   int64_t group_size;         /* sequences per advantage group                            */
-  int64_t vocab_chunk;        /* backward chunk width; 0 => 16384 (multiple of 128)       */
+  int64_t vocab_chunk;        /* backward chunk width; 0 => 16384 (a multiple of 256)      */
   int32_t ids_dtype;          /* PCP_I64 | PCP_I32                                        */
   int32_t mask_dtype;         /* PCP_F32 | PCP_BOOL                                       */
   const void* hidden_states;  /* [n_seq*rows, H] bf16                                     */
