@@ -3,7 +3,7 @@
 // logits[n, v] = sum_h hidden[n, h] * W[v, h] is a dense contraction; the loss
 // head only needs, per token, the log-sum-exp over v and the logit of its target
 // (forward), and dlogits = c_n * (onehot - softmax) (backward). The tile kernel
-// computes a 128 x 128 logits tile on v_mfma_f32_32x32x16_bf16 and reduces it in
+// computes a 256 x 256 logits tile on v_mfma_f32_32x32x16_bf16 and reduces it in
 // its epilogue, so full logits never exist in HBM:
 //   kFwd  -> per (token, vocab tile) partial (max, sum 2^(x*log2e - max)) and the
 //            target logit when the target falls in the tile;
@@ -37,7 +37,8 @@ constexpr int ROWB = BK * 2;      // bytes of one operand row in one stage
 constexpr int kOpBytes = BV * ROWB;             // 16 KB: one operand, one stage
 constexpr int kStageBytes = 2 * kOpBytes;       // 32 KB
 constexpr size_t kSmemGemm = NST * kStageBytes; // 32 KB per stage
-constexpr int NTHR = 256;         // 4 waves: 2 (vocab) x 2 (tokens), 128 x 128 each
+constexpr int NTHR = 512;         // 8 waves: 2 (vocab) x 4 (tokens), 128 x 64 each
+constexpr int NJ = 2;             // 32-column token blocks per wave
 constexpr int LDD = BV + 8;       // bf16 dlogits row in the backward epilogue (528 B, 16-B aligned)
 constexpr size_t kSmemEpi = (BT / 2) * LDD * sizeof(__bf16);   // half the token columns at a time
 constexpr size_t kSmem = kSmemGemm > kSmemEpi ? kSmemGemm : kSmemEpi;
@@ -47,8 +48,8 @@ constexpr int kPart = 128;        // vocab entries per log-sum-exp partial (one 
 // bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 constexpr int kWaitVm0 = wait_vm(0);
-constexpr int kWaitPrologue = wait_vm(8 * (NST - 2));   // stage 0 landed, NST - 2 later ones in flight
-constexpr int kWaitLoop = wait_vm(8 * (NST - 3));       // stage kb + 1 landed, NST - 3 later ones in flight
+constexpr int kWaitPrologue = wait_vm(4 * (NST - 2));   // stage 0 landed, NST - 2 later ones in flight
+constexpr int kWaitLoop = wait_vm(4 * (NST - 3));       // stage kb + 1 landed, NST - 3 later ones in flight
 static_assert(wait_vm(0) == 0x0F70 && wait_vm(8) == 0x0F78 && wait_vm(16) == 0x4F70 && wait_vm(24) == 0x4F78,
               "vmcnt encoding");
 
@@ -97,13 +98,16 @@ __device__ __forceinline__ void lm_barrier() {
 }
 
 // One 256 (vocab) x 256 (token) logits tile C[v][t] = sum_h W[v][h] * hidden[t][h].
-// Wave (wv, wt) owns vocab rows wv*128 + [0,128) and token columns wt*128 + [0,128)
-// as 4 x 4 blocks of v_mfma_f32_32x32x16_bf16. Result layout of a 32 x 32 block:
+// Eight waves, two per SIMD: wave (wv, wt) owns vocab rows wv*128 + [0,128) and token
+// columns wt*64 + [0,64) as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16 (128 accumulators,
+// so two waves share a SIMD and one issues MFMAs while the other waits on a load, a
+// fragment read or the barrier; measured 2-7% faster than four waves of 128 x 128,
+// which fill the register file). Result layout of a 32 x 32 block:
 // lane l holds token column l%32 and vocab rows 8*(r/4) + 4*(l/32) + r%4, r < 16.
 // Operands stream global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging)
 // through NST stages of BK hidden columns.
 template <int MODE>
-__global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
 lm_tile_kernel(LmTileArgs a) {
   using namespace lm;
   extern __shared__ __align__(16) char smem[];
@@ -114,7 +118,7 @@ lm_tile_kernel(LmTileArgs a) {
   const int v0 = (a.vt0 + tn) * BV;        // first vocab entry
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wv = wave >> 1, wt = wave & 1;
+  const int wv = wave >> 2, wt = wave & 3;
 
   // Operand row buffers: rows past V / N read 0 (range-checked lane offsets).
   const uint32_t rowbytes = static_cast<uint32_t>(a.H) * 2u;
@@ -124,21 +128,21 @@ lm_tile_kernel(LmTileArgs a) {
   const __amdgpu_buffer_rsrc_t rh =
       row_rsrc(reinterpret_cast<const char*>(a.A) + static_cast<int64_t>(m0) * rowbytes, rows_h * rowbytes);
 
-  // Direct-to-LDS loads: wave w fills rows 16*(4w+q) + lane/4, q < 4, of each operand;
+  // Direct-to-LDS loads: wave w fills rows 16*(2w+q) + lane/4, q < 2, of each operand;
   // lane writes LDS slot lane%4 of its row, which holds chunk (lane%4) ^ swz(row).
-  uint32_t doff[4];
+  uint32_t doff[2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int row = 16 * (4 * wave + q) + (lane >> 2);
+  for (int q = 0; q < 2; ++q) {
+    const int row = 16 * (2 * wave + q) + (lane >> 2);
     doff[q] = static_cast<uint32_t>(row) * rowbytes + 16u * static_cast<uint32_t>((lane & 3) ^ lm_swz(row));
   }
   auto issue = [&](int st, int buf) {
     char* base = smem + buf * kStageBytes;
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (4 * wave + q) * 1024), 16, doff[q] + koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (4 * wave + q) * 1024), 16, doff[q] + koff,
+    for (int q = 0; q < 2; ++q) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (2 * wave + q) * 1024), 16, doff[q] + koff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (2 * wave + q) * 1024), 16, doff[q] + koff,
                                                0, 0, 0);
     }
   };
@@ -147,39 +151,39 @@ lm_tile_kernel(LmTileArgs a) {
   // swizzle depends on lane%32 only, so one offset per k-step serves every block.
   const int sw = lm_swz(lane & 31);
   const int fo0 = 16 * ((0 + (lane >> 5)) ^ sw), fo1 = 16 * ((2 + (lane >> 5)) ^ sw);
-  const int offA = (wv * 128 + (lane & 31)) * ROWB, offB = kOpBytes + (wt * 128 + (lane & 31)) * ROWB;
-  bf16x8 af[2][4], bfr[2][4];
+  const int offA = (wv * 128 + (lane & 31)) * ROWB, offB = kOpBytes + (wt * 64 + (lane & 31)) * ROWB;
+  bf16x8 af[2][4], bfr[2][NJ];
   auto fload = [&](int set, int st, int kk) {
     const char* base = smem + (st % NST) * kStageBytes + (kk ? fo1 : fo0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(base + offA + i * 32 * ROWB);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bfr[set][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 32 * ROWB);
+    for (int j = 0; j < NJ; ++j) bfr[set][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 32 * ROWB);
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   auto mfmas = [&](int set) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], bfr[set][j], acc[i][j], 0, 0, 0);
   };
 
   // Pipeline: stage kb is read from LDS buffer kb % NST. Every iteration issues one
   // stage (kb + NST - 1, clamped to the last stage past the end: an L2 hit into a
-  // buffer nobody reads), so NST - 3 later stages (8 loads per wave each) are in
-  // flight when a stage is waited for: vmcnt(8 (NST - 3)), then the barrier makes
+  // buffer nobody reads), so NST - 3 later stages (4 loads per wave each) are in
+  // flight when a stage is waited for: vmcnt(4 (NST - 3)), then the barrier makes
   // every wave's loads of it visible. Branch-free, so the compiler's LDS waits stay
   // exact.
   // Issue order: one memory instruction per MFMA. The wave issues in order, so a
-  // burst of the stage's 8 direct-to-LDS loads right after the barrier held the
+  // burst of the stage's direct-to-LDS loads right after the barrier held the
   // MFMAs behind it whenever the memory pipeline pushed back; one load (or
   // fragment read) between consecutive MFMAs measured 6% faster on config 5
   // (11.72 -> 11.04 ms per forward launch).
@@ -193,11 +197,11 @@ lm_tile_kernel(LmTileArgs a) {
     fload(1, kb, 1);
     mfmas(0);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 6; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a DS read of k-step 1
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 0
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);    // the rest of k-step 0
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);    // the rest of k-step 0
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitLoop);                // stage kb+1 landed
     lm_barrier();
@@ -207,15 +211,16 @@ lm_tile_kernel(LmTileArgs a) {
     fload(0, kb + 1, 0);
     mfmas(1);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 4; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a load of the stage
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 1
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 4; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a DS read of the next k-step 0
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 1
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);    // the rest of the next k-step 0
   }
   fload(1, nk - 1, 1);
   mfmas(0);
@@ -240,13 +245,13 @@ lm_tile_kernel(LmTileArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[i][j][r] = vrow(i, r) < vlim ? acc[i][j][r] : kNegInf;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = m0 + wt * 128 + 32 * j + (lane & 31);
+    for (int j = 0; j < NJ; ++j) {
+      const int n = m0 + wt * 64 + 32 * j + (lane & 31);
       float mx = kNegInf;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -286,10 +291,10 @@ lm_tile_kernel(LmTileArgs a) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       __syncthreads();   // the pipeline's (or the previous half's) LDS reads are done
-      if (wt == h) {
+      if ((wt >> 1) == h) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tcol = 32 * j + (lane & 31);          // column within this half
+        for (int j = 0; j < NJ; ++j) {
+          const int tcol = (wt & 1) * 64 + 32 * j + (lane & 31);          // column within this half
           const int n = m0 + h * 128 + tcol;
           float cf = 0.f, l2 = 0.f;
           int64_t rel = -1;
@@ -319,8 +324,8 @@ lm_tile_kernel(LmTileArgs a) {
       const int cidx = tid & 31;
       const int col0 = v0 - a.vc0 + cidx * 8;
 #pragma unroll 4
-      for (int it = 0; it < BT / 2 / 8; ++it) {
-        const int t = it * 8 + (tid >> 5);
+      for (int it = 0; it < BT / 2 / (NTHR / 32); ++it) {
+        const int t = it * (NTHR / 32) + (tid >> 5);
         const int n = m0 + h * 128 + t;
         if (n < a.N && col0 < a.ldd) {
           const u32x4 w = *reinterpret_cast<const u32x4*>(Ds + t * LDD + cidx * 8);
