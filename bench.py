@@ -340,6 +340,10 @@ def bench_sample(args) -> None:
                      "kernel": "sample_part_kernel<F32T> + sample_select_kernel<F32T>", "kernel_ms": kernel_ms,
                      "algorithmic_bytes": alg},
     }
+    tfile = os.path.join(ROOT, "profiles", "traffic_sample.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
     if not args.no_cpu_baseline:
         from oracle import oracle as orc
         xh, uh = x.cpu().numpy(), u.cpu().numpy()
