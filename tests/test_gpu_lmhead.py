@@ -138,6 +138,26 @@ SMALL = [
 ]
 
 
+def _random_shapes(n, seed=77):
+    # Seeded shapes for the same check: hidden sizes of 2, 6 and 10 K stages,
+    # vocabularies off the 128 / 256 tile widths, token counts off the 32-column
+    # MFMA blocks, empty sequences, chunk widths including ones past V.
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        S = int(rng.integers(1, 4))
+        T = int(rng.integers(5, 160))
+        H = int(rng.choice([64, 192, 320]))
+        V = int(rng.integers(1, 2500))
+        chunk = int(rng.choice([0, 256, 768, 4096]))
+        lengths = [int(x) for x in rng.integers(0, T + 1, size=S)]
+        out.append((S, T, H, V, S, chunk, lengths))
+    return out
+
+
+SMALL += _random_shapes(6)
+
+
 @pytest.mark.parametrize("mode", [LossMode.REINFORCE, LossMode.GRPO_CLIP_KL])
 @pytest.mark.parametrize("shape", SMALL, ids=lambda s: f"S{s[0]}T{s[1]}H{s[2]}V{s[3]}c{s[5]}")
 def test_lmhead_small_vs_oracle(shape, mode):
