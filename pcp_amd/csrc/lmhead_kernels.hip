@@ -28,15 +28,12 @@ namespace lm {
 
 constexpr int BV = 256;           // vocab rows per tile (MFMA A operand: W rows)
 constexpr int BT = 256;           // tokens per tile (MFMA B operand: hidden rows)
-constexpr int BK = 32;            // hidden (K) per pipeline stage
-#ifndef PCP_LM_NST
-#define PCP_LM_NST 4
-#endif
-constexpr int NST = PCP_LM_NST;   // LDS stages: up to NST - 1 in flight while one is read
+constexpr int BK = 64;            // hidden (K) per pipeline stage (one barrier each)
+constexpr int NST = 2;            // LDS stages: one in flight while the other is read
 constexpr int ROWB = BK * 2;      // bytes of one operand row in one stage
-constexpr int kOpBytes = BV * ROWB;             // 16 KB: one operand, one stage
-constexpr int kStageBytes = 2 * kOpBytes;       // 32 KB
-constexpr size_t kSmemGemm = NST * kStageBytes; // 32 KB per stage
+constexpr int kOpBytes = BV * ROWB;             // 32 KB: one operand, one stage
+constexpr int kStageBytes = 2 * kOpBytes;       // 64 KB
+constexpr size_t kSmemGemm = NST * kStageBytes; // 128 KB
 constexpr int NTHR = 512;         // 8 waves: 2 (vocab) x 4 (tokens), 128 x 64 each
 constexpr int NJ = 2;             // 32-column token blocks per wave
 constexpr int LDD = BV + 8;       // bf16 dlogits row in the backward epilogue (528 B, 16-B aligned)
@@ -48,8 +45,7 @@ constexpr int kPart = 128;        // vocab entries per log-sum-exp partial (one 
 // bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 constexpr int kWaitVm0 = wait_vm(0);
-constexpr int kWaitPrologue = wait_vm(4 * (NST - 2));   // stage 0 landed, NST - 2 later ones in flight
-constexpr int kWaitLoop = wait_vm(4 * (NST - 3));       // stage kb + 1 landed, NST - 3 later ones in flight
+constexpr int kWaitStage = kWaitVm0;        // the one stage in flight has landed
 static_assert(wait_vm(0) == 0x0F70 && wait_vm(8) == 0x0F78 && wait_vm(16) == 0x4F70 && wait_vm(24) == 0x4F78,
               "vmcnt encoding");
 
@@ -57,12 +53,12 @@ static_assert(wait_vm(0) == 0x0F70 && wait_vm(8) == 0x0F78 && wait_vm(16) == 0x4
 
 #define LM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-// Slot of 16-byte chunk c of an operand row in LDS: c ^ lm_swz(row). Rows are 64
-// bytes (4 chunks) unpadded, as the direct-to-LDS loads write 1 KB per wave
-// contiguously; XOR with bits 2-3 of the row makes the MFMA fragment reads (32 rows,
-// one chunk) free of bank conflicts on gfx950 (measured with SQ_LDS_BANK_CONFLICT:
-// 0 per ds_read_b128, against 4 for bits 1-2 and 12 unswizzled).
-__device__ __forceinline__ int lm_swz(int row) { return (row >> 2) & 3; }
+// Slot of 16-byte chunk c of an operand row in LDS: c ^ lm_swz(row). Rows are 128
+// bytes (8 chunks) unpadded, as the direct-to-LDS loads write 1 KB per instruction
+// contiguously. Two rows share one 256-byte span of the 64 banks, so XOR with bits
+// 1-3 of the row spreads the 16 rows of an MFMA fragment read that share a chunk
+// over 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int lm_swz(int row) { return (row >> 1) & 7; }
 
 // Tile order: work item p -> (token tile, vocab tile). Consecutive workgroup ids
 // are dealt round-robin to the 8 XCDs, so ids are first regrouped per XCD; within
@@ -105,7 +101,7 @@ __device__ __forceinline__ void lm_barrier() {
 // which fill the register file). Result layout of a 32 x 32 block:
 // lane l holds token column l%32 and vocab rows 8*(r/4) + 4*(l/32) + r%4, r < 16.
 // Operands stream global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging)
-// through NST stages of BK hidden columns.
+// through two stages of BK hidden columns.
 template <int MODE>
 __global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
 lm_tile_kernel(LmTileArgs a) {
@@ -128,33 +124,36 @@ lm_tile_kernel(LmTileArgs a) {
   const __amdgpu_buffer_rsrc_t rh =
       row_rsrc(reinterpret_cast<const char*>(a.A) + static_cast<int64_t>(m0) * rowbytes, rows_h * rowbytes);
 
-  // Direct-to-LDS loads: wave w fills rows 16*(2w+q) + lane/4, q < 2, of each operand;
-  // lane writes LDS slot lane%4 of its row, which holds chunk (lane%4) ^ swz(row).
-  uint32_t doff[2];
+  // Direct-to-LDS loads: wave w fills rows 8*(4w+q) + lane/8, q < 4, of each operand;
+  // lane writes LDS slot lane%8 of its row, which holds chunk (lane%8) ^ swz(row).
+  uint32_t doff[4];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int row = 16 * (2 * wave + q) + (lane >> 2);
-    doff[q] = static_cast<uint32_t>(row) * rowbytes + 16u * static_cast<uint32_t>((lane & 3) ^ lm_swz(row));
+  for (int q = 0; q < 4; ++q) {
+    const int row = 8 * (4 * wave + q) + (lane >> 3);
+    doff[q] = static_cast<uint32_t>(row) * rowbytes + 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
   }
   auto issue = [&](int st, int buf) {
     char* base = smem + buf * kStageBytes;
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (2 * wave + q) * 1024), 16, doff[q] + koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (2 * wave + q) * 1024), 16, doff[q] + koff,
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (4 * wave + q) * 1024), 16, doff[q] + koff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (4 * wave + q) * 1024), 16, doff[q] + koff,
                                                0, 0, 0);
     }
   };
 
-  // Fragment reads: row (lane%32) of each 32-row block, chunk 2*kk + lane/32. The
-  // swizzle depends on lane%32 only, so one offset per k-step serves every block.
+  // Fragment reads: row (lane%32) of each 32-row block, chunk 2*kk + lane/32 for
+  // k-step kk < 4. The swizzle depends on lane%32 only, so one offset per k-step
+  // serves every block.
   const int sw = lm_swz(lane & 31);
-  const int fo0 = 16 * ((0 + (lane >> 5)) ^ sw), fo1 = 16 * ((2 + (lane >> 5)) ^ sw);
+  int fo[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) fo[kk] = 16 * ((2 * kk + (lane >> 5)) ^ sw);
   const int offA = (wv * 128 + (lane & 31)) * ROWB, offB = kOpBytes + (wt * 64 + (lane & 31)) * ROWB;
   bf16x8 af[2][4], bfr[2][NJ];
   auto fload = [&](int set, int st, int kk) {
-    const char* base = smem + (st % NST) * kStageBytes + (kk ? fo1 : fo0);
+    const char* base = smem + (st % NST) * kStageBytes + fo[kk];
 #pragma unroll
     for (int i = 0; i < 4; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(base + offA + i * 32 * ROWB);
 #pragma unroll
@@ -176,55 +175,70 @@ lm_tile_kernel(LmTileArgs a) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], bfr[set][j], acc[i][j], 0, 0, 0);
   };
 
-  // Pipeline: stage kb is read from LDS buffer kb % NST. Every iteration issues one
-  // stage (kb + NST - 1, clamped to the last stage past the end: an L2 hit into a
-  // buffer nobody reads), so NST - 3 later stages (4 loads per wave each) are in
-  // flight when a stage is waited for: vmcnt(4 (NST - 3)), then the barrier makes
-  // every wave's loads of it visible. Branch-free, so the compiler's LDS waits stay
-  // exact.
+  // Pipeline: stage kb is read from LDS buffer kb % 2 while stage kb + 1 loads into
+  // the other one (8 direct-to-LDS loads per wave; past the end the last stage is
+  // reloaded into a buffer nobody reads, an L2 hit). Each stage ends with vmcnt(0)
+  // and one barrier, which makes every wave's loads of the next stage visible and
+  // frees the buffer just read. Branch-free, so the compiler's LDS waits stay exact.
+  // With two waves per SIMD covering each other's waits, 64-deep stages (one barrier
+  // per 64 hidden columns, 64 KB in flight) measured 6% faster on config 5 than
+  // 32-deep ones with three in flight.
   // Issue order: one memory instruction per MFMA. The wave issues in order, so a
-  // burst of the stage's direct-to-LDS loads right after the barrier held the
-  // MFMAs behind it whenever the memory pipeline pushed back; one load (or
-  // fragment read) between consecutive MFMAs measured 6% faster on config 5
-  // (11.72 -> 11.04 ms per forward launch).
+  // burst of the stage's direct-to-LDS loads right after the barrier held the MFMAs
+  // behind it whenever the memory pipeline pushed back; one load (or fragment read)
+  // between consecutive MFMAs measured 6% faster on config 5.
   const int nk = a.H / BK;
-#pragma unroll
-  for (int st = 0; st < NST - 1; ++st) issue(min(st, nk - 1), st);
-  __builtin_amdgcn_s_waitcnt(kWaitPrologue);
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(kWaitStage);
   lm_barrier();
   fload(0, 0, 0);
-  for (int kb = 0; kb + 1 < nk; ++kb) {
+  // Per k-step and wave: 6 fragment reads (4 W, 2 hidden) and 8 MFMAs; the stage's
+  // 8 loads are spread over the first k-step's MFMAs.
+  for (int kb = 0; kb < nk; ++kb) {
+    // Buffer (kb + 1) % 2 held stage kb - 1, whose reads all completed before the
+    // last barrier; past the end the last stage is reloaded into it (nobody reads it).
+    issue(min(kb + 1, nk - 1), (kb + 1) & 1);
     fload(1, kb, 1);
     mfmas(0);
 #pragma unroll
     for (int q = 0; q < 6; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a DS read of k-step 1
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 0
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);    // the rest of k-step 0
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitLoop);                // stage kb+1 landed
-    lm_barrier();
-    // Buffer (kb + NST - 1) % NST held stage kb - 1, whose reads all completed before
-    // this barrier.
-    issue(min(kb + NST - 1, nk - 1), (kb + NST - 1) % NST);
-    fload(0, kb + 1, 0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    fload(0, kb, 2);
     mfmas(1);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a load of the stage
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 1
+    for (int q = 0; q < 6; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    fload(1, kb, 3);
+    mfmas(0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a DS read of the next k-step 0
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 1
+    for (int q = 0; q < 6; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);    // the rest of the next k-step 0
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitStage);               // stage kb+1 landed
+    lm_barrier();
+    fload(0, min(kb + 1, nk - 1), 0);
+    mfmas(1);
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   }
-  fload(1, nk - 1, 1);
-  mfmas(0);
-  mfmas(1);
   // Drain the trailing loads before any LDS reuse (the backward epilogue).
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
