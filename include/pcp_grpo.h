@@ -241,6 +241,22 @@ int pcp_grpo_advantages(pcp_ctx* ctx, const float* rewards, int64_t n, int64_t g
  * (graph_builder.zig:302-426). */
 int pcp_grpo_loss_fwd_bwd(pcp_ctx* ctx, const pcp_grpo_args* a);
 
+/* Allocation-free variant of pcp_grpo_loss_fwd_bwd. It has no counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments, results and
+ * error codes as pcp_grpo_loss_fwd_bwd, but it calls no hipMalloc / hipFree and makes
+ * no host allocation. Its work buffers (advantages, per-sequence lengths and sums, the
+ * loss, the row kernel's counter and, when a->token_loss is NULL, the per-token
+ * losses) live in one static device array of PCP_NOALLOC_SCRATCH_BYTES per GPU, which
+ * that GPU holds until the process ends. A request needing more than the array,
+ *   4*round256(4*n_seq) + 512 + (token_loss ? 0 : round256(4*n_seq*tok_seq_stride)),
+ * fails with PCP_ERR_OVERFLOW before any device work; passing token_loss removes the
+ * per-token part. Every call on one GPU shares that GPU's array, which keeps the last
+ * call's contents: calls that may overlap on one GPU (other streams or contexts) race
+ * and must be ordered by the caller. */
+#define PCP_NOALLOC_SCRATCH_BYTES (4u << 20)
+int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
+
 /*
  * a6: fused LM-head + GRPO loss (the LM head of tools/export_qwen_forward.py:146-147
  * and its VJP, src/autodiff/vjp_rules.zig:426-497). Tokens use the aligned layout:

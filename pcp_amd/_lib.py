@@ -45,6 +45,7 @@ class LossMode(enum.IntEnum):
 FLAG_ASYNC = 0x1
 FLAG_NO_ZERO_FILL = 0x2
 FLAG_FORCE_STREAMING = 0x4
+NOALLOC_SCRATCH_BYTES = 4 << 20
 IGNORE_INDEX = -100
 
 STATUS = {
@@ -143,6 +144,7 @@ SIGNATURES = {
     "pcp_grpo_logprob_fwd": (_I, [_VP, ctypes.POINTER(GrpoArgs)]),
     "pcp_grpo_advantages": (_I, [_VP, _VP, _I64, _I64, _F, _VP, _VP]),
     "pcp_grpo_loss_fwd_bwd": (_I, [_VP, ctypes.POINTER(GrpoArgs)]),
+    "pcp_grpo_loss_fwd_bwd_noalloc": (_I, [_VP, ctypes.POINTER(GrpoArgs)]),
     "pcp_lmhead_args_init": (None, [ctypes.POINTER(LmheadArgs)]),
     "pcp_grpo_lmhead_fwd_bwd": (_I, [_VP, ctypes.POINTER(LmheadArgs)]),
     "pcp_profile_start": (_I, [_VP, _I]),

@@ -5,8 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
-#include <set>
-#include <string>
+#include <cstring>
 #include <vector>
 
 #include "pcp_grpo.h"
@@ -18,12 +17,16 @@ struct HostStager;
 struct pcp_ctx {
   int device = 0;
   int backend = PCP_BACKEND_ROCM;
-  std::string last_error;
+  char last_error[512] = {};      // fixed buffer: reporting an error allocates nothing
   int* d_err = nullptr;          // device error word (kErr* bits)
   int* d_next_row = nullptr;     // row counter of the persistent row kernel (same allocation)
   void* scratch = nullptr;       // per-call work buffers, grown on demand
   size_t scratch_bytes = 0;
-  std::set<hipStream_t> pending;  // streams holding PCP_FLAG_ASYNC work
+  // Streams holding PCP_FLAG_ASYNC work (a fixed set, so recording one allocates nothing).
+  static constexpr int kMaxPending = 32;
+  hipStream_t pending[kMaxPending] = {};
+  int n_pending = 0;
+  void* noalloc_scratch = nullptr;  // this device's static work array (pcp_grpo_loss_fwd_bwd_noalloc)
   // Row-kernel timing (pcp_profile_start/stop): event pairs, next free pair.
   std::vector<hipEvent_t> prof_start, prof_stop;
   int prof_used = 0;
@@ -36,18 +39,27 @@ struct pcp_ctx {
 
 namespace pcp {
 
-// Last failure message of the calling thread; pcp_last_error(NULL) returns it,
-// so argument errors are reported even when no context exists.
-std::string& thread_error();
+// Last failure message of the calling thread (a thread-local 512-byte buffer);
+// pcp_last_error(NULL) returns it, so argument errors are reported even when no
+// context exists.
+char* thread_error();
+constexpr size_t kErrLen = 512;
+
+// Copy the calling thread's last message into ctx (argument errors found before the
+// context was known).
+inline void copy_thread_error(pcp_ctx* ctx) {
+  if (!ctx) return;
+  std::strncpy(ctx->last_error, thread_error(), kErrLen - 1);
+  ctx->last_error[kErrLen - 1] = 0;
+}
 
 inline int fail(pcp_ctx* ctx, int code, const char* fmt, ...) {
-  char buf[512];
+  char* buf = thread_error();
   va_list ap;
   va_start(ap, fmt);
-  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  std::vsnprintf(buf, kErrLen, fmt, ap);
   va_end(ap);
-  thread_error() = buf;
-  if (ctx) ctx->last_error = buf;
+  copy_thread_error(ctx);
   return code;
 }
 
@@ -77,6 +89,11 @@ int ensure_scratch(pcp_ctx* ctx, size_t bytes);
 
 // After synchronising: read and clear the device error word, map it to a status.
 int collect_device_errors(pcp_ctx* ctx);
+
+// Record a stream that holds PCP_FLAG_ASYNC work for pcp_sync. When the fixed set is
+// full the stream is synchronised at once instead (its errors still reach pcp_sync
+// through the error word).
+int add_pending(pcp_ctx* ctx, hipStream_t st);
 
 // Release the context's BLAS handle (defined with the LM-head path).
 void release_blas(pcp_ctx* ctx);

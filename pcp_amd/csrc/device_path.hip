@@ -9,6 +9,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 
 #include "context.hpp"
 #include "host_transfer.hpp"
@@ -18,9 +19,20 @@
 
 namespace pcp {
 
-std::string& thread_error() {
-  static thread_local std::string msg;
+char* thread_error() {
+  static thread_local char msg[kErrLen];
   return msg;
+}
+
+int add_pending(pcp_ctx* ctx, hipStream_t st) {
+  for (int i = 0; i < ctx->n_pending; ++i)
+    if (ctx->pending[i] == st) return PCP_OK;
+  if (ctx->n_pending < pcp_ctx::kMaxPending) {
+    ctx->pending[ctx->n_pending++] = st;
+    return PCP_OK;
+  }
+  hipError_t e = hipStreamSynchronize(st);
+  return e == hipSuccess ? PCP_OK : hip_fail(ctx, e, "hipStreamSynchronize");
 }
 
 int ensure_scratch(pcp_ctx* ctx, size_t bytes) {
@@ -62,7 +74,37 @@ int collect_device_errors(pcp_ctx* ctx) {
   return fail(ctx, PCP_ERR_NONFINITE, "a live row has a non-finite log-sum-exp (NaN/Inf logits)");
 }
 
+// Work buffers of pcp_grpo_loss_fwd_bwd_noalloc: one array per GPU, which holds it
+// until the process ends. Host code never passes this name to a kernel (on the host it
+// is only a stand-in for the symbol): pcp_init resolves the device address of each
+// GPU's copy with hipGetSymbolAddress and the entry point uses that address.
+static __device__ __align__(256) unsigned char scratch[PCP_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch array; the caller has made `device` current.
+int resolve_noalloc_scratch(int device, void** out) {
+  *out = nullptr;
+  if (device < 0 || device >= kMaxDevices)
+    return fail(nullptr, PCP_ERR_UNSUPPORTED, "device ordinal %d: the allocation-free path serves ordinals < %d",
+                device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return fail(nullptr, PCP_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    }
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return PCP_OK;
+}
 
 // Resolved geometry of a request.
 struct Geo {
@@ -137,39 +179,52 @@ inline size_t round256(size_t b) { return (b + 255) & ~static_cast<size_t>(255);
 
 int finish(pcp_ctx* ctx, const pcp_grpo_args* a, hipStream_t st) {
   if (a->flags & PCP_FLAG_ASYNC) {
-    ctx->pending.insert(st);
-    return PCP_OK;
+    return add_pending(ctx, st);
   }
   hipError_t e = hipStreamSynchronize(st);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
   return collect_device_errors(ctx);
 }
 
-int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op) {
+// noalloc: take the work buffers from the device's static scratch array instead of
+// the context's grow-only buffer (no allocation of any kind on this path).
+int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   Geo g;
   int rc = validate(a, op, &g);
   if (rc != PCP_OK) {
-    if (ctx) ctx->last_error = thread_error();
+    if (ctx) copy_thread_error(ctx);
     return rc;
   }
+
+  // Scratch: adv | seq_len | seq_scale | seq_val | loss | row counter | token_loss.
+  const size_t sv = round256(sizeof(float) * g.n_seq);
+  const bool need_tl = (op == kLoss) && a->token_loss == nullptr;
+  const size_t tl_bytes = need_tl ? round256(sizeof(float) * g.n_seq * g.tstride) : 0;
+  const size_t need = 4 * sv + 512 + tl_bytes;
+  if (noalloc && need > PCP_NOALLOC_SCRATCH_BYTES)
+    return fail(ctx, PCP_ERR_OVERFLOW,
+                "the allocation-free call needs %zu bytes of work space, more than its %u-byte array: pass "
+                "token_loss (n_seq*tok_seq_stride floats) or use pcp_grpo_loss_fwd_bwd",
+                need, static_cast<unsigned>(PCP_NOALLOC_SCRATCH_BYTES));
   if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  if (noalloc && !ctx->noalloc_scratch)
+    return fail(ctx, PCP_ERR_DEVICE, "the scratch array of device %d was not resolved at pcp_init", ctx->device);
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
   hipStream_t st = static_cast<hipStream_t>(a->stream);
 
-  // Scratch: adv | seq_len | seq_scale | seq_val | loss | token_loss.
-  const size_t sv = round256(sizeof(float) * g.n_seq);
-  const bool need_tl = (op == kLoss) && a->token_loss == nullptr;
-  const size_t tl_bytes = need_tl ? round256(sizeof(float) * g.n_seq * g.tstride) : 0;
-  rc = ensure_scratch(ctx, 4 * sv + 256 + tl_bytes);
-  if (rc != PCP_OK) return rc;
-  char* sp = static_cast<char*>(ctx->scratch);
+  if (!noalloc && (rc = ensure_scratch(ctx, need)) != PCP_OK) return rc;
+  char* sp = static_cast<char*>(noalloc ? ctx->noalloc_scratch : ctx->scratch);
   float* s_adv = reinterpret_cast<float*>(sp);
   float* s_len = reinterpret_cast<float*>(sp + sv);
   float* s_scale = reinterpret_cast<float*>(sp + 2 * sv);
   float* s_val = reinterpret_cast<float*>(sp + 3 * sv);
   float* s_loss = reinterpret_cast<float*>(sp + 4 * sv);
-  float* s_tl = need_tl ? reinterpret_cast<float*>(sp + 4 * sv + 256) : a->token_loss;
+  // The persistent row kernel's counter: a one-thread kernel zeroes it before each
+  // launch. The allocation-free path keeps it in the shared array, the other path in
+  // the context's own allocation.
+  int* s_next = noalloc ? reinterpret_cast<int*>(sp + 4 * sv + 256) : ctx->d_next_row;
+  float* s_tl = need_tl ? reinterpret_cast<float*>(sp + 4 * sv + 512) : a->token_loss;
 
   RowArgs ra;
   std::memset(&ra, 0, sizeof(ra));
@@ -177,7 +232,7 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op) {
   ra.ids = a->ids;
   ra.mask = a->mask;
   ra.err = ctx->d_err;
-  ra.next_row = ctx->d_next_row;
+  ra.next_row = s_next;
   ra.nrows = g.nrows;
   ra.vocab = g.vocab;
   ra.rows = g.rows;
@@ -300,6 +355,10 @@ int pcp_init(int backend, int device_ordinal, pcp_ctx** out) {
     delete c;
     return hip_fail(nullptr, e, "initialising the error word");
   }
+  // Resolve this device's copy of the allocation-free path's scratch array (once per
+  // device, with the device current). A failure here only disables that entry point,
+  // which then reports it.
+  if (resolve_noalloc_scratch(device_ordinal, &c->noalloc_scratch) != PCP_OK) copy_thread_error(c);
   *out = c;
   return PCP_OK;
 }
@@ -372,27 +431,27 @@ void pcp_destroy(pcp_ctx* ctx) {
 int pcp_get_backend_type(const pcp_ctx* ctx) { return ctx ? ctx->backend : PCP_ERR_INVALID_ARG; }
 
 const char* pcp_last_error(const pcp_ctx* ctx) {
-  return ctx ? ctx->last_error.c_str() : thread_error().c_str();
+  return ctx ? ctx->last_error : thread_error();
 }
 
 int pcp_sync(pcp_ctx* ctx) {
   if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
-  for (hipStream_t s : ctx->pending) {
-    e = hipStreamSynchronize(s);
-    if (e != hipSuccess) {
-      ctx->pending.clear();
-      return hip_fail(ctx, e, "hipStreamSynchronize");
-    }
+  const int n = ctx->n_pending;
+  ctx->n_pending = 0;
+  for (int i = 0; i < n; ++i) {
+    e = hipStreamSynchronize(ctx->pending[i]);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
   }
-  ctx->pending.clear();
   return collect_device_errors(ctx);
 }
 
 int pcp_grpo_logprob_fwd(pcp_ctx* ctx, const pcp_grpo_args* a) { return run(ctx, a, kLogprob); }
 
 int pcp_grpo_loss_fwd_bwd(pcp_ctx* ctx, const pcp_grpo_args* a) { return run(ctx, a, kLoss); }
+
+int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a) { return run(ctx, a, kLoss, true); }
 
 int pcp_grpo_advantages(pcp_ctx* ctx, const float* rewards, int64_t n, int64_t group_size,
                         float std_eps, float* adv, void* stream) {

@@ -492,7 +492,7 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
   if (rc != PCP_OK) goto arg_error;
   if (f == kLmhead) {
     rc = execute_lmhead(ctx, in, n_out, out_data, out_nbytes);
-    if (rc != PCP_OK && ctx) ctx->last_error = thread_error();
+    if (rc != PCP_OK && ctx) copy_thread_error(ctx);
     return rc;
   }
 
@@ -659,7 +659,7 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
   }
 
 arg_error:
-  if (ctx) ctx->last_error = thread_error();
+  if (ctx) copy_thread_error(ctx);
   return rc;
 }
 

@@ -77,7 +77,7 @@ int blas_status(pcp_ctx* ctx, rocblas_status s, const char* what) {
 int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   int rc = validate_lm(a);
   if (rc != PCP_OK) {
-    if (ctx) ctx->last_error = thread_error();
+    if (ctx) copy_thread_error(ctx);
     return rc;
   }
   if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
@@ -276,8 +276,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   }
 
   if (a->flags & PCP_FLAG_ASYNC) {
-    ctx->pending.insert(st);
-    return PCP_OK;
+    return add_pending(ctx, st);
   }
   if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
   return collect_device_errors(ctx);

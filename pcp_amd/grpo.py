@@ -125,12 +125,14 @@ def grpo_loss_fwd_bwd(logits: torch.Tensor, ids: torch.Tensor, mask: torch.Tenso
                       want_dlogits: bool = True, dlogits: torch.Tensor | None = None,
                       dlogits_dtype: torch.dtype | None = None, zero_fill: bool = True,
                       force_streaming: bool = False, outputs: GrpoOutputs | None = None,
-                      sync: bool = True, stream=None, ctx: Context | None = None) -> GrpoOutputs:
+                      sync: bool = True, stream=None, ctx: Context | None = None,
+                      noalloc: bool = False) -> GrpoOutputs:
     """Fused loss forward + dlogits backward (pcp_grpo_loss_fwd_bwd).
 
     Pass ``outputs`` (from a previous call of the same shape) to reuse its buffers
     instead of allocating: the benchmark does this so the timed region only runs
-    the kernels.
+    the kernels. ``noalloc`` calls pcp_grpo_loss_fwd_bwd_noalloc, whose work buffers
+    are the GPU's static array instead of the context's.
     """
     ctx = ctx or default_context(logits.device.index or 0)
     S, LS, V, TS, rows, tok_offset = _layout(logits, ids, rows, tok_offset)
@@ -164,7 +166,8 @@ def grpo_loss_fwd_bwd(logits: torch.Tensor, ids: torch.Tensor, mask: torch.Tenso
     a.flags = ((0 if sync else _lib.FLAG_ASYNC) | (0 if zero_fill else _lib.FLAG_NO_ZERO_FILL)
                | (_lib.FLAG_FORCE_STREAMING if force_streaming else 0))
     a.stream = _stream_handle(stream)
-    check(lib().pcp_grpo_loss_fwd_bwd(ctx.handle, ctypes.byref(a)), ctx.handle)
+    fn = lib().pcp_grpo_loss_fwd_bwd_noalloc if noalloc else lib().pcp_grpo_loss_fwd_bwd
+    check(fn(ctx.handle, ctypes.byref(a)), ctx.handle)
     return outputs
 
 

@@ -168,6 +168,19 @@ def test_lmhead_argument_errors_without_device(mutate, code, text):
     assert "context is NULL" in L.pcp_last_error(None).decode()
 
 
+def test_noalloc_rejects_oversized_requests_without_device():
+    # The allocation-free entry point checks its work space against the static array
+    # before it needs a context: 2^20 + 1 per-token losses do not fit in 4 MiB.
+    a = _valid_args()
+    a.rows = (1 << 20) + 1
+    rc = _lib.lib().pcp_grpo_loss_fwd_bwd_noalloc(None, ctypes.byref(a))
+    assert rc == -9
+    assert b"allocation-free" in _lib.lib().pcp_last_error(None)
+    a.rows = 4
+    rc = _lib.lib().pcp_grpo_loss_fwd_bwd_noalloc(None, ctypes.byref(a))
+    assert rc == -1 and b"context is NULL" in _lib.lib().pcp_last_error(None)
+
+
 def test_valid_args_then_null_context():
     L = _lib.lib()
     a = _valid_args()
