@@ -46,15 +46,79 @@ def algorithmic_bytes(cfg, lengths, mode_clip_kl: bool, zero_fill: bool = True) 
     return {"live_rows": live, "rows": rows, "per_live": per_live, "per_dead": per_dead, "bytes": total}
 
 
-def cpu_baseline(inp, cfg, mode_clip_kl: bool, budget_s: float = 12.0, chunk: int = 256) -> dict:
-    """Time the CPU oracle (fp32 reference op order, all threads) on consecutive row
-    chunks of the same inputs until about budget_s of compute has been spent."""
+def host_cpu_info() -> dict:
+    """The host the CPU baseline runs on: nproc, the CPUs this process may use, the
+    OpenMP thread count it was given and the /proc/cpuinfo model name."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    return {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "omp_num_threads": int(omp) if omp.isdigit() else None, "cpu_model": model}
+
+
+def cpu_threads() -> tuple[int, str]:
+    """Threads for the multi-threaded CPU baseline: every CPU this process may run on,
+    capped by OMP_NUM_THREADS when the host sets it (the GPU box allots each GPU job a
+    fixed share of host threads and sets OMP_NUM_THREADS to it; more would oversubscribe
+    CPUs that belong to other jobs)."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and 0 < int(omp) < aff:
+        return int(omp), f"OMP_NUM_THREADS={omp}: the host's thread allotment for this job ({aff} CPUs visible)"
+    return aff, "every CPU this process may run on"
+
+
+CPU_REPS = 5
+
+
+def median_timing(fn, reps: int = CPU_REPS) -> tuple[float, list]:
+    """One untimed warm-up call, then `reps` timed calls: (median seconds, all times)."""
+    import statistics
+
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def protocol_record(value, unit, threads, reason, kind, sample, value_1t=None, times=None, times_1t=None,
+                    note_1t="") -> dict:
+    """A cpu_baseline record: the median over CPU_REPS timed repetitions after a warm-up
+    at `threads` threads, the same on one thread, and the host it ran on."""
+    rec = {"value": value, "unit": unit, "cores": threads, "kind": kind, "sample": sample,
+           "threads_reason": reason, "warmup": 1, "reps": CPU_REPS, "statistic": "median"}
+    if value_1t is not None:
+        rec["value_1thread"] = value_1t
+    if times is not None:
+        rec["rep_seconds"] = [round(t, 6) for t in times]
+    if times_1t is not None:
+        rec["rep_seconds_1thread"] = [round(t, 6) for t in times_1t]
+    if note_1t:
+        rec["note_1thread"] = note_1t
+    rec.update(host_cpu_info())
+    return rec
+
+
+def cpu_baseline(inp, cfg, mode_clip_kl: bool, rows_mt: int = 2048, rows_1t: int = 256) -> dict:
+    """The CPU oracle (fp32 reference op order, OpenMP) on a fixed sample of the same
+    rows: rows_mt rows at the job's thread count and the first rows_1t of them on one
+    thread, each as a warm-up plus the median of CPU_REPS timed repetitions."""
     import numpy as np
     import torch
 
     from oracle import oracle as orc
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads, reason = cpu_threads()
     V, T = cfg.V, cfg.T
     flat = inp["logits"].view(-1, V)
     rflat = inp["ref_logits"].view(-1, V)
@@ -65,49 +129,52 @@ def cpu_baseline(inp, cfg, mode_clip_kl: bool, budget_s: float = 12.0, chunk: in
     Ls = orc.seq_lengths(mask, T, 0)
     old = inp["old_logp"].view(-1).cpu().numpy()
     nrows = flat.shape[0]
-    # Visit rows in a fixed pseudo-random order so the sample has the workload's live fraction.
-    order = np.random.default_rng(0).permutation(nrows)
-    spent, done, live_done = 0.0, 0, 0
-    while spent < budget_s and done < nrows:
-        idx = np.sort(order[done:done + chunk])
-        ti = torch.as_tensor(idx, device=flat.device)
-        L = flat.index_select(0, ti)
-        R = rflat.index_select(0, ti)
-        if L.dtype == torch.bfloat16:
-            L = L.view(torch.int16).cpu().numpy().view(np.uint16)
-            R = R.view(torch.int16).cpu().numpy().view(np.uint16)
-            dt = orc.BF16
-        else:
-            L, R, dt = L.cpu().numpy(), R.cpu().numpy(), orc.F32
-        seq = idx // T
-        t0 = time.perf_counter()
-        orc.grpo_rows(L, ids[idx], w[idx], adv[seq], Ls[seq], float(cfg.S), ref_logits=R if mode_clip_kl else None,
-                      old_logp=old[idx], loss_mode=orc.CLIP_KL if mode_clip_kl else orc.REINFORCE,
-                      clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, precision=orc.REF_F32, dtype=dt,
-                      nthreads=threads)
-        spent += time.perf_counter() - t0
-        done += len(idx)
-        live_done += int((w[idx] != 0).sum())
-    return {"value": live_done / spent, "unit": "valid tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{done} of {nrows} rows ({live_done} valid) in {spent:.1f} s: oracle fp32 reference-op-order "
-                      f"fwd+bwd (grpo_oracle.cpp, OpenMP {threads} threads)"}
+    # A fixed pseudo-random sample of rows, so it has the workload's live fraction.
+    idx = np.sort(np.random.default_rng(0).permutation(nrows)[:min(rows_mt, nrows)])
+    ti = torch.as_tensor(idx, device=flat.device)
+    L, R = flat.index_select(0, ti), rflat.index_select(0, ti)
+    if L.dtype == torch.bfloat16:
+        L = L.view(torch.int16).cpu().numpy().view(np.uint16)
+        R = R.view(torch.int16).cpu().numpy().view(np.uint16)
+        dt = orc.BF16
+    else:
+        L, R, dt = L.cpu().numpy(), R.cpu().numpy(), orc.F32
+    seq = idx // T
+
+    def run(n, nthreads):
+        orc.grpo_rows(L[:n], ids[idx[:n]], w[idx[:n]], adv[seq[:n]], Ls[seq[:n]], float(cfg.S),
+                      ref_logits=R[:n] if mode_clip_kl else None, old_logp=old[idx[:n]],
+                      loss_mode=orc.CLIP_KL if mode_clip_kl else orc.REINFORCE, clip_eps=cfg.clip_eps,
+                      kl_beta=cfg.kl_beta, precision=orc.REF_F32, dtype=dt, nthreads=nthreads)
+
+    n_mt, n_1t = len(idx), min(rows_1t, len(idx))
+    live_mt, live_1t = int((w[idx] != 0).sum()), int((w[idx[:n_1t]] != 0).sum())
+    med, times = median_timing(lambda: run(n_mt, threads))
+    med1, times1 = median_timing(lambda: run(n_1t, 1))
+    return protocol_record(
+        live_mt / med, "valid tokens/s", threads, reason, "port",
+        f"{n_mt} of {nrows} rows ({live_mt} valid), a fixed seeded sample; one thread: the first {n_1t} of them "
+        f"({live_1t} valid). Oracle fp32 reference-op-order fwd+bwd (grpo_oracle.cpp, OpenMP)",
+        value_1t=live_1t / med1, times=times, times_1t=times1)
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, 2.5 PFLOP/s
 
 
-def cpu_baseline_lmhead(inp, cfg, mode_clip_kl: bool, budget_s: float = 12.0, chunk: int = 64) -> dict:
-    """Time a CPU port of the fused LM-head step on token chunks of the same inputs:
+def cpu_baseline_lmhead(inp, cfg, mode_clip_kl: bool, tokens_mt: int = 64, tokens_1t: int = 8) -> dict:
+    """A CPU port of the fused LM-head step on a fixed token sample of the same inputs:
     fp32 logits hidden.W^T (and W_ref) on BLAS, the oracle's loss rows with dlogits
-    (fp32, reference op order), then dhidden = D.W and dW += D^T.hidden on BLAS."""
+    (fp32, reference op order), then dhidden = D.W and dW += D^T.hidden on BLAS. As
+    cpu_baseline: tokens_mt tokens at the job's thread count, tokens_1t on one thread,
+    each a warm-up plus the median of CPU_REPS repetitions."""
     import numpy as np
     import torch
     from threadpoolctl import threadpool_limits
 
     from oracle import oracle as orc
 
-    threads = min(os.cpu_count() or 1, 16)
-    V, T = cfg.V, cfg.T
+    threads, reason = cpu_threads()
+    T = cfg.T
     W = inp["weight"].float().cpu().numpy()
     Wr = inp["ref_weight"].float().cpu().numpy() if mode_clip_kl else None
     h_all = inp["hidden"]
@@ -118,28 +185,31 @@ def cpu_baseline_lmhead(inp, cfg, mode_clip_kl: bool, budget_s: float = 12.0, ch
     Ls = orc.seq_lengths(mask, T, 0)
     old = inp["old_logp"].view(-1).cpu().numpy()
     dW = np.zeros_like(W)
-    order = np.random.default_rng(0).permutation(len(ids))
-    spent, done, live_done = 0.0, 0, 0
-    with threadpool_limits(threads):
-        while spent < budget_s and done < len(ids):
-            idx = np.sort(order[done:done + chunk])
-            hc = h_all.index_select(0, torch.as_tensor(idx, device=h_all.device)).float().cpu().numpy()
-            seq = idx // T
-            t0 = time.perf_counter()
+    idx = np.sort(np.random.default_rng(0).permutation(len(ids))[:tokens_mt])
+    hc_all = h_all.index_select(0, torch.as_tensor(idx, device=h_all.device)).float().cpu().numpy()
+    seq = idx // T
+
+    def run(n, nthreads):
+        with threadpool_limits(nthreads):
+            hc = hc_all[:n]
             Lc = hc @ W.T
             Rc = hc @ Wr.T if mode_clip_kl else None
-            r = orc.grpo_rows(Lc, ids[idx], w[idx], adv[seq], Ls[seq], float(cfg.S), ref_logits=Rc,
-                              old_logp=old[idx], loss_mode=orc.CLIP_KL if mode_clip_kl else orc.REINFORCE,
+            r = orc.grpo_rows(Lc, ids[idx[:n]], w[idx[:n]], adv[seq[:n]], Ls[seq[:n]], float(cfg.S), ref_logits=Rc,
+                              old_logp=old[idx[:n]], loss_mode=orc.CLIP_KL if mode_clip_kl else orc.REINFORCE,
                               clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, precision=orc.REF_F32, dtype=orc.F32,
-                              nthreads=threads)
+                              nthreads=nthreads)
             _dh = r.dlogits @ W
-            dW += r.dlogits.T @ hc
-            spent += time.perf_counter() - t0
-            done += len(idx)
-            live_done += int((w[idx] != 0).sum())
-    return {"value": live_done / spent, "unit": "valid tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{done} of {len(ids)} tokens ({live_done} valid) in {spent:.1f} s: fp32 BLAS logits + "
-                      f"oracle loss rows (reference op order) + fp32 BLAS dhidden/dW, {threads} threads"}
+            dW[...] += r.dlogits.T @ hc
+
+    n1 = min(tokens_1t, len(idx))
+    live_mt, live_1t = int((w[idx] != 0).sum()), int((w[idx[:n1]] != 0).sum())
+    med, times = median_timing(lambda: run(len(idx), threads))
+    med1, times1 = median_timing(lambda: run(n1, 1))
+    return protocol_record(
+        live_mt / med, "valid tokens/s", threads, reason, "port",
+        f"{len(idx)} of {len(ids)} tokens ({live_mt} valid), a fixed seeded sample; one thread: the first {n1} "
+        f"({live_1t} valid). fp32 BLAS logits + oracle loss rows (reference op order) + fp32 BLAS dhidden/dW",
+        value_1t=live_1t / med1, times=times, times_1t=times1)
 
 
 def bench_lmhead(args) -> None:
@@ -228,7 +298,7 @@ def bench_lmhead(args) -> None:
         with open(tfile) as f:
             line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline_lmhead(inp, cfg, clip, budget_s=args.cpu_budget)
+        line["cpu_baseline"] = cpu_baseline_lmhead(inp, cfg, clip)
     print(json.dumps(line), flush=True)
 
 
@@ -297,12 +367,11 @@ def bench_nesterov(args) -> None:
         from oracle import oracle as orc
         n = P
         ps, vs, gs = (np.random.default_rng(0).standard_normal(n).astype(np.float32) for _ in range(3))
-        t0 = time.perf_counter()
-        orc.nesterov(ps, vs, gs, 1e-5, 0.9)
-        dt = time.perf_counter() - t0
-        line["cpu_baseline"] = {"value": n / dt, "unit": "params/s", "cores": 1, "kind": "port",
-                                "sample": f"{n} params in {dt:.2f} s: oracle f32 loop of nesterov.zig:86-97 "
-                                          "(step_oracle.cpp), one thread, as the reference's host loop"}
+        med, times = median_timing(lambda: orc.nesterov(ps, vs, gs, 1e-5, 0.9))
+        line["cpu_baseline"] = protocol_record(
+            n / med, "params/s", 1, "the reference's host loop (nesterov.zig:86-97) is single-threaded", "port",
+            f"{n} params: oracle f32 loop of nesterov.zig:86-97 (step_oracle.cpp), one thread",
+            value_1t=n / med, times=times)
     print(json.dumps(line), flush=True)
     opt.close()
 
@@ -347,13 +416,16 @@ def bench_sample(args) -> None:
     if not args.no_cpu_baseline:
         from oracle import oracle as orc
         xh, uh = x.cpu().numpy(), u.cpu().numpy()
-        t0 = time.perf_counter()
-        for r in range(R):
-            orc.sample(xh[r], T, float(uh[r]))
-        dt = time.perf_counter() - t0
-        line["cpu_baseline"] = {"value": R / dt, "unit": "sampled tokens/s", "cores": 1, "kind": "port",
-                                "sample": f"{R} rows in {dt:.2f} s: oracle f32 loop of math.zig:21-58 "
-                                          "(step_oracle.cpp), one thread, logits already in host memory"}
+
+        def run():
+            for r in range(R):
+                orc.sample(xh[r], T, float(uh[r]))
+
+        med, times = median_timing(run)
+        line["cpu_baseline"] = protocol_record(
+            R / med, "sampled tokens/s", 1, "the reference's sampler loop (math.zig:21-58) is single-threaded",
+            "port", f"{R} rows: oracle f32 loop of math.zig:21-58 (step_oracle.cpp), one thread, logits already "
+                    "in host memory", value_1t=R / med, times=times)
     print(json.dumps(line), flush=True)
 
 
@@ -406,14 +478,12 @@ def bench_b64(args) -> None:
         with open(tfile) as f:
             line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
     if not args.no_cpu_baseline:
-        host = raw[:3 << 28].cpu().numpy().tobytes()
-        t0 = time.perf_counter()
-        base64.b64encode(host)
-        dt = time.perf_counter() - t0
-        line["cpu_baseline"] = {"value": len(host) / dt, "unit": "bytes/s (weights, encode)", "cores": 1,
-                                "kind": "port", "sample": f"{len(host)} weight bytes encoded in {dt:.2f} s by "
-                                                          "Python's base64 (C, one thread), standing for the "
-                                                          "reference's host std.base64 encoder"}
+        host = raw[:3 << 26].cpu().numpy().tobytes()
+        med, times = median_timing(lambda: base64.b64encode(host))
+        line["cpu_baseline"] = protocol_record(
+            len(host) / med, "bytes/s (weights, encode)", 1, "the reference's std.base64 encoder runs on one thread",
+            "port", f"{len(host)} weight bytes encoded by Python's base64 (C, one thread), standing for the "
+                    "reference's host std.base64 encoder", value_1t=len(host) / med, times=times)
     print(json.dumps(line), flush=True)
 
 
@@ -470,29 +540,32 @@ def bench_logprob(args) -> None:
     if not args.no_cpu_baseline:
         from oracle import oracle as orc
 
-        threads = min(os.cpu_count() or 1, 16)
+        threads, reason = cpu_threads()
         flat = inp["logits"].view(-1, cfg.V)
         ids = inp["ids"].view(-1).cpu().numpy()
         livei = np.nonzero(inp["mask"].view(-1).cpu().numpy() != 0)[0]
-        order = np.random.default_rng(0).permutation(livei)
-        spent, done, chunk = 0.0, 0, 256
-        while spent < args.cpu_budget and done < len(order):
-            idx = np.sort(order[done:done + chunk])
-            ti = torch.as_tensor(idx, device=dev)
-            for src in ([flat] if args.policy_only else [flat, inp["ref_logits"].view(-1, cfg.V)]):
-                blk = src.index_select(0, ti)
-                if blk.dtype == torch.bfloat16:
-                    host, dt = blk.view(torch.int16).cpu().numpy().view(np.uint16), orc.BF16
-                else:
-                    host, dt = blk.cpu().numpy(), orc.F32
-                t0 = time.perf_counter()
-                orc.logprob(host, ids[idx], dtype=dt, precision=orc.REF_F32, nthreads=threads)
-                spent += time.perf_counter() - t0
-            done += len(idx)
-        line["cpu_baseline"] = {"value": done / spent, "unit": "valid tokens/s", "cores": threads, "kind": "port",
-                                "sample": f"{done} of {live} valid rows in {spent:.1f} s: oracle fp32 "
-                                          f"reference-op-order log-softmax + gather of the {what} rows "
-                                          f"(grpo_oracle.cpp, OpenMP {threads} threads)"}
+        idx = np.sort(np.random.default_rng(0).permutation(livei)[:2048])
+        ti = torch.as_tensor(idx, device=dev)
+        blocks = []
+        for src in ([flat] if args.policy_only else [flat, inp["ref_logits"].view(-1, cfg.V)]):
+            blk = src.index_select(0, ti)
+            if blk.dtype == torch.bfloat16:
+                blocks.append((blk.view(torch.int16).cpu().numpy().view(np.uint16), orc.BF16))
+            else:
+                blocks.append((blk.cpu().numpy(), orc.F32))
+
+        def run(n, nthreads):
+            for host, dt in blocks:
+                orc.logprob(host[:n], ids[idx[:n]], dtype=dt, precision=orc.REF_F32, nthreads=nthreads)
+
+        n1 = min(256, len(idx))
+        med, times = median_timing(lambda: run(len(idx), threads))
+        med1, times1 = median_timing(lambda: run(n1, 1))
+        line["cpu_baseline"] = protocol_record(
+            len(idx) / med, "valid tokens/s", threads, reason, "port",
+            f"{len(idx)} of {live} valid rows, a fixed seeded sample (one thread: the first {n1}): oracle fp32 "
+            f"reference-op-order log-softmax + gather of the {what} rows (grpo_oracle.cpp, OpenMP)",
+            value_1t=n1 / med1, times=times, times_1t=times1)
     print(json.dumps(line), flush=True)
 
 
@@ -581,11 +654,15 @@ def main() -> None:
                          "b64: the UPDATE_WEIGHTS payload codec")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
+    ap.add_argument("--no-zero-fill", action="store_true",
+                    help="loss workload: leave the dlogits rows of masked and pad tokens unwritten "
+                         "(PCP_FLAG_NO_ZERO_FILL); algorithmic bytes then count live rows only")
+    ap.add_argument("--exact-bf16", action="store_true",
+                    help="loss workload: PCP_FLAG_EXACT_BF16 (no f16 softmax terms in the bf16 dlogits pass)")
     ap.add_argument("--policy-only", action="store_true", help="logprob workload: the policy rows only")
     ap.add_argument("--final-norm", action="store_true",
                     help="config 5: fuse the decoder's final RMSNorm (hidden = the last layer's output)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--copy-calibration-gib", type=float, default=0.0,
                     help="run one device-to-device copy of this many GiB first: under rocprofv3 --pmc its "
                          "FETCH_SIZE / WRITE_SIZE give the counters' scale factors")
@@ -638,7 +715,8 @@ def main() -> None:
     ctx = grpo.default_context(0)
     kw = dict(rewards=inp["rewards"], group_size=cfg.group, ref_logits=inp["ref_logits"] if clip else None,
               old_logp=inp["old_logp"], loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta,
-              force_streaming=args.force_streaming, ctx=ctx)
+              force_streaming=args.force_streaming, zero_fill=not args.no_zero_fill,
+              exact_bf16=args.exact_bf16, ctx=ctx)
     out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], **kw)  # allocates outputs
     for _ in range(args.warmup):
         grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], outputs=out, sync=False, **kw)
@@ -658,7 +736,7 @@ def main() -> None:
     check(lib().pcp_profile_stop(ctx.handle, ctypes.byref(n_l), ctypes.byref(tot)), ctx.handle)
     kernel_ms = tot.value / max(n_l.value, 1)
 
-    ab = algorithmic_bytes(cfg, inp["lengths"], clip)
+    ab = algorithmic_bytes(cfg, inp["lengths"], clip, zero_fill=not args.no_zero_fill)
     ms_step = elapsed * 1e3 / args.steps
     value = ab["live_rows"] / (ms_step / 1e3)
     achieved = ab["bytes"] / (kernel_ms / 1e3) / 1e9
@@ -676,8 +754,12 @@ def main() -> None:
         "dtype": cfg.dtype,
         "data": "synthetic (seeded Philox/PCG64 inputs of the configuration)",
         "config": {"workload": f"config{cfg.key} {cfg.name}: {cfg.prompts} prompts x G={cfg.group}, T={cfg.T}, "
-                               f"V={cfg.V}, {cfg.dtype} logits, loss={args.mode}",
-                   "rows": ab["rows"], "valid_rows": ab["live_rows"], "global_batch": cfg.S, "seq_len": cfg.T},
+                               f"V={cfg.V}, {cfg.dtype} logits, loss={args.mode}"
+                               + (", dlogits of masked rows left unwritten (no zero-fill)" if args.no_zero_fill
+                                  else "")
+                               + (", bf16 dlogits rounded once from f32 (exact mode)" if args.exact_bf16 else ""),
+                   "rows": ab["rows"], "valid_rows": ab["live_rows"], "global_batch": cfg.S, "seq_len": cfg.T,
+                   "zero_fill": not args.no_zero_fill},
         "step_gbs": ab["bytes"] / (ms_step / 1e3) / 1e9,
         "rows_per_s": ab["rows"] / (ms_step / 1e3),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -686,12 +768,13 @@ def main() -> None:
                      "kernel_ms": kernel_ms, "algorithmic_bytes": ab["bytes"]},
         "setup_s": t_setup,
     }
-    tfile = os.path.join(ROOT, "profiles", f"traffic_config{cfg.key}_{args.mode}.json")
+    tfile = os.path.join(ROOT, "profiles", f"traffic_config{cfg.key}_{args.mode}"
+                                           f"{'_no_zero_fill' if args.no_zero_fill else ''}.json")
     if os.path.exists(tfile):
         with open(tfile) as f:
             line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(inp, cfg, clip, budget_s=args.cpu_budget)
+        line["cpu_baseline"] = cpu_baseline(inp, cfg, clip)
     print(json.dumps(line), flush=True)
 
 

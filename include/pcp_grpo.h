@@ -96,6 +96,12 @@ typedef enum pcp_loss_mode {
 #define PCP_FLAG_NO_ZERO_FILL 0x2u     /* leave dlogits rows of masked / pad tokens untouched */
 #define PCP_FLAG_FORCE_STREAMING 0x4u  /* use the two-read streaming kernel even when the
                                           register-resident one fits (testing / comparison)  */
+/* bf16 logits -> bf16 dlogits: every output is the f32 result rounded once to nearest
+ * even. By default the resident kernel keeps the softmax terms of the sum pass as f16
+ * (unit roundoff 2^-11) and scales them into dlogits, which saves one exponential per
+ * element (3-5% of the step at configs 2-4) and adds up to 2^-11 of |dlogit| before
+ * the bf16 rounding. */
+#define PCP_FLAG_EXACT_BF16 0x8u
 
 /* The token id that contributes nothing (F.cross_entropy ignore_index; the
  * "compare NE -100" select in models/tests/qwen_test.mlir:267-280). */

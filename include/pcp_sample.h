@@ -32,6 +32,8 @@ extern "C" {
  *  - otherwise the first index i with sum_{j<=i} e_j >= uniforms[r] * sum_j e_j,
  *    e_j = exp((logit_j - max) / temperature) (:27-53); a NaN or +Inf logit, or a row
  *    of -Inf, makes the sum NaN and gives vocab - 1, the reference's fallback (:56).
+ *    A NaN temperature is not below 1e-6, so it samples too, and every row gives
+ *    vocab - 1 for the same reason; +Inf makes every finite term 1 (uniform draw).
  * 1 <= n_rows <= PCP_SAMPLE_MAX_ROWS. ids[r] receives the token (int64, device). uniforms (device, n_rows floats in
  * [0, 1)) may be NULL when temperature < 1e-6. The kernel sums in a fixed parallel
  * order, not the reference's sequential f32 loop, so a draw whose threshold lies

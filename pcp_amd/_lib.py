@@ -45,6 +45,7 @@ class LossMode(enum.IntEnum):
 FLAG_ASYNC = 0x1
 FLAG_NO_ZERO_FILL = 0x2
 FLAG_FORCE_STREAMING = 0x4
+FLAG_EXACT_BF16 = 0x8
 NOALLOC_SCRATCH_BYTES = 4 << 20
 IGNORE_INDEX = -100
 

@@ -278,8 +278,9 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   const bool edge_ok = !ra.dlogits || (a->dlogits_dtype == a->logits_dtype &&
                                        ((reinterpret_cast<uintptr_t>(a->logits) ^
                                          reinterpret_cast<uintptr_t>(ra.dlogits)) & 15u) == 0);
-  const RowPlan plan = plan_rows(in_bytes, g.vocab, al, edge_ok, ra.dlogits == nullptr,
-                                 (a->flags & PCP_FLAG_FORCE_STREAMING) != 0);
+  RowPlan plan = plan_rows(in_bytes, g.vocab, al, edge_ok, ra.dlogits == nullptr,
+                           (a->flags & PCP_FLAG_FORCE_STREAMING) != 0);
+  plan.exact = (a->flags & PCP_FLAG_EXACT_BF16) ? 1 : 0;
   const int out_dt = ra.dlogits ? a->dlogits_dtype : a->logits_dtype;
   const bool timed = ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
   if (timed) {

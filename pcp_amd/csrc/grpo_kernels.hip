@@ -101,21 +101,24 @@ __device__ __forceinline__ void edge_state(const void* p, const RowSpan& sp, int
 // ---------------------------------------------------------------------------
 // Register-resident fused forward+backward.
 //   TI/TO: input / output codecs; BLOCK lanes; NCH 16-byte chunks per lane
-//   (row capacity BLOCK*NCH*16 bytes); RB reference chunks per batch.
+//   (row capacity BLOCK*NCH*16 bytes); RB reference chunks per batch; CACHE: bf16 ->
+//   bf16 rows keep the sum pass's softmax terms as f16 for the dlogits pass (false:
+//   that pass recomputes them, so each output is the f32 result rounded once).
 // Requirements (checked on the host): V <= BLOCK*NCH*EPV; without EDGE, V % EPV == 0
 // and 16-byte aligned rows. EDGE: rows may start off 16 bytes, and dlogits rows have
 // the logits rows' element type and offset mod 16: the aligned interior is held and
 // stored as vectors, the head and tail (under EPV elements each) by threads 0..13 one
 // element each. dlogits == nullptr: forward only (log-probs).
 // ---------------------------------------------------------------------------
-template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE>
+template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE, bool CACHE>
 __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row, float* lds) {
   constexpr int EPV = 16 / TI::kBytes;
   constexpr uint32_t kChunkBytes = BLOCK * 16;          // one chunk: 16 bytes per lane
   constexpr uint32_t kOutVec = EPV * TO::kBytes;        // output bytes per input vector
   // bf16 logits -> bf16 dlogits: the sum pass's softmax terms are cached (f16) and
   // scaled into dlogits, one exponential per element fewer. Other pairs recompute.
-  constexpr bool kCache = __is_same(TI, BF16T) && __is_same(TO, BF16T);
+  constexpr bool kBf16Pair = __is_same(TI, BF16T) && __is_same(TO, BF16T);
+  constexpr bool kCache = kBf16Pair && CACHE;
   constexpr int kPrefetch = PCP_RES_PREFETCH;   // reference batches in flight ahead of the math
   const int tid = threadIdx.x;
   const RowMeta r = row_meta(a, row);
@@ -187,7 +190,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
     for (int k = 0; k < NCH; ++k) {
       if (k * BLOCK + tid < nv) {
         const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
-        if constexpr (kCache) {
+        if constexpr (kBf16Pair) {
           // bf16 halves by byte permutes: the same values as unpack(), but not
           // merged with the sum pass's unpacks, which would keep 152 f32 values
           // live from here to the sum of the last chunk.
@@ -302,6 +305,17 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
         o[2 * q] = f * static_cast<float>(h[0]);
         o[2 * q + 1] = f * static_cast<float>(h[1]);
       }
+    } else if constexpr (kBf16Pair) {
+      // The words pass through an opaque copy: otherwise the compiler reuses the sum
+      // pass's unpacked values here and keeps all of them live across the merge.
+      uint32_t u[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        u[q] = w[q];
+        asm volatile("" : "+v"(u[q]));
+      }
+#pragma unroll
+      for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(TI::unpack(u, j), kLog2e, -lse2));
     } else {
 #pragma unroll
       for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -lse2));
@@ -334,18 +348,18 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
 template <typename TI, typename TO>
 constexpr bool kPersistentRows = !(__is_same(TI, BF16T) && __is_same(TO, F32T));
 
-template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE>
+template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE, bool CACHE>
 __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   __shared__ float lds[4 * (BLOCK / 64)];
   __shared__ int s_next[2];
   if constexpr (!kPersistentRows<TI, TO>) {
-    resident_row<TI, TO, BLOCK, NCH, RB, EDGE>(a, blockIdx.x, lds);
+    resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>(a, blockIdx.x, lds);
     return;
   }
   int64_t row = blockIdx.x;
   for (int i = 0; row < a.nrows; ++i) {
     if (threadIdx.x == 0) s_next[i & 1] = atomicAdd(a.next_row, 1) + static_cast<int>(gridDim.x);
-    resident_row<TI, TO, BLOCK, NCH, RB, EDGE>(a, row, lds);
+    resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>(a, row, lds);
     __syncthreads();   // s_next visible; this row's LDS reads done before the next row writes
     row = s_next[i & 1];
   }
@@ -726,7 +740,7 @@ loss_final_kernel(const float* seq_val, int64_t n_seq, float loss_norm, float* l
 // ---------------------------------------------------------------------------
 namespace {
 
-template <typename TI, typename TO, int BLOCK, int NCH, bool EDGE>
+template <typename TI, typename TO, int BLOCK, int NCH, bool EDGE, bool CACHE>
 hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
   // RB = 2: the largest reference batch that needs no register spill next to a
   // 19-chunk resident row at 128 VGPRs (4 spills 9 VGPRs and measured ~1% slower).
@@ -741,7 +755,7 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e == hipSuccess)
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &occ, reinterpret_cast<const void*>(&grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE>), BLOCK, 0);
+          &occ, reinterpret_cast<const void*>(&grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>), BLOCK, 0);
     if (e != hipSuccess) return e;
     slots = cus * (occ > 0 ? occ : 1);
     cached.store(slots, std::memory_order_relaxed);
@@ -749,7 +763,7 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
   const int64_t grid = kPersistentRows<TI, TO> ? (nrows < slots ? nrows : slots) : nrows;
   if (grid <= 0) return hipSuccess;
   if (kPersistentRows<TI, TO>) reset_counter_kernel<<<1, 1, 0, st>>>(a.next_row);
-  grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE><<<dim3(static_cast<unsigned>(grid)), dim3(BLOCK), 0, st>>>(a);
+  grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE, CACHE><<<dim3(static_cast<unsigned>(grid)), dim3(BLOCK), 0, st>>>(a);
   return hipGetLastError();
 }
 
@@ -788,37 +802,43 @@ struct ResCfg {
 constexpr ResCfg kResCfgs[] = {{256, 1},   {256, 2},   {256, 4},   {1024, 2}, {1024, 4},
                                {1024, 8},  {1024, 12}, {1024, 16}, {1024, 19}, {1024, 20}};
 
-// Rows off 16 bytes (EDGE) need dlogits of the logits' element type.
+// Rows off 16 bytes (EDGE) need dlogits of the logits' element type. Only bf16 -> bf16
+// rows have the f16 softmax cache, so only they have instances without it (exact).
 template <typename TI, typename TO, int BLOCK, int NCH>
-hipError_t launch_resident_cfg(bool edge, const RowArgs& a, int64_t nrows, hipStream_t st) {
+hipError_t launch_resident_cfg(bool edge, bool exact, const RowArgs& a, int64_t nrows, hipStream_t st) {
+  if constexpr (__is_same(TI, BF16T) && __is_same(TO, BF16T)) {
+    if (exact)
+      return edge ? launch_resident<TI, TO, BLOCK, NCH, true, false>(a, nrows, st)
+                  : launch_resident<TI, TO, BLOCK, NCH, false, false>(a, nrows, st);
+  }
   if constexpr (__is_same(TI, TO)) {
-    if (edge) return launch_resident<TI, TO, BLOCK, NCH, true>(a, nrows, st);
+    if (edge) return launch_resident<TI, TO, BLOCK, NCH, true, true>(a, nrows, st);
   } else {
     if (edge) return hipErrorInvalidValue;
   }
-  return launch_resident<TI, TO, BLOCK, NCH, false>(a, nrows, st);
+  return launch_resident<TI, TO, BLOCK, NCH, false, true>(a, nrows, st);
 }
 
 template <typename TI, typename TO>
-hipError_t dispatch_resident(int cfg, bool edge, const RowArgs& a, int64_t nrows, hipStream_t st) {
+hipError_t dispatch_resident(int cfg, bool edge, bool exact, const RowArgs& a, int64_t nrows, hipStream_t st) {
   switch (cfg) {
-    case 0: return launch_resident_cfg<TI, TO, 256, 1>(edge, a, nrows, st);
-    case 1: return launch_resident_cfg<TI, TO, 256, 2>(edge, a, nrows, st);
-    case 2: return launch_resident_cfg<TI, TO, 256, 4>(edge, a, nrows, st);
-    case 3: return launch_resident_cfg<TI, TO, 1024, 2>(edge, a, nrows, st);
-    case 4: return launch_resident_cfg<TI, TO, 1024, 4>(edge, a, nrows, st);
-    case 5: return launch_resident_cfg<TI, TO, 1024, 8>(edge, a, nrows, st);
-    case 6: return launch_resident_cfg<TI, TO, 1024, 12>(edge, a, nrows, st);
-    case 7: return launch_resident_cfg<TI, TO, 1024, 16>(edge, a, nrows, st);
-    case 8: return launch_resident_cfg<TI, TO, 1024, 19>(edge, a, nrows, st);
-    case 9: return launch_resident_cfg<TI, TO, 1024, 20>(edge, a, nrows, st);
+    case 0: return launch_resident_cfg<TI, TO, 256, 1>(edge, exact, a, nrows, st);
+    case 1: return launch_resident_cfg<TI, TO, 256, 2>(edge, exact, a, nrows, st);
+    case 2: return launch_resident_cfg<TI, TO, 256, 4>(edge, exact, a, nrows, st);
+    case 3: return launch_resident_cfg<TI, TO, 1024, 2>(edge, exact, a, nrows, st);
+    case 4: return launch_resident_cfg<TI, TO, 1024, 4>(edge, exact, a, nrows, st);
+    case 5: return launch_resident_cfg<TI, TO, 1024, 8>(edge, exact, a, nrows, st);
+    case 6: return launch_resident_cfg<TI, TO, 1024, 12>(edge, exact, a, nrows, st);
+    case 7: return launch_resident_cfg<TI, TO, 1024, 16>(edge, exact, a, nrows, st);
+    case 8: return launch_resident_cfg<TI, TO, 1024, 19>(edge, exact, a, nrows, st);
+    case 9: return launch_resident_cfg<TI, TO, 1024, 20>(edge, exact, a, nrows, st);
   }
   return hipErrorInvalidValue;
 }
 
 template <typename TI, typename TO>
 hipError_t dispatch_rows(const RowPlan& p, const RowArgs& a, int64_t nrows, hipStream_t st) {
-  if (p.kind == RowPlan::kResident) return dispatch_resident<TI, TO>(p.cfg, p.edge != 0, a, nrows, st);
+  if (p.kind == RowPlan::kResident) return dispatch_resident<TI, TO>(p.cfg, p.edge != 0, p.exact != 0, a, nrows, st);
   if (p.kind == RowPlan::kForward) return launch_fwd<TI>(a, nrows, st);
   if (p.kind == RowPlan::kStreamVec) return launch_stream<TI, TO, true>(a, nrows, st);
   return launch_stream<TI, TO, false>(a, nrows, st);
@@ -835,6 +855,7 @@ RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool edge_ok, boo
   p.block = 1024;
   p.nch = 0;
   p.edge = 0;
+  p.exact = 0;
   if (force_stream) return p;
   // The forward kernel takes rows of any alignment. It addresses a row through a
   // 32-bit buffer offset that runs up to one batch past the row end: rows up to 2 GiB

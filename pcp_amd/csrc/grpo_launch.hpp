@@ -16,6 +16,7 @@ struct RowPlan {
   int block;  // lanes per workgroup
   int nch;    // resident 16-byte chunks per lane
   int edge;   // resident rows off 16 bytes (head / tail element-wise)
+  int exact;  // bf16 -> bf16 resident rows without the f16 softmax cache (PCP_FLAG_EXACT_BF16)
 };
 
 // in_bytes: logits element size; aligned16: every row base is 16-byte aligned;

@@ -40,20 +40,35 @@ struct SampleArgs {
 };
 
 template <typename TI>
-__device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, int64_t vocab, int64_t b, int lane,
-                                           float (&x)[16 / TI::kBytes]) {
+__device__ __forceinline__ const void* row_ptr(const SampleArgs& a, int64_t row) {
+  return static_cast<const char*>(a.logits) + row * a.row_stride * TI::kBytes;
+}
+
+// The row's descriptor covers its whole dwords only (the range check is per dword), so
+// no load reaches past the row: the last element of an odd bf16 row shares its dword
+// with the bytes after the row and is read on its own (load_block).
+template <typename TI>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const SampleArgs& a, int64_t row) {
+  return row_rsrc(row_ptr<TI>(a, row), static_cast<uint32_t>(a.vocab * TI::kBytes) & ~3u);
+}
+
+// Lane `lane`'s EPL elements of 64-lane block b of a row (-inf past `vocab`).
+template <typename TI>
+__device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, const void* row, int64_t vocab, int64_t b,
+                                           int lane, float (&x)[16 / TI::kBytes]) {
   constexpr int EPL = 16 / TI::kBytes;
   const int64_t e0 = b * (64 * EPL) + static_cast<int64_t>(lane) * EPL;
   const u32x4 w = buf_ld16<true>(r, static_cast<uint32_t>(e0 * TI::kBytes));
   const uint32_t ws[4] = {w[0], w[1], w[2], w[3]};
 #pragma unroll
   for (int j = 0; j < EPL; ++j) x[j] = (e0 + j < vocab) ? TI::unpack(ws, j) : kNegInf;
-}
-
-template <typename TI>
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const SampleArgs& a, int64_t row) {
-  return row_rsrc(static_cast<const char*>(a.logits) + row * a.row_stride * TI::kBytes,
-                  static_cast<uint32_t>(a.vocab * TI::kBytes));
+  if constexpr (TI::kBytes == 2) {
+    if (vocab & 1) {
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (e0 + j == vocab - 1) x[j] = TI::load1(row, vocab - 1);
+    }
+  }
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -102,7 +117,8 @@ __global__ void __launch_bounds__(64 * kWaves) sample_part_kernel(SampleArgs a) 
   const int64_t b0 = static_cast<int64_t>(g) * kBlocksPerWg + wave * kBlocksPerWave;
   float x[kBlocksPerWave][EPL];
 #pragma unroll
-  for (int u = 0; u < kBlocksPerWave; ++u) load_block<TI>(r, b0 + u < a.nb ? V : 0, b0 + u, lane, x[u]);
+  for (int u = 0; u < kBlocksPerWave; ++u)
+    load_block<TI>(r, row_ptr<TI>(a, row), b0 + u < a.nb ? V : 0, b0 + u, lane, x[u]);
   if (a.greedy) {
     float best = kNegInf;
     int64_t bi = V;                                  // no value above -inf yet
@@ -245,7 +261,7 @@ __global__ void __launch_bounds__(64) sample_select_kernel(SampleArgs a) {
 
   // Re-read that block and scan it in element order.
   float x[EPL];
-  load_block<TI>(row_buffer<TI>(a, row), V, hb, lane, x);
+  load_block<TI>(row_buffer<TI>(a, row), row_ptr<TI>(a, row), V, hb, lane, x);
   double e[EPL], lane_sum = 0.0;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
@@ -299,9 +315,12 @@ extern "C" int pcp_sample_tokens(pcp_ctx* ctx, const void* logits, int dtype, in
   if (!logits || !ids) return fail(ctx, PCP_ERR_INVALID_ARG, "logits / ids is NULL");
   if ((reinterpret_cast<uintptr_t>(logits) & 15u) || ((row_stride * esize) & 15))
     return fail(ctx, PCP_ERR_INVALID_ARG, "logits rows must start on 16-byte boundaries");
-  const bool greedy = !(temperature >= 1e-6f);
-  if (!greedy && !uniforms) return fail(ctx, PCP_ERR_INVALID_ARG, "uniforms is NULL with temperature >= 1e-6");
-  if (!std::isfinite(temperature) && !greedy) return fail(ctx, PCP_ERR_INVALID_ARG, "temperature must be finite");
+  // math.zig:23: greedy only when temperature < 1e-6. A NaN temperature takes the
+  // sampling path there: every term is NaN, no cumulative sum reaches the threshold and
+  // the row gives len - 1, as it does here (the scale log2(e)/T is NaN).
+  const bool greedy = temperature < 1e-6f;
+  if (!greedy && !uniforms)
+    return fail(ctx, PCP_ERR_INVALID_ARG, "uniforms is NULL and temperature is not below 1e-6");
   if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");

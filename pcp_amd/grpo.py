@@ -124,9 +124,9 @@ def grpo_loss_fwd_bwd(logits: torch.Tensor, ids: torch.Tensor, mask: torch.Tenso
                       std_eps: float = 1e-8, rows: int | None = None, tok_offset: int = 0,
                       want_dlogits: bool = True, dlogits: torch.Tensor | None = None,
                       dlogits_dtype: torch.dtype | None = None, zero_fill: bool = True,
-                      force_streaming: bool = False, outputs: GrpoOutputs | None = None,
-                      sync: bool = True, stream=None, ctx: Context | None = None,
-                      noalloc: bool = False) -> GrpoOutputs:
+                      force_streaming: bool = False, exact_bf16: bool = False,
+                      outputs: GrpoOutputs | None = None, sync: bool = True, stream=None,
+                      ctx: Context | None = None, noalloc: bool = False) -> GrpoOutputs:
     """Fused loss forward + dlogits backward (pcp_grpo_loss_fwd_bwd).
 
     Pass ``outputs`` (from a previous call of the same shape) to reuse its buffers
@@ -164,7 +164,8 @@ def grpo_loss_fwd_bwd(logits: torch.Tensor, ids: torch.Tensor, mask: torch.Tenso
     a.loss_mode = int(loss_mode)
     a.clip_eps, a.kl_beta, a.std_eps, a.loss_norm = clip_eps, kl_beta, std_eps, loss_norm
     a.flags = ((0 if sync else _lib.FLAG_ASYNC) | (0 if zero_fill else _lib.FLAG_NO_ZERO_FILL)
-               | (_lib.FLAG_FORCE_STREAMING if force_streaming else 0))
+               | (_lib.FLAG_FORCE_STREAMING if force_streaming else 0)
+               | (_lib.FLAG_EXACT_BF16 if exact_bf16 else 0))
     a.stream = _stream_handle(stream)
     fn = lib().pcp_grpo_loss_fwd_bwd_noalloc if noalloc else lib().pcp_grpo_loss_fwd_bwd
     check(fn(ctx.handle, ctypes.byref(a)), ctx.handle)

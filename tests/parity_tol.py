@@ -5,10 +5,27 @@ array helpers (shared by the logits-input and the fused LM-head tests).
   loss:                                the log-prob bar propagated through dloss/dlogp and
                                        dloss/dref, plus 1e-5 of the sum of |contributions|
   dlogits, f32 output:                 |d| <= 1e-4 (north star) and <= 1e-5*|exact| + floor_row
-  dlogits, bf16 output:                |d| <= (2^-8 + 4e-6)*|exact| + floor_row
+  dlogits, bf16 output:                |d| <= (2^-8 + 2^-11 + 1.3e-5)*|exact| + (1 + 2^-6)*floor_row
+  dlogits, bf16 output, exact mode:    |d| <= (2^-8 + 1.1e-5)*|exact| + (1 + 2^-7)*floor_row
 floor_row (coef_floor) is what the f32 log-prob error allows in the row's
 coefficient c: c is built from exp(logp - old) and expm1(ref - logp), whose terms
 can cancel.
+
+The 16-bit bars follow from the f32 bar. Let o' be the f32 result, with
+|o' - d| <= 1e-5*|d| + floor_row (the f32 bar). A 16-bit output rounded to nearest
+even is off by at most its unit roundoff times the value: 2^-8 for bf16 (8 significant
+bits), 2^-11 for f16.
+  Exact mode (PCP_FLAG_EXACT_BF16, and every path other than bf16 -> bf16 resident
+  rows): out = round(o'), so |out - d| <= 2^-8*|o'| + |o' - d|
+  <= (2^-8 + 1.1e-5)*|d| + (1 + 2^-7)*floor_row.
+  Default bf16 -> bf16 resident rows scale the sum pass's softmax terms, kept as f16,
+  into dlogits: o = f * f16(e) with f = -c * 2^(m - lse) and e <= 1. The f16 rounding
+  adds at most 2^-11 of the term (2^-25 absolute below f16's normal range, which is
+  |c| * 2^-25 in o, since 2^(m - lse) <= 1), so |o - o'| <= 2^-11*|o'| + |c|*2^-25 and
+    |out - d| <= 2^-8*|o| + |o - o'| + |o' - d|
+              <= (2^-8 + 2^-11 + 2^-19)*|o'| + |o' - d| + (1 + 2^-8)*|c|*2^-25
+              <= (2^-8 + 2^-11 + 1.3e-5)*|d| + (1 + 2^-6)*floor_row,
+  using |o'| <= |d| + |o' - d| and floor_row >= 1e-5*|c| (so |c|*2^-24 < 2^-7*floor_row).
 """
 import numpy as np
 import torch
@@ -98,14 +115,22 @@ def tok_to_rows(a, rows, off, LS):
     return out
 
 
-def assert_dlogits(got, want, floor_rows, bf16_out):
-    """floor_rows: per-row absolute floor (coef_floor), broadcast over the vocabulary."""
+BF16_CACHED_REL = 2.0 ** -8 + 2.0 ** -11 + 1.3e-5
+BF16_EXACT_REL = 2.0 ** -8 + 1.1e-5
+
+
+def assert_dlogits(got, want, floor_rows, bf16_out, exact=False):
+    """floor_rows: per-row absolute floor (coef_floor), broadcast over the vocabulary.
+    bf16_out: a 16-bit output (bf16 or f16). exact: the output is the f32 result rounded
+    once (PCP_FLAG_EXACT_BF16, or a path without the f16 softmax cache)."""
     got = got.astype(np.float64)
     want = want.astype(np.float64)
     fl = np.asarray(floor_rows, np.float64)[..., None]
     err = np.abs(got - want)
-    if bf16_out:
-        tol = (2.0 ** -8 + 4e-6) * np.abs(want) + fl
+    if bf16_out and exact:
+        tol = BF16_EXACT_REL * np.abs(want) + (1 + 2.0 ** -7) * fl
+    elif bf16_out:
+        tol = BF16_CACHED_REL * np.abs(want) + (1 + 2.0 ** -6) * fl
     else:
         tol = 1e-5 * np.abs(want) + fl
         assert err.max() <= 1e-4

@@ -253,6 +253,50 @@ def test_sampler_closed_forms_and_specials():
     assert [orc.sample(y[r], 1.0, 0.5) for r in range(4)] == [417, 999, 999, 999]
 
 
+@pytest.mark.parametrize("V", [1001, 5003, 151937])
+def test_sampler_odd_bf16_rows_last_element(V):
+    """bf16 rows of odd length: the last element shares its dword with the bytes after
+    the row, so it is read on its own. The maximum (greedy) or all the mass (sampling)
+    at index V - 1, in a wider buffer whose bytes after the row hold a larger value."""
+    rng = np.random.default_rng(V)
+    R, LD = 8, V + 7
+    full = (rng.standard_normal((R, LD)) * 2).astype(np.float32)
+    full[:, V - 1] = 40.0
+    full[:, V:] = 90.0                                # outside the rows: never read
+    xd = torch.from_numpy(full).to(DEV).to(torch.bfloat16)
+    rows = torch.empty((R, (LD + 7) // 8 * 8), dtype=torch.bfloat16, device=DEV)
+    rows[:, :LD] = xd
+    view = rows[:, :V]
+    assert int(step.sample_tokens(view, 0.0)[0]) == V - 1
+    assert np.all(step.sample_tokens(view, 0.0).cpu().numpy() == V - 1)
+    u = rng.random(R).astype(np.float32)
+    got = step.sample_tokens(view, 1.0, t(u)).cpu().numpy()
+    assert np.all(got == V - 1), got
+    full[:, V - 1] = -40.0                            # and when the last element carries nothing
+    rows[:, :LD] = torch.from_numpy(full).to(DEV).to(torch.bfloat16)
+    got = step.sample_tokens(view, 0.0).cpu().numpy()
+    want = np.array([orc.sample(rows[r, :V].float().cpu().numpy(), 0.0) for r in range(R)])
+    assert np.array_equal(got, want) and not np.any(got == V - 1)
+
+
+def test_sampler_nan_and_inf_temperature():
+    """math.zig:23 takes the greedy branch only for temperature < 1e-6. NaN samples and
+    every term is NaN, so the row gives len - 1; +Inf makes every finite term 1 (a
+    uniform draw); -Inf is greedy."""
+    rng = np.random.default_rng(25)
+    R, V = 6, 4096
+    x = (rng.standard_normal((R, V)) * 2).astype(np.float32)
+    u = np.array([0.1, 0.5, 0.9, 0.0, 0.33, 0.75], np.float32)
+    got = step.sample_tokens(t(x), float("nan"), t(u)).cpu().numpy()
+    assert np.all(got == V - 1)
+    assert [orc.sample(x[r], float("nan"), float(u[r])) for r in range(R)] == [V - 1] * R
+    got = step.sample_tokens(t(x), float("inf"), t(u)).cpu().numpy()
+    want = np.maximum(np.ceil(u.astype(np.float64) * V) - 1, 0).astype(np.int64)
+    assert np.array_equal(got, want), (got, want)
+    got = step.sample_tokens(t(x), float("-inf")).cpu().numpy()
+    assert np.array_equal(got, x.argmax(1))
+
+
 def test_sampler_bf16_and_strided_rows():
     rng = np.random.default_rng(23)
     R, V, LD = 16, 5000, 5120                         # rows inside a wider buffer
