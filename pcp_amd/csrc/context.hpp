@@ -31,7 +31,6 @@ struct pcp_ctx {
   std::vector<hipEvent_t> prof_start, prof_stop;
   int prof_used = 0;
   bool prof_on = false;
-  void* blas = nullptr;           // rocblas_handle, created on first LM-head backward
   int* h_count = nullptr;         // pinned host word: live-token count of the LM-head path
   pcp::HostStager* stager = nullptr;  // pinned staging ring of the host-bytes path
   hipStream_t xs[3] = {};         // host-bytes path: upload, compute and download streams
@@ -94,9 +93,6 @@ int collect_device_errors(pcp_ctx* ctx);
 // full the stream is synchronised at once instead (its errors still reach pcp_sync
 // through the error word).
 int add_pending(pcp_ctx* ctx, hipStream_t st);
-
-// Release the context's BLAS handle (defined with the LM-head path).
-void release_blas(pcp_ctx* ctx);
 
 // pcp_profile_start/stop: HIP events around a timed launch on its stream. prof_begin
 // returns whether this launch is timed (profiling on and an event pair left).

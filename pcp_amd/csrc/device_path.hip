@@ -418,7 +418,6 @@ void pcp_destroy(pcp_ctx* ctx) {
   if (hipSetDevice(ctx->device) == hipSuccess) {
     (void)hipDeviceSynchronize();
     release_profile_events(ctx);
-    release_blas(ctx);
     if (ctx->h_count) (void)hipHostFree(ctx->h_count);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     destroy_stager(ctx);

@@ -16,6 +16,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cstring>
+
 #include "grpo_device.hpp"
 #include "lmhead_launch.hpp"
 
@@ -108,37 +110,67 @@ lm_tile_kernel(LmTileArgs a) {
   using namespace lm;
   extern __shared__ __align__(16) char smem[];
 
+  // The product this workgroup works on: the loss-head modes read rows of H elements
+  // of hidden (A) and W (B); kLmGemm takes one of its (up to) two products.
+  int pid = blockIdx.x;
+  const void* opA = a.A;
+  const void* opB = a.B;
+  int N = a.N, V = a.V, K = a.H, lda = a.H, ldb = a.H, ntt = a.ntt, nvt = a.nvt, gm = a.group_m, vt0 = a.vt0;
+  float* C = nullptr;
+  int ldc = 0, accumulate = 0;
+  if constexpr (MODE == kLmGemm) {
+    const int p = pid >= a.gemm[0].tiles ? 1 : 0;
+    if (p) pid -= a.gemm[0].tiles;
+    const LmTileArgs::Gemm& g = a.gemm[p];
+    opA = g.A;
+    opB = g.B;
+    N = g.N;
+    V = g.V;
+    K = g.K;
+    lda = g.lda;
+    ldb = g.ldb;
+    ntt = g.ntt;
+    nvt = g.nvt;
+    gm = g.group_m;
+    vt0 = 0;
+    C = g.C;
+    ldc = g.ldc;
+    accumulate = g.accumulate;
+  }
   int tm, tn;
-  if (!lm_tile_coords(blockIdx.x, a.ntt, a.nvt, a.group_m, tm, tn)) return;
+  if (!lm_tile_coords(pid, ntt, nvt, gm, tm, tn)) return;
   const int m0 = tm * BT;                  // first token
-  const int v0 = (a.vt0 + tn) * BV;        // first vocab entry
+  const int v0 = (vt0 + tn) * BV;          // first vocab entry
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wv = wave >> 2, wt = wave & 3;
 
   // Operand row buffers: rows past V / N read 0 (range-checked lane offsets).
-  const uint32_t rowbytes = static_cast<uint32_t>(a.H) * 2u;
-  const int rows_w = min(BV, a.V - v0), rows_h = min(BT, a.N - m0);
+  const uint32_t wbytes = static_cast<uint32_t>(ldb) * 2u;
+  const uint32_t hbytes = static_cast<uint32_t>(lda) * 2u;
+  const int rows_w = min(BV, V - v0), rows_h = min(BT, N - m0);
   const __amdgpu_buffer_rsrc_t rw =
-      row_rsrc(reinterpret_cast<const char*>(a.B) + static_cast<int64_t>(v0) * rowbytes, rows_w * rowbytes);
+      row_rsrc(reinterpret_cast<const char*>(opB) + static_cast<int64_t>(v0) * wbytes, rows_w * wbytes);
   const __amdgpu_buffer_rsrc_t rh =
-      row_rsrc(reinterpret_cast<const char*>(a.A) + static_cast<int64_t>(m0) * rowbytes, rows_h * rowbytes);
+      row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0) * hbytes, rows_h * hbytes);
 
   // Direct-to-LDS loads: wave w fills rows 8*(4w+q) + lane/8, q < 4, of each operand;
   // lane writes LDS slot lane%8 of its row, which holds chunk (lane%8) ^ swz(row).
-  uint32_t doff[4];
+  uint32_t dofw[4], dofh[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int row = 8 * (4 * wave + q) + (lane >> 3);
-    doff[q] = static_cast<uint32_t>(row) * rowbytes + 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
+    const uint32_t c16 = 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
+    dofw[q] = static_cast<uint32_t>(row) * wbytes + c16;
+    dofh[q] = static_cast<uint32_t>(row) * hbytes + c16;
   }
   auto issue = [&](int st, int buf) {
     char* base = smem + buf * kStageBytes;
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (4 * wave + q) * 1024), 16, doff[q] + koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (4 * wave + q) * 1024), 16, doff[q] + koff,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (4 * wave + q) * 1024), 16, dofw[q] + koff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (4 * wave + q) * 1024), 16, dofh[q] + koff,
                                                0, 0, 0);
     }
   };
@@ -187,7 +219,7 @@ lm_tile_kernel(LmTileArgs a) {
   // burst of the stage's direct-to-LDS loads right after the barrier held the MFMAs
   // behind it whenever the memory pipeline pushed back; one load (or fragment read)
   // between consecutive MFMAs measured 6% faster on config 5.
-  const int nk = a.H / BK;
+  const int nk = K / BK;
   issue(0, 0);
   __builtin_amdgcn_s_waitcnt(kWaitStage);
   lm_barrier();
@@ -244,7 +276,7 @@ lm_tile_kernel(LmTileArgs a) {
 
   const int vw = v0 + wv * 128;                 // first vocab row of this wave
   const int half = lane >> 5;
-  const bool full_v = vw + 128 <= a.V;
+  const bool full_v = vw + 128 <= V;
   // Vocab row of acc[i][*][r] relative to vw.
   auto vrow = [&](int i, int r) { return 32 * i + 8 * (r >> 2) + 4 * half + (r & 3); };
 
@@ -295,6 +327,24 @@ lm_tile_kernel(LmTileArgs a) {
         }
       }
     }
+  } else if constexpr (MODE == kLmGemm) {
+    // C[v][t] (+)= the tile; rows past V and columns past N are not stored. For fixed
+    // (i, r) lanes 0-31 and 32-63 each write 32 consecutive floats of one row.
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = m0 + wt * 64 + 32 * j + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int vr = vw + vrow(i, r);
+          if (vr < V) {
+            float* p = C + static_cast<int64_t>(vr) * ldc + n;
+            *p = accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+          }
+        }
+    }
   } else {
     // dlogits[t][v] = coef_t * (onehot - 2^(x*log2e - lse2_t)) in bf16, staged as a
     // token-major tile in LDS (one half of the token columns at a time), then
@@ -317,6 +367,15 @@ lm_tile_kernel(LmTileArgs a) {
             l2 = a.lse2[n];
             rel = lm_id(a, n) - vw;
           }
+          // Vocab-major copy (tokens contiguous, for dW = D^T * hidden). Each lane holds
+          // one token and 4 consecutive vocab rows; a 4 x 4 transpose within each quad of
+          // lanes (two DPP exchanges) leaves lane l with vocab row l%4 of the quad's 4
+          // tokens, stored as 8 bytes. Token columns [N, ldt) are written as 0 (cf = 0
+          // there), vocab rows past the chunk not at all.
+          const int nq = n & ~3;
+          const bool dt_on = a.dchunk_t != nullptr && nq < a.ldt;
+          uint16_t* dtq = static_cast<uint16_t*>(a.dchunk_t) +
+                          (static_cast<int64_t>(v0 - a.vc0 + wv * 128 + (lane & 3)) * a.ldt + nq);
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -330,6 +389,22 @@ lm_tile_kernel(LmTileArgs a) {
               }
               const uint32_t lo = pack2<BF16T>(d[0], d[1]), hi = pack2<BF16T>(d[2], d[3]);
               *reinterpret_cast<uint2*>(Ds + tcol * LDD + wv * 128 + vrow(i, 4 * q)) = make_uint2(lo, hi);
+              if (a.dchunk_t) {
+                // Step 1, lanes l and l^2: lanes with bit 1 clear keep rows 0-1 and take the
+                // partner's rows 0-1 (tokens s, s+2); the others keep rows 2-3.
+                const bool b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
+                const uint32_t y = static_cast<uint32_t>(
+                    __builtin_amdgcn_update_dpp(0, static_cast<int>(b1 ? lo : hi), 0x4E, 0xF, 0xF, false));
+                const uint32_t P = b1 ? y : lo, Q = b1 ? hi : y;
+                // Step 2, lanes l and l^1: bit 0 clear keeps the even row, set the odd row.
+                const uint32_t snd = b0 ? ((P & 0xFFFFu) | (Q << 16)) : ((P >> 16) | (Q & 0xFFFF0000u));
+                const uint32_t rcv = static_cast<uint32_t>(
+                    __builtin_amdgcn_update_dpp(0, static_cast<int>(snd), 0xB1, 0xF, 0xF, false));
+                const uint32_t o0 = b0 ? ((rcv & 0xFFFFu) | (P & 0xFFFF0000u)) : ((P & 0xFFFFu) | (rcv << 16));
+                const uint32_t o1 = b0 ? ((rcv >> 16) | (Q & 0xFFFF0000u)) : ((Q & 0xFFFFu) | (rcv & 0xFFFF0000u));
+                if (dt_on && v0 - a.vc0 + wv * 128 + vrow(i, 4 * q) + 3 < a.ldd)
+                  *reinterpret_cast<uint2*>(dtq + static_cast<int64_t>(vrow(i, 4 * q)) * a.ldt) = make_uint2(o0, o1);
+              }
             }
         }
       }
@@ -477,6 +552,38 @@ __global__ void __launch_bounds__(256) lm_scatter_rows_kernel(const u32x4* src, 
   }
 }
 
+// bf16 transpose through LDS, 64 x 64 tiles: 16-byte loads along source rows, 16-byte
+// stores along destination rows (the 8 stores of one destination row's 128 bytes come
+// from the 8 row groups of the same workgroup). Source rows past R read as 0, so the
+// destination is zero-padded up to ld_dst.
+__global__ void __launch_bounds__(256) lm_transpose_kernel(LmTransposeArgs a) {
+  __shared__ uint16_t t[64][72];
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int rr = it * 32 + (tid >> 3), cc = (tid & 7) * 8;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r0 + rr < a.R && c0 + cc < a.C)
+      v = *reinterpret_cast<const u32x4*>(a.src + static_cast<int64_t>(r0 + rr) * a.ld_src + c0 + cc);
+    *reinterpret_cast<u32x4*>(&t[rr][cc]) = v;
+  }
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int g = wave * 2 + it;          // row group: source rows 8g .. 8g+7
+    const int c = lane;                   // source column = destination row
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w[k] = static_cast<uint32_t>(t[8 * g + 2 * k][c]) | (static_cast<uint32_t>(t[8 * g + 2 * k + 1][c]) << 16);
+    const int64_t r = r0 + 8 * g;
+    if (c0 + c < a.C && r < a.ld_dst)
+      *reinterpret_cast<u32x4*>(a.dst + static_cast<int64_t>(c0 + c) * a.ld_dst + r) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
 __global__ void __launch_bounds__(256) lm_zero_kernel(float* dst, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
     dst[i] = 0.f;
@@ -511,22 +618,43 @@ int lm_group_m(int mode, int ntt) {
   return ntt;
 }
 
+template <int MODE>
+hipError_t launch_tiles_mode(const LmTileArgs& a, int grid, hipStream_t st) {
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
+  if (e != hipSuccess) return e;
+  lm_tile_kernel<MODE><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
+  return hipGetLastError();
+}
+
 hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {
   LmTileArgs a = args;
   a.group_m = lm_group_m(mode, a.ntt);
   const int total = a.ntt * a.nvt;
+  if (total <= 0) return hipSuccess;
   const int grid = ((total + 7) / 8) * 8;
-  if (mode == kLmFwd) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<kLmFwd>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
-    if (e != hipSuccess) return e;
-    lm_tile_kernel<kLmFwd><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
-  } else {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<kLmBwd>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
-    if (e != hipSuccess) return e;
-    lm_tile_kernel<kLmBwd><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
+  if (mode == kLmFwd) return launch_tiles_mode<kLmFwd>(a, grid, st);
+  return launch_tiles_mode<kLmBwd>(a, grid, st);
+}
+
+hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, hipStream_t st) {
+  LmTileArgs a;
+  std::memset(&a, 0, sizeof(a));
+  int grid = 0;
+  for (int p = 0; p < n_gemm && p < 2; ++p) {
+    a.gemm[p] = g[p];
+    a.gemm[p].group_m = lm_group_m(kLmGemm, g[p].ntt);
+    a.gemm[p].tiles = ((g[p].ntt * g[p].nvt + 7) / 8) * 8;   // whole XCD rounds per product
+    grid += a.gemm[p].tiles;
   }
+  if (grid <= 0) return hipSuccess;
+  return launch_tiles_mode<kLmGemm>(a, grid, st);
+}
+
+hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st) {
+  if (a.C <= 0 || a.ld_dst <= 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>((a.ld_dst + 63) / 64));
+  lm_transpose_kernel<<<grid, dim3(256), 0, st>>>(a);
   return hipGetLastError();
 }
 

@@ -8,14 +8,16 @@ namespace pcp {
 
 struct RowArgs;
 
-enum { kLmFwd = 0, kLmBwd = 1 };
+enum { kLmFwd = 0, kLmBwd = 1, kLmGemm = 2 };
 
 constexpr int kLmTileV = 256;    // vocab entries per tile
 constexpr int kLmTileT = 256;    // tokens per tile
 constexpr int kLmPart = 128;     // vocab entries per log-sum-exp partial
 
 // One launch covers token tiles [0, ntt) x vocab tiles [vt0, vt0 + nvt) of
-// kLmTileT x kLmTileV.
+// kLmTileT x kLmTileV. kLmGemm reuses the roles for plain products
+// C[v][t] = sum_k B[v][k] * A[t][k] (both operands K-contiguous, bf16): "vocab" rows
+// come from B, "token" rows from A.
 struct LmTileArgs {
   const void* A;        // hidden [N, H] bf16, row-major
   const void* B;        // weight [V, H] bf16, row-major
@@ -33,6 +35,31 @@ struct LmTileArgs {
   const float* coef;    // [N] d loss / d logp
   void* dchunk;         // [N, ldd] bf16 dlogits of vocab [vc0, vc0 + ldd)
   int vc0, ldd;
+  void* dchunk_t;       // [ldd, ldt] the same dlogits vocab-major (tokens contiguous), or nullptr;
+  int ldt;              //   tokens [N, ldt) are written as 0
+  // kLmGemm: up to two independent products in one launch (gemm[0] takes the first
+  // gemm[0].tiles workgroups, gemm[1] the rest); the fields above are unused.
+  struct Gemm {
+    const void* A;      // [N, lda] bf16: "token" rows (result columns)
+    const void* B;      // [V, ldb] bf16: "vocab" rows (result rows)
+    int N, V, K;        // K % 64 == 0, K <= lda, ldb
+    int lda, ldb;       // row strides in elements
+    float* C;           // [V, ldc] f32 result
+    int ldc;
+    int accumulate;     // 1: C += product, 0: C = product
+    int ntt, nvt;       // tiles over N and over V
+    int group_m;        // set by launch_lm_gemms
+    int tiles;          // workgroups of this product (ntt * nvt rounded up to 8)
+  } gemm[2];
+};
+
+// dst[c][r] = src[r][c] for r < R, c < C; dst[c][r] = 0 for R <= r < ld_dst (bf16).
+struct LmTransposeArgs {
+  const uint16_t* src;
+  int64_t ld_src;
+  int R, C;
+  uint16_t* dst;
+  int64_t ld_dst;
 };
 
 struct LmReduceArgs {
@@ -98,6 +125,10 @@ hipError_t launch_lm_gather_rows(const void* src, void* dst, const int* live, in
 hipError_t launch_lm_scatter_rows(const float* src, float* dst, const int* cidx, int N, int H, hipStream_t st);
 hipError_t launch_lm_zero(float* dst, int64_t n, hipStream_t st);
 hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st);
+// One launch of one or two products (n_gemm = 1 or 2; fields per LmTileArgs::Gemm,
+// group_m and tiles are filled in here). The longer product should come first.
+hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, hipStream_t st);
+hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st);
 hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st);
 hipError_t launch_lm_terms(const RowArgs& ra, const LmTermsArgs& a, hipStream_t st);
 

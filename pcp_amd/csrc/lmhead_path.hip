@@ -8,13 +8,14 @@
 // per-(token, vocab tile) log-sum-exp partials and the target logit; one wave per
 // token merges the partials. Then the GRPO terms per token and the loss reduction
 // (the same kernels as the logits-input path). Backward, per vocab chunk: logits
-// tiles recomputed into bf16 dlogits, then two plain GEMMs on rocBLAS:
-//   dhidden (+)= dlogits_chunk * W_chunk,   dW_chunk = dlogits_chunk^T * hidden,
+// tiles recomputed into bf16 dlogits D (token-major, and vocab-major for dW), then two
+// products on the same MFMA tile kernel (kLmGemm, both operands K-contiguous):
+//   dhidden (+)= D_chunk * W_chunk      (W_chunk transposed per chunk),
+//   dW_chunk    = D_chunk^T * hidden    (the compact hidden rows transposed once),
 // and the compact dhidden rows are scattered back (zero rows for dead tokens).
 // This mirrors the LM head's VJP (src/autodiff/vjp_rules.zig:426-497, matmulVJP).
 
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <cstdint>
 #include <cstring>
@@ -42,6 +43,11 @@ int validate_lm(const pcp_lmhead_args* a) {
   int64_t n;
   if (mul_overflows(a->n_seq, a->rows, &n) || n > (1 << 28))
     return fail(nullptr, PCP_ERR_OVERFLOW, "n_seq * rows exceeds 2^28 tokens");
+  // dW reads 256-row slabs of the vocab-major dlogits and of the transposed hidden rows
+  // (one row per vocab entry or hidden column, one element per token) through 32-bit
+  // buffer offsets.
+  if (a->dweight && n > (1 << 22))
+    return fail(nullptr, PCP_ERR_OVERFLOW, "dweight takes at most 2^22 tokens per call (got %lld)", (long long)n);
   if (a->vocab_chunk < 0 || a->vocab_chunk % kLmTileV != 0)
     return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab_chunk must be a multiple of %d", kLmTileV);
   if (!a->hidden_states || !a->weight || !a->ids) return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden_states / weight / ids is NULL");
@@ -67,11 +73,6 @@ int validate_lm(const pcp_lmhead_args* a) {
                        reinterpret_cast<uintptr_t>(a->ref_weight);
   if (al & 15u) return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden_states / weights must be 16-byte aligned");
   return PCP_OK;
-}
-
-int blas_status(pcp_ctx* ctx, rocblas_status s, const char* what) {
-  if (s == rocblas_status_success) return PCP_OK;
-  return fail(ctx, PCP_ERR_DEVICE, "%s: rocBLAS status %d", what, static_cast<int>(s));
 }
 
 int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
@@ -105,6 +106,12 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_part = take(8 * static_cast<size_t>(N) * npart);
   const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
   const size_t o_chunk = bwd ? take(2 * static_cast<size_t>(N) * chunk) : 0;
+  // Token-padded width of the vocab-major dlogits and the transposed hidden rows (the
+  // dW product's K, a multiple of the 64-deep pipeline stage).
+  const int64_t ldt_max = (N + 63) / 64 * 64;
+  const size_t o_dt = a->dweight ? take(2 * static_cast<size_t>(chunk) * ldt_max) : 0;
+  const size_t o_ht = a->dweight ? take(2 * static_cast<size_t>(H) * ldt_max) : 0;
+  const size_t o_wt = want_dy ? take(2 * static_cast<size_t>(H) * chunk) : 0;
   const size_t o_dhc = want_dy ? take(4 * static_cast<size_t>(N) * H) : 0;
   const size_t o_rstd = norm ? take(4 * N) : 0;
   const size_t o_gpart = a->dnorm_weight ? take(4 * static_cast<size_t>(kLmNormSlices) * H) : 0;
@@ -215,54 +222,70 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       return hip_fail(ctx, e, "zero dnorm_weight");
   }
   if (bwd && nl > 0) {
-    if (!ctx->blas) {
-      rocblas_handle h = nullptr;
-      if ((rc = blas_status(ctx, rocblas_create_handle(&h), "rocblas_create_handle")) != PCP_OK) return rc;
-      ctx->blas = h;
-    }
-    rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
-    if ((rc = blas_status(ctx, rocblas_set_stream(h, st), "rocblas_set_stream")) != PCP_OK) return rc;
+    const int ldt = static_cast<int>((nl + 63) / 64 * 64);
     ta.B = a->weight;
     ta.lse2 = F(o_l2);
     ta.coef = F(o_coef);
     ta.dchunk = sp + o_chunk;
     ta.ldd = static_cast<int>(chunk);
+    ta.dchunk_t = a->dweight ? sp + o_dt : nullptr;
+    ta.ldt = ldt;
     float* dhc = want_dy ? F(o_dhc) : nullptr;
-    const float one = 1.f, zero = 0.f;
+    if (a->dweight) {
+      // hidden^T [H, ldt]: the dW product's token operand, zero past the live tokens.
+      const LmTransposeArgs tr{reinterpret_cast<const uint16_t*>(sp + o_hid), H, nl, static_cast<int>(H),
+                               reinterpret_cast<uint16_t*>(sp + o_ht), ldt};
+      if ((e = launch_lm_transpose(tr, st)) != hipSuccess) return hip_fail(ctx, e, "transposing hidden rows");
+    }
     for (int64_t vc0 = 0; vc0 < V; vc0 += chunk) {
       const int64_t w = (V - vc0 < chunk) ? V - vc0 : chunk;
       ta.vc0 = static_cast<int>(vc0);
       ta.vt0 = static_cast<int>(vc0 / kLmTileV);
       ta.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
       if ((e = launch_lm_tiles(kLmBwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head backward tiles");
-      const void* wc = static_cast<const char*>(a->weight) + vc0 * H * 2;
+      // The chunk's two products in one launch (they are independent): the longer one
+      // (dhidden, K = the chunk width, over fewer tiles) first, so the shorter dW tiles
+      // fill the CUs its last round leaves idle.
+      LmTileArgs::Gemm g[2];
+      int ng = 0;
+      std::memset(g, 0, sizeof(g));
       if (want_dy) {
-        // Column-major view: dhidden_c^T [H, nl] (+)= W_c^T [H, w] * D^T [w, nl].
-        rc = blas_status(ctx,
-                         rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_none, static_cast<int>(H),
-                                         nl, static_cast<int>(w), &one, wc, rocblas_datatype_bf16_r,
-                                         static_cast<int>(H), ta.dchunk, rocblas_datatype_bf16_r,
-                                         static_cast<int>(chunk), vc0 == 0 ? &zero : &one, dhc,
-                                         rocblas_datatype_f32_r, static_cast<int>(H), dhc,
-                                         rocblas_datatype_f32_r, static_cast<int>(H), rocblas_datatype_f32_r,
-                                         rocblas_gemm_algo_standard, 0, 0),
-                         "dhidden GEMM");
-        if (rc != PCP_OK) return rc;
+        // W_chunk^T [H, chunk], zero past the chunk's w vocab entries (as D's columns).
+        const LmTransposeArgs tr{static_cast<const uint16_t*>(a->weight) + vc0 * H, H, static_cast<int>(w),
+                                 static_cast<int>(H), reinterpret_cast<uint16_t*>(sp + o_wt), chunk};
+        if ((e = launch_lm_transpose(tr, st)) != hipSuccess) return hip_fail(ctx, e, "transposing W chunk");
+        // dhidden_c[t][h] (+)= sum_v D[t][v] * W^T[h][v]: rows = live tokens, columns = H.
+        LmTileArgs::Gemm& d = g[ng++];
+        d.B = sp + o_chunk;
+        d.ldb = static_cast<int>(chunk);
+        d.V = nl;
+        d.A = sp + o_wt;
+        d.lda = static_cast<int>(chunk);
+        d.N = static_cast<int>(H);
+        d.K = static_cast<int>((w + 63) / 64 * 64);
+        d.nvt = (nl + kLmTileV - 1) / kLmTileV;
+        d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
+        d.C = dhc;
+        d.ldc = static_cast<int>(H);
+        d.accumulate = vc0 > 0;
       }
       if (a->dweight) {
-        // Column-major view: dW_c^T [H, w] = hidden_c^T [H, nl] * D [nl, w].
-        float* dw = a->dweight + vc0 * H;
-        rc = blas_status(ctx,
-                         rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_transpose, static_cast<int>(H),
-                                         static_cast<int>(w), nl, &one, sp + o_hid,
-                                         rocblas_datatype_bf16_r, static_cast<int>(H), ta.dchunk,
-                                         rocblas_datatype_bf16_r, static_cast<int>(chunk), &zero, dw,
-                                         rocblas_datatype_f32_r, static_cast<int>(H), dw, rocblas_datatype_f32_r,
-                                         static_cast<int>(H), rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
-                                         0),
-                         "dweight GEMM");
-        if (rc != PCP_OK) return rc;
+        // dW[v][h] = sum_t D^T[v][t] * hidden^T[h][t]: rows = the chunk's vocab, columns = H.
+        LmTileArgs::Gemm& d = g[ng++];
+        d.B = sp + o_dt;
+        d.ldb = ldt;
+        d.V = static_cast<int>(w);
+        d.A = sp + o_ht;
+        d.lda = ldt;
+        d.N = static_cast<int>(H);
+        d.K = ldt;
+        d.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
+        d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
+        d.C = a->dweight + vc0 * H;
+        d.ldc = static_cast<int>(H);
+        d.accumulate = 0;
       }
+      if ((e = launch_lm_gemms(g, ng, st)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
     }
     if (norm && want_dy) {
       const LmNormBwdArgs nb{dhc, static_cast<const uint16_t*>(a->hidden_states), a->norm_weight, F(o_rstd),
@@ -283,13 +306,6 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
 }
 
 }  // namespace
-
-void release_blas(pcp_ctx* ctx) {
-  if (ctx && ctx->blas) {
-    (void)rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
-    ctx->blas = nullptr;
-  }
-}
 
 }  // namespace pcp
 
