@@ -104,7 +104,9 @@ __device__ __forceinline__ void lm_barrier() {
 // lane l holds token column l%32 and vocab rows 8*(r/4) + 4*(l/32) + r%4, r < 16.
 // Operands stream global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging)
 // through two stages of BK hidden columns.
-template <int MODE>
+// ATR (kLmGemm): the token-role operand is stored K-major and its fragments are read
+// with ds_read_b64_tr_b16 (see below).
+template <int MODE, bool ATR = false>
 __global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
 lm_tile_kernel(LmTileArgs a) {
   using namespace lm;
@@ -117,7 +119,7 @@ lm_tile_kernel(LmTileArgs a) {
   const void* opB = a.B;
   int N = a.N, V = a.V, K = a.H, lda = a.H, ldb = a.H, ntt = a.ntt, nvt = a.nvt, gm = a.group_m, vt0 = a.vt0;
   float* C = nullptr;
-  int ldc = 0, accumulate = 0;
+  int ldc = 0, accumulate = 0, transpose_c = 0, krows_a = 0;
   if constexpr (MODE == kLmGemm) {
     const int p = pid >= a.gemm[0].tiles ? 1 : 0;
     if (p) pid -= a.gemm[0].tiles;
@@ -136,6 +138,8 @@ lm_tile_kernel(LmTileArgs a) {
     C = g.C;
     ldc = g.ldc;
     accumulate = g.accumulate;
+    transpose_c = g.transpose_c;
+    krows_a = g.krows_a;
   }
   int tm, tn;
   if (!lm_tile_coords(pid, ntt, nvt, gm, tm, tn)) return;
@@ -151,26 +155,45 @@ lm_tile_kernel(LmTileArgs a) {
   const int rows_w = min(BV, V - v0), rows_h = min(BT, N - m0);
   const __amdgpu_buffer_rsrc_t rw =
       row_rsrc(reinterpret_cast<const char*>(opB) + static_cast<int64_t>(v0) * wbytes, rows_w * wbytes);
+  // K-major token operand (ATR): the tile is columns [m0, m0 + 256) of rows k; rows
+  // past krows_a fall outside the descriptor and read 0. The range check drops a whole
+  // 16-byte load that runs past the end, so the last row's extent is rounded up to 8
+  // columns (the operand's rows are at least that wide). Columns past N belong to
+  // result columns that are not stored.
   const __amdgpu_buffer_rsrc_t rh =
-      row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0) * hbytes, rows_h * hbytes);
+      ATR ? row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0) * 2,
+                     krows_a > 0 ? static_cast<uint32_t>(krows_a - 1) * hbytes +
+                                       static_cast<uint32_t>((rows_h + 7) & ~7) * 2u
+                                 : 0u)
+          : row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0) * hbytes, rows_h * hbytes);
 
   // Direct-to-LDS loads: wave w fills rows 8*(4w+q) + lane/8, q < 4, of each operand;
   // lane writes LDS slot lane%8 of its row, which holds chunk (lane%8) ^ swz(row).
+  // A K-major operand's stage is 64 k-rows of 512 bytes (256 columns): instruction q
+  // of wave w fills k-rows 2*(4w+q) + lane/32, and LDS slot lane%32 of a k-row holds
+  // 16-byte chunk (lane%32) ^ 4*(k-row % 4), so the transpose reads below, which take
+  // 64 bytes from each of 8 k-rows (k-row % 4 = 0..3, twice), hit every bank twice.
   uint32_t dofw[4], dofh[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int row = 8 * (4 * wave + q) + (lane >> 3);
     const uint32_t c16 = 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
     dofw[q] = static_cast<uint32_t>(row) * wbytes + c16;
-    dofh[q] = static_cast<uint32_t>(row) * hbytes + c16;
+    if constexpr (ATR) {
+      const int krow = 2 * (4 * wave + q) + (lane >> 5);
+      dofh[q] = static_cast<uint32_t>(krow) * hbytes + 16u * static_cast<uint32_t>((lane & 31) ^ (4 * (krow & 3)));
+    } else {
+      dofh[q] = static_cast<uint32_t>(row) * hbytes + c16;
+    }
   }
   auto issue = [&](int st, int buf) {
     char* base = smem + buf * kStageBytes;
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
+    const uint32_t kofh = ATR ? static_cast<uint32_t>(st) * BK * hbytes : koff;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (4 * wave + q) * 1024), 16, dofw[q] + koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (4 * wave + q) * 1024), 16, dofh[q] + koff,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (4 * wave + q) * 1024), 16, dofh[q] + kofh,
                                                0, 0, 0);
     }
   };
@@ -183,13 +206,41 @@ lm_tile_kernel(LmTileArgs a) {
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) fo[kk] = 16 * ((2 * kk + (lane >> 5)) ^ sw);
   const int offA = (wv * 128 + (lane & 31)) * ROWB, offB = kOpBytes + (wt * 64 + (lane & 31)) * ROWB;
+  // K-major token operand: ds_read_b64_tr_b16 hands lane i of each 16-lane block the
+  // element i%4 of the 8-byte chunks addressed by source lanes i/4 + 4k (k < 4). Source
+  // lane j of block b points at k-row k0 + j/4, columns 16*(b%2) + 4*(j%4) of the
+  // fragment's 32, so lane l receives column l%32 at k-rows k0 .. k0 + 3: with k0 =
+  // 16*kk + 8*(l/32) and a second read 4 rows on, the MFMA operand layout (column l%32,
+  // k = 8*(l/32) + 0..7). offBt[j] is the part of the address fixed per lane and block.
+  int offBt[NJ];
+  if constexpr (ATR) {
+    const int x = (lane >> 2) & 3;   // = k-row % 4 of this lane's source row
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int chunk = 8 * wt + 4 * j + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+      offBt[j] = kOpBytes + (8 * (lane >> 5) + x) * 512 + 16 * (chunk ^ (4 * x)) + 8 * (lane & 1);
+    }
+  }
   bf16x8 af[2][4], bfr[2][NJ];
   auto fload = [&](int set, int st, int kk) {
     const char* base = smem + (st % NST) * kStageBytes + fo[kk];
 #pragma unroll
     for (int i = 0; i < 4; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(base + offA + i * 32 * ROWB);
+    if constexpr (ATR) {
+      typedef short v4i16 __attribute__((ext_vector_type(4)));
+      const char* tb = smem + (st % NST) * kStageBytes + kk * 16 * 512;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) bfr[set][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 32 * ROWB);
+      for (int j = 0; j < NJ; ++j) {
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)LM_LDS(tb + offBt[j]));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)LM_LDS(tb + offBt[j] + 4 * 512));
+        bfr[set][j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) bfr[set][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 32 * ROWB);
+    }
   };
 
   f32x16 acc[4][NJ];
@@ -230,6 +281,9 @@ lm_tile_kernel(LmTileArgs a) {
   for (int kb = 0; kb < nk; ++kb) {
     // Buffer (kb + 1) % 2 held stage kb - 1, whose reads all completed before the
     // last barrier; past the end the last stage is reloaded into it (nobody reads it).
+    // Fragment reads per k-step: 6 (4 vocab-role + 2 token-role), or 8 when the token
+    // role takes two transpose reads per fragment.
+    constexpr int kRd = ATR ? 8 : 6;
     issue(min(kb + 1, nk - 1), (kb + 1) & 1);
     fload(1, kb, 1);
     mfmas(0);
@@ -241,35 +295,36 @@ lm_tile_kernel(LmTileArgs a) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);  // half of the stage's loads
+      if constexpr (ATR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
     fload(0, kb, 2);
     mfmas(1);
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
+    for (int q = 0; q < kRd; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    if constexpr (!ATR) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     fload(1, kb, 3);
     mfmas(0);
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
+    for (int q = 0; q < kRd; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    if constexpr (!ATR) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitStage);               // stage kb+1 landed
     lm_barrier();
     fload(0, min(kb + 1, nk - 1), 0);
     mfmas(1);
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
+    for (int q = 0; q < kRd; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    if constexpr (!ATR) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   }
   // Drain the trailing loads before any LDS reuse (the backward epilogue).
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -329,21 +384,43 @@ lm_tile_kernel(LmTileArgs a) {
     }
   } else if constexpr (MODE == kLmGemm) {
     // C[v][t] (+)= the tile; rows past V and columns past N are not stored. For fixed
-    // (i, r) lanes 0-31 and 32-63 each write 32 consecutive floats of one row.
+    // (i, r) lanes 0-31 and 32-63 each write 32 consecutive floats of one row. With
+    // transpose_c the lane's 4 consecutive rows of a column are one 16-byte store.
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int n = m0 + wt * 64 + 32 * j + (lane & 31);
       if (n >= N) continue;
+      if (transpose_c) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int vr = vw + vrow(i, r);
-          if (vr < V) {
-            float* p = C + static_cast<int64_t>(vr) * ldc + n;
-            *p = accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+          for (int q = 0; q < 4; ++q) {
+            const int vr = vw + vrow(i, 4 * q);
+            if (vr < V) {
+              float4* p = reinterpret_cast<float4*>(C + static_cast<int64_t>(n) * ldc + vr);
+              float4 v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+              if (accumulate) {
+                const float4 o = *p;
+                v.x += o.x;
+                v.y += o.y;
+                v.z += o.z;
+                v.w += o.w;
+              }
+              *p = v;
+            }
           }
-        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int vr = vw + vrow(i, r);
+            if (vr < V) {
+              float* p = C + static_cast<int64_t>(vr) * ldc + n;
+              *p = accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+            }
+          }
+      }
     }
   } else {
     // dlogits[t][v] = coef_t * (onehot - 2^(x*log2e - lse2_t)) in bf16, staged as a
@@ -367,15 +444,6 @@ lm_tile_kernel(LmTileArgs a) {
             l2 = a.lse2[n];
             rel = lm_id(a, n) - vw;
           }
-          // Vocab-major copy (tokens contiguous, for dW = D^T * hidden). Each lane holds
-          // one token and 4 consecutive vocab rows; a 4 x 4 transpose within each quad of
-          // lanes (two DPP exchanges) leaves lane l with vocab row l%4 of the quad's 4
-          // tokens, stored as 8 bytes. Token columns [N, ldt) are written as 0 (cf = 0
-          // there), vocab rows past the chunk not at all.
-          const int nq = n & ~3;
-          const bool dt_on = a.dchunk_t != nullptr && nq < a.ldt;
-          uint16_t* dtq = static_cast<uint16_t*>(a.dchunk_t) +
-                          (static_cast<int64_t>(v0 - a.vc0 + wv * 128 + (lane & 3)) * a.ldt + nq);
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -389,22 +457,6 @@ lm_tile_kernel(LmTileArgs a) {
               }
               const uint32_t lo = pack2<BF16T>(d[0], d[1]), hi = pack2<BF16T>(d[2], d[3]);
               *reinterpret_cast<uint2*>(Ds + tcol * LDD + wv * 128 + vrow(i, 4 * q)) = make_uint2(lo, hi);
-              if (a.dchunk_t) {
-                // Step 1, lanes l and l^2: lanes with bit 1 clear keep rows 0-1 and take the
-                // partner's rows 0-1 (tokens s, s+2); the others keep rows 2-3.
-                const bool b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
-                const uint32_t y = static_cast<uint32_t>(
-                    __builtin_amdgcn_update_dpp(0, static_cast<int>(b1 ? lo : hi), 0x4E, 0xF, 0xF, false));
-                const uint32_t P = b1 ? y : lo, Q = b1 ? hi : y;
-                // Step 2, lanes l and l^1: bit 0 clear keeps the even row, set the odd row.
-                const uint32_t snd = b0 ? ((P & 0xFFFFu) | (Q << 16)) : ((P >> 16) | (Q & 0xFFFF0000u));
-                const uint32_t rcv = static_cast<uint32_t>(
-                    __builtin_amdgcn_update_dpp(0, static_cast<int>(snd), 0xB1, 0xF, 0xF, false));
-                const uint32_t o0 = b0 ? ((rcv & 0xFFFFu) | (P & 0xFFFF0000u)) : ((P & 0xFFFFu) | (rcv << 16));
-                const uint32_t o1 = b0 ? ((rcv >> 16) | (Q & 0xFFFF0000u)) : ((Q & 0xFFFFu) | (rcv & 0xFFFF0000u));
-                if (dt_on && v0 - a.vc0 + wv * 128 + vrow(i, 4 * q) + 3 < a.ldd)
-                  *reinterpret_cast<uint2*>(dtq + static_cast<int64_t>(vrow(i, 4 * q)) * a.ldt) = make_uint2(o0, o1);
-              }
             }
         }
       }
@@ -620,10 +672,11 @@ int lm_group_m(int mode, int ntt) {
 
 template <int MODE>
 hipError_t launch_tiles_mode(const LmTileArgs& a, int grid, hipStream_t st) {
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE>),
+  constexpr bool kAtr = MODE == kLmGemm;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE, kAtr>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
   if (e != hipSuccess) return e;
-  lm_tile_kernel<MODE><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
+  lm_tile_kernel<MODE, kAtr><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
   return hipGetLastError();
 }
 

@@ -35,17 +35,19 @@ struct LmTileArgs {
   const float* coef;    // [N] d loss / d logp
   void* dchunk;         // [N, ldd] bf16 dlogits of vocab [vc0, vc0 + ldd)
   int vc0, ldd;
-  void* dchunk_t;       // [ldd, ldt] the same dlogits vocab-major (tokens contiguous), or nullptr;
-  int ldt;              //   tokens [N, ldt) are written as 0
   // kLmGemm: up to two independent products in one launch (gemm[0] takes the first
   // gemm[0].tiles workgroups, gemm[1] the rest); the fields above are unused.
+  // result[v][t] = sum_k B[v][k] * A(k, t): B rows are K-contiguous, A is stored
+  // K-major (element (k, t) at A[k * lda + t]) and read with LDS transpose loads.
   struct Gemm {
-    const void* A;      // [N, lda] bf16: "token" rows (result columns)
-    const void* B;      // [V, ldb] bf16: "vocab" rows (result rows)
-    int N, V, K;        // K % 64 == 0, K <= lda, ldb
-    int lda, ldb;       // row strides in elements
-    float* C;           // [V, ldc] f32 result
-    int ldc;
+    const void* A;      // [krows_a, lda] bf16, K-major: "token" columns (result columns)
+    const void* B;      // [V, ldb] bf16, K-contiguous: "vocab" rows (result rows)
+    int N, V, K;        // K % 64 == 0, K <= ldb
+    int lda, ldb;       // row strides in elements (lda >= N rounded up to 8)
+    int krows_a;        // rows of A that exist; rows [krows_a, K) read as 0
+    float* C;           // f32 result: row v, column t at C[v * ldc + t], or at
+    int ldc;            //   C[t * ldc + v] with transpose_c (then V % 4 == 0)
+    int transpose_c;
     int accumulate;     // 1: C += product, 0: C = product
     int ntt, nvt;       // tiles over N and over V
     int group_m;        // set by launch_lm_gemms

@@ -8,10 +8,13 @@
 // per-(token, vocab tile) log-sum-exp partials and the target logit; one wave per
 // token merges the partials. Then the GRPO terms per token and the loss reduction
 // (the same kernels as the logits-input path). Backward, per vocab chunk: logits
-// tiles recomputed into bf16 dlogits D (token-major, and vocab-major for dW), then two
-// products on the same MFMA tile kernel (kLmGemm, both operands K-contiguous):
-//   dhidden (+)= D_chunk * W_chunk      (W_chunk transposed per chunk),
-//   dW_chunk    = D_chunk^T * hidden    (the compact hidden rows transposed once),
+// tiles recomputed into bf16 dlogits D (token-major), then two products on the same
+// MFMA tile kernel (kLmGemm: one operand K-contiguous, the other read K-major with LDS
+// transpose loads), in one launch:
+//   dhidden (+)= D_chunk * W_chunk               (W_chunk read K-major as stored),
+//   dW_chunk^T  = hidden^T * D_chunk, stored transposed into dW's rows
+//                                                (D_chunk read K-major as stored; the
+//                                                 compact hidden rows transposed once),
 // and the compact dhidden rows are scattered back (zero rows for dead tokens).
 // This mirrors the LM head's VJP (src/autodiff/vjp_rules.zig:426-497, matmulVJP).
 
@@ -43,11 +46,17 @@ int validate_lm(const pcp_lmhead_args* a) {
   int64_t n;
   if (mul_overflows(a->n_seq, a->rows, &n) || n > (1 << 28))
     return fail(nullptr, PCP_ERR_OVERFLOW, "n_seq * rows exceeds 2^28 tokens");
-  // dW reads 256-row slabs of the vocab-major dlogits and of the transposed hidden rows
-  // (one row per vocab entry or hidden column, one element per token) through 32-bit
-  // buffer offsets.
-  if (a->dweight && n > (1 << 22))
-    return fail(nullptr, PCP_ERR_OVERFLOW, "dweight takes at most 2^22 tokens per call (got %lld)", (long long)n);
+  // The products address a dlogits chunk [tokens, chunk] and a W chunk [chunk, H] with
+  // 32-bit buffer offsets.
+  {
+    const int64_t ch = a->vocab_chunk ? a->vocab_chunk : kDefaultChunk;
+    if ((a->dweight || a->dhidden || a->dnorm_weight) &&
+        ((n + 63) / 64 * 64 * ch * 2 >= (int64_t{1} << 32) || ch * a->hidden * 2 >= (int64_t{1} << 32)))
+      return fail(nullptr, PCP_ERR_OVERFLOW,
+                  "tokens x vocab_chunk and vocab_chunk x hidden must stay under 2^31 elements for the "
+                  "backward (%lld tokens, chunk %lld, hidden %lld): pass a smaller vocab_chunk",
+                  (long long)n, (long long)ch, (long long)a->hidden);
+  }
   if (a->vocab_chunk < 0 || a->vocab_chunk % kLmTileV != 0)
     return fail(nullptr, PCP_ERR_INVALID_ARG, "vocab_chunk must be a multiple of %d", kLmTileV);
   if (!a->hidden_states || !a->weight || !a->ids) return fail(nullptr, PCP_ERR_INVALID_ARG, "hidden_states / weight / ids is NULL");
@@ -106,12 +115,10 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_part = take(8 * static_cast<size_t>(N) * npart);
   const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
   const size_t o_chunk = bwd ? take(2 * static_cast<size_t>(N) * chunk) : 0;
-  // Token-padded width of the vocab-major dlogits and the transposed hidden rows (the
-  // dW product's K, a multiple of the 64-deep pipeline stage).
+  // Token-padded width of the transposed hidden rows (the dW product's K, a multiple
+  // of the 64-deep pipeline stage).
   const int64_t ldt_max = (N + 63) / 64 * 64;
-  const size_t o_dt = a->dweight ? take(2 * static_cast<size_t>(chunk) * ldt_max) : 0;
   const size_t o_ht = a->dweight ? take(2 * static_cast<size_t>(H) * ldt_max) : 0;
-  const size_t o_wt = want_dy ? take(2 * static_cast<size_t>(H) * chunk) : 0;
   const size_t o_dhc = want_dy ? take(4 * static_cast<size_t>(N) * H) : 0;
   const size_t o_rstd = norm ? take(4 * N) : 0;
   const size_t o_gpart = a->dnorm_weight ? take(4 * static_cast<size_t>(kLmNormSlices) * H) : 0;
@@ -228,8 +235,6 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     ta.coef = F(o_coef);
     ta.dchunk = sp + o_chunk;
     ta.ldd = static_cast<int>(chunk);
-    ta.dchunk_t = a->dweight ? sp + o_dt : nullptr;
-    ta.ldt = ldt;
     float* dhc = want_dy ? F(o_dhc) : nullptr;
     if (a->dweight) {
       // hidden^T [H, ldt]: the dW product's token operand, zero past the live tokens.
@@ -250,17 +255,15 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       int ng = 0;
       std::memset(g, 0, sizeof(g));
       if (want_dy) {
-        // W_chunk^T [H, chunk], zero past the chunk's w vocab entries (as D's columns).
-        const LmTransposeArgs tr{static_cast<const uint16_t*>(a->weight) + vc0 * H, H, static_cast<int>(w),
-                                 static_cast<int>(H), reinterpret_cast<uint16_t*>(sp + o_wt), chunk};
-        if ((e = launch_lm_transpose(tr, st)) != hipSuccess) return hip_fail(ctx, e, "transposing W chunk");
-        // dhidden_c[t][h] (+)= sum_v D[t][v] * W^T[h][v]: rows = live tokens, columns = H.
+        // dhidden_c[t][h] (+)= sum_v D[t][v] * W[vc0 + v][h]: rows = live tokens, columns
+        // = H; W rows past the chunk's w read as 0 (as D's columns there are 0).
         LmTileArgs::Gemm& d = g[ng++];
         d.B = sp + o_chunk;
         d.ldb = static_cast<int>(chunk);
         d.V = nl;
-        d.A = sp + o_wt;
-        d.lda = static_cast<int>(chunk);
+        d.A = static_cast<const uint16_t*>(a->weight) + vc0 * H;
+        d.lda = static_cast<int>(H);
+        d.krows_a = static_cast<int>(w);
         d.N = static_cast<int>(H);
         d.K = static_cast<int>((w + 63) / 64 * 64);
         d.nvt = (nl + kLmTileV - 1) / kLmTileV;
@@ -270,19 +273,22 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         d.accumulate = vc0 > 0;
       }
       if (a->dweight) {
-        // dW[v][h] = sum_t D^T[v][t] * hidden^T[h][t]: rows = the chunk's vocab, columns = H.
+        // dW[vc0 + v][h] = sum_t hidden^T[h][t] * D[t][v]: result rows = H, columns = the
+        // chunk's vocab, stored transposed; D rows past the live tokens read as 0.
         LmTileArgs::Gemm& d = g[ng++];
-        d.B = sp + o_dt;
+        d.B = sp + o_ht;
         d.ldb = ldt;
-        d.V = static_cast<int>(w);
-        d.A = sp + o_ht;
-        d.lda = ldt;
-        d.N = static_cast<int>(H);
+        d.V = static_cast<int>(H);
+        d.A = sp + o_chunk;
+        d.lda = static_cast<int>(chunk);
+        d.krows_a = nl;
+        d.N = static_cast<int>(w);
         d.K = ldt;
-        d.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
-        d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
+        d.nvt = static_cast<int>((H + kLmTileV - 1) / kLmTileV);
+        d.ntt = static_cast<int>((w + kLmTileT - 1) / kLmTileT);
         d.C = a->dweight + vc0 * H;
         d.ldc = static_cast<int>(H);
+        d.transpose_c = 1;
         d.accumulate = 0;
       }
       if ((e = launch_lm_gemms(g, ng, st)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");

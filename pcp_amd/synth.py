@@ -72,9 +72,9 @@ CONFIGS = {
 class LmheadConfig:
     """Configuration 5: fused LM-head + GRPO log-prob. hidden [N, H] ~ N(0, 1),
     W [V, H] ~ N(0, 0.02^2), W_ref = W + N(0, 0.002^2), all bf16; tokens drawn from
-    softmax(hidden W^T) would need the logits, so targets are uniform in [0, V)
-    (the loss terms do not depend on how targets were drawn); lengths, rewards and
-    groups as configuration 2 (G=8, T=512)."""
+    softmax(hidden W^T) by Gumbel-max as in configuration 2 (the logits are formed
+    once, in token chunks, for the draw only); lengths, rewards and groups as
+    configuration 2 (G=8, T=512)."""
     key: int = 5
     name: str = "fused-lm-head"
     prompts: int = 4
@@ -120,11 +120,32 @@ def make_lmhead_inputs(cfg: LmheadConfig, device="cuda"):
     check(lib().pcp_synth_logits(weight.data_ptr(), ref_weight.data_ptr(), weight.numel(), int(DType.bf16),
                                  ctypes.c_float(cfg.std_w), ctypes.c_float(cfg.std_r), cfg.seed + 11, stream))
     rng = np.random.default_rng(cfg.seed + 12)
-    ids = torch.from_numpy(rng.integers(0, V, size=(S, T)).astype(np.int64)).to(device)
+    ids = sample_lmhead_ids(hidden, weight, cfg.seed + 13, chunk=1024).view(S, T)
     mask = torch.from_numpy(mask_from_lengths(lengths, T)).to(device)
     old_shift = torch.from_numpy((rng.standard_normal((S, T)) * cfg.old_noise).astype(np.float32)).to(device)
     return {"hidden": hidden, "weight": weight, "ref_weight": ref_weight, "ids": ids, "mask": mask,
             "rewards": torch.from_numpy(rewards).to(device), "old_shift": old_shift, "lengths": lengths}
+
+
+def sample_lmhead_ids(hidden, weight, seed: int, chunk: int = 1024):
+    """One token per hidden row drawn from softmax(hidden W^T) with the library's
+    Gumbel-max sampler (pcp_synth_sample_tokens, as the logits configurations), over
+    token chunks of bf16 logits formed by torch for the draw only (seed + chunk index
+    keeps the noise of every chunk distinct). Returns int64 [N] on the device."""
+    import torch
+    import torch.nn.functional as F
+
+    N = hidden.shape[0]
+    V = weight.shape[0]
+    ids = torch.empty(N, dtype=torch.int64, device=hidden.device)
+    stream = torch.cuda.current_stream().cuda_stream or None
+    for k, n0 in enumerate(range(0, N, chunk)):
+        logits = F.linear(hidden[n0:n0 + chunk], weight).contiguous()
+        n = logits.shape[0]
+        check(lib().pcp_synth_sample_tokens(logits.data_ptr(), int(DType.bf16), n, V, seed + k,
+                                            ids[n0:n0 + n].data_ptr(), stream))
+        del logits
+    return ids
 
 
 def per_sequence(cfg) -> tuple[np.ndarray, np.ndarray]:
