@@ -187,10 +187,15 @@ int pcp_sync(pcp_ctx* ctx);
  * Host-bytes path. ~ WorkerBackend.executeFunction (worker_backend.zig:27-33),
  * IreeBackend.execute (iree.zig:336-442). `fn` names one of:
  *
- *  "grpo_loss_fwd_bwd" (also "main", the executeTrainingStep name, iree.zig:463-486)
+ *  "grpo_loss_fwd_bwd"
  *     the reference loss head: in  (logits[G,T,V] bf16|f16|f32, input_ids[G,T] i64|i32,
  *                                   attention_mask[G,T] f32|bool, advantages[G] f32)
  *                              out (loss f32[], dlogits[G,T,V] logits dtype)
+ *  "main" (executeTrainingStep's name, iree.zig:463-486) is the training VMFB's whole
+ *     step, [params..., buffers..., ids, mask, adv] -> parameter gradients
+ *     (graph_builder.zig:302-426, rl_shepherd.zig:529-604). This library holds only its
+ *     loss head, so "main" returns PCP_ERR_UNSUPPORTED with a message naming the split:
+ *     the model forward to logits, "grpo_loss_fwd_bwd", the model backward from dlogits.
  *  "grpo_clip_kl_fwd_bwd"
  *     in  (logits[S,T,V], ref_logits[S,T,V], input_ids[S,T], attention_mask[S,T],
  *          old_logp f32[S,T], rewards f32[S], hyper f32[4] = {group_size, clip_eps,

@@ -33,7 +33,7 @@ from dataclasses import dataclass
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libpcp_oracle.so")
+_LIB_PATH = os.environ.get("PCP_ORACLE_LIB") or os.path.join(_HERE, "libpcp_oracle.so")
 
 F16, BF16, F32, F64 = 0, 1, 2, 3
 EXACT, REF_F32, FAITHFUL = 0, 1, 2

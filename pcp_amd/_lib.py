@@ -11,7 +11,9 @@ import enum
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libpcp_grpo.so")
+# PCP_GRPO_LIB selects another build of the same library (the host-sanitizer build of
+# the CPU test run); by default the in-tree one.
+LIB_PATH = os.environ.get("PCP_GRPO_LIB") or os.path.join(_HERE, "libpcp_grpo.so")
 
 
 class DType(enum.IntEnum):

@@ -3,7 +3,8 @@
 Mirrors the interface the GRPO step reaches (src/backends/worker_backend.zig:7-62,
 src/backends/iree.zig:38-497): ``init(backend, device_id)``, ``execute(artifact,
 function_name, inputs_data, input_shapes, input_dtypes) -> list of output bytes``,
-``executeFunction``, ``executeTrainingStep`` (function "main"), ``getBackendType``,
+``executeFunction``, ``executeTrainingStep`` (function "main", which this library answers
+with PCP_ERR_UNSUPPORTED: it holds the loss head, not the whole step), ``getBackendType``,
 ``deinit`` and ``asWorkerBackend``. Inputs are borrowed host byte buffers,
 outputs are owned by the caller, errors raise PcpError with the library's status
 (the Zig error union's analogue). The ``artifact`` argument is accepted for
@@ -62,7 +63,9 @@ class HipGrpoBackend:
         return self.execute(artifact, function_name, inputs_data, input_shapes, input_dtypes)
 
     def executeTrainingStep(self, artifact, inputs_data, input_shapes, input_dtypes=None):
-        # iree.zig:463-486 runs "main"; here "main" is the reference loss head.
+        # iree.zig:463-486 runs the VMFB's "main", the whole training step. The library
+        # holds only its loss head, so this raises PcpError (PCP_ERR_UNSUPPORTED) with a
+        # message naming the split: forward to logits, "grpo_loss_fwd_bwd", backward.
         return self.execute(artifact, "main", inputs_data, input_shapes, input_dtypes)
 
     def asWorkerBackend(self) -> "WorkerBackend":

@@ -300,10 +300,11 @@ int run_loss_groups(pcp_ctx* ctx, const pcp_grpo_args& full, const In& L, const 
 
 // ---- functions ------------------------------------------------------------
 
-enum Fn { kLossFwdBwd, kClipKl, kLogprob, kAdvantages, kLmhead, kUnknown };
+enum Fn { kLossFwdBwd, kClipKl, kLogprob, kAdvantages, kLmhead, kMain, kUnknown };
 
 Fn lookup(const char* fn) {
-  if (!std::strcmp(fn, "grpo_loss_fwd_bwd") || !std::strcmp(fn, "main")) return kLossFwdBwd;
+  if (!std::strcmp(fn, "grpo_loss_fwd_bwd")) return kLossFwdBwd;
+  if (!std::strcmp(fn, "main")) return kMain;
   if (!std::strcmp(fn, "grpo_clip_kl_fwd_bwd")) return kClipKl;
   if (!std::strcmp(fn, "grpo_logprob_fwd")) return kLogprob;
   if (!std::strcmp(fn, "grpo_advantages")) return kAdvantages;
@@ -468,6 +469,12 @@ int execute(pcp_ctx* ctx, const char* fn, int n_in, const void* const* data, con
   *out_nbytes = nullptr;
   const Fn f = lookup(fn);
   if (f == kUnknown) return fail(ctx, PCP_ERR_UNKNOWN_FUNCTION, "no function named '%s'", fn);
+  if (f == kMain)
+    return fail(ctx, PCP_ERR_UNSUPPORTED,
+                "'main' is the training VMFB's whole step ([params..., buffers..., input_ids, attention_mask, "
+                "advantages] -> parameter gradients); this library is its loss head only: run the model "
+                "forward to logits, call 'grpo_loss_fwd_bwd' (logits, input_ids, attention_mask, advantages) "
+                "-> (loss, dlogits), then the model backward seeded with dlogits");
 
   static const int kDefLoss[] = {PCP_F32, PCP_I64, PCP_F32, PCP_F32};
   static const int kDefClip[] = {PCP_F32, PCP_F32, PCP_I64, PCP_F32, PCP_F32, PCP_F32, PCP_F32};

@@ -214,31 +214,45 @@ def test_execute_argument_errors_without_device():
         execute_raw(None, "no_such_fn", data, shapes, dts)
     assert e.value.code == -7
     with pytest.raises(PcpError) as e:
-        execute_raw(None, "main", data[:3], shapes[:3], dts[:3])
+        execute_raw(None, "grpo_loss_fwd_bwd", data[:3], shapes[:3], dts[:3])
     assert e.value.code == -8
     with pytest.raises(PcpError) as e:
-        execute_raw(None, "main", data, [shapes[0], (2, 4), shapes[2], shapes[3]], dts)
+        execute_raw(None, "grpo_loss_fwd_bwd", data, [shapes[0], (2, 4), shapes[2], shapes[3]], dts)
     assert e.value.code == -1   # byte count does not match the shape
     with pytest.raises(PcpError) as e:
-        execute_raw(None, "main", data, shapes, [DType.f64, DType.i64, DType.f32, DType.f32])
+        execute_raw(None, "grpo_loss_fwd_bwd", data, shapes, [DType.f64, DType.i64, DType.f32, DType.f32])
     assert e.value.code == -1   # f64 bytes != f32 bytes for the same shape -> size mismatch first
     bad = np.array(data[0], np.float64)
     with pytest.raises(PcpError) as e:
-        execute_raw(None, "main", [bad] + data[1:], shapes, [DType.f64, DType.i64, DType.f32, DType.f32])
+        execute_raw(None, "grpo_loss_fwd_bwd", [bad] + data[1:], shapes, [DType.f64, DType.i64, DType.f32, DType.f32])
     assert e.value.code == -2
     ids = data[1].copy()
     ids[1, 3] = 11                  # == V: out of range
     with pytest.raises(PcpError) as e:
-        execute_raw(None, "main", [data[0], ids, data[2], data[3]], shapes, dts)
+        execute_raw(None, "grpo_loss_fwd_bwd", [data[0], ids, data[2], data[3]], shapes, dts)
     assert e.value.code == -3
     ids[1, 3] = -100                # the ignore index is accepted
     with pytest.raises(PcpError) as e:
-        execute_raw(None, "main", [data[0], ids, data[2], data[3]], shapes, dts)
+        execute_raw(None, "grpo_loss_fwd_bwd", [data[0], ids, data[2], data[3]], shapes, dts)
     assert e.value.code == -1 and "context is NULL" in str(e.value)
     # dtypes == NULL selects the function's defaults (f32 / i64)
     with pytest.raises(PcpError) as e:
-        execute_raw(None, "main", data, shapes, None)
+        execute_raw(None, "grpo_loss_fwd_bwd", data, shapes, None)
     assert "context is NULL" in str(e.value)
+
+
+def test_execute_main_names_the_split():
+    # The reference's "main" is the whole training step (params in, parameter gradients
+    # out); the library holds its loss head only and says how to split the VMFB.
+    data, shapes = _ref_inputs()
+    with pytest.raises(PcpError) as e:
+        execute_raw(None, "main", data, shapes, [DType.f32, DType.i64, DType.f32, DType.f32])
+    assert e.value.code == -10
+    msg = str(e.value)
+    assert "grpo_loss_fwd_bwd" in msg and "forward to logits" in msg and "backward seeded with dlogits" in msg
+    with pytest.raises(PcpError) as e:
+        HipGrpoBackend(None, _lib.Backend.rocm, 0).executeTrainingStep(None, data, shapes)
+    assert e.value.code == -10
 
 
 def _lm_inputs(S=2, T=6, H=64, V=40):

@@ -349,15 +349,98 @@ def test_execute_reference_signature():
     be = HipGrpoBackend.init()
     wb = be.asWorkerBackend()
     S, T, V = c["logits"].shape
-    outs = wb.executeTrainingStep(None, [c["logits"], c["ids"], c["mask"], c["advantages"]],
-                                  [c["logits"].shape, c["ids"].shape, c["mask"].shape, c["advantages"].shape],
-                                  [DType.f32, DType.i64, DType.f32, DType.f32])
+    args = ([c["logits"], c["ids"], c["mask"], c["advantages"]],
+            [c["logits"].shape, c["ids"].shape, c["mask"].shape, c["advantages"].shape],
+            [DType.f32, DType.i64, DType.f32, DType.f32])
+    outs = wb.executeFunction(None, "grpo_loss_fwd_bwd", *args)
+    with pytest.raises(PcpError) as e:   # the whole step ("main") is not this library's
+        wb.executeTrainingStep(None, *args)
+    assert e.value.code == -10
     loss = np.frombuffer(outs[0], np.float32)[0]
     dl = np.frombuffer(outs[1], np.float32).reshape(S, T, V)
     assert abs(loss - c["exp_loss"]) <= golden_loss_tol(c)
     assert_dlogits(dl, c["exp_dlogits"], golden_floor_rows(c), False)
     assert not np.any(dl[:, T - 1])  # the sliced-off last position gets a zero gradient
     be.deinit()
+
+
+C_HOST = r"""
+/* A C caller of the host-bytes boundary, as INTEGRATION.md's Zig binding compiles:
+ * pcp_init -> pcp_execute("grpo_loss_fwd_bwd") -> pcp_free -> pcp_destroy.
+ * argv: S T V dir; reads dir/{logits,ids,mask,adv}.bin, writes dir/{loss,dlogits}.bin. */
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include "pcp_grpo.h"
+static void* slurp(const char* dir, const char* name, size_t n) {
+  char path[1024]; snprintf(path, sizeof path, "%s/%s", dir, name);
+  FILE* f = fopen(path, "rb"); void* p = malloc(n);
+  if (!f || !p || fread(p, 1, n, f) != n) { fprintf(stderr, "read %s\n", path); exit(3); }
+  fclose(f); return p;
+}
+static void spill(const char* dir, const char* name, const void* p, size_t n) {
+  char path[1024]; snprintf(path, sizeof path, "%s/%s", dir, name);
+  FILE* f = fopen(path, "wb");
+  if (!f || fwrite(p, 1, n, f) != n) { fprintf(stderr, "write %s\n", path); exit(3); }
+  fclose(f);
+}
+int main(int argc, char** argv) {
+  if (argc != 5) return 2;
+  const int64_t S = atoll(argv[1]), T = atoll(argv[2]), V = atoll(argv[3]);
+  const char* dir = argv[4];
+  const size_t nb[4] = {(size_t)(S * T * V) * 4, (size_t)(S * T) * 8, (size_t)(S * T) * 4, (size_t)S * 4};
+  const void* data[4] = {slurp(dir, "logits.bin", nb[0]), slurp(dir, "ids.bin", nb[1]),
+                         slurp(dir, "mask.bin", nb[2]), slurp(dir, "adv.bin", nb[3])};
+  const int64_t s0[3] = {S, T, V}, s1[2] = {S, T}, s3[1] = {S};
+  const int64_t* shapes[4] = {s0, s1, s1, s3};
+  const int ranks[4] = {3, 2, 2, 1};
+  const int dtypes[4] = {PCP_F32, PCP_I64, PCP_F32, PCP_F32};
+  pcp_ctx* ctx = NULL;
+  int rc = pcp_init(PCP_BACKEND_ROCM, 0, &ctx);
+  if (rc != PCP_OK) { fprintf(stderr, "pcp_init %d: %s\n", rc, pcp_last_error(NULL)); return 4; }
+  int n_out = 0; void** outs = NULL; size_t* sizes = NULL;
+  rc = pcp_execute(ctx, "grpo_loss_fwd_bwd", 4, data, nb, shapes, ranks, dtypes, &n_out, &outs, &sizes);
+  if (rc != PCP_OK) { fprintf(stderr, "pcp_execute %d: %s\n", rc, pcp_last_error(ctx)); return 5; }
+  if (n_out != 2 || sizes[0] != 4 || sizes[1] != nb[0]) { fprintf(stderr, "outputs %d\n", n_out); return 6; }
+  spill(dir, "loss.bin", outs[0], sizes[0]);
+  spill(dir, "dlogits.bin", outs[1], sizes[1]);
+  pcp_free(ctx, n_out, outs, sizes);
+  pcp_destroy(ctx);
+  for (int i = 0; i < 4; ++i) free((void*)data[i]);
+  printf("ok %d outputs\n", n_out);
+  return 0;
+}
+"""
+
+
+def test_c_host_execute_end_to_end(tmp_path):
+    """INTEGRATION.md's call sequence from a compiled C host on the golden case
+    v64_shifted (the reference's shifted layout): the loss and dlogits it writes match the
+    torch float64 fixture at the golden bars."""
+    import subprocess
+    from pcp_amd import _lib
+
+    c = CASES["v64_shifted"]
+    S, T, V = c["logits"].shape
+    for name, key, dt in [("logits.bin", "logits", np.float32), ("ids.bin", "ids", np.int64),
+                          ("mask.bin", "mask", np.float32), ("adv.bin", "advantages", np.float32)]:
+        np.ascontiguousarray(c[key], dtype=dt).tofile(tmp_path / name)
+    src = tmp_path / "host.c"
+    src.write_text(C_HOST)
+    exe = tmp_path / "host"
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    subprocess.run(["gcc", "-std=c99", "-O1", "-I", inc, str(src), "-L", libdir, "-lpcp_grpo",
+                    f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
+    print(f"C host: pcp_execute(grpo_loss_fwd_bwd) on v64_shifted S={S} T={T} V={V}", flush=True)
+    r = subprocess.run([str(exe), str(S), str(T), str(V), str(tmp_path)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+    loss = np.fromfile(tmp_path / "loss.bin", np.float32)[0]
+    dl = np.fromfile(tmp_path / "dlogits.bin", np.float32).reshape(S, T, V)
+    assert abs(loss - c["exp_loss"]) <= golden_loss_tol(c)
+    assert_dlogits(dl, c["exp_dlogits"], golden_floor_rows(c), False)
+    assert not np.any(dl[:, T - 1])
 
 
 def test_execute_clip_kl_and_logprob():
