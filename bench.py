@@ -377,16 +377,21 @@ def bench_nesterov(args) -> None:
 
 
 def bench_sample(args) -> None:
-    """The rollout sampler: one decoding step of the 64 rollouts of configuration 2
-    (8 prompts x G=8) over f32 logits [64, 151936] in HBM (Sampler.sample,
-    math.zig:21-58, at temperature 0.7, the reference's default, generation_engine.zig:163)."""
+    """The rollout sampler over f32 logits [R, 151936] in HBM (Sampler.sample,
+    math.zig:21-58, at temperature 0.7, the reference's default, generation_engine.zig:163).
+    R = 64 (--rows, default) is one decoding step of configuration 2's 64 rollouts; R = 1
+    is the reference's own call pattern, one row per generated token. Every call returns
+    with the tokens on the device (the library synchronises), so ms_per_step is the
+    latency of one call. The CPU baseline is the reference's path for the same rows: copy
+    the logits to host memory (600 KB per row, generation_engine.zig:255-268), then the
+    sequential sampler loop."""
     import numpy as np
     import torch
 
     from pcp_amd import step
 
     dev = torch.device("cuda:0")
-    R, V, T = 64, 151936, 0.7
+    R, V, T = args.rows, 151936, 0.7
     gen = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn((R, V), device=dev, generator=gen) * 3
     u = torch.rand(R, device=dev, generator=gen)
@@ -399,33 +404,36 @@ def bench_sample(args) -> None:
     ms_step = elapsed * 1e3 / args.steps
     alg = R * V * 4 + R * 4 + R * 8
     line = {
-        "metric": "rollout sampler tokens/s and achieved HBM GB/s, 64 rows x V=151936 f32",
+        "metric": f"rollout sampler tokens/s and achieved HBM GB/s, {R} row{'s' if R > 1 else ''} x V=151936 f32",
         "value": R / (ms_step / 1e3), "unit": "sampled tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic (torch normal logits, uniform draws)",
-        "config": {"workload": f"Sampler.sample at T={T} over {R} rows of {V} f32 logits", "rows": R, "vocab": V},
+        "config": {"workload": f"Sampler.sample at T={T} over {R} rows of {V} f32 logits", "rows": R, "vocab": V,
+                   "latency_us_per_call": ms_step * 1e3},
         "roofline": {"bound": "hbm", "achieved": alg / (kernel_ms / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": alg / (kernel_ms / 1e3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "sample_part_kernel<F32T> + sample_select_kernel<F32T>", "kernel_ms": kernel_ms,
-                     "algorithmic_bytes": alg},
+                     "kernel": "sampler kernels (one call)", "kernel_ms": kernel_ms, "algorithmic_bytes": alg},
     }
-    tfile = os.path.join(ROOT, "profiles", "traffic_sample.json")
+    tfile = os.path.join(ROOT, "profiles", "traffic_sample.json" if R == 64 else f"traffic_sample_rows{R}.json")
     if os.path.exists(tfile):
         with open(tfile) as f:
             line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
     if not args.no_cpu_baseline:
         from oracle import oracle as orc
-        xh, uh = x.cpu().numpy(), u.cpu().numpy()
+        uh = u.cpu().numpy()
 
         def run():
+            xh = x.cpu().numpy()                       # the per-step device-to-host copy of the logits
             for r in range(R):
                 orc.sample(xh[r], T, float(uh[r]))
 
         med, times = median_timing(run)
         line["cpu_baseline"] = protocol_record(
             R / med, "sampled tokens/s", 1, "the reference's sampler loop (math.zig:21-58) is single-threaded",
-            "port", f"{R} rows: oracle f32 loop of math.zig:21-58 (step_oracle.cpp), one thread, logits already "
-                    "in host memory", value_1t=R / med, times=times)
+            "port", f"{R} row{'s' if R > 1 else ''}: device-to-host copy of the f32 logits ({R * V * 4} bytes, "
+                    "generation_engine.zig:255-268) + oracle f32 loop of math.zig:21-58 (step_oracle.cpp), one "
+                    "thread", value_1t=R / med, times=times)
+        line["cpu_baseline"]["latency_us_per_call"] = med * 1e6
     print(json.dumps(line), flush=True)
 
 
@@ -660,6 +668,9 @@ def main() -> None:
     ap.add_argument("--exact-bf16", action="store_true",
                     help="loss workload: PCP_FLAG_EXACT_BF16 (no f16 softmax terms in the bf16 dlogits pass)")
     ap.add_argument("--policy-only", action="store_true", help="logprob workload: the policy rows only")
+    ap.add_argument("--rows", type=int, default=64,
+                    help="sample workload: rows per call (64: a decoding step of config 2; 1: the reference's "
+                         "one row per generated token)")
     ap.add_argument("--final-norm", action="store_true",
                     help="config 5: fuse the decoder's final RMSNorm (hidden = the last layer's output)")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -297,6 +297,33 @@ def test_sampler_nan_and_inf_temperature():
     assert np.array_equal(got, x.argmax(1))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T", [0.0, 0.7])
+def test_sampler_few_rows_match_batch(dtype, T):
+    """Small batches (the reference samples one row per generated token): the first rows
+    of a 5-row call and the same rows alone give the same tokens, and each is the exact
+    inverse CDF (greedy: the first maximum)."""
+    rng = np.random.default_rng(26)
+    V = 151936
+    x = (rng.standard_normal((5, V)) * 2.5).astype(np.float32)
+    x[2, [7, 90001]] = 40.0                           # a tie: the first maximum wins
+    xd = torch.from_numpy(x).to(DEV).to(dtype)
+    u = rng.random(5).astype(np.float32)
+    five = step.sample_tokens(xd, T, t(u) if T > 0 else None).cpu().numpy()
+    xh = xd.float().cpu().numpy()
+    for R in (1, 3, 4):
+        few = step.sample_tokens(xd[:R], T, t(u[:R]) if T > 0 else None).cpu().numpy()
+        assert np.array_equal(few, five[:R]), (R, few, five[:R])
+    for r in range(5):
+        if T == 0.0:
+            assert five[r] == int(np.argmax(xh[r]))
+            continue
+        c = _exact_cdf(xh[r], T)
+        thr = float(u[r]) * c[-1]
+        g = five[r]
+        assert c[g] >= thr - 1e-6 * c[-1] and (g == 0 or c[g - 1] <= thr + 1e-6 * c[-1]), (r, g)
+
+
 def test_sampler_bf16_and_strided_rows():
     rng = np.random.default_rng(23)
     R, V, LD = 16, 5000, 5120                         # rows inside a wider buffer
