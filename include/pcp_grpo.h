@@ -260,7 +260,8 @@ int pcp_grpo_loss_fwd_bwd(pcp_ctx* ctx, const pcp_grpo_args* a);
  * loss, the row kernel's counter and, when a->token_loss is NULL, the per-token
  * losses) live in one static device array of PCP_NOALLOC_SCRATCH_BYTES per GPU, which
  * that GPU holds until the process ends. A request needing more than the array,
- *   4*round256(4*n_seq) + 512 + (token_loss ? 0 : round256(4*n_seq*tok_seq_stride)),
+ *   4*round256(4*n_seq) + 512 + (token_loss ? 0 : round256(4*n_seq*tok_seq_stride))
+ *     + (PCP_FLAG_NO_ZERO_FILL and dlogits ? round256(4*n_seq*logit_seq_stride) : 0),
  * fails with PCP_ERR_OVERFLOW before any device work; passing token_loss removes the
  * per-token part. Every call on one GPU shares that GPU's array, which keeps the last
  * call's contents: calls that may overlap on one GPU (other streams or contexts) race

@@ -196,11 +196,14 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
     return rc;
   }
 
-  // Scratch: adv | seq_len | seq_scale | seq_val | loss | row counter | token_loss.
+  // Scratch: adv | seq_len | seq_scale | seq_val | loss | row counter, live-row count |
+  // token_loss | live-row list (without zero-fill).
   const size_t sv = round256(sizeof(float) * g.n_seq);
   const bool need_tl = (op == kLoss) && a->token_loss == nullptr;
   const size_t tl_bytes = need_tl ? round256(sizeof(float) * g.n_seq * g.tstride) : 0;
-  const size_t need = 4 * sv + 512 + tl_bytes;
+  const bool need_list = (op == kLoss) && a->dlogits != nullptr && (a->flags & PCP_FLAG_NO_ZERO_FILL);
+  const size_t list_bytes = need_list ? round256(sizeof(int) * static_cast<size_t>(g.nrows)) : 0;
+  const size_t need = 4 * sv + 512 + tl_bytes + list_bytes;
   if (noalloc && need > PCP_NOALLOC_SCRATCH_BYTES)
     return fail(ctx, PCP_ERR_OVERFLOW,
                 "the allocation-free call needs %zu bytes of work space, more than its %u-byte array: pass "
@@ -224,7 +227,9 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   // launch. The allocation-free path keeps it in the shared array, the other path in
   // the context's own allocation.
   int* s_next = noalloc ? reinterpret_cast<int*>(sp + 4 * sv + 256) : ctx->d_next_row;
+  int* s_count = reinterpret_cast<int*>(sp + 4 * sv + 256 + 64);
   float* s_tl = need_tl ? reinterpret_cast<float*>(sp + 4 * sv + 512) : a->token_loss;
+  int* s_list = need_list ? reinterpret_cast<int*>(sp + 4 * sv + 512 + tl_bytes) : nullptr;
 
   RowArgs ra;
   std::memset(&ra, 0, sizeof(ra));
@@ -233,6 +238,8 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   ra.mask = a->mask;
   ra.err = ctx->d_err;
   ra.next_row = s_next;
+  ra.row_list = s_list;
+  ra.row_count = s_list ? s_count : nullptr;
   ra.nrows = g.nrows;
   ra.vocab = g.vocab;
   ra.rows = g.rows;

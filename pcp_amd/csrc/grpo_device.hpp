@@ -293,6 +293,11 @@ struct RowArgs {
   float* token_loss;
   int* err;
   int* next_row;           // persistent row kernel: rows handed out past the first grid
+  // Without zero-fill: the live rows' indices and their count, filled by
+  // live_rows_kernel before the persistent row kernel, which then visits only those
+  // rows. nullptr: every row in order.
+  int* row_list;
+  int* row_count;
   int64_t nrows;           // logits rows of the launch
   int64_t vocab;
   int64_t rows;

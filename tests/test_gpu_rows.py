@@ -89,23 +89,29 @@ def test_peaked_bf16_rows(V, S, T):
     print(f"  cached vs exact: {np.mean(ulps[normal] != 0):.2%} of normal-range elements one ulp apart", flush=True)
 
 
-# (kind, logits dtype, V, dlogits dtype, force_streaming, shifted layout)
+# (kind, logits dtype, V, dlogits dtype, force_streaming, shifted layout, live fraction of the mask)
 ZF_CASES = [
-    ("resident", "bf16", 4096, "bf16", False, False),
-    ("resident-shifted", "bf16", 151936, "bf16", False, True),
-    ("resident-edge", "bf16", 5003, "bf16", False, True),
-    ("resident-f32", "f32", 3000, "f32", False, False),
-    ("resident-bf16-to-f32", "bf16", 4096, "f32", False, True),
-    ("stream-vec", "bf16", 4096, "bf16", True, True),
-    ("stream-scalar", "bf16", 5003, "f32", False, False),
+    ("resident", "bf16", 4096, "bf16", False, False, 0.7),
+    ("resident-sparse", "bf16", 4096, "bf16", False, False, 0.25),
+    ("resident-shifted", "bf16", 151936, "bf16", False, True, 0.7),
+    ("resident-shifted-sparse", "bf16", 151936, "bf16", False, True, 0.2),
+    ("resident-edge", "bf16", 5003, "bf16", False, True, 0.7),
+    ("resident-edge-sparse", "bf16", 5003, "bf16", False, False, 0.3),
+    ("resident-f32", "f32", 3000, "f32", False, False, 0.7),
+    ("resident-f32-sparse", "f32", 3000, "f32", False, True, 0.25),
+    ("resident-bf16-to-f32", "bf16", 4096, "f32", False, True, 0.7),
+    ("stream-vec", "bf16", 4096, "bf16", True, True, 0.7),
+    ("stream-scalar", "bf16", 5003, "f32", False, False, 0.7),
 ]
 
 
-@pytest.mark.parametrize("kind,dt,V,odt,stream,shifted", ZF_CASES, ids=[c[0] for c in ZF_CASES])
-def test_no_zero_fill_leaves_dead_rows(kind, dt, V, odt, stream, shifted):
+@pytest.mark.parametrize("kind,dt,V,odt,stream,shifted,live", ZF_CASES, ids=[c[0] for c in ZF_CASES])
+def test_no_zero_fill_leaves_dead_rows(kind, dt, V, odt, stream, shifted, live):
     """PCP_FLAG_NO_ZERO_FILL: dlogits rows of masked, ignored (-100) and pad tokens keep
     what the caller put there, bit for bit; live rows match the oracle. Resident
-    (aligned and off-16-byte rows), f32 and mixed-precision, and both streaming kernels."""
+    (aligned and off-16-byte rows), f32 and mixed-precision, and both streaming kernels.
+    The persistent kernels visit only the listed live rows when fewer than half the rows
+    are live (the sparse cases) and every row otherwise."""
     rng = np.random.default_rng(V + 7 * len(kind))
     S, T, G = 4, 9, 2
     rows, off = (T - 1, 1) if shifted else (T, 0)
@@ -117,7 +123,7 @@ def test_no_zero_fill_leaves_dead_rows(kind, dt, V, odt, stream, shifted):
         x, ref, odt_orc = x32, r32, orc.F32
     ids = rng.integers(0, V, size=(S, T)).astype(np.int64)
     ids[rng.random((S, T)) < 0.15] = -100
-    mask = (rng.random((S, T)) < 0.7).astype(np.float32)
+    mask = (rng.random((S, T)) < live).astype(np.float32)
     mask[1] = 0.0                                        # one empty sequence
     rewards = np.array([1.0, 0.0, 0.25, 0.75], np.float32)
     sel = np.ascontiguousarray(x[:, :rows]).reshape(S * rows, V)
