@@ -32,6 +32,8 @@ struct pcp_ctx {
   int prof_used = 0;
   bool prof_on = false;
   int* h_count = nullptr;         // pinned host word: live-token count of the LM-head path
+  void* lm_dbuf = nullptr;        // LM-head backward operand (softmax cache / dlogits chunk), grown on demand
+  size_t lm_dbuf_bytes = 0;
   pcp::HostStager* stager = nullptr;  // pinned staging ring of the host-bytes path
   hipStream_t xs[3] = {};         // host-bytes path: upload, compute and download streams
 };

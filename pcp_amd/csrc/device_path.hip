@@ -427,6 +427,7 @@ void pcp_destroy(pcp_ctx* ctx) {
     release_profile_events(ctx);
     if (ctx->h_count) (void)hipHostFree(ctx->h_count);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->lm_dbuf) (void)hipFree(ctx->lm_dbuf);
     destroy_stager(ctx);
     for (hipStream_t x : ctx->xs)
       if (x) (void)hipStreamDestroy(x);

@@ -421,7 +421,6 @@ __global__ void __launch_bounds__(256) live_rows_kernel(RowArgs a) {
   }
   const uint64_t bal = __ballot(live);
   if (bal == 0) return;
-  const int lane = threadIdx.x & 63;
   const int before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0));
   int base = 0;

@@ -6,8 +6,10 @@
 // computes a 256 x 256 logits tile on v_mfma_f32_32x32x16_bf16 and reduces it in
 // its epilogue, so full logits never exist in HBM:
 //   kFwd  -> per (token, vocab tile) partial (max, sum 2^(x*log2e - max)) and the
-//            target logit when the target falls in the tile;
-//   kBwd  -> dlogits for one vocab chunk in bf16, for the dhidden / dW GEMMs.
+//            target logit when the target falls in the tile; with ECACHE also every
+//            term 2^(x*log2e - max) as f16 (the softmax cache of the backward);
+//   kBwd  -> dlogits for one vocab chunk in bf16, for the dhidden / dW GEMMs (the
+//            backward without the cache recomputes the logits this way).
 //
 // Reference: the LM head and loss of tools/export_qwen_forward.py:146-163
 // (self.model.lm_head(hidden) then F.cross_entropy), and matmulVJP
@@ -106,7 +108,8 @@ __device__ __forceinline__ void lm_barrier() {
 // through two stages of BK hidden columns.
 // ATR (kLmGemm): the token-role operand is stored K-major and its fragments are read
 // with ds_read_b64_tr_b16 (see below).
-template <int MODE, bool ATR = false>
+// ECACHE (kLmFwd): the epilogue also stores the softmax terms (see there).
+template <int MODE, bool ATR = false, bool ECACHE = false>
 __global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
 lm_tile_kernel(LmTileArgs a) {
   using namespace lm;
@@ -363,9 +366,38 @@ lm_tile_kernel(LmTileArgs a) {
       const float ref = ms_ref(m2);
       float s = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i) {
+        float ev[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s += hw_exp2(fmaf(acc[i][j][r], kLog2e, -ref));
+        for (int r = 0; r < 16; ++r) {
+          ev[r] = hw_exp2(fmaf(acc[i][j][r], kLog2e, -ref));
+          s += ev[r];
+        }
+        if constexpr (ECACHE) {
+          // Softmax cache: ecache[n][v] = f16(2^(x*log2e - ref)), token-major rows of lde
+          // (vocab past V holds 0). The lane's 16 terms are vocab rows 8q + 4*half + 0..3
+          // (q < 4) of this 32-row block; one v_permlane32_swap per register pair trades
+          // groups with the partner lane l^32, after which the lane holds 8 consecutive
+          // rows (16p + 8*half + 0..7 for pair p) and writes them as one 16-byte store.
+          uint32_t g[8];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            g[2 * q] = pack2<F16T>(ev[4 * q], ev[4 * q + 1]);
+            g[2 * q + 1] = pack2<F16T>(ev[4 * q + 2], ev[4 * q + 3]);
+          }
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            // Lanes 32-63 of the first operand trade with lanes 0-31 of the second.
+            const auto lo = __builtin_amdgcn_permlane32_swap(g[4 * p], g[4 * p + 2], false, false);
+            const auto hi = __builtin_amdgcn_permlane32_swap(g[4 * p + 1], g[4 * p + 3], false, false);
+            const int64_t c = vw + 32 * i + 16 * p + 8 * half;
+            if (n < a.N && c < a.lde) {
+              const u32x4 w = {lo[0], hi[0], lo[1], hi[1]};
+              *reinterpret_cast<u32x4*>(a.ecache + static_cast<int64_t>(n) * a.lde + c) = w;
+            }
+          }
+        }
+      }
       s += __shfl_xor(s, 32);
       if (n < a.N && any_v) {
         if (half == 0) a.part[static_cast<int64_t>(n) * a.ldp + vw / kPart] = make_float2(m2, s);
@@ -495,6 +527,41 @@ __global__ void __launch_bounds__(256) lm_reduce_kernel(LmReduceArgs a) {
     ms_merge(m, s, om, os);
   }
   if (lane == 0) a.lse2[n] = m + log2f(s);
+}
+
+// dlogits from the forward's softmax cache, in place (f16 terms -> bf16 D, same
+// buffer, 16 bytes per thread): D[n][v] = -c_n * e * 2^(ref - lse2_n), with ref the
+// exponent reference of v's 128-entry partial (from the policy's partials), except
+// at the target, where D = c_n - c_n * 2^(tgt_n*log2e - lse2_n) from the f32 target
+// logit, as the recomputing backward forms it. Columns past V and rows with c_n = 0
+// are written as 0.
+__global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
+  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (c0 >= a.ld) return;
+  for (int64_t row = blockIdx.y; row < a.n; row += gridDim.y) {
+    u32x4* p = reinterpret_cast<u32x4*>(a.d + row * a.ld + c0);
+    const float cf = a.coef[row];
+    u32x4 out = {0u, 0u, 0u, 0u};
+    if (cf != 0.f && c0 < a.V) {
+      const float l2 = a.lse2[row];
+      const float ref = ms_ref(a.part[row * a.ldp + c0 / kLmPart].x);
+      const float f = -cf * hw_exp2(ref - l2);
+      const u32x4 w = *p;
+      const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
+      const int64_t rel = static_cast<int64_t>(a.ids[row]) - c0;
+      float d[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) d[k] = c0 + k < a.V ? f * F16T::unpack(ww, k) : 0.f;
+      if (rel >= 0 && rel < 8) {
+        const float pt = hw_exp2(fmaf(a.tgt[row], kLog2e, -l2));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf * pt + cf : d[k];
+      }
+      out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
+                  pack2<BF16T>(d[6], d[7])};
+    }
+    *p = out;
+  }
 }
 
 // GRPO terms per token from logp / ref logp (token_terms); also masks logp for
@@ -670,13 +737,13 @@ int lm_group_m(int mode, int ntt) {
   return ntt;
 }
 
-template <int MODE>
+template <int MODE, bool EC = false>
 hipError_t launch_tiles_mode(const LmTileArgs& a, int grid, hipStream_t st) {
   constexpr bool kAtr = MODE == kLmGemm;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE, kAtr>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE, kAtr, EC>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
   if (e != hipSuccess) return e;
-  lm_tile_kernel<MODE, kAtr><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
+  lm_tile_kernel<MODE, kAtr, EC><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
   return hipGetLastError();
 }
 
@@ -686,7 +753,8 @@ hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {
   const int total = a.ntt * a.nvt;
   if (total <= 0) return hipSuccess;
   const int grid = ((total + 7) / 8) * 8;
-  if (mode == kLmFwd) return launch_tiles_mode<kLmFwd>(a, grid, st);
+  if (mode == kLmFwd)
+    return a.ecache ? launch_tiles_mode<kLmFwd, true>(a, grid, st) : launch_tiles_mode<kLmFwd>(a, grid, st);
   return launch_tiles_mode<kLmBwd>(a, grid, st);
 }
 
@@ -713,6 +781,13 @@ hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st) {
 
 hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st) {
   lm_reduce_kernel<<<dim3(static_cast<unsigned>((a.N + 3) / 4)), dim3(256), 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_dcache(const LmDcacheArgs& a, hipStream_t st) {
+  if (a.n <= 0 || a.ld <= 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((a.ld / 8 + 255) / 256), static_cast<unsigned>(a.n < 65535 ? a.n : 65535));
+  lm_dcache_kernel<<<grid, dim3(256), 0, st>>>(a);
   return hipGetLastError();
 }
 

@@ -30,6 +30,8 @@ struct LmTileArgs {
   float2* part;         // [N, ldp]: per kLmPart vocab entries (max * log2e, sum 2^(x*log2e - max*log2e))
   int ldp;              // ceil(V / kLmPart)
   float* tgt;           // [N] target logit
+  uint16_t* ecache;     // or nullptr: [N, lde] f16 softmax terms 2^(x*log2e - ref) of the
+  int64_t lde;          //   partial's reference ref (lde % 64 == 0, >= V; 0 past V)
   // kLmBwd
   const float* lse2;    // [N] base-2 log-sum-exp
   const float* coef;    // [N] d loss / d logp
@@ -62,6 +64,20 @@ struct LmTransposeArgs {
   int R, C;
   uint16_t* dst;
   int64_t ld_dst;
+};
+
+// In place over the softmax cache: d[n][v] (f16 term) -> bf16 dlogits, v < ld.
+struct LmDcacheArgs {
+  uint16_t* d;            // [n, ld]
+  int64_t ld;             // multiple of 8, >= V
+  int64_t n;              // live tokens
+  int64_t V;
+  const float2* part;     // [n, ldp] the policy's forward partials
+  int ldp;
+  const float* lse2;      // [n]
+  const float* coef;      // [n]
+  const float* tgt;       // [n] target logit
+  const int* ids;         // [n] compact target ids
 };
 
 struct LmReduceArgs {
@@ -132,6 +148,7 @@ hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st);
 hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, hipStream_t st);
 hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st);
 hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st);
+hipError_t launch_lm_dcache(const LmDcacheArgs& a, hipStream_t st);
 hipError_t launch_lm_terms(const RowArgs& ra, const LmTermsArgs& a, hipStream_t st);
 
 }  // namespace pcp

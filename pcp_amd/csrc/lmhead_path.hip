@@ -36,6 +36,29 @@ constexpr int64_t kDefaultChunk = 16384;
 
 inline size_t r256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
+// Grow ctx->lm_dbuf to at least `bytes` (grow-only; synchronises before freeing the
+// old buffer, which earlier asynchronous calls may still use). A failed hipMalloc
+// leaves no buffer and no sticky error.
+hipError_t grow_dbuf(pcp_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->lm_dbuf_bytes) return hipSuccess;
+  if (ctx->lm_dbuf) {
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    (void)hipFree(ctx->lm_dbuf);
+    ctx->lm_dbuf = nullptr;
+    ctx->lm_dbuf_bytes = 0;
+  }
+  const size_t want = (bytes + 0xFFFFF) & ~static_cast<size_t>(0xFFFFF);
+  const hipError_t e = hipMalloc(&ctx->lm_dbuf, want);
+  if (e != hipSuccess) {
+    ctx->lm_dbuf = nullptr;
+    (void)hipGetLastError();
+    return e;
+  }
+  ctx->lm_dbuf_bytes = want;
+  return hipSuccess;
+}
+
 int validate_lm(const pcp_lmhead_args* a) {
   if (!a) return fail(nullptr, PCP_ERR_INVALID_ARG, "args is NULL");
   if (a->n_seq < 1 || a->rows < 1) return fail(nullptr, PCP_ERR_INVALID_ARG, "n_seq and rows must be >= 1");
@@ -114,7 +137,6 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_hid = take(2 * static_cast<size_t>(N) * H);
   const size_t o_part = take(8 * static_cast<size_t>(N) * npart);
   const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
-  const size_t o_chunk = bwd ? take(2 * static_cast<size_t>(N) * chunk) : 0;
   // Token-padded width of the transposed hidden rows (the dW product's K, a multiple
   // of the 64-deep pipeline stage).
   const int64_t ldt_max = (N + 63) / 64 * 64;
@@ -143,6 +165,29 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const int nl = *ctx->h_count;
   if (nl < 0 || nl > N) return fail(ctx, PCP_ERR_DEVICE, "live-token count %d out of range", nl);
   const int ntl = (nl + kLmTileT - 1) / kLmTileT;
+
+  // The backward's bf16 operand: by default the whole-vocabulary softmax cache
+  // [nl, ldv] (the policy forward stores its f16 terms there, a pass rewrites them as
+  // dlogits); with an explicit vocab_chunk, PCP_FLAG_EXACT_BF16, products past the
+  // 32-bit buffer offsets, or no memory for the cache, one dlogits chunk [nl, chunk]
+  // that the backward refills by recomputing the logits.
+  const int64_t ldv = (V + 63) / 64 * 64;
+  const int64_t ldt = (static_cast<int64_t>(nl) + 63) / 64 * 64;
+  bool cached = false;
+  if (bwd && nl > 0) {
+    const int64_t k32 = int64_t{1} << 32;
+    if (a->vocab_chunk == 0 && !(a->flags & PCP_FLAG_EXACT_BF16) && ldt * ldv * 2 < k32 && ldv * H * 2 < k32) {
+      e = grow_dbuf(ctx, 2 * static_cast<size_t>(nl) * ldv);
+      if (e == hipSuccess) cached = true;
+      else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the softmax cache");
+    }
+    if (!cached && (e = grow_dbuf(ctx, 2 * static_cast<size_t>(nl) * chunk)) != hipSuccess) {
+      if (e == hipErrorOutOfMemory)
+        return fail(ctx, PCP_ERR_OOM, "hipMalloc of the %lld x %lld dlogits chunk failed", (long long)nl,
+                    (long long)chunk);
+      return hip_fail(ctx, e, "allocating the dlogits chunk");
+    }
+  }
   if (norm) {
     if ((e = launch_lm_norm_rows(a->hidden_states, a->norm_weight, a->norm_eps, I(o_live), nl, static_cast<int>(H),
                                  sp + o_hid, F(o_rstd), st)) != hipSuccess)
@@ -180,9 +225,15 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   ta.part = part;
   ta.ldp = npart;
   LmReduceArgs rd{part, nl, npart, npart, nullptr};
-  for (int m = 0; m < (ref && nl > 0 ? 2 : nl > 0 ? 1 : 0); ++m) {
+  const int nmodel = nl > 0 ? (ref ? 2 : 1) : 0;
+  for (int k = 0; k < nmodel; ++k) {
+    // The reference model first, so the policy's partials stay in `part` for the
+    // softmax cache's pass.
+    const int m = nmodel - 1 - k;
     ta.B = m == 0 ? a->weight : a->ref_weight;
     ta.tgt = F(m == 0 ? o_tgt : o_rtgt);
+    ta.ecache = m == 0 && cached ? static_cast<uint16_t*>(ctx->lm_dbuf) : nullptr;
+    ta.lde = ldv;
     const bool timed = m == 0 && ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
     if (timed && (e = hipEventRecord(ctx->prof_start[ctx->prof_used], st)) != hipSuccess)
       return hip_fail(ctx, e, "hipEventRecord");
@@ -229,12 +280,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       return hip_fail(ctx, e, "zero dnorm_weight");
   }
   if (bwd && nl > 0) {
-    const int ldt = static_cast<int>((nl + 63) / 64 * 64);
-    ta.B = a->weight;
-    ta.lse2 = F(o_l2);
-    ta.coef = F(o_coef);
-    ta.dchunk = sp + o_chunk;
-    ta.ldd = static_cast<int>(chunk);
+    char* dbuf = static_cast<char*>(ctx->lm_dbuf);
     float* dhc = want_dy ? F(o_dhc) : nullptr;
     if (a->dweight) {
       // hidden^T [H, ldt]: the dW product's token operand, zero past the live tokens.
@@ -242,24 +288,20 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
                                reinterpret_cast<uint16_t*>(sp + o_ht), ldt};
       if ((e = launch_lm_transpose(tr, st)) != hipSuccess) return hip_fail(ctx, e, "transposing hidden rows");
     }
-    for (int64_t vc0 = 0; vc0 < V; vc0 += chunk) {
-      const int64_t w = (V - vc0 < chunk) ? V - vc0 : chunk;
-      ta.vc0 = static_cast<int>(vc0);
-      ta.vt0 = static_cast<int>(vc0 / kLmTileV);
-      ta.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
-      if ((e = launch_lm_tiles(kLmBwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head backward tiles");
-      // The chunk's two products in one launch (they are independent): the longer one
-      // (dhidden, K = the chunk width, over fewer tiles) first, so the shorter dW tiles
-      // fill the CUs its last round leaves idle.
+    // The products of one vocab range [vc0, vc0 + w) of D (token-major rows of ldd
+    // columns at dbuf), in one launch (they are independent): the longer one (dhidden,
+    // K = the range, over fewer tiles) first, so the shorter dW tiles fill the CUs its
+    // last round leaves idle.
+    auto products = [&](int64_t vc0, int64_t w, int64_t ldd) -> hipError_t {
       LmTileArgs::Gemm g[2];
       int ng = 0;
       std::memset(g, 0, sizeof(g));
       if (want_dy) {
         // dhidden_c[t][h] (+)= sum_v D[t][v] * W[vc0 + v][h]: rows = live tokens, columns
-        // = H; W rows past the chunk's w read as 0 (as D's columns there are 0).
+        // = H; W rows past the range read as 0 (as D's columns there are 0).
         LmTileArgs::Gemm& d = g[ng++];
-        d.B = sp + o_chunk;
-        d.ldb = static_cast<int>(chunk);
+        d.B = dbuf;
+        d.ldb = static_cast<int>(ldd);
         d.V = nl;
         d.A = static_cast<const uint16_t*>(a->weight) + vc0 * H;
         d.lda = static_cast<int>(H);
@@ -274,16 +316,16 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       }
       if (a->dweight) {
         // dW[vc0 + v][h] = sum_t hidden^T[h][t] * D[t][v]: result rows = H, columns = the
-        // chunk's vocab, stored transposed; D rows past the live tokens read as 0.
+        // range's vocab, stored transposed; D rows past the live tokens read as 0.
         LmTileArgs::Gemm& d = g[ng++];
         d.B = sp + o_ht;
-        d.ldb = ldt;
+        d.ldb = static_cast<int>(ldt);
         d.V = static_cast<int>(H);
-        d.A = sp + o_chunk;
-        d.lda = static_cast<int>(chunk);
+        d.A = dbuf;
+        d.lda = static_cast<int>(ldd);
         d.krows_a = nl;
         d.N = static_cast<int>(w);
-        d.K = ldt;
+        d.K = static_cast<int>(ldt);
         d.nvt = static_cast<int>((H + kLmTileV - 1) / kLmTileV);
         d.ntt = static_cast<int>((w + kLmTileT - 1) / kLmTileT);
         d.C = a->dweight + vc0 * H;
@@ -291,7 +333,30 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         d.transpose_c = 1;
         d.accumulate = 0;
       }
-      if ((e = launch_lm_gemms(g, ng, st)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
+      return launch_lm_gemms(g, ng, st);
+    };
+    if (cached) {
+      // D over the whole vocabulary from the cache, then both products once (K = the
+      // vocabulary for dhidden, the live tokens for dW).
+      const LmDcacheArgs dc{reinterpret_cast<uint16_t*>(dbuf), ldv, nl, V, part, npart,
+                            F(o_l2), F(o_coef), F(o_tgt), I(o_idsc)};
+      if ((e = launch_lm_dcache(dc, st)) != hipSuccess) return hip_fail(ctx, e, "dlogits from the softmax cache");
+      if ((e = products(0, V, ldv)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
+    } else {
+      ta.B = a->weight;
+      ta.lse2 = F(o_l2);
+      ta.coef = F(o_coef);
+      ta.dchunk = dbuf;
+      ta.ldd = static_cast<int>(chunk);
+      ta.ecache = nullptr;
+      for (int64_t vc0 = 0; vc0 < V; vc0 += chunk) {
+        const int64_t w = (V - vc0 < chunk) ? V - vc0 : chunk;
+        ta.vc0 = static_cast<int>(vc0);
+        ta.vt0 = static_cast<int>(vc0 / kLmTileV);
+        ta.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
+        if ((e = launch_lm_tiles(kLmBwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head backward tiles");
+        if ((e = products(vc0, w, chunk)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
+      }
     }
     if (norm && want_dy) {
       const LmNormBwdArgs nb{dhc, static_cast<const uint16_t*>(a->hidden_states), a->norm_weight, F(o_rstd),

@@ -221,13 +221,16 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
                    rewards: torch.Tensor | None = None, group_size: int = 1, old_logp: torch.Tensor | None = None,
                    loss_mode: int = LossMode.REINFORCE, clip_eps: float = 0.2, kl_beta: float = 0.04,
                    loss_norm: float = 0.0, std_eps: float = 1e-8, want_grads: bool = True, vocab_chunk: int = 0,
-                   norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6,
+                   norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6, exact_bf16: bool = False,
                    outputs: LmheadOutputs | None = None, sync: bool = True, stream=None,
                    ctx: Context | None = None) -> LmheadOutputs:
     """Fused LM-head + GRPO loss (pcp_grpo_lmhead_fwd_bwd). hidden [S*T, H] bf16,
     weight / ref_weight [V, H] bf16, ids / mask / old_logp [S, T]. With norm_weight
     (f32 [H]) the decoder's final RMSNorm is fused in: hidden is the last layer's
-    output before the norm, and dhidden / dnorm_weight are the gradients there."""
+    output before the norm, and dhidden / dnorm_weight are the gradients there.
+    vocab_chunk 0 lets the library keep the forward's softmax terms (f16) for the
+    backward; a chunk width, or exact_bf16 (PCP_FLAG_EXACT_BF16), recomputes the
+    logits per chunk instead."""
     ctx = ctx or default_context(hidden.device.index or 0)
     if ids.dim() != 2:
         raise PcpError(-1, "ids must be [S, T]")
@@ -269,7 +272,7 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
     a.norm_weight, a.dnorm_weight, a.norm_eps = _ptr(norm_weight), _ptr(outputs.dnorm_weight), norm_eps
     a.loss_mode = int(loss_mode)
     a.clip_eps, a.kl_beta, a.std_eps, a.loss_norm = clip_eps, kl_beta, std_eps, loss_norm
-    a.flags = 0 if sync else _lib.FLAG_ASYNC
+    a.flags = (0 if sync else _lib.FLAG_ASYNC) | (_lib.FLAG_EXACT_BF16 if exact_bf16 else 0)
     a.stream = _stream_handle(stream)
     check(lib().pcp_grpo_lmhead_fwd_bwd(ctx.handle, ctypes.byref(a)), ctx.handle)
     return outputs

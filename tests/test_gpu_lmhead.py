@@ -12,10 +12,17 @@ Tolerances:
   log-probs, token losses, loss: as the logits-input path (parity_tol). The tile
     kernel sums products of bf16 values, each exact in f32, so its f32 accumulation
     error is far below the 1e-5 * max(1, |lse|) bar.
-  dhidden, dW: the device rounds D to bf16 (2^-9 relative at most) before the two
+  dhidden, dW: the device rounds D to bf16 (2^-8 relative at most) before the two
     GEMMs and c carries the coef_floor error, so elementwise
     |dh - dh*| <= E . |W| and |dW - dW*| <= E^T . |hidden| with
     E = (2^-8 + 1e-4) |D| + 2 floor_n (onehot + p).
+    By default (vocab_chunk 0) the backward takes the softmax terms from the forward:
+    e = 2^(x log2e - m_b), with m_b the largest logit of the 128-entry block b holding
+    v, stored as f16 (2^-11 relative, or 2^-25 absolute below f16's normal range) and
+    scaled by 2^(m_b - lse). Off the target that adds
+    (1 + 2^-7) |c| (2^-11 p + 2^-25 exp(m_b - lse)) to E (the 2^-7 covers the bf16
+    rounding of the larger value); the target's D comes from the f32 target logit as
+    without the cache.
 """
 import numpy as np
 import pytest
@@ -67,15 +74,32 @@ def oracle_case(c, mode, clip_eps=0.2, kl_beta=0.04):
     return L, lse, rlse, old, r
 
 
-def run_device(c, mode, old, *, vocab_chunk=0, want_grads=True, ids=None, mask=None, clip_eps=0.2, kl_beta=0.04):
+def run_device(c, mode, old, *, vocab_chunk=0, want_grads=True, ids=None, mask=None, clip_eps=0.2, kl_beta=0.04,
+               exact_bf16=False):
     return grpo.lmhead_fwd_bwd(dev(c["hb"]), dev(c["wb"]), dev(c["ids"]) if ids is None else ids,
                                dev(c["mask"]) if mask is None else mask, ref_weight=dev(c["rb"]),
                                rewards=dev(c["rewards"]), group_size=c["G"], old_logp=dev(old), loss_mode=mode,
-                               clip_eps=clip_eps, kl_beta=kl_beta, vocab_chunk=vocab_chunk, want_grads=want_grads)
+                               clip_eps=clip_eps, kl_beta=kl_beta, vocab_chunk=vocab_chunk, want_grads=want_grads,
+                               exact_bf16=exact_bf16)
 
 
-def grad_bounds(c, L, lse, r, mode, old, kl_beta=0.04, clip_eps=0.2):
-    """(want_dh, tol_dh, want_dw, tol_dw) in float64."""
+def cache_error(L, lse, coef, ids):
+    """Per-element bound on what the f16 softmax cache adds to D (module docstring)."""
+    N, V = L.shape
+    nb = (V + 127) // 128
+    Lp = np.full((N, nb * 128), -np.inf)
+    Lp[:, :V] = L
+    blk = np.repeat(Lp.reshape(N, nb, 128).max(2), 128, axis=1)[:, :V]
+    X = (1 + 2.0 ** -7) * np.abs(coef)[:, None] * (2.0 ** -11 * np.exp(L - lse[:, None])
+                                                   + 2.0 ** -25 * np.exp(blk - lse[:, None]))
+    live = (coef != 0) & (ids >= 0) & (ids < V)
+    X[np.nonzero(live)[0], ids[live]] = 0.0
+    return X
+
+
+def grad_bounds(c, L, lse, r, mode, old, kl_beta=0.04, clip_eps=0.2, cached=True):
+    """(want_dh, tol_dh, want_dw, tol_dw) in float64. cached: the backward used the
+    forward's softmax cache (vocab_chunk 0 without PCP_FLAG_EXACT_BF16)."""
     S, T, V = c["S"], c["T"], c["V"]
     ids = c["ids"].reshape(-1)
     coef = r.coef.reshape(-1)
@@ -92,6 +116,8 @@ def grad_bounds(c, L, lse, r, mode, old, kl_beta=0.04, clip_eps=0.2):
     onehot[np.arange(len(ids)), np.clip(ids, 0, V - 1)] = 1.0
     E = (2.0 ** -8 + 1e-4) * np.abs(D) + 2.0 * fl[:, None] * (onehot + P)
     E[fl == 0] = (2.0 ** -8 + 1e-4) * np.abs(D[fl == 0])
+    if cached:
+        E += cache_error(L, lse, coef, ids)
     W = np.abs(orc.bf16_to_f32(c["wb"]).astype(np.float64))
     h = np.abs(orc.bf16_to_f32(c["hb"]).astype(np.float64))
     return dh, E @ W + 1e-30, dw, E.T @ h + 1e-30
@@ -168,7 +194,7 @@ def test_lmhead_small_vs_oracle(shape, mode):
     out = run_device(c, mode, old, vocab_chunk=chunk)
     torch.cuda.synchronize()
     check_forward(c, out, L, lse, rlse, r, mode)
-    check_grads(out, *grad_bounds(c, L, lse, r, mode, old))
+    check_grads(out, *grad_bounds(c, L, lse, r, mode, old, cached=chunk == 0))
 
 
 def test_lmhead_ignore_index_int32_bool_mask_and_no_grads():
@@ -290,14 +316,36 @@ def test_execute_lmhead_final_norm_shifted():
     assert np.array_equal(np.frombuffer(outs[6], np.float32), ref.dnorm_weight.cpu().numpy())
 
 
-def test_lmhead_deterministic():
+@pytest.mark.parametrize("chunk", [512, 0], ids=["chunked", "cached"])
+def test_lmhead_deterministic(chunk):
     c = make_case(2, 70, 128, 900, 2, seed=5, lengths=[70, 33])
     old = np.full((2, 70), -7.0, np.float32)
-    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=512)
-    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=512)
+    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk)
+    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk)
     torch.cuda.synchronize()
     for f in ("loss", "logp", "ref_logp", "token_loss", "dhidden", "dweight"):
         assert torch.equal(getattr(a, f), getattr(b, f)), f
+
+
+def test_lmhead_exact_flag_recomputes():
+    """PCP_FLAG_EXACT_BF16 with the default vocab_chunk takes the recomputing backward:
+    bit for bit the result of an explicit 16384-wide chunk, inside the bound without the
+    cache term. The default (cached) backward meets its own bound, and its forward
+    outputs are those of the exact call."""
+    c = make_case(3, 90, 192, 2500, 3, seed=31, lengths=[90, 61, 12])
+    mode = LossMode.GRPO_CLIP_KL
+    L, lse, rlse, old, r = oracle_case(c, mode)
+    ex = run_device(c, mode, old, exact_bf16=True)
+    ch = run_device(c, mode, old, vocab_chunk=16384)
+    ca = run_device(c, mode, old)
+    torch.cuda.synchronize()
+    for f in ("loss", "logp", "ref_logp", "token_loss", "dhidden", "dweight"):
+        assert torch.equal(getattr(ex, f), getattr(ch, f)), f
+    for f in ("loss", "logp", "ref_logp", "token_loss"):
+        assert torch.equal(getattr(ca, f), getattr(ex, f)), f
+    check_forward(c, ex, L, lse, rlse, r, mode)
+    check_grads(ex, *grad_bounds(c, L, lse, r, mode, old, cached=False))
+    check_grads(ca, *grad_bounds(c, L, lse, r, mode, old, cached=True))
 
 
 def test_lmhead_errors():
@@ -387,7 +435,7 @@ def test_lmhead_final_norm_vs_oracle(shape, mode):
     out = run_device_norm(c, mode, old, vocab_chunk=chunk)
     torch.cuda.synchronize()
     check_forward(c, out, L, lse, rlse, r, mode)
-    want_dy, tol_dy, want_dw, tol_dw = grad_bounds(c, L, lse, r, mode, old)
+    want_dy, tol_dy, want_dw, tol_dw = grad_bounds(c, L, lse, r, mode, old, cached=chunk == 0)
     dw = out.dweight.cpu().numpy().astype(np.float64)
     assert not np.any(np.abs(dw - want_dw) > tol_dw), np.abs(dw - want_dw).max()
     n_live = int((c["mask"] != 0).sum())
@@ -495,14 +543,21 @@ def _torch_reference(inp, coef=None, chunk=2048):
         if coef is not None:
             cc = coef[n0:n0 + chunk]
             P = torch.exp(Lc - l[:, None])
-            del Lc
             D = -P * cc[:, None]
             D.scatter_add_(1, idc[:, None], cc[:, None])
             E = (2.0 ** -8 + 1e-4) * D.abs()
             # c is exact up to f32 rounding here (REINFORCE), so the softmax term carries
             # only the log-prob error: |c| * 1e-5 * max(1, |lse|) * p.
             E += (cc.abs() * 1e-5 * l.abs().clamp(min=1.0))[:, None] * P
-            del P
+            # The default backward's f16 softmax cache (cache_error, in torch).
+            V = Lc.shape[1]
+            nb = (V + 127) // 128
+            blk = torch.nn.functional.pad(Lc, (0, nb * 128 - V), value=-float("inf")).view(-1, nb, 128).amax(2)
+            X = torch.exp(blk - l[:, None]).repeat_interleave(128, dim=1)[:, :V]
+            X = (1 + 2.0 ** -7) * cc.abs()[:, None] * (2.0 ** -11 * P + 2.0 ** -25 * X)
+            X.scatter_(1, idc[:, None], 0.0)
+            E += X
+            del P, X, blk, Lc
             dh[n0:n0 + chunk] = D @ Wf
             tol_dh[n0:n0 + chunk] = E @ Wa
             dw += D.T @ hc
