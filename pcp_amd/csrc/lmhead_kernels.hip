@@ -529,38 +529,84 @@ __global__ void __launch_bounds__(256) lm_reduce_kernel(LmReduceArgs a) {
   if (lane == 0) a.lse2[n] = m + log2f(s);
 }
 
-// dlogits from the forward's softmax cache, in place (f16 terms -> bf16 D, same
-// buffer, 16 bytes per thread): D[n][v] = -c_n * e * 2^(ref - lse2_n), with ref the
-// exponent reference of v's 128-entry partial (from the policy's partials), except
-// at the target, where D = c_n - c_n * 2^(tgt_n*log2e - lse2_n) from the f32 target
-// logit, as the recomputing backward forms it. Columns past V and rows with c_n = 0
-// are written as 0.
+// 64 x 64 bf16 tiles staged in LDS for a transpose: rows of 66 elements (33 words),
+// so the column reads below, 8 rows apart per lane group, fall on distinct banks.
+constexpr int kTilePitch = 66;
+
+// t[r][c .. c+7] = v (c % 8 == 0), as four 32-bit writes (rows are 4-byte aligned).
+__device__ __forceinline__ void tile_put8(uint16_t* t, int r, int c, u32x4 v) {
+  uint32_t* w = reinterpret_cast<uint32_t*>(t + r * kTilePitch + c);
+  w[0] = v[0];
+  w[1] = v[1];
+  w[2] = v[2];
+  w[3] = v[3];
+}
+
+// Column c of rows r .. r+7, packed as 8 bf16.
+__device__ __forceinline__ u32x4 tile_col8(const uint16_t* t, int r, int c) {
+  uint32_t w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    w[k] = static_cast<uint32_t>(t[(r + 2 * k) * kTilePitch + c]) |
+           (static_cast<uint32_t>(t[(r + 2 * k + 1) * kTilePitch + c]) << 16);
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// dlogits from the forward's softmax cache, per 64 x 64 tile (tokens x vocab): D is
+// written in place over the cache (f16 terms -> bf16, token-major, the dhidden
+// product's operand) and transposed through LDS into Dt [ldv, ldt] (vocab-major,
+// the dW product's operand; tokens past n are 0). D[n][v] = -c_n * e * 2^(ref -
+// lse2_n), with ref the exponent reference of v's 128-entry partial (from the
+// policy's partials), except at the target, where D = c_n - c_n * 2^(tgt_n*log2e -
+// lse2_n) from the f32 target logit, as the recomputing backward forms it. Columns
+// past V and rows with c_n = 0 are 0.
 __global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
-  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
-  if (c0 >= a.ld) return;
-  for (int64_t row = blockIdx.y; row < a.n; row += gridDim.y) {
-    u32x4* p = reinterpret_cast<u32x4*>(a.d + row * a.ld + c0);
-    const float cf = a.coef[row];
-    u32x4 out = {0u, 0u, 0u, 0u};
-    if (cf != 0.f && c0 < a.V) {
-      const float l2 = a.lse2[row];
-      const float ref = ms_ref(a.part[row * a.ldp + c0 / kLmPart].x);
-      const float f = -cf * hw_exp2(ref - l2);
-      const u32x4 w = *p;
-      const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
-      const int64_t rel = static_cast<int64_t>(a.ids[row]) - c0;
-      float d[8];
+  __shared__ uint16_t t[64 * kTilePitch];    // [token][vocab] bf16
+  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int tid = threadIdx.x;
+  const int64_t ntile = a.ldt / 64;
+  for (int64_t tb = blockIdx.y; tb < ntile; tb += gridDim.y) {
+    const int64_t r0 = tb * 64;
+    const int cc = (tid & 7) * 8;
+    const int64_t c0 = v0 + cc;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) d[k] = c0 + k < a.V ? f * F16T::unpack(ww, k) : 0.f;
-      if (rel >= 0 && rel < 8) {
-        const float pt = hw_exp2(fmaf(a.tgt[row], kLog2e, -l2));
+    for (int it = 0; it < 2; ++it) {
+      const int rr = (tid >> 3) + 32 * it;
+      const int64_t row = r0 + rr;
+      u32x4 out = {0u, 0u, 0u, 0u};
+      if (row < a.n) {
+        u32x4* p = reinterpret_cast<u32x4*>(a.d + row * a.ld + c0);
+        const float cf = a.coef[row];
+        if (cf != 0.f && c0 < a.V) {
+          const float l2 = a.lse2[row];
+          const float ref = ms_ref(a.part[row * a.ldp + c0 / kLmPart].x);
+          const float f = -cf * hw_exp2(ref - l2);
+          const u32x4 w = *p;
+          const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
+          const int64_t rel = static_cast<int64_t>(a.ids[row]) - c0;
+          float d[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf * pt + cf : d[k];
+          for (int k = 0; k < 8; ++k) d[k] = c0 + k < a.V ? f * F16T::unpack(ww, k) : 0.f;
+          if (rel >= 0 && rel < 8) {
+            const float pt = hw_exp2(fmaf(a.tgt[row], kLog2e, -l2));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf * pt + cf : d[k];
+          }
+          out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
+                      pack2<BF16T>(d[6], d[7])};
+        }
+        *p = out;
       }
-      out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
-                  pack2<BF16T>(d[6], d[7])};
+      tile_put8(t, rr, cc, out);
     }
-    *p = out;
+    __syncthreads();
+    // Dt row v0 + c, tokens r0 + 8g .. +7: eight lanes write one row's 128 bytes.
+#pragma unroll
+    for (int it = 0; it < 2 && a.dt; ++it) {
+      const int c = (tid >> 3) + 32 * it, g = tid & 7;
+      *reinterpret_cast<u32x4*>(a.dt + (v0 + c) * a.ldt + r0 + 8 * g) = tile_col8(t, 8 * g, c);
+    }
+    __syncthreads();
   }
 }
 
@@ -671,12 +717,11 @@ __global__ void __launch_bounds__(256) lm_scatter_rows_kernel(const u32x4* src, 
   }
 }
 
-// bf16 transpose through LDS, 64 x 64 tiles: 16-byte loads along source rows, 16-byte
-// stores along destination rows (the 8 stores of one destination row's 128 bytes come
-// from the 8 row groups of the same workgroup). Source rows past R read as 0, so the
-// destination is zero-padded up to ld_dst.
+// bf16 transpose through LDS, 64 x 64 tiles: 16-byte loads along source rows and
+// 16-byte stores along destination rows, eight lanes per 128-byte row segment on both
+// sides. Source rows past R read as 0, so the destination is zero-padded up to ld_dst.
 __global__ void __launch_bounds__(256) lm_transpose_kernel(LmTransposeArgs a) {
-  __shared__ uint16_t t[64][72];
+  __shared__ uint16_t t[64 * kTilePitch];
   const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
   const int tid = threadIdx.x;
 #pragma unroll
@@ -685,21 +730,16 @@ __global__ void __launch_bounds__(256) lm_transpose_kernel(LmTransposeArgs a) {
     u32x4 v = {0u, 0u, 0u, 0u};
     if (r0 + rr < a.R && c0 + cc < a.C)
       v = *reinterpret_cast<const u32x4*>(a.src + static_cast<int64_t>(r0 + rr) * a.ld_src + c0 + cc);
-    *reinterpret_cast<u32x4*>(&t[rr][cc]) = v;
+    tile_put8(t, rr, cc, v);
   }
   __syncthreads();
-  const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
-    const int g = wave * 2 + it;          // row group: source rows 8g .. 8g+7
-    const int c = lane;                   // source column = destination row
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      w[k] = static_cast<uint32_t>(t[8 * g + 2 * k][c]) | (static_cast<uint32_t>(t[8 * g + 2 * k + 1][c]) << 16);
+    const int c = (tid >> 3) + 32 * it;   // source column = destination row
+    const int g = tid & 7;                // source rows 8g .. 8g+7
     const int64_t r = r0 + 8 * g;
     if (c0 + c < a.C && r < a.ld_dst)
-      *reinterpret_cast<u32x4*>(a.dst + static_cast<int64_t>(c0 + c) * a.ld_dst + r) = u32x4{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4*>(a.dst + static_cast<int64_t>(c0 + c) * a.ld_dst + r) = tile_col8(t, 8 * g, c);
   }
 }
 
@@ -737,9 +777,8 @@ int lm_group_m(int mode, int ntt) {
   return ntt;
 }
 
-template <int MODE, bool EC = false>
+template <int MODE, bool EC = false, bool kAtr = MODE == kLmGemm>
 hipError_t launch_tiles_mode(const LmTileArgs& a, int grid, hipStream_t st) {
-  constexpr bool kAtr = MODE == kLmGemm;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE, kAtr, EC>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
   if (e != hipSuccess) return e;
@@ -758,7 +797,7 @@ hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {
   return launch_tiles_mode<kLmBwd>(a, grid, st);
 }
 
-hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, hipStream_t st) {
+hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, bool k_major_a, hipStream_t st) {
   LmTileArgs a;
   std::memset(&a, 0, sizeof(a));
   int grid = 0;
@@ -769,6 +808,7 @@ hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, hipStream_t st
     grid += a.gemm[p].tiles;
   }
   if (grid <= 0) return hipSuccess;
+  if (!k_major_a) return launch_tiles_mode<kLmGemm, false, false>(a, grid, st);
   return launch_tiles_mode<kLmGemm>(a, grid, st);
 }
 
@@ -786,7 +826,8 @@ hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st) {
 
 hipError_t launch_lm_dcache(const LmDcacheArgs& a, hipStream_t st) {
   if (a.n <= 0 || a.ld <= 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((a.ld / 8 + 255) / 256), static_cast<unsigned>(a.n < 65535 ? a.n : 65535));
+  const int64_t ntile = a.ldt / 64;
+  const dim3 grid(static_cast<unsigned>(a.ld / 64), static_cast<unsigned>(ntile < 65535 ? ntile : 65535));
   lm_dcache_kernel<<<grid, dim3(256), 0, st>>>(a);
   return hipGetLastError();
 }

@@ -39,14 +39,15 @@ struct LmTileArgs {
   int vc0, ldd;
   // kLmGemm: up to two independent products in one launch (gemm[0] takes the first
   // gemm[0].tiles workgroups, gemm[1] the rest); the fields above are unused.
-  // result[v][t] = sum_k B[v][k] * A(k, t): B rows are K-contiguous, A is stored
-  // K-major (element (k, t) at A[k * lda + t]) and read with LDS transpose loads.
+  // result[v][t] = sum_k B[v][k] * A(k, t): B rows are K-contiguous; A is either
+  // K-contiguous too (element (k, t) at A[t * lda + k]) or stored K-major (at
+  // A[k * lda + t]) and read with LDS transpose loads (launch_lm_gemms' k_major_a).
   struct Gemm {
-    const void* A;      // [krows_a, lda] bf16, K-major: "token" columns (result columns)
+    const void* A;      // [krows_a, lda] K-major or [N, lda] bf16: "token" columns (result columns)
     const void* B;      // [V, ldb] bf16, K-contiguous: "vocab" rows (result rows)
     int N, V, K;        // K % 64 == 0, K <= ldb
     int lda, ldb;       // row strides in elements (lda >= N rounded up to 8)
-    int krows_a;        // rows of A that exist; rows [krows_a, K) read as 0
+    int krows_a;        // K-major A: rows that exist; rows [krows_a, K) read as 0
     float* C;           // f32 result: row v, column t at C[v * ldc + t], or at
     int ldc;            //   C[t * ldc + v] with transpose_c (then V % 4 == 0)
     int transpose_c;
@@ -66,11 +67,14 @@ struct LmTransposeArgs {
   int64_t ld_dst;
 };
 
-// In place over the softmax cache: d[n][v] (f16 term) -> bf16 dlogits, v < ld.
+// Over the softmax cache: d[n][v] (f16 term) -> bf16 dlogits in place, and the same
+// values transposed into dt[v][n] (zero for n <= token < ldt).
 struct LmDcacheArgs {
   uint16_t* d;            // [n, ld]
-  int64_t ld;             // multiple of 8, >= V
+  int64_t ld;             // multiple of 64, >= V
   int64_t n;              // live tokens
+  uint16_t* dt;           // [ld, ldt]
+  int64_t ldt;            // multiple of 64, >= n
   int64_t V;
   const float2* part;     // [n, ldp] the policy's forward partials
   int ldp;
@@ -145,7 +149,9 @@ hipError_t launch_lm_zero(float* dst, int64_t n, hipStream_t st);
 hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st);
 // One launch of one or two products (n_gemm = 1 or 2; fields per LmTileArgs::Gemm,
 // group_m and tiles are filled in here). The longer product should come first.
-hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, hipStream_t st);
+// k_major_a: A is stored K-major (read with LDS transpose loads); otherwise A is
+// K-contiguous like B ([N, lda], krows_a unused).
+hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, bool k_major_a, hipStream_t st);
 hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st);
 hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st);
 hipError_t launch_lm_dcache(const LmDcacheArgs& a, hipStream_t st);

@@ -33,6 +33,9 @@ namespace pcp {
 namespace {
 
 constexpr int64_t kDefaultChunk = 16384;
+// Largest backward workspace (softmax cache, D^T, W^T) the default path allocates:
+// 7.1 GB at configuration 5 (9,603 live tokens, V = 151,936, H = 4,096).
+constexpr size_t kCacheBudget = size_t{16} << 30;
 
 inline size_t r256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
@@ -166,18 +169,21 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   if (nl < 0 || nl > N) return fail(ctx, PCP_ERR_DEVICE, "live-token count %d out of range", nl);
   const int ntl = (nl + kLmTileT - 1) / kLmTileT;
 
-  // The backward's bf16 operand: by default the whole-vocabulary softmax cache
-  // [nl, ldv] (the policy forward stores its f16 terms there, a pass rewrites them as
-  // dlogits); with an explicit vocab_chunk, PCP_FLAG_EXACT_BF16, products past the
-  // 32-bit buffer offsets, or no memory for the cache, one dlogits chunk [nl, chunk]
-  // that the backward refills by recomputing the logits.
+  // The backward's bf16 operands. By default: the whole-vocabulary softmax cache
+  // [nl, ldv] (the policy forward stores its f16 terms there; a pass rewrites them as
+  // dlogits D and writes D^T [ldv, ldt] beside it) and W^T [H, ldv], so both products
+  // read K-contiguous operands. With an explicit vocab_chunk, PCP_FLAG_EXACT_BF16, more
+  // than kCacheBudget bytes, or no memory for them: one dlogits chunk [nl, chunk] that
+  // the backward refills by recomputing the logits.
   const int64_t ldv = (V + 63) / 64 * 64;
   const int64_t ldt = (static_cast<int64_t>(nl) + 63) / 64 * 64;
+  const size_t o_dt = 2 * static_cast<size_t>(nl) * ldv;
+  const size_t o_wt = o_dt + (a->dweight ? 2 * static_cast<size_t>(ldv) * ldt : 0);
+  const size_t cache_bytes = o_wt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
   bool cached = false;
   if (bwd && nl > 0) {
-    const int64_t k32 = int64_t{1} << 32;
-    if (a->vocab_chunk == 0 && !(a->flags & PCP_FLAG_EXACT_BF16) && ldt * ldv * 2 < k32 && ldv * H * 2 < k32) {
-      e = grow_dbuf(ctx, 2 * static_cast<size_t>(nl) * ldv);
+    if (a->vocab_chunk == 0 && !(a->flags & PCP_FLAG_EXACT_BF16) && cache_bytes <= kCacheBudget) {
+      e = grow_dbuf(ctx, cache_bytes);
       if (e == hipSuccess) cached = true;
       else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the softmax cache");
     }
@@ -288,10 +294,11 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
                                reinterpret_cast<uint16_t*>(sp + o_ht), ldt};
       if ((e = launch_lm_transpose(tr, st)) != hipSuccess) return hip_fail(ctx, e, "transposing hidden rows");
     }
-    // The products of one vocab range [vc0, vc0 + w) of D (token-major rows of ldd
-    // columns at dbuf), in one launch (they are independent): the longer one (dhidden,
-    // K = the range, over fewer tiles) first, so the shorter dW tiles fill the CUs its
-    // last round leaves idle.
+    // Chunked backward: the products of one vocab range [vc0, vc0 + w) of D
+    // (token-major rows of ldd columns at dbuf), in one launch (they are independent):
+    // the longer one (dhidden, K = the range, over fewer tiles) first, so the shorter
+    // dW tiles fill the CUs its last round leaves idle. D is read K-major for dW and W
+    // K-major for dhidden, with LDS transpose loads, so no chunk is transposed.
     auto products = [&](int64_t vc0, int64_t w, int64_t ldd) -> hipError_t {
       LmTileArgs::Gemm g[2];
       int ng = 0;
@@ -333,15 +340,55 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         d.transpose_c = 1;
         d.accumulate = 0;
       }
-      return launch_lm_gemms(g, ng, st);
+      return launch_lm_gemms(g, ng, true, st);
     };
     if (cached) {
-      // D over the whole vocabulary from the cache, then both products once (K = the
-      // vocabulary for dhidden, the live tokens for dW).
-      const LmDcacheArgs dc{reinterpret_cast<uint16_t*>(dbuf), ldv, nl, V, part, npart,
+      // D and D^T over the whole vocabulary from the cache, W^T, then both products in
+      // one launch on K-contiguous operands (K = the vocabulary for dhidden, the live
+      // tokens for dW; dhidden's 608 long tiles at configuration 5 go first).
+      uint16_t* dt = a->dweight ? reinterpret_cast<uint16_t*>(dbuf + o_dt) : nullptr;
+      uint16_t* wt = want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_wt) : nullptr;
+      const LmDcacheArgs dc{reinterpret_cast<uint16_t*>(dbuf), ldv, nl, dt, ldt, V, part, npart,
                             F(o_l2), F(o_coef), F(o_tgt), I(o_idsc)};
       if ((e = launch_lm_dcache(dc, st)) != hipSuccess) return hip_fail(ctx, e, "dlogits from the softmax cache");
-      if ((e = products(0, V, ldv)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
+      LmTileArgs::Gemm g[2];
+      int ng = 0;
+      std::memset(g, 0, sizeof(g));
+      if (want_dy) {
+        // W^T [H, ldv], zero past V.
+        const LmTransposeArgs tw{static_cast<const uint16_t*>(a->weight), H, static_cast<int>(V), static_cast<int>(H),
+                                 wt, ldv};
+        if ((e = launch_lm_transpose(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
+        // dhidden_c[t][h] = sum_v D[t][v] * W^T[h][v].
+        LmTileArgs::Gemm& d = g[ng++];
+        d.B = dbuf;
+        d.ldb = static_cast<int>(ldv);
+        d.V = nl;
+        d.A = wt;
+        d.lda = static_cast<int>(ldv);
+        d.N = static_cast<int>(H);
+        d.K = static_cast<int>(ldv);
+        d.nvt = (nl + kLmTileV - 1) / kLmTileV;
+        d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
+        d.C = dhc;
+        d.ldc = static_cast<int>(H);
+      }
+      if (a->dweight) {
+        // dW[v][h] = sum_t D^T[v][t] * hidden^T[h][t].
+        LmTileArgs::Gemm& d = g[ng++];
+        d.B = dt;
+        d.ldb = static_cast<int>(ldt);
+        d.V = static_cast<int>(V);
+        d.A = sp + o_ht;
+        d.lda = static_cast<int>(ldt);
+        d.N = static_cast<int>(H);
+        d.K = static_cast<int>(ldt);
+        d.nvt = static_cast<int>((V + kLmTileV - 1) / kLmTileV);
+        d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
+        d.C = a->dweight;
+        d.ldc = static_cast<int>(H);
+      }
+      if ((e = launch_lm_gemms(g, ng, false, st)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
     } else {
       ta.B = a->weight;
       ta.lse2 = F(o_l2);
