@@ -262,11 +262,13 @@ def bench_lmhead(args) -> None:
     live = int(inp["mask"].sum().item())
     ms_step = elapsed * 1e3 / args.steps
     # Dense products per step over the live (compacted) tokens: forward logits per
-    # model, recomputed logits, dhidden, dW. Masked tokens carry no loss weight and
-    # no gradient, so the algorithm needs 2*H*V flops per live token per product.
-    products = (2 if clip else 1) + 3
+    # model, dhidden, dW (the backward reads the forward's softmax cache, so no logits
+    # are recomputed). Masked tokens carry no loss weight and no gradient, so the
+    # algorithm needs 2*H*V flops per live token per product. The timed launch is the
+    # dominant kernel: dhidden and dW in one launch of the MFMA tile kernel.
+    products = (2 if clip else 1) + 2
     step_flops = products * 2.0 * live * H * V
-    tile_flops = 2.0 * live * H * V
+    tile_flops = 2 * 2.0 * live * H * V
     achieved = tile_flops / (kernel_ms / 1e3) / 1e12
     line = {
         "metric": "GRPO fused LM-head + loss fwd+bwd tokens/s, H=4096, V=151936 bf16",
@@ -289,7 +291,7 @@ def bench_lmhead(args) -> None:
         "dense_equivalent_tflops": products * 2.0 * N * H * V / (ms_step / 1e3) / 1e12,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
-                     "kernel": "lm_tile_kernel<kLmFwd> (policy logits tiles)", "kernel_ms": kernel_ms,
+                     "kernel": "lm_tile_kernel<kLmGemm> (dhidden + dW products, one launch)", "kernel_ms": kernel_ms,
                      "algorithmic_flops": tile_flops},
         "setup_s": t_setup,
     }

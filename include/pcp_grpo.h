@@ -100,7 +100,8 @@ typedef enum pcp_loss_mode {
  * even. By default the resident kernel keeps the softmax terms of the sum pass as f16
  * (unit roundoff 2^-11) and scales them into dlogits, which saves one exponential per
  * element (3-5% of the step at configs 2-4) and adds up to 2^-11 of |dlogit| before
- * the bf16 rounding. */
+ * the bf16 rounding. On pcp_grpo_lmhead_fwd_bwd it selects the recomputing backward,
+ * whose bf16 dlogits operand is likewise the f32 value rounded once. */
 #define PCP_FLAG_EXACT_BF16 0x8u
 
 /* The token id that contributes nothing (F.cross_entropy ignore_index; the
@@ -273,10 +274,16 @@ int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
  * a6: fused LM-head + GRPO loss (the LM head of tools/export_qwen_forward.py:146-147
  * and its VJP, src/autodiff/vjp_rules.zig:426-497). Tokens use the aligned layout:
  * token t of sequence s is row s*rows + t of hidden_states and scores ids[s*rows+t].
- * logits = hidden_states * weight^T are computed in 128 x 128 tiles on bf16 MFMA and
- * reduced in-tile (per-token log-sum-exp and target logit); full logits are never
- * stored. The backward recomputes logit tiles per vocab chunk into bf16 dlogits and
- * runs dhidden = dlogits * weight and dweight = dlogits^T * hidden_states (fp32).
+ * logits = hidden_states * weight^T are computed in 256 x 256 tiles on bf16 MFMA and
+ * reduced in-tile (per-token log-sum-exp and target logit); full f32 logits are never
+ * stored. By default (vocab_chunk 0) the policy forward also keeps its softmax terms
+ * as f16 (one 2-byte term per live token and vocab entry), the backward turns them into
+ * bf16 dlogits and runs dhidden = dlogits * weight and dweight = dlogits^T *
+ * hidden_states (fp32) over the whole vocabulary. The f16 term adds at most 2^-11 of
+ * |c * softmax| to an off-target dlogit before its bf16 rounding. With an explicit
+ * vocab_chunk, PCP_FLAG_EXACT_BF16, or a backward workspace above 16 GiB, the backward
+ * recomputes the logit tiles per vocab chunk instead (dlogits = the f32 value rounded
+ * once), in memory bounded by the chunk.
  */
 typedef struct pcp_lmhead_args {
   int64_t n_seq;              /* sequences                                                */
@@ -284,7 +291,8 @@ typedef struct pcp_lmhead_args {
   int64_t hidden;             /* H; multiple of 64                                        */
   int64_t vocab;              /* V                                                        */
   int64_t group_size;         /* sequences per advantage group                            */
-  int64_t vocab_chunk;        /* backward chunk width; 0 => 16384 (a multiple of 256)      */
+  int64_t vocab_chunk;        /* 0: softmax cache (see above); else the recomputing
+                                 backward's chunk width (a multiple of 256)               */
   int32_t ids_dtype;          /* PCP_I64 | PCP_I32                                        */
   int32_t mask_dtype;         /* PCP_F32 | PCP_BOOL                                       */
   const void* hidden_states;  /* [n_seq*rows, H] bf16                                     */
@@ -307,7 +315,7 @@ typedef struct pcp_lmhead_args {
   float kl_beta;
   float std_eps;
   float loss_norm;            /* 0 => n_seq                                               */
-  uint32_t flags;             /* PCP_FLAG_ASYNC                                           */
+  uint32_t flags;             /* PCP_FLAG_ASYNC | PCP_FLAG_EXACT_BF16                     */
   void* stream;
   /* The decoder's final RMSNorm (Qwen2RMSNorm: the model.norm that
    * tools/export_qwen_forward.py:112 applies before lm_head), fused at both ends. With

@@ -2,20 +2,22 @@
 //
 // Live tokens (mask != 0, id in [0, V)) are compacted first: a masked or ignored
 // token has zero loss weight and zero gradient, so only live hidden rows enter the
-// products. The live count sizes the GEMMs, so the call reads it back once (one
-// stream synchronisation, also under PCP_FLAG_ASYNC).
-// Forward, per model (policy, then reference): MFMA logits tiles reduced in-tile to
+// products. The live count sizes the products and the backward's buffer, so the call
+// reads it back once (one stream synchronisation, also under PCP_FLAG_ASYNC).
+// Forward, per model (reference, then policy): MFMA logits tiles reduced in-tile to
 // per-(token, vocab tile) log-sum-exp partials and the target logit; one wave per
 // token merges the partials. Then the GRPO terms per token and the loss reduction
-// (the same kernels as the logits-input path). Backward, per vocab chunk: logits
-// tiles recomputed into bf16 dlogits D (token-major), then two products on the same
-// MFMA tile kernel (kLmGemm: one operand K-contiguous, the other read K-major with LDS
-// transpose loads), in one launch:
-//   dhidden (+)= D_chunk * W_chunk               (W_chunk read K-major as stored),
-//   dW_chunk^T  = hidden^T * D_chunk, stored transposed into dW's rows
-//                                                (D_chunk read K-major as stored; the
-//                                                 compact hidden rows transposed once),
-// and the compact dhidden rows are scattered back (zero rows for dead tokens).
+// (the same kernels as the logits-input path).
+// Backward, by default: the policy forward also stored its softmax terms (f16); one
+// pass turns them into bf16 dlogits D in place and writes D^T, W is transposed once,
+// and one launch of the MFMA tile kernel (kLmGemm, both operands K-contiguous) runs
+//   dhidden = D * W      over the whole vocabulary (rows: live tokens), and
+//   dW      = D^T * hidden over the live tokens (rows: vocab).
+// Chunked backward (an explicit vocab_chunk, PCP_FLAG_EXACT_BF16, or a workspace
+// past kCacheBudget): per vocab chunk, logits tiles recomputed into bf16 D, then the
+// same two products with one operand read K-major through LDS transpose loads,
+// dhidden accumulating over the chunks.
+// Either way the compact dhidden rows are scattered back (zero rows for dead tokens).
 // This mirrors the LM head's VJP (src/autodiff/vjp_rules.zig:426-497, matmulVJP).
 
 #include <hip/hip_runtime.h>
@@ -240,7 +242,9 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     ta.tgt = F(m == 0 ? o_tgt : o_rtgt);
     ta.ecache = m == 0 && cached ? static_cast<uint16_t*>(ctx->lm_dbuf) : nullptr;
     ta.lde = ldv;
-    const bool timed = m == 0 && ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
+    // pcp_profile_start timing: the policy forward tiles when the backward is chunked,
+    // the products launch (below) when it reads the softmax cache.
+    const bool timed = m == 0 && !cached && ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
     if (timed && (e = hipEventRecord(ctx->prof_start[ctx->prof_used], st)) != hipSuccess)
       return hip_fail(ctx, e, "hipEventRecord");
     if ((e = launch_lm_tiles(kLmFwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head forward tiles");
@@ -388,7 +392,12 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         d.C = a->dweight;
         d.ldc = static_cast<int>(H);
       }
+      const bool timed = ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
+      if (timed && (e = hipEventRecord(ctx->prof_start[ctx->prof_used], st)) != hipSuccess)
+        return hip_fail(ctx, e, "hipEventRecord");
       if ((e = launch_lm_gemms(g, ng, false, st)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
+      if (timed && (e = hipEventRecord(ctx->prof_stop[ctx->prof_used++], st)) != hipSuccess)
+        return hip_fail(ctx, e, "hipEventRecord");
     } else {
       ta.B = a->weight;
       ta.lse2 = F(o_l2);
