@@ -31,7 +31,6 @@ struct pcp_ctx {
   std::vector<hipEvent_t> prof_start, prof_stop;
   int prof_used = 0;
   bool prof_on = false;
-  int* h_count = nullptr;         // pinned host word: live-token count of the LM-head path
   void* lm_dbuf = nullptr;        // LM-head backward operand (softmax cache / dlogits chunk), grown on demand
   size_t lm_dbuf_bytes = 0;
   pcp::HostStager* stager = nullptr;  // pinned staging ring of the host-bytes path

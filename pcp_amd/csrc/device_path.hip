@@ -425,7 +425,6 @@ void pcp_destroy(pcp_ctx* ctx) {
   if (hipSetDevice(ctx->device) == hipSuccess) {
     (void)hipDeviceSynchronize();
     release_profile_events(ctx);
-    if (ctx->h_count) (void)hipHostFree(ctx->h_count);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->lm_dbuf) (void)hipFree(ctx->lm_dbuf);
     destroy_stager(ctx);

@@ -64,16 +64,11 @@ static_assert(wait_vm(0) == 0x0F70 && wait_vm(8) == 0x0F78 && wait_vm(16) == 0x4
 // over 16 distinct 16-byte bank groups.
 __device__ __forceinline__ int lm_swz(int row) { return (row >> 1) & 7; }
 
-// Tile order: work item p -> (token tile, vocab tile). Consecutive workgroup ids
-// are dealt round-robin to the 8 XCDs, so ids are first regrouped per XCD; within
-// an XCD, groups of group_m token tiles sweep the vocab tiles together, so the
-// workgroups resident on one XCD read the same operand K-slabs from its L2, and W
-// comes from HBM once per group.
-__device__ __forceinline__ bool lm_tile_coords(int pid, int ntt, int nvt, int group_m, int& tm, int& tn) {
-  const int total = ntt * nvt;
-  const int per_xcd = (total + 7) / 8;
-  const int p = (pid % 8) * per_xcd + pid / 8;
-  if (p >= total) return false;
+// Tile order: work item p -> (token tile, vocab tile). Each XCD works through its own
+// contiguous range of work items (see lm_tile_kernel); within it, groups
+// of group_m token tiles sweep the vocab tiles together, so the workgroups resident on
+// one XCD read the same operand K-slabs from its L2, and W comes from HBM once per group.
+__device__ __forceinline__ void lm_tile_of(int p, int ntt, int nvt, int group_m, int& tm, int& tn) {
   const int group = group_m * nvt;
   const int g = p / group;
   const int first_m = g * group_m;
@@ -81,7 +76,34 @@ __device__ __forceinline__ bool lm_tile_coords(int pid, int ntt, int nvt, int gr
   const int q = p - g * group;
   tm = first_m + q % gm;
   tn = q / gm;
-  return true;
+}
+
+// Token tiles per group in the tile order. lm_tile_coords gives each XCD a
+// contiguous eighth of the work items; the forward measured fastest with the
+// smallest group (at least 8 token tiles) whose boundaries fall on those eighths:
+// 8 * group a multiple of the token tiles, or the token tiles a multiple of
+// 8 * group. Forward launch, H = 4096, V = 151936, all tokens live, interleaved on
+// one box (ms):
+//   token tiles 10:  groups of 10  2.70 | 8 (misaligned)   2.85
+//   token tiles 20:  groups of 10  5.39 | 20 5.43-5.46
+//   token tiles 32:  groups of 8   8.73-8.82 | 16 8.91-8.99 | 32 9.45-9.50
+//   token tiles 38:  groups of 19  10.28 | 13 10.70-10.81 | 10 11.02-11.09 | 8 11.05 (config 5)
+//   token tiles 64:  groups of 8   17.46-17.53 | 16 17.88-17.94 | 32 18.59-18.61 | 64 18.26-18.28
+//   token tiles 128: groups of 8   34.86-34.93 | 16 36.87-36.91 | 32 38.25-38.28
+// The backward's chunks (64 vocab tiles) measured best with groups of 4 at config 5
+// (step 55.3 ms against 55.6 with 8; 2 matched 4, 1 and 38 were slower), and so did
+// the whole-vocabulary products of the cached backward (dhidden / dW groups of 4 / 4:
+// step 42.19-42.25 ms; 4 / 8 42.28, 4 / 2 42.43, 4 / 16 42.65, 8 / 16 42.75, 2 / 16
+// 43.0, 16 / 16 43.1). The forward computes its group in the kernel from the live
+// token count.
+constexpr int kLmBwdGroup = 4;
+
+__host__ __device__ inline int lm_group_m(int mode, int ntt) {
+  if (ntt < 1) return 1;
+  if (mode != kLmFwd) return ntt < kLmBwdGroup ? ntt : kLmBwdGroup;
+  for (int g = ntt < 8 ? ntt : 8; g < ntt; ++g)
+    if ((8 * g) % ntt == 0 || ntt % (8 * g) == 0) return g;
+  return ntt;
 }
 
 __device__ __forceinline__ int64_t lm_id(const LmTileArgs& a, int n) {
@@ -109,24 +131,21 @@ __device__ __forceinline__ void lm_barrier() {
 // ATR (kLmGemm): the token-role operand is stored K-major and its fragments are read
 // with ds_read_b64_tr_b16 (see below).
 // ECACHE (kLmFwd): the epilogue also stores the softmax terms (see there).
-template <int MODE, bool ATR = false, bool ECACHE = false>
-__global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
-lm_tile_kernel(LmTileArgs a) {
+// Tile p of product prod (kLmGemm; the loss-head modes have one), called by
+// lm_tile_kernel's work loop.
+template <int MODE, bool ATR, bool ECACHE>
+__device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, char* smem) {
   using namespace lm;
-  extern __shared__ __align__(16) char smem[];
 
-  // The product this workgroup works on: the loss-head modes read rows of H elements
-  // of hidden (A) and W (B); kLmGemm takes one of its (up to) two products.
-  int pid = blockIdx.x;
+  // The product: the loss-head modes read rows of H elements of hidden (A) and W (B);
+  // kLmGemm takes one of its (up to) two products.
   const void* opA = a.A;
   const void* opB = a.B;
-  int N = a.N, V = a.V, K = a.H, lda = a.H, ldb = a.H, ntt = a.ntt, nvt = a.nvt, gm = a.group_m, vt0 = a.vt0;
+  int N = a.N, V = a.V, K = a.H, lda = a.H, ldb = a.H, ntt = a.ntt, nvt = a.nvt, gm = 1, vt0 = a.vt0;
   float* C = nullptr;
   int ldc = 0, accumulate = 0, transpose_c = 0, krows_a = 0;
   if constexpr (MODE == kLmGemm) {
-    const int p = pid >= a.gemm[0].tiles ? 1 : 0;
-    if (p) pid -= a.gemm[0].tiles;
-    const LmTileArgs::Gemm& g = a.gemm[p];
+    const LmTileArgs::Gemm& g = a.gemm[prod];
     opA = g.A;
     opB = g.B;
     N = g.N;
@@ -143,9 +162,22 @@ lm_tile_kernel(LmTileArgs a) {
     accumulate = g.accumulate;
     transpose_c = g.transpose_c;
     krows_a = g.krows_a;
+    if (g.vcount) {
+      V = min(V, *g.vcount);
+      nvt = (V + BV - 1) / BV;
+    }
+    if (g.kcount) {
+      krows_a = min(K, *g.kcount);
+      K = min(K, (krows_a + BK - 1) / BK * BK);
+    }
+  } else {
+    // Tiles over the live tokens only (the grid covers all N).
+    N = min(N, *a.count);
+    ntt = (N + BT - 1) / BT;
+    gm = lm_group_m(MODE, ntt);
   }
   int tm, tn;
-  if (!lm_tile_coords(pid, ntt, nvt, gm, tm, tn)) return;
+  lm_tile_of(p, ntt, nvt, gm, tm, tn);
   const int m0 = tm * BT;                  // first token
   const int v0 = (vt0 + tn) * BV;          // first vocab entry
   const int tid = threadIdx.x;
@@ -391,7 +423,7 @@ lm_tile_kernel(LmTileArgs a) {
             const auto lo = __builtin_amdgcn_permlane32_swap(g[4 * p], g[4 * p + 2], false, false);
             const auto hi = __builtin_amdgcn_permlane32_swap(g[4 * p + 1], g[4 * p + 3], false, false);
             const int64_t c = vw + 32 * i + 16 * p + 8 * half;
-            if (n < a.N && c < a.lde) {
+            if (n < N && c < a.lde) {
               const u32x4 w = {lo[0], hi[0], lo[1], hi[1]};
               *reinterpret_cast<u32x4*>(a.ecache + static_cast<int64_t>(n) * a.lde + c) = w;
             }
@@ -399,7 +431,7 @@ lm_tile_kernel(LmTileArgs a) {
         }
       }
       s += __shfl_xor(s, 32);
-      if (n < a.N && any_v) {
+      if (n < N && any_v) {
         if (half == 0) a.part[static_cast<int64_t>(n) * a.ldp + vw / kPart] = make_float2(m2, s);
         const int64_t rel = lm_id(a, n) - vw;
         if (rel >= 0 && rel < 128) {
@@ -471,7 +503,7 @@ lm_tile_kernel(LmTileArgs a) {
           const int n = m0 + h * 128 + tcol;
           float cf = 0.f, l2 = 0.f;
           int64_t rel = -1;
-          if (n < a.N) {
+          if (n < N) {
             cf = a.coef[n];
             l2 = a.lse2[n];
             rel = lm_id(a, n) - vw;
@@ -500,7 +532,7 @@ lm_tile_kernel(LmTileArgs a) {
       for (int it = 0; it < BT / 2 / (NTHR / 32); ++it) {
         const int t = it * (NTHR / 32) + (tid >> 5);
         const int n = m0 + h * 128 + t;
-        if (n < a.N && col0 < a.ldd) {
+        if (n < N && col0 < a.ldd) {
           const u32x4 w = *reinterpret_cast<const u32x4*>(Ds + t * LDD + cidx * 8);
           *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.dchunk) + static_cast<int64_t>(n) * a.ldd + col0) = w;
         }
@@ -514,7 +546,7 @@ lm_tile_kernel(LmTileArgs a) {
 __global__ void __launch_bounds__(256) lm_reduce_kernel(LmReduceArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-  if (n >= a.N) return;
+  if (n >= *a.count) return;
   float m = kNegInf, s = 0.f;
   const float2* p = a.part + n * a.ldp;
   for (int t = lane; t < a.nvt; t += 64) {
@@ -527,6 +559,44 @@ __global__ void __launch_bounds__(256) lm_reduce_kernel(LmReduceArgs a) {
     ms_merge(m, s, om, os);
   }
   if (lane == 0) a.lse2[n] = m + log2f(s);
+}
+
+// Tiles of product prod at this launch's live sizes (the kLmGemm row / K counts and
+// the loss-head modes' token count are read from device memory).
+template <int MODE>
+__device__ __forceinline__ int lm_total_tiles(const LmTileArgs& a, int prod) {
+  using namespace lm;
+  if constexpr (MODE == kLmGemm) {
+    const LmTileArgs::Gemm& g = a.gemm[prod];
+    const int V = g.vcount ? min(g.V, *g.vcount) : g.V;
+    return g.ntt * ((V + BV - 1) / BV);
+  } else {
+    const int N = min(a.N, *a.count);
+    return ((N + BT - 1) / BT) * a.nvt;
+  }
+}
+
+// One workgroup per tile. Workgroup ids are dealt round-robin to the 8 XCDs, so
+// workgroup b runs on XCD b % 8 and takes item b / 8 of that XCD's contiguous eighth of
+// every product's tiles (products in order). The grid is sized for every token and
+// the tiles for the live ones, so items past the XCD's share exit at once. Measured at
+// config 5 against a persistent grid of one workgroup per CU that takes tiles from
+// per-XCD atomic queues: 43.5 against 43.9 ms of kernel time per step (the queue's
+// per-tile barriers and atomic cost more than these early exits), and against a
+// persistent static split, 46.2 ms.
+template <int MODE, bool ATR = false, bool ECACHE = false>
+__global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
+lm_tile_kernel(LmTileArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  const int xcd = blockIdx.x % 8, i = blockIdx.x / 8;
+  const int t0 = lm_total_tiles<MODE>(a, 0);
+  const int t1 = (MODE == kLmGemm && a.n_gemm > 1) ? lm_total_tiles<MODE>(a, 1) : 0;
+  const int per0 = (t0 + 7) / 8, per1 = (t1 + 7) / 8;
+  if (i >= per0 + per1) return;
+  const int prod = i < per0 ? 0 : 1;
+  const int p = prod == 0 ? xcd * per0 + i : xcd * per1 + (i - per0);
+  if (p >= (prod == 0 ? t0 : t1)) return;
+  lm_tile<MODE, ATR, ECACHE>(a, prod, p, smem);
 }
 
 // 64 x 64 bf16 tiles staged in LDS for a transpose: rows of 66 elements (33 words),
@@ -552,6 +622,10 @@ __device__ __forceinline__ u32x4 tile_col8(const uint16_t* t, int r, int c) {
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
+// Vocab tiles of 64 per lm_dcache_kernel block: fewer blocks, so fewer of them idle
+// past the live token count.
+constexpr int kDcacheVocabTiles = 4;
+
 // dlogits from the forward's softmax cache, per 64 x 64 tile (tokens x vocab): D is
 // written in place over the cache (f16 terms -> bf16, token-major, the dhidden
 // product's operand) and transposed through LDS into Dt [ldv, ldt] (vocab-major,
@@ -562,41 +636,59 @@ __device__ __forceinline__ u32x4 tile_col8(const uint16_t* t, int r, int c) {
 // past V and rows with c_n = 0 are 0.
 __global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
   __shared__ uint16_t t[64 * kTilePitch];    // [token][vocab] bf16
-  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * 64;
   const int tid = threadIdx.x;
-  const int64_t ntile = a.ldt / 64;
-  for (int64_t tb = blockIdx.y; tb < ntile; tb += gridDim.y) {
+  const int64_t n = *a.count;
+  const int64_t ntile = (n + 63) / 64;     // token tiles that the dW product reads
+  for (int64_t tb = blockIdx.x; tb < ntile; tb += gridDim.x)
+  for (int vs = 0; vs < kDcacheVocabTiles; ++vs) {
+    const int64_t v0 = (static_cast<int64_t>(blockIdx.y) * kDcacheVocabTiles + vs) * 64;
+    if (v0 >= a.ld) break;
     const int64_t r0 = tb * 64;
     const int cc = (tid & 7) * 8;
     const int64_t c0 = v0 + cc;
+    // Both rows' loads first (one round trip): the f16 terms and the row's scalars.
+    u32x4 w[2];
+    float cf[2], l2[2], m2[2], tg[2];
+    int id[2];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int64_t row = r0 + (tid >> 3) + 32 * it;
+      w[it] = u32x4{0u, 0u, 0u, 0u};
+      cf[it] = 0.f;
+      l2[it] = m2[it] = tg[it] = 0.f;
+      id[it] = -1;
+      if (row < n) {
+        cf[it] = a.coef[row];
+        l2[it] = a.lse2[row];
+        id[it] = a.ids[row];
+        tg[it] = a.tgt[row];
+        if (c0 < a.V) {
+          w[it] = *reinterpret_cast<const u32x4*>(a.d + row * a.ld + c0);
+          m2[it] = a.part[row * a.ldp + c0 / kLmPart].x;
+        }
+      }
+    }
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
       const int rr = (tid >> 3) + 32 * it;
       const int64_t row = r0 + rr;
       u32x4 out = {0u, 0u, 0u, 0u};
-      if (row < a.n) {
-        u32x4* p = reinterpret_cast<u32x4*>(a.d + row * a.ld + c0);
-        const float cf = a.coef[row];
-        if (cf != 0.f && c0 < a.V) {
-          const float l2 = a.lse2[row];
-          const float ref = ms_ref(a.part[row * a.ldp + c0 / kLmPart].x);
-          const float f = -cf * hw_exp2(ref - l2);
-          const u32x4 w = *p;
-          const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
-          const int64_t rel = static_cast<int64_t>(a.ids[row]) - c0;
-          float d[8];
+      if (row < n && cf[it] != 0.f && c0 < a.V) {
+        const float f = -cf[it] * hw_exp2(ms_ref(m2[it]) - l2[it]);
+        const uint32_t ww[4] = {w[it][0], w[it][1], w[it][2], w[it][3]};
+        const int64_t rel = static_cast<int64_t>(id[it]) - c0;
+        float d[8];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) d[k] = c0 + k < a.V ? f * F16T::unpack(ww, k) : 0.f;
-          if (rel >= 0 && rel < 8) {
-            const float pt = hw_exp2(fmaf(a.tgt[row], kLog2e, -l2));
+        for (int k = 0; k < 8; ++k) d[k] = c0 + k < a.V ? f * F16T::unpack(ww, k) : 0.f;
+        if (rel >= 0 && rel < 8) {
+          const float pt = hw_exp2(fmaf(tg[it], kLog2e, -l2[it]));
 #pragma unroll
-            for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf * pt + cf : d[k];
-          }
-          out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
-                      pack2<BF16T>(d[6], d[7])};
+          for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf[it] * pt + cf[it] : d[k];
         }
-        *p = out;
+        out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
+                    pack2<BF16T>(d[6], d[7])};
       }
+      if (row < n) *reinterpret_cast<u32x4*>(a.d + row * a.ld + c0) = out;
       tile_put8(t, rr, cc, out);
     }
     __syncthreads();
@@ -695,8 +787,10 @@ __global__ void __launch_bounds__(1024) lm_compact_kernel(LmCompactArgs a) {
   if (tid == 0) a.count[0] = base_s;
 }
 
-__global__ void __launch_bounds__(256) lm_gather_rows_kernel(const u32x4* src, u32x4* dst, const int* live, int H) {
+__global__ void __launch_bounds__(256) lm_gather_rows_kernel(const u32x4* src, u32x4* dst, const int* live,
+                                                              const int* count, int H) {
   const int c = blockIdx.x;
+  if (c >= *count) return;
   const int nv = H / 8;  // 16-byte vectors per bf16 row
   const u32x4* s = src + static_cast<int64_t>(live[c]) * nv;
   u32x4* d = dst + static_cast<int64_t>(c) * nv;
@@ -722,13 +816,16 @@ __global__ void __launch_bounds__(256) lm_scatter_rows_kernel(const u32x4* src, 
 // sides. Source rows past R read as 0, so the destination is zero-padded up to ld_dst.
 __global__ void __launch_bounds__(256) lm_transpose_kernel(LmTransposeArgs a) {
   __shared__ uint16_t t[64 * kTilePitch];
+  const int R = a.rcount ? min(a.R, *a.rcount) : a.R;
+  const int64_t rend = min(a.ld_dst, (static_cast<int64_t>(R) + 63) / 64 * 64);   // destination columns written
   const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  if (r0 >= rend) return;
   const int tid = threadIdx.x;
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int rr = it * 32 + (tid >> 3), cc = (tid & 7) * 8;
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (r0 + rr < a.R && c0 + cc < a.C)
+    if (r0 + rr < R && c0 + cc < a.C)
       v = *reinterpret_cast<const u32x4*>(a.src + static_cast<int64_t>(r0 + rr) * a.ld_src + c0 + cc);
     tile_put8(t, rr, cc, v);
   }
@@ -738,7 +835,7 @@ __global__ void __launch_bounds__(256) lm_transpose_kernel(LmTransposeArgs a) {
     const int c = (tid >> 3) + 32 * it;   // source column = destination row
     const int g = tid & 7;                // source rows 8g .. 8g+7
     const int64_t r = r0 + 8 * g;
-    if (c0 + c < a.C && r < a.ld_dst)
+    if (c0 + c < a.C && r < rend)
       *reinterpret_cast<u32x4*>(a.dst + static_cast<int64_t>(c0 + c) * a.ld_dst + r) = tile_col8(t, 8 * g, c);
   }
 }
@@ -753,45 +850,21 @@ __global__ void __launch_bounds__(256) lm_zero_kernel(float* dst, int64_t n) {
 // ---------------------------------------------------------------------------
 size_t lm_tile_smem_bytes() { return lm::kSmem; }
 
-// Token tiles per group in the tile order. lm_tile_coords gives each XCD a
-// contiguous eighth of the work items; the forward measured fastest with the
-// smallest group (at least 8 token tiles) whose boundaries fall on those eighths:
-// 8 * group a multiple of the token tiles, or the token tiles a multiple of
-// 8 * group. Forward launch, H = 4096, V = 151936, all tokens live, interleaved on
-// one box (ms):
-//   token tiles 10:  groups of 10  2.70 | 8 (misaligned)   2.85
-//   token tiles 20:  groups of 10  5.39 | 20 5.43-5.46
-//   token tiles 32:  groups of 8   8.73-8.82 | 16 8.91-8.99 | 32 9.45-9.50
-//   token tiles 38:  groups of 19  10.28 | 13 10.70-10.81 | 10 11.02-11.09 | 8 11.05 (config 5)
-//   token tiles 64:  groups of 8   17.46-17.53 | 16 17.88-17.94 | 32 18.59-18.61 | 64 18.26-18.28
-//   token tiles 128: groups of 8   34.86-34.93 | 16 36.87-36.91 | 32 38.25-38.28
-// The backward's chunks (64 vocab tiles) measured best with groups of 4 at config 5
-// (step 55.3 ms against 55.6 with 8; 2 matched 4, 1 and 38 were slower).
-constexpr int kLmBwdGroup = 4;
-
-int lm_group_m(int mode, int ntt) {
-  if (ntt < 1) return 1;
-  if (mode != kLmFwd) return ntt < kLmBwdGroup ? ntt : kLmBwdGroup;
-  for (int g = ntt < 8 ? ntt : 8; g < ntt; ++g)
-    if ((8 * g) % ntt == 0 || ntt % (8 * g) == 0) return g;
-  return ntt;
-}
-
 template <int MODE, bool EC = false, bool kAtr = MODE == kLmGemm>
-hipError_t launch_tiles_mode(const LmTileArgs& a, int grid, hipStream_t st) {
+hipError_t launch_tiles_mode(const LmTileArgs& a, int max_tiles, hipStream_t st) {
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE, kAtr, EC>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
   if (e != hipSuccess) return e;
+  // Items per XCD at the largest sizes: each product rounds its share up separately.
+  const int grid = 8 * ((max_tiles + 7) / 8 + (MODE == kLmGemm && a.n_gemm > 1 ? 1 : 0));
   lm_tile_kernel<MODE, kAtr, EC><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
   return hipGetLastError();
 }
 
 hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {
   LmTileArgs a = args;
-  a.group_m = lm_group_m(mode, a.ntt);
-  const int total = a.ntt * a.nvt;
-  if (total <= 0) return hipSuccess;
-  const int grid = ((total + 7) / 8) * 8;
+  const int grid = a.ntt * a.nvt;   // tiles at the largest token count
+  if (grid <= 0) return hipSuccess;
   if (mode == kLmFwd)
     return a.ecache ? launch_tiles_mode<kLmFwd, true>(a, grid, st) : launch_tiles_mode<kLmFwd>(a, grid, st);
   return launch_tiles_mode<kLmBwd>(a, grid, st);
@@ -801,11 +874,11 @@ hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, bool k_major_a
   LmTileArgs a;
   std::memset(&a, 0, sizeof(a));
   int grid = 0;
-  for (int p = 0; p < n_gemm && p < 2; ++p) {
+  a.n_gemm = n_gemm < 2 ? n_gemm : 2;
+  for (int p = 0; p < a.n_gemm; ++p) {
     a.gemm[p] = g[p];
     a.gemm[p].group_m = lm_group_m(kLmGemm, g[p].ntt);
-    a.gemm[p].tiles = ((g[p].ntt * g[p].nvt + 7) / 8) * 8;   // whole XCD rounds per product
-    grid += a.gemm[p].tiles;
+    grid += g[p].ntt * g[p].nvt;
   }
   if (grid <= 0) return hipSuccess;
   if (!k_major_a) return launch_tiles_mode<kLmGemm, false, false>(a, grid, st);
@@ -825,9 +898,14 @@ hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_lm_dcache(const LmDcacheArgs& a, hipStream_t st) {
-  if (a.n <= 0 || a.ld <= 0) return hipSuccess;
+  if (a.ldt <= 0 || a.ld <= 0) return hipSuccess;
+  // Token tiles are the grid's fast dimension: the blocks past the live count (the grid
+  // is sized for every token) are interleaved with live ones instead of forming a tail.
+  // At config 5, 1.95 ms with an exact grid (host-read count), 2.08 ms with the dead
+  // blocks as a tail or with a 16-row grid looping over token tiles.
   const int64_t ntile = a.ldt / 64;
-  const dim3 grid(static_cast<unsigned>(a.ld / 64), static_cast<unsigned>(ntile < 65535 ? ntile : 65535));
+  const int64_t vblocks = (a.ld / 64 + kDcacheVocabTiles - 1) / kDcacheVocabTiles;
+  const dim3 grid(static_cast<unsigned>(ntile < 65535 ? ntile : 65535), static_cast<unsigned>(vblocks));
   lm_dcache_kernel<<<grid, dim3(256), 0, st>>>(a);
   return hipGetLastError();
 }
@@ -837,10 +915,11 @@ hipError_t launch_lm_compact(const LmCompactArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_lm_gather_rows(const void* src, void* dst, const int* live, int n, int H, hipStream_t st) {
+hipError_t launch_lm_gather_rows(const void* src, void* dst, const int* live, const int* count, int n, int H,
+                                 hipStream_t st) {
   if (n <= 0) return hipSuccess;
   lm_gather_rows_kernel<<<dim3(n), dim3(256), 0, st>>>(static_cast<const u32x4*>(src), static_cast<u32x4*>(dst),
-                                                       live, H);
+                                                       live, count, H);
   return hipGetLastError();
 }
 

@@ -21,9 +21,10 @@ constexpr int kLmPart = 128;     // vocab entries per log-sum-exp partial
 struct LmTileArgs {
   const void* A;        // hidden [N, H] bf16, row-major
   const void* B;        // weight [V, H] bf16, row-major
-  int N, V, H;          // H % 64 == 0
-  int vt0, nvt, ntt;
-  int group_m;          // token tiles per group in the tile order (set by launch_lm_tiles)
+  int N, V, H;          // H % 64 == 0; N bounds *count
+  int vt0, nvt, ntt;    // ntt: token tiles of N (sizes the grid); the kernel uses *count's
+  const int* count;     // [1] live tokens (device): the kLmFwd / kLmBwd tiles cover rows < *count
+  int n_gemm;           // kLmGemm: products in gemm[] (1 or 2)
   const void* ids;      // [N] target ids
   int ids_i64;
   // kLmFwd
@@ -37,8 +38,8 @@ struct LmTileArgs {
   const float* coef;    // [N] d loss / d logp
   void* dchunk;         // [N, ldd] bf16 dlogits of vocab [vc0, vc0 + ldd)
   int vc0, ldd;
-  // kLmGemm: up to two independent products in one launch (gemm[0] takes the first
-  // gemm[0].tiles workgroups, gemm[1] the rest); the fields above are unused.
+  // kLmGemm: up to two independent products in one launch (each XCD takes its share of
+  // gemm[0]'s tiles, then of gemm[1]'s); the fields above are unused.
   // result[v][t] = sum_k B[v][k] * A(k, t): B rows are K-contiguous; A is either
   // K-contiguous too (element (k, t) at A[t * lda + k]) or stored K-major (at
   // A[k * lda + t]) and read with LDS transpose loads (launch_lm_gemms' k_major_a).
@@ -48,33 +49,37 @@ struct LmTileArgs {
     int N, V, K;        // K % 64 == 0, K <= ldb
     int lda, ldb;       // row strides in elements (lda >= N rounded up to 8)
     int krows_a;        // K-major A: rows that exist; rows [krows_a, K) read as 0
+    const int* vcount;  // or nullptr: V = *vcount (<= V; tiles past it exit)
+    const int* kcount;  // or nullptr: K = *kcount rounded up to 64 (<= K), krows_a = *kcount
     float* C;           // f32 result: row v, column t at C[v * ldc + t], or at
     int ldc;            //   C[t * ldc + v] with transpose_c (then V % 4 == 0)
     int transpose_c;
     int accumulate;     // 1: C += product, 0: C = product
-    int ntt, nvt;       // tiles over N and over V
+    int ntt, nvt;       // tiles over N and over V (nvt at the largest V)
     int group_m;        // set by launch_lm_gemms
-    int tiles;          // workgroups of this product (ntt * nvt rounded up to 8)
   } gemm[2];
 };
 
-// dst[c][r] = src[r][c] for r < R, c < C; dst[c][r] = 0 for R <= r < ld_dst (bf16).
+// dst[c][r] = src[r][c] for r < R, c < C; dst[c][r] = 0 for R <= r < min(ld_dst, R
+// rounded up to 64) (bf16). With rcount, R = *rcount (device; at most the R given).
 struct LmTransposeArgs {
   const uint16_t* src;
   int64_t ld_src;
   int R, C;
   uint16_t* dst;
   int64_t ld_dst;
+  const int* rcount;
 };
 
-// Over the softmax cache: d[n][v] (f16 term) -> bf16 dlogits in place, and the same
-// values transposed into dt[v][n] (zero for n <= token < ldt).
+// Over the softmax cache: d[n][v] (f16 term) -> bf16 dlogits in place for n < *count,
+// and the same values transposed into dt[v][n], zero for *count <= n < *count rounded
+// up to 64 (columns past that are not written).
 struct LmDcacheArgs {
-  uint16_t* d;            // [n, ld]
+  uint16_t* d;            // [ldt, ld]
   int64_t ld;             // multiple of 64, >= V
-  int64_t n;              // live tokens
-  uint16_t* dt;           // [ld, ldt]
-  int64_t ldt;            // multiple of 64, >= n
+  const int* count;       // [1] live tokens (device)
+  uint16_t* dt;           // [ld, ldt] or nullptr
+  int64_t ldt;            // multiple of 64, >= *count
   int64_t V;
   const float2* part;     // [n, ldp] the policy's forward partials
   int ldp;
@@ -86,7 +91,8 @@ struct LmDcacheArgs {
 
 struct LmReduceArgs {
   const float2* part;
-  int64_t N;
+  int64_t N;              // bounds *count (the grid)
+  const int* count;       // [1] live tokens (device)
   int ldp, nvt;
   float* lse2;          // out
 };
@@ -128,29 +134,29 @@ struct LmNormBwdArgs {
   const int* live;        // [n_live] compact index -> token
   int64_t N;
   int H;
-  int n_live;
-  int nslice;             // lm_norm_slices(n_live)
+  const int* count;       // [1] n_live (device)
   float* dh;              // [N, H] or nullptr
-  float* gpart;           // [nslice, H] dgamma partials, or nullptr
+  float* gpart;           // [kLmNormSlices, H] dgamma partials, or nullptr
   float* dgamma;          // [H] or nullptr
 };
 
-int lm_norm_slices(int n_live);
-hipError_t launch_lm_norm_rows(const void* h, const float* gamma, float eps, const int* live, int n, int H, void* y,
-                               float* rstd, hipStream_t st);
+// y / rstd rows c < *count from live[c]; n bounds the count (the grid).
+hipError_t launch_lm_norm_rows(const void* h, const float* gamma, float eps, const int* live, const int* count,
+                               int n, int H, void* y, float* rstd, hipStream_t st);
 hipError_t launch_lm_norm_bwd(const LmNormBwdArgs& a, hipStream_t st);
 
 hipError_t launch_lm_compact(const LmCompactArgs& a, hipStream_t st);
-// dst[c, :] = src[live[c], :] for c < n (bf16 rows of H elements, H % 64 == 0).
-hipError_t launch_lm_gather_rows(const void* src, void* dst, const int* live, int n, int H, hipStream_t st);
+// dst[c, :] = src[live[c], :] for c < *count <= n (bf16 rows of H elements, H % 64 == 0).
+hipError_t launch_lm_gather_rows(const void* src, void* dst, const int* live, const int* count, int n, int H,
+                                 hipStream_t st);
 // dst[t, :] = cidx[t] >= 0 ? src[cidx[t], :] : 0 for t < N (f32 rows of H elements).
 hipError_t launch_lm_scatter_rows(const float* src, float* dst, const int* cidx, int N, int H, hipStream_t st);
 hipError_t launch_lm_zero(float* dst, int64_t n, hipStream_t st);
 hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st);
 // One launch of one or two products (n_gemm = 1 or 2; fields per LmTileArgs::Gemm,
-// group_m and tiles are filled in here). The longer product should come first.
-// k_major_a: A is stored K-major (read with LDS transpose loads); otherwise A is
-// K-contiguous like B ([N, lda], krows_a unused).
+// group_m is filled in here). The longer product should come first. k_major_a: A is
+// stored K-major (read with LDS transpose loads); otherwise A is K-contiguous like B
+// ([N, lda], krows_a unused).
 hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, bool k_major_a, hipStream_t st);
 hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st);
 hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st);

@@ -2,8 +2,9 @@
 //
 // Live tokens (mask != 0, id in [0, V)) are compacted first: a masked or ignored
 // token has zero loss weight and zero gradient, so only live hidden rows enter the
-// products. The live count sizes the products and the backward's buffer, so the call
-// reads it back once (one stream synchronisation, also under PCP_FLAG_ASYNC).
+// products. The live count stays on the device: buffers and grids are sized for all
+// tokens and every kernel reads the count, so the call never waits for the device
+// (PCP_FLAG_ASYNC returns after enqueueing, and the call can be captured in a graph).
 // Forward, per model (reference, then policy): MFMA logits tiles reduced in-tile to
 // per-(token, vocab tile) log-sum-exp partials and the target logit; one wave per
 // token merges the partials. Then the GRPO terms per token and the loss reduction
@@ -142,17 +143,16 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_hid = take(2 * static_cast<size_t>(N) * H);
   const size_t o_part = take(8 * static_cast<size_t>(N) * npart);
   const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
-  // Token-padded width of the transposed hidden rows (the dW product's K, a multiple
-  // of the 64-deep pipeline stage).
-  const int64_t ldt_max = (N + 63) / 64 * 64;
+  // Row stride, in tokens, of the transposed operands (hidden^T, D^T): a multiple of the
+  // 64-deep pipeline stage, and off multiples of 256 (a 2^k-byte stride puts the rows
+  // that one block writes or one tile reads on the same HBM channels).
+  const int64_t ldt_max = (N + 63) / 64 * 64 + ((N + 63) / 64 * 64 % 256 == 0 ? 64 : 0);
   const size_t o_ht = a->dweight ? take(2 * static_cast<size_t>(H) * ldt_max) : 0;
   const size_t o_dhc = want_dy ? take(4 * static_cast<size_t>(N) * H) : 0;
   const size_t o_rstd = norm ? take(4 * N) : 0;
   const size_t o_gpart = a->dnorm_weight ? take(4 * static_cast<size_t>(kLmNormSlices) * H) : 0;
   rc = ensure_scratch(ctx, off);
   if (rc != PCP_OK) return rc;
-  if (!ctx->h_count && (e = hipHostMalloc(reinterpret_cast<void**>(&ctx->h_count), sizeof(int))) != hipSuccess)
-    return hip_fail(ctx, e, "hipHostMalloc");
   char* sp = static_cast<char*>(ctx->scratch);
   auto F = [&](size_t o) { return reinterpret_cast<float*>(sp + o); };
   auto I = [&](size_t o) { return reinterpret_cast<int*>(sp + o); };
@@ -160,48 +160,47 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   float2* part = reinterpret_cast<float2*>(sp + o_part);
   const int mask_u8 = a->mask_dtype == PCP_BOOL;
 
-  // Live-token compaction; the count comes back to size the products.
-  LmCompactArgs ca{a->ids, a->ids_dtype == PCP_I64, a->mask, mask_u8, static_cast<int>(N), static_cast<int>(V),
-                   I(o_live), I(o_cidx), I(o_idsc), I(o_cnt)};
-  if ((e = launch_lm_compact(ca, st)) != hipSuccess) return hip_fail(ctx, e, "compaction launch");
-  if ((e = hipMemcpyAsync(ctx->h_count, I(o_cnt), sizeof(int), hipMemcpyDeviceToHost, st)) != hipSuccess)
-    return hip_fail(ctx, e, "reading the live-token count");
-  if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
-  const int nl = *ctx->h_count;
-  if (nl < 0 || nl > N) return fail(ctx, PCP_ERR_DEVICE, "live-token count %d out of range", nl);
-  const int ntl = (nl + kLmTileT - 1) / kLmTileT;
-
-  // The backward's bf16 operands. By default: the whole-vocabulary softmax cache
-  // [nl, ldv] (the policy forward stores its f16 terms there; a pass rewrites them as
-  // dlogits D and writes D^T [ldv, ldt] beside it) and W^T [H, ldv], so both products
-  // read K-contiguous operands. With an explicit vocab_chunk, PCP_FLAG_EXACT_BF16, more
-  // than kCacheBudget bytes, or no memory for them: one dlogits chunk [nl, chunk] that
-  // the backward refills by recomputing the logits.
+  // The backward's bf16 operands, sized for all N tokens (the live count stays on the
+  // device). By default: the whole-vocabulary softmax cache [N, ldv] (the policy forward
+  // stores its f16 terms there; a pass rewrites them as dlogits D and writes D^T
+  // [ldv, ldt] beside it) and W^T [H, ldv], so both products read K-contiguous
+  // operands. With an explicit vocab_chunk, PCP_FLAG_EXACT_BF16, more than kCacheBudget
+  // bytes, or no memory for them: one dlogits chunk [N, chunk] that the backward refills
+  // by recomputing the logits.
   const int64_t ldv = (V + 63) / 64 * 64;
-  const int64_t ldt = (static_cast<int64_t>(nl) + 63) / 64 * 64;
-  const size_t o_dt = 2 * static_cast<size_t>(nl) * ldv;
+  const int64_t ldt = ldt_max;
+  const size_t o_dt = 2 * static_cast<size_t>(ldt) * ldv;
   const size_t o_wt = o_dt + (a->dweight ? 2 * static_cast<size_t>(ldv) * ldt : 0);
   const size_t cache_bytes = o_wt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
   bool cached = false;
-  if (bwd && nl > 0) {
+  if (bwd) {
     if (a->vocab_chunk == 0 && !(a->flags & PCP_FLAG_EXACT_BF16) && cache_bytes <= kCacheBudget) {
       e = grow_dbuf(ctx, cache_bytes);
       if (e == hipSuccess) cached = true;
       else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the softmax cache");
     }
-    if (!cached && (e = grow_dbuf(ctx, 2 * static_cast<size_t>(nl) * chunk)) != hipSuccess) {
+    if (!cached && (e = grow_dbuf(ctx, 2 * static_cast<size_t>(N) * chunk)) != hipSuccess) {
       if (e == hipErrorOutOfMemory)
-        return fail(ctx, PCP_ERR_OOM, "hipMalloc of the %lld x %lld dlogits chunk failed", (long long)nl,
+        return fail(ctx, PCP_ERR_OOM, "hipMalloc of the %lld x %lld dlogits chunk failed", (long long)N,
                     (long long)chunk);
       return hip_fail(ctx, e, "allocating the dlogits chunk");
     }
   }
+
+  // Live-token compaction. The count stays on the device: every kernel below reads it
+  // (grids cover all N tokens; work past the count exits or is zero), so the call never
+  // waits for the device.
+  const int* cnt = I(o_cnt);
+  LmCompactArgs ca{a->ids, a->ids_dtype == PCP_I64, a->mask, mask_u8, static_cast<int>(N), static_cast<int>(V),
+                   I(o_live), I(o_cidx), I(o_idsc), I(o_cnt)};
+  if ((e = launch_lm_compact(ca, st)) != hipSuccess) return hip_fail(ctx, e, "compaction launch");
+  const int ntl = static_cast<int>((N + kLmTileT - 1) / kLmTileT);
   if (norm) {
-    if ((e = launch_lm_norm_rows(a->hidden_states, a->norm_weight, a->norm_eps, I(o_live), nl, static_cast<int>(H),
-                                 sp + o_hid, F(o_rstd), st)) != hipSuccess)
+    if ((e = launch_lm_norm_rows(a->hidden_states, a->norm_weight, a->norm_eps, I(o_live), cnt, static_cast<int>(N),
+                                 static_cast<int>(H), sp + o_hid, F(o_rstd), st)) != hipSuccess)
       return hip_fail(ctx, e, "final norm of live hidden rows");
-  } else if ((e = launch_lm_gather_rows(a->hidden_states, sp + o_hid, I(o_live), nl, static_cast<int>(H), st)) !=
-             hipSuccess) {
+  } else if ((e = launch_lm_gather_rows(a->hidden_states, sp + o_hid, I(o_live), cnt, static_cast<int>(N),
+                                        static_cast<int>(H), st)) != hipSuccess) {
     return hip_fail(ctx, e, "gathering live hidden rows");
   }
 
@@ -222,7 +221,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   LmTileArgs ta;
   std::memset(&ta, 0, sizeof(ta));
   ta.A = sp + o_hid;
-  ta.N = nl;
+  ta.N = static_cast<int>(N);
+  ta.count = cnt;
   ta.V = static_cast<int>(V);
   ta.H = static_cast<int>(H);
   ta.vt0 = 0;
@@ -232,8 +232,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   ta.ids_i64 = 0;
   ta.part = part;
   ta.ldp = npart;
-  LmReduceArgs rd{part, nl, npart, npart, nullptr};
-  const int nmodel = nl > 0 ? (ref ? 2 : 1) : 0;
+  LmReduceArgs rd{part, N, cnt, npart, npart, nullptr};
+  const int nmodel = ref ? 2 : 1;
   for (int k = 0; k < nmodel; ++k) {
     // The reference model first, so the policy's partials stay in `part` for the
     // softmax cache's pass.
@@ -282,20 +282,15 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
                               F(o_val), a->loss ? a->loss : F(o_loss), st)) != hipSuccess)
     return hip_fail(ctx, e, "loss reduction");
 
-  // Backward per vocab chunk over the live tokens; no live token: zero gradients.
-  if (bwd && nl == 0) {
-    if (a->dhidden && (e = launch_lm_zero(a->dhidden, N * H, st)) != hipSuccess) return hip_fail(ctx, e, "zero dhidden");
-    if (a->dweight && (e = launch_lm_zero(a->dweight, V * H, st)) != hipSuccess) return hip_fail(ctx, e, "zero dW");
-    if (a->dnorm_weight && (e = launch_lm_zero(a->dnorm_weight, H, st)) != hipSuccess)
-      return hip_fail(ctx, e, "zero dnorm_weight");
-  }
-  if (bwd && nl > 0) {
+  // Backward over the live tokens. With none, the products have no tiles (dhidden) or
+  // an empty K (dW: zero), and dead rows are written as zero, so every gradient is 0.
+  if (bwd) {
     char* dbuf = static_cast<char*>(ctx->lm_dbuf);
     float* dhc = want_dy ? F(o_dhc) : nullptr;
     if (a->dweight) {
       // hidden^T [H, ldt]: the dW product's token operand, zero past the live tokens.
-      const LmTransposeArgs tr{reinterpret_cast<const uint16_t*>(sp + o_hid), H, nl, static_cast<int>(H),
-                               reinterpret_cast<uint16_t*>(sp + o_ht), ldt};
+      const LmTransposeArgs tr{reinterpret_cast<const uint16_t*>(sp + o_hid), H, static_cast<int>(N),
+                               static_cast<int>(H), reinterpret_cast<uint16_t*>(sp + o_ht), ldt, cnt};
       if ((e = launch_lm_transpose(tr, st)) != hipSuccess) return hip_fail(ctx, e, "transposing hidden rows");
     }
     // Chunked backward: the products of one vocab range [vc0, vc0 + w) of D
@@ -313,13 +308,14 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         LmTileArgs::Gemm& d = g[ng++];
         d.B = dbuf;
         d.ldb = static_cast<int>(ldd);
-        d.V = nl;
+        d.V = static_cast<int>(N);
+        d.vcount = cnt;
         d.A = static_cast<const uint16_t*>(a->weight) + vc0 * H;
         d.lda = static_cast<int>(H);
         d.krows_a = static_cast<int>(w);
         d.N = static_cast<int>(H);
         d.K = static_cast<int>((w + 63) / 64 * 64);
-        d.nvt = (nl + kLmTileV - 1) / kLmTileV;
+        d.nvt = ntl;
         d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
         d.C = dhc;
         d.ldc = static_cast<int>(H);
@@ -334,7 +330,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         d.V = static_cast<int>(H);
         d.A = dbuf;
         d.lda = static_cast<int>(ldd);
-        d.krows_a = nl;
+        d.krows_a = static_cast<int>(N);
+        d.kcount = cnt;
         d.N = static_cast<int>(w);
         d.K = static_cast<int>(ldt);
         d.nvt = static_cast<int>((H + kLmTileV - 1) / kLmTileV);
@@ -352,7 +349,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       // tokens for dW; dhidden's 608 long tiles at configuration 5 go first).
       uint16_t* dt = a->dweight ? reinterpret_cast<uint16_t*>(dbuf + o_dt) : nullptr;
       uint16_t* wt = want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_wt) : nullptr;
-      const LmDcacheArgs dc{reinterpret_cast<uint16_t*>(dbuf), ldv, nl, dt, ldt, V, part, npart,
+      const LmDcacheArgs dc{reinterpret_cast<uint16_t*>(dbuf), ldv, cnt, dt, ldt, V, part, npart,
                             F(o_l2), F(o_coef), F(o_tgt), I(o_idsc)};
       if ((e = launch_lm_dcache(dc, st)) != hipSuccess) return hip_fail(ctx, e, "dlogits from the softmax cache");
       LmTileArgs::Gemm g[2];
@@ -361,18 +358,19 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       if (want_dy) {
         // W^T [H, ldv], zero past V.
         const LmTransposeArgs tw{static_cast<const uint16_t*>(a->weight), H, static_cast<int>(V), static_cast<int>(H),
-                                 wt, ldv};
+                                 wt, ldv, nullptr};
         if ((e = launch_lm_transpose(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
         // dhidden_c[t][h] = sum_v D[t][v] * W^T[h][v].
         LmTileArgs::Gemm& d = g[ng++];
         d.B = dbuf;
         d.ldb = static_cast<int>(ldv);
-        d.V = nl;
+        d.V = static_cast<int>(N);
+        d.vcount = cnt;
         d.A = wt;
         d.lda = static_cast<int>(ldv);
         d.N = static_cast<int>(H);
         d.K = static_cast<int>(ldv);
-        d.nvt = (nl + kLmTileV - 1) / kLmTileV;
+        d.nvt = ntl;
         d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
         d.C = dhc;
         d.ldc = static_cast<int>(H);
@@ -387,6 +385,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         d.lda = static_cast<int>(ldt);
         d.N = static_cast<int>(H);
         d.K = static_cast<int>(ldt);
+        d.kcount = cnt;
         d.nvt = static_cast<int>((V + kLmTileV - 1) / kLmTileV);
         d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
         d.C = a->dweight;
@@ -395,7 +394,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       const bool timed = ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
       if (timed && (e = hipEventRecord(ctx->prof_start[ctx->prof_used], st)) != hipSuccess)
         return hip_fail(ctx, e, "hipEventRecord");
-      if ((e = launch_lm_gemms(g, ng, false, st)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
+      if ((e = launch_lm_gemms(g, ng, false, st)) != hipSuccess)
+        return hip_fail(ctx, e, "dhidden / dweight products");
       if (timed && (e = hipEventRecord(ctx->prof_stop[ctx->prof_used++], st)) != hipSuccess)
         return hip_fail(ctx, e, "hipEventRecord");
     } else {
@@ -416,7 +416,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     }
     if (norm && want_dy) {
       const LmNormBwdArgs nb{dhc, static_cast<const uint16_t*>(a->hidden_states), a->norm_weight, F(o_rstd),
-                             I(o_cidx), I(o_live), N, static_cast<int>(H), nl, lm_norm_slices(nl), a->dhidden,
+                             I(o_cidx), I(o_live), N, static_cast<int>(H), cnt, a->dhidden,
                              a->dnorm_weight ? F(o_gpart) : nullptr, a->dnorm_weight};
       if ((e = launch_lm_norm_bwd(nb, st)) != hipSuccess) return hip_fail(ctx, e, "final norm backward");
     } else if (!norm && a->dhidden && (e = launch_lm_scatter_rows(dhc, a->dhidden, I(o_cidx), static_cast<int>(N),

@@ -50,14 +50,17 @@ __device__ __forceinline__ float block_sum_fixed(float v, float* red) {
   return s;
 }
 
-// One block per live row c (token live[c]): y[c] = bf16(gamma * bf16(h * r)), rstd[c] = r.
+// One block per live row c < *count (token live[c]): y[c] = bf16(gamma * bf16(h * r)),
+// rstd[c] = r. The grid covers every token; blocks past the live count return.
 template <int PER>
 __global__ void __launch_bounds__(256) lm_norm_rows_kernel(const uint16_t* __restrict__ h,
                                                            const float* __restrict__ gamma, float eps,
-                                                           const int* __restrict__ live, int H,
+                                                           const int* __restrict__ live,
+                                                           const int* __restrict__ count, int H,
                                                            uint16_t* __restrict__ y, float* __restrict__ rstd) {
   __shared__ float red[4];
   const int c = blockIdx.x;
+  if (c >= *count) return;
   const uint16_t* hr = h + static_cast<int64_t>(live[c]) * H;
   float v[PER];
   float ss = 0.f;
@@ -126,34 +129,36 @@ __global__ void __launch_bounds__(256) lm_norm_dx_kernel(LmNormBwdArgs a) {
 }
 
 // dgamma partials: block (x, y) sums column k = 256 x + lane over live rows
-// c = y, y + nslice, ... : dy[c, k] * bf16(h[live[c], k] * r[c]) (the forward's rounded
-// normalised value), written to gpart[y, k]. Lanes read consecutive columns.
+// c = y, y + kLmNormSlices, ... : dy[c, k] * bf16(h[live[c], k] * r[c]) (the forward's
+// rounded normalised value), written to gpart[y, k] (0 for slices past the live count).
+// Lanes read consecutive columns.
 __global__ void __launch_bounds__(256) lm_norm_dgamma_part_kernel(LmNormBwdArgs a) {
   const int k = blockIdx.x * 256 + threadIdx.x;
   if (k >= a.H) return;
   const int H = a.H;
+  const int n_live = *a.count;
   float acc = 0.f;
-  for (int c = blockIdx.y; c < a.n_live; c += a.nslice) {
+  for (int c = blockIdx.y; c < n_live; c += kLmNormSlices) {
     const float x = bf16_round(bf16_to_f32(a.h[static_cast<int64_t>(a.live[c]) * H + k]) * a.rstd[c]);
     acc += a.dyc[static_cast<int64_t>(c) * H + k] * x;
   }
   a.gpart[static_cast<int64_t>(blockIdx.y) * H + k] = acc;
 }
 
-__global__ void __launch_bounds__(256) lm_norm_dgamma_kernel(const float* __restrict__ gpart, int nslice, int H,
+__global__ void __launch_bounds__(256) lm_norm_dgamma_kernel(const float* __restrict__ gpart, int H,
                                                              float* __restrict__ dgamma) {
   const int k = blockIdx.x * 256 + threadIdx.x;
   if (k >= H) return;
   float s = 0.f;
-  for (int b = 0; b < nslice; ++b) s += gpart[static_cast<int64_t>(b) * H + k];
+  for (int b = 0; b < kLmNormSlices; ++b) s += gpart[static_cast<int64_t>(b) * H + k];
   dgamma[k] = s;
 }
 
 template <int PER>
-hipError_t norm_rows(const void* h, const float* gamma, float eps, const int* live, int n, int H, void* y, float* rstd,
-                     hipStream_t st) {
-  lm_norm_rows_kernel<PER><<<dim3(n), dim3(256), 0, st>>>(static_cast<const uint16_t*>(h), gamma, eps, live, H,
-                                                          static_cast<uint16_t*>(y), rstd);
+hipError_t norm_rows(const void* h, const float* gamma, float eps, const int* live, const int* count, int n, int H,
+                     void* y, float* rstd, hipStream_t st) {
+  lm_norm_rows_kernel<PER><<<dim3(n), dim3(256), 0, st>>>(static_cast<const uint16_t*>(h), gamma, eps, live, count,
+                                                          H, static_cast<uint16_t*>(y), rstd);
   return hipGetLastError();
 }
 
@@ -165,17 +170,15 @@ hipError_t norm_dx(const LmNormBwdArgs& a, hipStream_t st) {
 
 }  // namespace
 
-int lm_norm_slices(int n_live) { return n_live < kLmNormSlices ? (n_live > 0 ? n_live : 1) : kLmNormSlices; }
-
-hipError_t launch_lm_norm_rows(const void* h, const float* gamma, float eps, const int* live, int n, int H, void* y,
-                               float* rstd, hipStream_t st) {
+hipError_t launch_lm_norm_rows(const void* h, const float* gamma, float eps, const int* live, const int* count,
+                               int n, int H, void* y, float* rstd, hipStream_t st) {
   if (n <= 0) return hipSuccess;
-  if (H <= 256) return norm_rows<1>(h, gamma, eps, live, n, H, y, rstd, st);
-  if (H <= 512) return norm_rows<2>(h, gamma, eps, live, n, H, y, rstd, st);
-  if (H <= 1024) return norm_rows<4>(h, gamma, eps, live, n, H, y, rstd, st);
-  if (H <= 2048) return norm_rows<8>(h, gamma, eps, live, n, H, y, rstd, st);
-  if (H <= 4096) return norm_rows<16>(h, gamma, eps, live, n, H, y, rstd, st);
-  if (H <= kLmNormMaxHidden) return norm_rows<32>(h, gamma, eps, live, n, H, y, rstd, st);
+  if (H <= 256) return norm_rows<1>(h, gamma, eps, live, count, n, H, y, rstd, st);
+  if (H <= 512) return norm_rows<2>(h, gamma, eps, live, count, n, H, y, rstd, st);
+  if (H <= 1024) return norm_rows<4>(h, gamma, eps, live, count, n, H, y, rstd, st);
+  if (H <= 2048) return norm_rows<8>(h, gamma, eps, live, count, n, H, y, rstd, st);
+  if (H <= 4096) return norm_rows<16>(h, gamma, eps, live, count, n, H, y, rstd, st);
+  if (H <= kLmNormMaxHidden) return norm_rows<32>(h, gamma, eps, live, count, n, H, y, rstd, st);
   return hipErrorInvalidValue;
 }
 
@@ -189,9 +192,9 @@ hipError_t launch_lm_norm_bwd(const LmNormBwdArgs& a, hipStream_t st) {
     else return hipErrorInvalidValue;
     if (e != hipSuccess) return e;
   }
-  if (!a.dgamma || a.n_live <= 0) return e;
-  lm_norm_dgamma_part_kernel<<<dim3((a.H + 255) / 256, a.nslice), dim3(256), 0, st>>>(a);
-  lm_norm_dgamma_kernel<<<dim3((a.H + 255) / 256), dim3(256), 0, st>>>(a.gpart, a.nslice, a.H, a.dgamma);
+  if (!a.dgamma) return e;
+  lm_norm_dgamma_part_kernel<<<dim3((a.H + 255) / 256, kLmNormSlices), dim3(256), 0, st>>>(a);
+  lm_norm_dgamma_kernel<<<dim3((a.H + 255) / 256), dim3(256), 0, st>>>(a.gpart, a.H, a.dgamma);
   return hipGetLastError();
 }
 

@@ -24,6 +24,8 @@ Tolerances:
     rounding of the larger value); the target's D comes from the f32 target logit as
     without the cache.
 """
+import time
+
 import numpy as np
 import pytest
 import torch
@@ -161,6 +163,10 @@ SMALL = [
     # 10,900 = 43 token tiles: one forward group, backward groups of 4 and a last of 3.
     (2, 3000, 64, 300, 2, 256, [3000, 3000]),
     (4, 3000, 64, 300, 2, 256, [3000, 3000, 3000, 1900]),
+    # 3,100 live of 6,000 tokens: grids sized for 24 token tiles run 13, and dhidden
+    # accumulates over two chunks, so a tile computed twice would show.
+    (2, 3000, 64, 300, 2, 256, [3000, 100]),
+    (2, 3000, 64, 300, 2, 0, [3000, 100]),
 ]
 
 
@@ -214,13 +220,37 @@ def test_lmhead_ignore_index_int32_bool_mask_and_no_grads():
 
 
 def test_lmhead_all_masked_and_no_mask():
+    """No live token: the loss, log-probs and every gradient are 0 on the cached and the
+    chunked backward (the live count stays on the device; the products run with no
+    token tiles / an empty K), with and without the fused final norm; outputs are
+    pre-filled with NaN so that a skipped write shows. Then mask = NULL."""
     c = make_case(2, 20, 64, 500, 2, seed=9, lengths=[20, 20])
     old = np.full((2, 20), -6.0, np.float32)
     zero = torch.zeros((2, 20), dtype=torch.float32, device=DEV)
-    out = run_device(c, LossMode.GRPO_CLIP_KL, old, mask=zero)
-    torch.cuda.synchronize()
-    assert float(out.loss) == 0.0 and not out.logp.any() and not out.token_loss.any()
-    assert not out.dhidden.any() and not out.dweight.any()
+    nan = float("nan")
+    for chunk in (0, 256):
+        outs = grpo.LmheadOutputs(loss=torch.full((), nan, device=DEV), logp=torch.full((2, 20), nan, device=DEV),
+                                  ref_logp=torch.full((2, 20), nan, device=DEV),
+                                  token_loss=torch.full((2, 20), nan, device=DEV),
+                                  advantages=torch.full((2,), nan, device=DEV),
+                                  dhidden=torch.full((40, 64), nan, device=DEV), dweight=torch.full((500, 64), nan, device=DEV))
+        out = grpo.lmhead_fwd_bwd(dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), zero, ref_weight=dev(c["rb"]),
+                                  rewards=dev(c["rewards"]), group_size=2, old_logp=dev(old),
+                                  loss_mode=LossMode.GRPO_CLIP_KL, vocab_chunk=chunk, outputs=outs)
+        torch.cuda.synchronize()
+        assert float(out.loss) == 0.0 and not out.logp.any() and not out.token_loss.any()
+        assert not out.dhidden.any() and not out.dweight.any()
+        cn = make_norm_case(2, 20, 64, 500, 2, seed=10, lengths=[20, 20])
+        outs = grpo.LmheadOutputs(loss=torch.full((), nan, device=DEV), logp=torch.full((2, 20), nan, device=DEV),
+                                  ref_logp=None, token_loss=torch.full((2, 20), nan, device=DEV),
+                                  advantages=torch.full((2,), nan, device=DEV),
+                                  dhidden=torch.full((40, 64), nan, device=DEV), dweight=torch.full((500, 64), nan, device=DEV),
+                                  dnorm_weight=torch.full((64,), nan, device=DEV))
+        out = grpo.lmhead_fwd_bwd(dev(cn["h"]), dev(cn["wb"]), dev(cn["ids"]), zero, rewards=dev(cn["rewards"]),
+                                  group_size=2, vocab_chunk=chunk, norm_weight=dev(cn["gamma"]), outputs=outs)
+        torch.cuda.synchronize()
+        assert float(out.loss) == 0.0 and not out.logp.any()
+        assert not out.dhidden.any() and not out.dweight.any() and not out.dnorm_weight.any()
     # mask = NULL: every token with an in-range id is live (same result as an all-ones mask).
     L, lse, rlse, old, r = oracle_case(c, LossMode.GRPO_CLIP_KL)
     out = grpo.lmhead_fwd_bwd(dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), None, ref_weight=dev(c["rb"]),
@@ -346,6 +376,65 @@ def test_lmhead_exact_flag_recomputes():
     check_forward(c, ex, L, lse, rlse, r, mode)
     check_grads(ex, *grad_bounds(c, L, lse, r, mode, old, cached=False))
     check_grads(ca, *grad_bounds(c, L, lse, r, mode, old, cached=True))
+
+
+def test_lmhead_async_does_not_wait():
+    """PCP_FLAG_ASYNC: the call only enqueues (the live-token count is never read back).
+    Queued behind a bounded spin kernel of ~0.2 s, the call returns long before the spin
+    ends, and the results equal a synchronous call's."""
+    c = make_case(2, 70, 128, 900, 2, seed=5, lengths=[70, 33])
+    old = np.full((2, 70), -7.0, np.float32)
+    want = run_device(c, LossMode.GRPO_CLIP_KL, old)
+    args = (dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), dev(c["mask"]))
+    kw = dict(ref_weight=dev(c["rb"]), rewards=dev(c["rewards"]), group_size=2, old_logp=dev(old),
+              loss_mode=LossMode.GRPO_CLIP_KL)
+    ctx = grpo.default_context(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    torch.cuda._sleep(400_000_000)             # a bounded spin: ~0.2 s at 2 GHz
+    t1 = time.perf_counter()
+    got = grpo.lmhead_fwd_bwd(*args, sync=False, ctx=ctx, **kw)
+    t2 = time.perf_counter()
+    busy = not torch.cuda.current_stream().query()
+    ctx.sync()
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
+    print(f"async LM head: enqueue {1e3 * (t2 - t1):.2f} ms, spin + call {1e3 * (t3 - t0):.1f} ms", flush=True)
+    assert busy and t3 - t0 > 0.05, "the spin kernel did not hold the stream"
+    assert t2 - t1 < 0.5 * (t3 - t0), "the async call waited for the device"
+    for f in ("loss", "logp", "ref_logp", "token_loss", "dhidden", "dweight"):
+        assert torch.equal(getattr(got, f), getattr(want, f)), f
+
+
+@pytest.mark.parametrize("chunk", [0, 512], ids=["cached", "chunked"])
+def test_lmhead_graph_capture_replays(chunk):
+    """The call captured in a HIP graph (asynchronous, no host read): three replays with
+    eager work between them (outputs overwritten with NaN) each equal an eager call bit
+    for bit."""
+    c = make_case(2, 70, 128, 900, 2, seed=43, lengths=[70, 41])
+    old = np.full((2, 70), -7.0, np.float32)
+    args = (dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), dev(c["mask"]))
+    kw = dict(ref_weight=dev(c["rb"]), rewards=dev(c["rewards"]), group_size=2, old_logp=dev(old),
+              loss_mode=LossMode.GRPO_CLIP_KL, vocab_chunk=chunk)
+    want = grpo.lmhead_fwd_bwd(*args, **kw)
+    out = grpo.lmhead_fwd_bwd(*args, **kw)     # the graph's outputs; buffers already grown
+    ctx = grpo.default_context(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        grpo.lmhead_fwd_bwd(*args, outputs=out, sync=False, ctx=ctx, **kw)
+    ctx.sync()
+    fields = ("loss", "logp", "ref_logp", "token_loss", "advantages", "dhidden", "dweight")
+    for rep in range(3):
+        for f in fields:
+            getattr(out, f).fill_(float("nan"))
+        torch.cuda.synchronize()
+        print(f"graph replay {rep} ({'cached' if chunk == 0 else 'chunked'})", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        for f in fields:
+            assert torch.equal(getattr(out, f), getattr(want, f)), (rep, f)
+    ctx.sync()
 
 
 def test_lmhead_errors():
