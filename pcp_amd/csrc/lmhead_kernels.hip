@@ -38,8 +38,19 @@ constexpr int ROWB = BK * 2;      // bytes of one operand row in one stage
 constexpr int kOpBytes = BV * ROWB;             // 32 KB: one operand, one stage
 constexpr int kStageBytes = 2 * kOpBytes;       // 64 KB
 constexpr size_t kSmemGemm = NST * kStageBytes; // 128 KB
-constexpr int NTHR = 512;         // 8 waves: 2 (vocab) x 4 (tokens), 128 x 64 each
-constexpr int NJ = 2;             // 32-column token blocks per wave
+// Waves per workgroup: 8 (two per SIMD; 2 along the vocab x 4 along the tokens, 128 x
+// 64 each, 128 accumulators). The code also builds with 4 (one per SIMD; 2 x 2, 128 x
+// 128 each, 256 accumulators in AGPRs, a third fewer LDS fragment bytes per flop):
+// parity-green, but 10-15% slower at config 5 (step 47.3 against 42.6 ms; forward tiles
+// 11.0-11.4 against 9.5-9.9 ms), as one wave per SIMD cannot cover its own waits.
+constexpr int NW = 8;
+static_assert(NW == 8 || NW == 4, "8 or 4 waves");
+constexpr int NTHR = 64 * NW;
+constexpr int WPE = NW / 4;       // waves per SIMD
+constexpr int WT = NW / 2;        // waves along the tokens
+constexpr int TW = 256 / WT;      // token columns per wave
+constexpr int NJ = TW / 32;       // 32-column token blocks per wave
+constexpr int QN = 32 / NW;       // direct-to-LDS loads per wave per operand per stage
 constexpr int LDD = BV + 8;       // bf16 dlogits row in the backward epilogue (528 B, 16-B aligned)
 constexpr size_t kSmemEpi = (BT / 2) * LDD * sizeof(__bf16);   // half the token columns at a time
 constexpr size_t kSmem = kSmemGemm > kSmemEpi ? kSmemGemm : kSmemEpi;
@@ -182,7 +193,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   const int v0 = (vt0 + tn) * BV;          // first vocab entry
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wv = wave >> 2, wt = wave & 3;
+  const int wv = wave / WT, wt = wave % WT;
 
   // Operand row buffers: rows past V / N read 0 (range-checked lane offsets).
   const uint32_t wbytes = static_cast<uint32_t>(ldb) * 2u;
@@ -208,14 +219,14 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   // of wave w fills k-rows 2*(4w+q) + lane/32, and LDS slot lane%32 of a k-row holds
   // 16-byte chunk (lane%32) ^ 4*(k-row % 4), so the transpose reads below, which take
   // 64 bytes from each of 8 k-rows (k-row % 4 = 0..3, twice), hit every bank twice.
-  uint32_t dofw[4], dofh[4];
+  uint32_t dofw[QN], dofh[QN];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int row = 8 * (4 * wave + q) + (lane >> 3);
+  for (int q = 0; q < QN; ++q) {
+    const int row = 8 * (QN * wave + q) + (lane >> 3);
     const uint32_t c16 = 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
     dofw[q] = static_cast<uint32_t>(row) * wbytes + c16;
     if constexpr (ATR) {
-      const int krow = 2 * (4 * wave + q) + (lane >> 5);
+      const int krow = 2 * (QN * wave + q) + (lane >> 5);
       dofh[q] = static_cast<uint32_t>(krow) * hbytes + 16u * static_cast<uint32_t>((lane & 31) ^ (4 * (krow & 3)));
     } else {
       dofh[q] = static_cast<uint32_t>(row) * hbytes + c16;
@@ -226,9 +237,9 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
     const uint32_t kofh = ATR ? static_cast<uint32_t>(st) * BK * hbytes : koff;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (4 * wave + q) * 1024), 16, dofw[q] + koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (4 * wave + q) * 1024), 16, dofh[q] + kofh,
+    for (int q = 0; q < QN; ++q) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (QN * wave + q) * 1024), 16, dofw[q] + koff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (QN * wave + q) * 1024), 16, dofh[q] + kofh,
                                                0, 0, 0);
     }
   };
@@ -240,7 +251,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   int fo[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) fo[kk] = 16 * ((2 * kk + (lane >> 5)) ^ sw);
-  const int offA = (wv * 128 + (lane & 31)) * ROWB, offB = kOpBytes + (wt * 64 + (lane & 31)) * ROWB;
+  const int offA = (wv * 128 + (lane & 31)) * ROWB, offB = kOpBytes + (wt * TW + (lane & 31)) * ROWB;
   // K-major token operand: ds_read_b64_tr_b16 hands lane i of each 16-lane block the
   // element i%4 of the 8-byte chunks addressed by source lanes i/4 + 4k (k < 4). Source
   // lane j of block b points at k-row k0 + j/4, columns 16*(b%2) + 4*(j%4) of the
@@ -252,7 +263,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
     const int x = (lane >> 2) & 3;   // = k-row % 4 of this lane's source row
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int chunk = 8 * wt + 4 * j + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+      const int chunk = (wt * TW) / 8 + 4 * j + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
       offBt[j] = kOpBytes + (8 * (lane >> 5) + x) * 512 + 16 * (chunk ^ (4 * x)) + 8 * (lane & 1);
     }
   }
@@ -310,56 +321,52 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   __builtin_amdgcn_s_waitcnt(kWaitStage);
   lm_barrier();
   fload(0, 0, 0);
-  // Per k-step and wave: 6 fragment reads (4 W, 2 hidden) and 8 MFMAs; the stage's
-  // 8 loads follow the first k-step's fragment reads, in two groups of 4 between its
-  // last MFMAs (1-2% faster than one load per MFMA with these 64-deep stages).
+  // Per k-step and wave: kRd fragment reads (4 vocab-role, NJ token-role, or 2 NJ when
+  // the token role takes two transpose reads per fragment) and 4 NJ MFMAs, one read per
+  // MFMA and the rest of the MFMAs after them. The stage's loads follow the first
+  // k-step's fragment reads in groups of 4 between its next MFMAs (with 8 waves, 1-2%
+  // faster than one load per MFMA with these 64-deep stages).
+  constexpr int kRd = 4 + (ATR ? 2 : 1) * NJ, kMf = 4 * NJ, kLdG = 2 * QN / 4;
+  constexpr int kRd0 = kRd - (ATR ? kLdG : 0);   // reads before the loads in the first k-step
+  static_assert(kRd <= kMf && kRd0 + kLdG <= kMf, "schedule");
+  auto sched_step = [&]() {
+#pragma unroll
+    for (int q = 0; q < kRd; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // a fragment read of the next k-step
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // an MFMA of this one
+    }
+    if constexpr (kMf > kRd) __builtin_amdgcn_sched_group_barrier(0x008, kMf - kRd, 0);
+  };
   for (int kb = 0; kb < nk; ++kb) {
     // Buffer (kb + 1) % 2 held stage kb - 1, whose reads all completed before the
     // last barrier; past the end the last stage is reloaded into it (nobody reads it).
-    // Fragment reads per k-step: 6 (4 vocab-role + 2 token-role), or 8 when the token
-    // role takes two transpose reads per fragment.
-    constexpr int kRd = ATR ? 8 : 6;
     issue(min(kb + 1, nk - 1), (kb + 1) & 1);
     fload(1, kb, 1);
     mfmas(0);
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
+    for (int q = 0; q < kRd0; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a fragment read of k-step 1
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of k-step 0
     }
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);  // half of the stage's loads
+    for (int q = 0; q < kLdG; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);  // 4 of the stage's loads
       if constexpr (ATR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
+    if constexpr (kMf > kRd0 + kLdG) __builtin_amdgcn_sched_group_barrier(0x008, kMf - kRd0 - kLdG, 0);
     fload(0, kb, 2);
     mfmas(1);
-#pragma unroll
-    for (int q = 0; q < kRd; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    }
-    if constexpr (!ATR) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    sched_step();
     fload(1, kb, 3);
     mfmas(0);
-#pragma unroll
-    for (int q = 0; q < kRd; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    }
-    if constexpr (!ATR) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    sched_step();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitStage);               // stage kb+1 landed
     lm_barrier();
     fload(0, min(kb + 1, nk - 1), 0);
     mfmas(1);
-#pragma unroll
-    for (int q = 0; q < kRd; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    }
-    if constexpr (!ATR) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    sched_step();
   }
   // Drain the trailing loads before any LDS reuse (the backward epilogue).
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -387,7 +394,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
     }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int n = m0 + wt * 64 + 32 * j + (lane & 31);
+      const int n = m0 + wt * TW + 32 * j + (lane & 31);
       float mx = kNegInf;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -452,7 +459,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
     // transpose_c the lane's 4 consecutive rows of a column are one 16-byte store.
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int n = m0 + wt * 64 + 32 * j + (lane & 31);
+      const int n = m0 + wt * TW + 32 * j + (lane & 31);
       if (n >= N) continue;
       if (transpose_c) {
 #pragma unroll
@@ -496,10 +503,10 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       __syncthreads();   // the pipeline's (or the previous half's) LDS reads are done
-      if ((wt >> 1) == h) {
+      if ((wt * TW) / 128 == h) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          const int tcol = (wt & 1) * 64 + 32 * j + (lane & 31);          // column within this half
+          const int tcol = (wt * TW) % 128 + 32 * j + (lane & 31);        // column within this half
           const int n = m0 + h * 128 + tcol;
           float cf = 0.f, l2 = 0.f;
           int64_t rel = -1;
@@ -585,7 +592,7 @@ __device__ __forceinline__ int lm_total_tiles(const LmTileArgs& a, int prod) {
 // per-tile barriers and atomic cost more than these early exits), and against a
 // persistent static split, 46.2 ms.
 template <int MODE, bool ATR = false, bool ECACHE = false>
-__global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(lm::WPE, lm::WPE)))
 lm_tile_kernel(LmTileArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int xcd = blockIdx.x % 8, i = blockIdx.x / 8;
