@@ -141,9 +141,8 @@ __device__ __forceinline__ void lm_barrier() {
 // through two stages of BK hidden columns.
 // ATR (kLmGemm): the token-role operand is stored K-major and its fragments are read
 // with ds_read_b64_tr_b16 (see below).
-// ECACHE (kLmFwd): the epilogue also stores the softmax terms (see there).
-// Tile p of product prod (kLmGemm; the loss-head modes have one), called by
-// lm_tile_kernel's work loop.
+// ECACHE (kLmFwd): the epilogue of model 0 also stores the softmax terms (see there).
+// Tile p of product prod (kLmGemm), or of model prod (kLmFwd), called by lm_tile_kernel.
 template <int MODE, bool ATR, bool ECACHE>
 __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, char* smem) {
   using namespace lm;
@@ -151,7 +150,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   // The product: the loss-head modes read rows of H elements of hidden (A) and W (B);
   // kLmGemm takes one of its (up to) two products.
   const void* opA = a.A;
-  const void* opB = a.B;
+  const void* opB = MODE == kLmFwd && prod == 1 ? a.B2 : a.B;
   int N = a.N, V = a.V, K = a.H, lda = a.H, ldb = a.H, ntt = a.ntt, nvt = a.nvt, gm = 1, vt0 = a.vt0;
   float* C = nullptr;
   int ldc = 0, accumulate = 0, transpose_c = 0, krows_a = 0;
@@ -412,7 +411,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
           ev[r] = hw_exp2(fmaf(acc[i][j][r], kLog2e, -ref));
           s += ev[r];
         }
-        if constexpr (ECACHE) {
+        if (ECACHE && prod == 0) {
           // Softmax cache: ecache[n][v] = f16(2^(x*log2e - ref)), token-major rows of lde
           // (vocab past V holds 0). The lane's 16 terms are vocab rows 8q + 4*half + 0..3
           // (q < 4) of this 32-row block; one v_permlane32_swap per register pair trades
@@ -439,7 +438,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
       }
       s += __shfl_xor(s, 32);
       if (n < N && any_v) {
-        if (half == 0) a.part[static_cast<int64_t>(n) * a.ldp + vw / kPart] = make_float2(m2, s);
+        if (half == 0) (prod ? a.part2 : a.part)[static_cast<int64_t>(n) * a.ldp + vw / kPart] = make_float2(m2, s);
         const int64_t rel = lm_id(a, n) - vw;
         if (rel >= 0 && rel < 128) {
           const int rr = static_cast<int>(rel) & 31, isel = static_cast<int>(rel) >> 5;
@@ -449,7 +448,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) val = (i == isel && r == rsel) ? acc[i][j][r] : val;
-          if (((rr >> 2) & 1) == half) a.tgt[n] = val;
+          if (((rr >> 2) & 1) == half) (prod ? a.tgt2 : a.tgt)[n] = val;
         }
       }
     }
@@ -596,6 +595,17 @@ __global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(l
 lm_tile_kernel(LmTileArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int xcd = blockIdx.x % 8, i = blockIdx.x / 8;
+  if constexpr (MODE == kLmFwd) {
+    // Both models' tiles of one (token, vocab) pair are consecutive items, so they run
+    // side by side on one XCD and read each hidden slab from its L2 once.
+    const int nm = a.n_model > 1 ? 2 : 1;
+    const int tt = lm_total_tiles<MODE>(a, 0) * nm;
+    const int per = (tt + 7) / 8;
+    const int p = xcd * per + i;
+    if (i >= per || p >= tt) return;
+    lm_tile<MODE, ATR, ECACHE>(a, p % nm, p / nm, smem);
+    return;
+  }
   const int t0 = lm_total_tiles<MODE>(a, 0);
   const int t1 = (MODE == kLmGemm && a.n_gemm > 1) ? lm_total_tiles<MODE>(a, 1) : 0;
   const int per0 = (t0 + 7) / 8, per1 = (t1 + 7) / 8;
@@ -870,7 +880,7 @@ hipError_t launch_tiles_mode(const LmTileArgs& a, int max_tiles, hipStream_t st)
 
 hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {
   LmTileArgs a = args;
-  const int grid = a.ntt * a.nvt;   // tiles at the largest token count
+  const int grid = a.ntt * a.nvt * (mode == kLmFwd && a.n_model > 1 ? 2 : 1);   // tiles at the largest token count
   if (grid <= 0) return hipSuccess;
   if (mode == kLmFwd)
     return a.ecache ? launch_tiles_mode<kLmFwd, true>(a, grid, st) : launch_tiles_mode<kLmFwd>(a, grid, st);

@@ -27,10 +27,15 @@ struct LmTileArgs {
   int n_gemm;           // kLmGemm: products in gemm[] (1 or 2)
   const void* ids;      // [N] target ids
   int ids_i64;
-  // kLmFwd
+  // kLmFwd (model 0: B, part, tgt, ecache; with n_model = 2 also model 1: B2, part2,
+  // tgt2, in the same launch, its tiles interleaved with model 0's)
   float2* part;         // [N, ldp]: per kLmPart vocab entries (max * log2e, sum 2^(x*log2e - max*log2e))
   int ldp;              // ceil(V / kLmPart)
   float* tgt;           // [N] target logit
+  int n_model;          // 1 or 2
+  const void* B2;       // [V, H] bf16: model 1's weight
+  float2* part2;
+  float* tgt2;
   uint16_t* ecache;     // or nullptr: [N, lde] f16 softmax terms 2^(x*log2e - ref) of the
   int64_t lde;          //   partial's reference ref (lde % 64 == 0, >= V; 0 past V)
   // kLmBwd

@@ -142,6 +142,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_live = take(4 * N), o_cidx = take(4 * N), o_idsc = take(4 * N), o_cnt = take(4);
   const size_t o_hid = take(2 * static_cast<size_t>(N) * H);
   const size_t o_part = take(8 * static_cast<size_t>(N) * npart);
+  const size_t o_part2 = ref ? take(8 * static_cast<size_t>(N) * npart) : 0;
   const size_t o_tgt = take(4 * N), o_l2 = take(4 * N), o_rtgt = take(4 * N), o_rl2 = take(4 * N), o_coef = take(4 * N);
   // Row stride, in tokens, of the transposed operands (hidden^T, D^T): a multiple of the
   // 64-deep pipeline stage, and off multiples of 256 (a 2^k-byte stride puts the rows
@@ -232,25 +233,31 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   ta.ids_i64 = 0;
   ta.part = part;
   ta.ldp = npart;
-  LmReduceArgs rd{part, N, cnt, npart, npart, nullptr};
-  const int nmodel = ref ? 2 : 1;
-  for (int k = 0; k < nmodel; ++k) {
-    // The reference model first, so the policy's partials stay in `part` for the
-    // softmax cache's pass.
-    const int m = nmodel - 1 - k;
-    ta.B = m == 0 ? a->weight : a->ref_weight;
-    ta.tgt = F(m == 0 ? o_tgt : o_rtgt);
-    ta.ecache = m == 0 && cached ? static_cast<uint16_t*>(ctx->lm_dbuf) : nullptr;
-    ta.lde = ldv;
-    // pcp_profile_start timing: the policy forward tiles when the backward is chunked,
-    // the products launch (below) when it reads the softmax cache.
-    const bool timed = m == 0 && !cached && ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
+  // Both models in one launch (their tiles interleaved, so each hidden slab is read once
+  // for both), then one merge per model.
+  ta.B = a->weight;
+  ta.tgt = F(o_tgt);
+  ta.ecache = cached ? static_cast<uint16_t*>(ctx->lm_dbuf) : nullptr;
+  ta.lde = ldv;
+  ta.n_model = ref ? 2 : 1;
+  if (ref) {
+    ta.B2 = a->ref_weight;
+    ta.tgt2 = F(o_rtgt);
+    ta.part2 = reinterpret_cast<float2*>(sp + o_part2);
+  }
+  {
+    // pcp_profile_start timing: the forward launch when the backward is chunked, the
+    // products launch (below) when it reads the softmax cache.
+    const bool timed = !cached && ctx->prof_on && ctx->prof_used < static_cast<int>(ctx->prof_start.size());
     if (timed && (e = hipEventRecord(ctx->prof_start[ctx->prof_used], st)) != hipSuccess)
       return hip_fail(ctx, e, "hipEventRecord");
     if ((e = launch_lm_tiles(kLmFwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head forward tiles");
     if (timed && (e = hipEventRecord(ctx->prof_stop[ctx->prof_used++], st)) != hipSuccess)
       return hip_fail(ctx, e, "hipEventRecord");
-    rd.lse2 = F(m == 0 ? o_l2 : o_rl2);
+  }
+  for (int m = 0; m < (ref ? 2 : 1); ++m) {
+    const LmReduceArgs rd{m == 0 ? part : reinterpret_cast<float2*>(sp + o_part2), N, cnt, npart, npart,
+                          F(m == 0 ? o_l2 : o_rl2)};
     if ((e = launch_lm_reduce(rd, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head reduce");
   }
 
