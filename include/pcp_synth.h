@@ -36,6 +36,18 @@ int pcp_synth_logits(void* policy, void* ref, int64_t n, int dtype, float std_p,
 int pcp_synth_sample_tokens(const void* logits, int dtype, int64_t nrows, int64_t vocab,
                             uint64_t seed, int64_t* ids, void* stream);
 
+/* Target ids for the fused LM-head configuration (config 5): one token per hidden row
+ * drawn from softmax(hidden[row, :] . weight^T) by Gumbel-max, as
+ * pcp_synth_sample_tokens draws from given logits. The logits are formed in f32 with the
+ * library's bf16 MFMA tile kernel, `chunk` rows at a time in ctx's work buffer
+ * (chunk * vocab * 4 bytes; chunk 0 => 1024), and chunk k is drawn with seed + k.
+ * hidden [n, hidden_dim] and weight [vocab, hidden_dim] bf16, row-major and 16-byte
+ * aligned; hidden_dim a positive multiple of 64. ids is int64 [n]. */
+struct pcp_ctx;
+int pcp_synth_lmhead_tokens(struct pcp_ctx* ctx, const void* hidden, const void* weight, int64_t n,
+                            int64_t hidden_dim, int64_t vocab, int64_t chunk, uint64_t seed, int64_t* ids,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

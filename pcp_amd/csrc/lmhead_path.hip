@@ -31,6 +31,7 @@
 #include "grpo_launch.hpp"
 #include "lmhead_launch.hpp"
 #include "pcp_grpo.h"
+#include "pcp_synth.h"
 
 namespace pcp {
 namespace {
@@ -446,6 +447,47 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
 using namespace pcp;
 
 extern "C" {
+
+int pcp_synth_lmhead_tokens(pcp_ctx* ctx, const void* hidden, const void* weight, int64_t n, int64_t hidden_dim,
+                            int64_t vocab, int64_t chunk, uint64_t seed, int64_t* ids, void* stream) {
+  using namespace pcp;
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  if (!hidden || !weight || !ids || n < 0 || n > (int64_t{1} << 28) || vocab < 1 || vocab > (1 << 30) ||
+      hidden_dim < 64 || hidden_dim % 64 != 0 || hidden_dim > (1 << 20) || chunk < 0 ||
+      ((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(weight)) & 15u))
+    return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_synth_lmhead_tokens: bad arguments");
+  if (n == 0) return PCP_OK;
+  const int64_t rows = chunk > 0 ? (chunk < n ? chunk : n) : (n < 1024 ? n : 1024);
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  int rc = ensure_scratch(ctx, 4 * static_cast<size_t>(rows) * vocab);
+  if (rc != PCP_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* logits = static_cast<float*>(ctx->scratch);
+  for (int64_t n0 = 0, k = 0; n0 < n; n0 += rows, ++k) {
+    const int64_t m = n - n0 < rows ? n - n0 : rows;
+    // logits[t][v] = sum_h hidden[n0 + t][h] * weight[v][h]: token rows in the product's
+    // row role, vocabulary in its column role, both operands K-contiguous.
+    LmTileArgs::Gemm g;
+    std::memset(&g, 0, sizeof(g));
+    g.B = static_cast<const uint16_t*>(hidden) + n0 * hidden_dim;
+    g.ldb = static_cast<int>(hidden_dim);
+    g.V = static_cast<int>(m);
+    g.A = weight;
+    g.lda = static_cast<int>(hidden_dim);
+    g.N = static_cast<int>(vocab);
+    g.K = static_cast<int>(hidden_dim);
+    g.nvt = static_cast<int>((m + kLmTileV - 1) / kLmTileV);
+    g.ntt = static_cast<int>((vocab + kLmTileT - 1) / kLmTileT);
+    g.C = logits;
+    g.ldc = static_cast<int>(vocab);
+    if ((e = launch_lm_gemms(&g, 1, false, st)) != hipSuccess) return hip_fail(ctx, e, "logits tiles");
+    rc = pcp_synth_sample_tokens(logits, PCP_F32, m, vocab, seed + static_cast<uint64_t>(k), ids + n0, stream);
+    if (rc != PCP_OK) return rc;
+  }
+  return PCP_OK;
+}
+
 
 void pcp_lmhead_args_init(pcp_lmhead_args* a) {
   if (!a) return;

@@ -127,24 +127,22 @@ def make_lmhead_inputs(cfg: LmheadConfig, device="cuda"):
             "rewards": torch.from_numpy(rewards).to(device), "old_shift": old_shift, "lengths": lengths}
 
 
-def sample_lmhead_ids(hidden, weight, seed: int, chunk: int = 1024):
-    """One token per hidden row drawn from softmax(hidden W^T) with the library's
-    Gumbel-max sampler (pcp_synth_sample_tokens, as the logits configurations), over
-    token chunks of bf16 logits formed by torch for the draw only (seed + chunk index
-    keeps the noise of every chunk distinct). Returns int64 [N] on the device."""
+def sample_lmhead_ids(hidden, weight, seed: int, chunk: int = 1024, ctx=None):
+    """One token per hidden row drawn from softmax(hidden W^T) by Gumbel-max
+    (pcp_synth_lmhead_tokens: f32 logits from the library's MFMA tile kernel, `chunk`
+    rows at a time, chunk k drawn with seed + k, as pcp_synth_sample_tokens draws for
+    the logits configurations). Returns int64 [N] on the device."""
     import torch
-    import torch.nn.functional as F
 
-    N = hidden.shape[0]
+    from .grpo import default_context
+
+    ctx = ctx or default_context(hidden.device.index or 0)
+    N, H = hidden.shape
     V = weight.shape[0]
     ids = torch.empty(N, dtype=torch.int64, device=hidden.device)
     stream = torch.cuda.current_stream().cuda_stream or None
-    for k, n0 in enumerate(range(0, N, chunk)):
-        logits = F.linear(hidden[n0:n0 + chunk], weight).contiguous()
-        n = logits.shape[0]
-        check(lib().pcp_synth_sample_tokens(logits.data_ptr(), int(DType.bf16), n, V, seed + k,
-                                            ids[n0:n0 + n].data_ptr(), stream))
-        del logits
+    check(lib().pcp_synth_lmhead_tokens(ctx.handle, hidden.data_ptr(), weight.data_ptr(), N, H, V, chunk, seed,
+                                        ids.data_ptr(), stream), ctx.handle)
     return ids
 
 

@@ -437,6 +437,38 @@ def test_lmhead_graph_capture_replays(chunk):
     ctx.sync()
 
 
+def test_synth_lmhead_tokens_gumbel_argmax():
+    """pcp_synth_lmhead_tokens (config 5's target ids) draws argmax_v(logit + g) per row
+    with g = -log(-log u), u from Philox(seed + chunk index, tag 3, row-in-chunk * V + v)
+    as pcp_synth_sample_tokens draws. With the noise recomputed on the host (the Philox
+    is pinned by known answers in test_abi.py) and the logits exact in float64, every
+    drawn id scores within 1e-4 of its row's best (the device forms f32 logits and f32
+    logarithms); chunks of 16 over 40 rows cover the per-chunk seeds."""
+    rng = np.random.default_rng(91)
+    N, H, V, seed, chunk = 40, 128, 700, 1234, 16
+    hb = bf16_bits(rng, (N, H), 1.0)
+    wb = bf16_bits(rng, (V, H), 0.25)
+    ids = synth.sample_lmhead_ids(dev(hb), dev(wb), seed, chunk=chunk).cpu().numpy()
+    assert ids.shape == (N,) and ids.min() >= 0 and ids.max() < V
+    L = orc.lmhead_logits(hb, wb)
+    scale = np.float32(2.3283064365386963e-10)
+    for r in range(N):
+        k, rl = divmod(r, chunk)
+        sk = seed + k
+        flat = rl * V + np.arange(V)
+        u = np.empty(V, np.uint32)
+        for q in range(flat[0] // 4, flat[-1] // 4 + 1):
+            words = synth.philox([q & 0xFFFFFFFF, q >> 32, 3, 0], [sk & 0xFFFFFFFF, sk >> 32])
+            for j in range(4):
+                v = 4 * q + j - rl * V
+                if 0 <= v < V:
+                    u[v] = words[j]
+        uf = (u.astype(np.float32) + np.float32(0.5)) * scale
+        score = L[r] - np.log(-np.log(uf.astype(np.float64)))
+        assert score[ids[r]] >= score.max() - 1e-4 * max(1.0, abs(score.max())), (r, ids[r], int(score.argmax()))
+    assert len(set(ids.tolist())) > N // 2
+
+
 def test_lmhead_errors():
     c = make_case(1, 16, 64, 300, 1, seed=3, lengths=[16])
     old = np.zeros((1, 16), np.float32)
