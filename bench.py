@@ -497,6 +497,53 @@ def bench_b64(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def bench_hbm_roof(args) -> None:
+    """The practical HBM roof (pcp_hbm_stream): read-only, write-only, copy and the
+    row kernel's 2-read : 1-write mix over --roof-gib GiB buffers, plain and with
+    nontemporal loads and stores. A step is one stream of each kind; `value` is the mix
+    (the headline kernel's access pattern) in GB/s of bytes moved."""
+    import torch
+
+    from pcp_amd._lib import check, lib
+    from pcp_amd.grpo import default_context
+
+    dev = torch.device("cuda:0")
+    nbytes = int(args.roof_gib * (1 << 30)) // 16 * 16
+    a = torch.full((nbytes // 4,), 7, dtype=torch.int32, device=dev)
+    b = torch.full_like(a, 3)
+    c = torch.empty_like(a)
+    ctx = default_context(0)
+    stream = torch.cuda.current_stream().cuda_stream or None
+    moved = {0: 1, 1: 1, 2: 2, 3: 3}
+    names = {0: "read", 1: "write", 2: "copy", 3: "mix2r1w"}
+    res = {}
+    for nt in (0, 1):
+        for kind in range(4):
+            call = lambda: check(lib().pcp_hbm_stream(ctx.handle, kind, nt, a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                                                      nbytes, stream), ctx.handle)
+            for _ in range(args.warmup):
+                call()
+            torch.cuda.synchronize()
+            ms, _ = _timed_calls(ctx, args.steps, call)
+            res[names[kind] + ("_nt" if nt else "")] = {"kernel_ms": ms, "gbs": moved[kind] * nbytes / (ms / 1e3) / 1e9}
+    if not torch.equal(c, a ^ b):
+        raise SystemExit("mix stream result differs")
+    mix = max(res["mix2r1w"]["gbs"], res["mix2r1w_nt"]["gbs"])
+    best = "mix2r1w_nt" if res["mix2r1w_nt"]["gbs"] >= res["mix2r1w"]["gbs"] else "mix2r1w"
+    line = {
+        "metric": "HBM stream bandwidth, 2 reads : 1 write (the row kernel's mix)", "value": mix * 1e9,
+        "unit": "bytes/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": sum(r["kernel_ms"] for r in res.values()), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u32", "data": "constant device buffers",
+        "config": {"workload": f"pcp_hbm_stream over {nbytes} bytes per buffer", "bytes": nbytes},
+        "roofline": {"bound": "hbm", "achieved": mix, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": mix / HBM_PEAK_GBS,
+                     "traffic": None, "kernel": f"hbm_stream_kernel ({best})", "kernel_ms": res[best]["kernel_ms"],
+                     "algorithmic_bytes": 3 * nbytes},
+        "streams": res,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def bench_logprob(args) -> None:
     """Forward-only log-probs (pcp_grpo_logprob_fwd: log-softmax + sampled-token gather
     of the policy rows, and of the reference rows unless --policy-only) over the
@@ -657,11 +704,13 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--workload", choices=["loss", "logprob", "execute", "nesterov", "sample", "b64"], default="loss",
+    ap.add_argument("--workload", choices=["loss", "logprob", "execute", "nesterov", "sample", "b64", "hbm_roof"],
+                    default="loss",
                     help="loss: the GRPO loss head of --config (the headline metric); logprob: forward-only "
                          "log-probs of --config's rows; execute: the host-bytes boundary (PCIe-inclusive); nesterov: the "
                          "optimizer step over Qwen2.5-0.5B's parameters; sample: the rollout sampler; "
-                         "b64: the UPDATE_WEIGHTS payload codec")
+                         "b64: the UPDATE_WEIGHTS payload codec; hbm_roof: the practical HBM roof (stream probes)")
+    ap.add_argument("--roof-gib", type=float, default=4.0, help="hbm_roof workload: bytes per buffer, in GiB")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
     ap.add_argument("--no-zero-fill", action="store_true",
@@ -708,6 +757,9 @@ def main() -> None:
         return
     if args.workload == "b64":
         bench_b64(args)
+        return
+    if args.workload == "hbm_roof":
+        bench_hbm_roof(args)
         return
     if args.workload == "logprob":
         bench_logprob(args)

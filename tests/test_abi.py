@@ -429,3 +429,18 @@ def test_weights_and_base64_errors_without_device(tmp_path):
     n = ctypes.c_int64()
     assert L.pcp_base64_decode(None, 0x1000, 6, 0x2000, ctypes.byref(n), None) == -1
     assert "multiple of 4" in L.pcp_last_error(None).decode()
+
+
+def test_hbm_stream_argument_errors_without_device():
+    """pcp_hbm_stream rejects a bad kind, a size off 16 bytes, NULL or misaligned buffers
+    before any device work (the context check comes after them)."""
+    L = _lib.lib()
+    assert L.pcp_hbm_stream(None, 4, 0, 0x1000, 0x2000, 0x3000, 1 << 20, None) == -1
+    assert "kind" in L.pcp_last_error(None).decode()
+    assert L.pcp_hbm_stream(None, 2, 0, 0x1000, None, 0x3000, 1000, None) == -1
+    assert L.pcp_hbm_stream(None, 3, 1, 0x1000, None, 0x3000, 1 << 20, None) == -1
+    assert "NULL" in L.pcp_last_error(None).decode()
+    assert L.pcp_hbm_stream(None, 2, 0, 0x1008, None, 0x3000, 1 << 20, None) == -1
+    assert L.pcp_hbm_stream(None, 0, 0, 0x1000, None, None, 1 << 20, None) == -1
+    assert L.pcp_hbm_stream(None, 1, 0, None, None, 0x3000, 1 << 20, None) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()
