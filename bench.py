@@ -500,8 +500,9 @@ def bench_b64(args) -> None:
 def bench_hbm_roof(args) -> None:
     """The practical HBM roof (pcp_hbm_stream): read-only, write-only, copy and the
     row kernel's 2-read : 1-write mix over --roof-gib GiB buffers, plain and with
-    nontemporal loads and stores. A step is one stream of each kind; `value` is the mix
-    (the headline kernel's access pattern) in GB/s of bytes moved."""
+    nontemporal loads and stores, at 1 and 4 vectors per lane; each kind's best shape is
+    its roof. `value` is the mix (the headline kernel's access pattern) in GB/s of bytes
+    moved."""
     import torch
 
     from pcp_amd._lib import check, lib
@@ -517,19 +518,23 @@ def bench_hbm_roof(args) -> None:
     moved = {0: 1, 1: 1, 2: 2, 3: 3}
     names = {0: "read", 1: "write", 2: "copy", 3: "mix2r1w"}
     res = {}
-    for nt in (0, 1):
-        for kind in range(4):
-            call = lambda: check(lib().pcp_hbm_stream(ctx.handle, kind, nt, a.data_ptr(), b.data_ptr(), c.data_ptr(),
-                                                      nbytes, stream), ctx.handle)
-            for _ in range(args.warmup):
-                call()
-            torch.cuda.synchronize()
-            ms, _ = _timed_calls(ctx, args.steps, call)
-            res[names[kind] + ("_nt" if nt else "")] = {"kernel_ms": ms, "gbs": moved[kind] * nbytes / (ms / 1e3) / 1e9}
+    for vpt in (1, 4):
+        for nt in (0, 1):
+            for kind in range(4):
+                call = lambda: check(lib().pcp_hbm_stream(ctx.handle, kind, nt, vpt, a.data_ptr(), b.data_ptr(),
+                                                          c.data_ptr(), nbytes, stream), ctx.handle)
+                for _ in range(args.warmup):
+                    call()
+                torch.cuda.synchronize()
+                ms, _ = _timed_calls(ctx, args.steps, call)
+                res[f"{names[kind]}{'_nt' if nt else ''}_v{vpt}"] = {"kernel_ms": ms,
+                                                                    "gbs": moved[kind] * nbytes / (ms / 1e3) / 1e9}
     if not torch.equal(c, a ^ b):
         raise SystemExit("mix stream result differs")
-    mix = max(res["mix2r1w"]["gbs"], res["mix2r1w_nt"]["gbs"])
-    best = "mix2r1w_nt" if res["mix2r1w_nt"]["gbs"] >= res["mix2r1w"]["gbs"] else "mix2r1w"
+    roof = {n: max((v for k, v in res.items() if k.split("_")[0] == n), key=lambda v: v["gbs"])["gbs"]
+            for n in names.values()}
+    best = max((k for k in res if k.startswith("mix2r1w")), key=lambda k: res[k]["gbs"])
+    mix = res[best]["gbs"]
     line = {
         "metric": "HBM stream bandwidth, 2 reads : 1 write (the row kernel's mix)", "value": mix * 1e9,
         "unit": "bytes/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -540,6 +545,7 @@ def bench_hbm_roof(args) -> None:
                      "traffic": None, "kernel": f"hbm_stream_kernel ({best})", "kernel_ms": res[best]["kernel_ms"],
                      "algorithmic_bytes": 3 * nbytes},
         "streams": res,
+        "roof_gbs": roof,
     }
     print(json.dumps(line), flush=True)
 

@@ -23,10 +23,12 @@ struct pcp_ctx;
  *   kind 1 write: writes c
  *   kind 2 copy:  c = a
  *   kind 3 mix:   c = a ^ b                    (two reads per write)
- * nontemporal != 0 uses nontemporal loads and stores. Asynchronous on `stream`; timed
- * by pcp_profile_start / pcp_profile_stop like the other entry points. */
-int pcp_hbm_stream(struct pcp_ctx* ctx, int kind, int nontemporal, const void* a, const void* b, void* c,
-                   int64_t bytes, void* stream);
+ * nontemporal != 0 uses nontemporal loads and stores. The grid is flat: each 256-lane
+ * workgroup moves 256 x vectors_per_lane (1, 2, 4 or 8) 16-byte vectors. Asynchronous
+ * on `stream`; timed by pcp_profile_start / pcp_profile_stop like the other entry
+ * points. */
+int pcp_hbm_stream(struct pcp_ctx* ctx, int kind, int nontemporal, int vectors_per_lane, const void* a,
+                   const void* b, void* c, int64_t bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -9,8 +9,10 @@
 //                                             + reference logits in, dlogits out)
 //
 // Each kind comes plain or with nontemporal loads and stores (the streaming hint the
-// row kernel uses). 16-byte vectors, eight per thread per iteration, grid-stride over a
-// grid of 32 workgroups per CU (8 per CU was slower).
+// row kernel uses), over a flat grid: each 256-lane workgroup moves 256 x VPT 16-byte
+// vectors, VPT = 1, 2, 4 or 8 per lane. One vector per lane writes fastest (6.8 TB/s
+// against 5.6-5.8 TB/s for a grid of 32 workgroups per CU striding 8 per lane), so the
+// benchmark reports the best shape of each kind.
 
 #include <hip/hip_runtime.h>
 
@@ -25,7 +27,6 @@ namespace pcp {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kVec = 8;   // 16-byte vectors per thread per iteration (4 and 16 measured slower)
 
 template <bool NT>
 __device__ __forceinline__ u32x4 ld(const u32x4* p) {
@@ -38,31 +39,30 @@ __device__ __forceinline__ void st(u32x4* p, u32x4 v) {
   else *p = v;
 }
 
-// KIND: 0 read, 1 write, 2 copy, 3 mix.
-template <int KIND, bool NT>
+// KIND: 0 read, 1 write, 2 copy, 3 mix. Workgroup w moves vectors [w * 256 * VPT, ...),
+// lane t the ones at t + 256 k (coalesced per instruction).
+template <int KIND, bool NT, int VPT>
 __global__ void __launch_bounds__(kThreads) hbm_stream_kernel(const u32x4* a, const u32x4* b, u32x4* c, int64_t n16,
                                                               u32x4* sink) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVec;
-  u32x4 acc = {0u, 0u, 0u, 0u};
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kVec + threadIdx.x; base < n16; base += stride) {
-    u32x4 x[kVec], y[kVec];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * VPT + threadIdx.x;
+  u32x4 x[VPT], y[VPT];
 #pragma unroll
-    for (int k = 0; k < kVec; ++k) {
-      const int64_t i = base + k * kThreads;
-      if (i < n16) {
-        if constexpr (KIND == 0 || KIND == 2 || KIND == 3) x[k] = ld<NT>(a + i);
-        if constexpr (KIND == 3) y[k] = ld<NT>(b + i);
-      }
+  for (int k = 0; k < VPT; ++k) {
+    const int64_t i = base + k * kThreads;
+    if (i < n16) {
+      if constexpr (KIND == 0 || KIND == 2 || KIND == 3) x[k] = ld<NT>(a + i);
+      if constexpr (KIND == 3) y[k] = ld<NT>(b + i);
     }
+  }
+  u32x4 acc = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int k = 0; k < kVec; ++k) {
-      const int64_t i = base + k * kThreads;
-      if (i < n16) {
-        if constexpr (KIND == 0) acc ^= x[k];
-        if constexpr (KIND == 1) st<NT>(c + i, u32x4{static_cast<uint32_t>(i), 1u, 2u, 3u});
-        if constexpr (KIND == 2) st<NT>(c + i, x[k]);
-        if constexpr (KIND == 3) st<NT>(c + i, x[k] ^ y[k]);
-      }
+  for (int k = 0; k < VPT; ++k) {
+    const int64_t i = base + k * kThreads;
+    if (i < n16) {
+      if constexpr (KIND == 0) acc ^= x[k];
+      if constexpr (KIND == 1) st<NT>(c + i, u32x4{static_cast<uint32_t>(i), 1u, 2u, 3u});
+      if constexpr (KIND == 2) st<NT>(c + i, x[k]);
+      if constexpr (KIND == 3) st<NT>(c + i, x[k] ^ y[k]);
     }
   }
   // The read kernel keeps its loads by a store that only an all-ones XOR would make.
@@ -70,21 +70,35 @@ __global__ void __launch_bounds__(kThreads) hbm_stream_kernel(const u32x4* a, co
     if (acc[0] == 0xFFFFFFFFu && acc[1] == 0xFFFFFFFFu && acc[2] == 0xFFFFFFFFu && acc[3] == 0xFFFFFFFFu) *sink = acc;
 }
 
-template <int KIND, bool NT>
-hipError_t launch(const void* a, const void* b, void* c, int64_t n16, unsigned grid, hipStream_t st) {
-  hbm_stream_kernel<KIND, NT><<<grid, kThreads, 0, st>>>(static_cast<const u32x4*>(a), static_cast<const u32x4*>(b),
-                                                         static_cast<u32x4*>(c), n16, static_cast<u32x4*>(c));
+template <int KIND, bool NT, int VPT>
+hipError_t launch(const void* a, const void* b, void* c, int64_t n16, hipStream_t st) {
+  const int64_t grid = (n16 + kThreads * VPT - 1) / (kThreads * VPT);
+  hbm_stream_kernel<KIND, NT, VPT><<<dim3(static_cast<unsigned>(grid)), kThreads, 0, st>>>(
+      static_cast<const u32x4*>(a), static_cast<const u32x4*>(b), static_cast<u32x4*>(c), n16, static_cast<u32x4*>(c));
   return hipGetLastError();
+}
+
+template <int KIND, bool NT>
+hipError_t launch_vpt(int vpt, const void* a, const void* b, void* c, int64_t n16, hipStream_t st) {
+  switch (vpt) {
+    case 1: return launch<KIND, NT, 1>(a, b, c, n16, st);
+    case 2: return launch<KIND, NT, 2>(a, b, c, n16, st);
+    case 4: return launch<KIND, NT, 4>(a, b, c, n16, st);
+    default: return launch<KIND, NT, 8>(a, b, c, n16, st);
+  }
 }
 
 }  // namespace
 }  // namespace pcp
 
-extern "C" int pcp_hbm_stream(pcp_ctx* ctx, int kind, int nontemporal, const void* a, const void* b, void* c,
-                              int64_t bytes, void* stream) {
+extern "C" int pcp_hbm_stream(pcp_ctx* ctx, int kind, int nontemporal, int vectors_per_lane, const void* a,
+                              const void* b, void* c, int64_t bytes, void* stream) {
   using namespace pcp;
-  if (kind < 0 || kind > 3 || bytes < 16 || bytes % 16 != 0)
+  if (kind < 0 || kind > 3 || bytes < 16 || bytes % 16 != 0 || bytes / 16 > (int64_t{1} << 38))
     return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_hbm_stream: kind must be 0..3 and bytes a positive multiple of 16");
+  const int vpt = vectors_per_lane;
+  if (vpt != 1 && vpt != 2 && vpt != 4 && vpt != 8)
+    return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_hbm_stream: vectors_per_lane must be 1, 2, 4 or 8");
   const bool need_a = kind != 1, need_b = kind == 3, need_c = kind != 0;
   if ((need_a && !a) || (need_b && !b) || (need_c && !c) || (kind == 0 && !c) ||
       ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c)) & 15u))
@@ -92,24 +106,18 @@ extern "C" int pcp_hbm_stream(pcp_ctx* ctx, int kind, int nontemporal, const voi
   if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                              hipSuccess)
-    cus = 256;
   const int64_t n16 = bytes / 16;
-  const int64_t want = (n16 + kThreads * kVec - 1) / (kThreads * kVec);
-  const unsigned grid = static_cast<unsigned>(want < 32 * cus ? want : 32 * cus);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool timed = prof_begin(ctx, st);
   switch (kind * 2 + (nontemporal ? 1 : 0)) {
-    case 0: e = launch<0, false>(a, b, c, n16, grid, st); break;
-    case 1: e = launch<0, true>(a, b, c, n16, grid, st); break;
-    case 2: e = launch<1, false>(a, b, c, n16, grid, st); break;
-    case 3: e = launch<1, true>(a, b, c, n16, grid, st); break;
-    case 4: e = launch<2, false>(a, b, c, n16, grid, st); break;
-    case 5: e = launch<2, true>(a, b, c, n16, grid, st); break;
-    case 6: e = launch<3, false>(a, b, c, n16, grid, st); break;
-    default: e = launch<3, true>(a, b, c, n16, grid, st); break;
+    case 0: e = launch_vpt<0, false>(vpt, a, b, c, n16, st); break;
+    case 1: e = launch_vpt<0, true>(vpt, a, b, c, n16, st); break;
+    case 2: e = launch_vpt<1, false>(vpt, a, b, c, n16, st); break;
+    case 3: e = launch_vpt<1, true>(vpt, a, b, c, n16, st); break;
+    case 4: e = launch_vpt<2, false>(vpt, a, b, c, n16, st); break;
+    case 5: e = launch_vpt<2, true>(vpt, a, b, c, n16, st); break;
+    case 6: e = launch_vpt<3, false>(vpt, a, b, c, n16, st); break;
+    default: e = launch_vpt<3, true>(vpt, a, b, c, n16, st); break;
   }
   prof_end(ctx, st, timed);
   if (e != hipSuccess) return hip_fail(ctx, e, "pcp_hbm_stream launch");

@@ -432,15 +432,17 @@ def test_weights_and_base64_errors_without_device(tmp_path):
 
 
 def test_hbm_stream_argument_errors_without_device():
-    """pcp_hbm_stream rejects a bad kind, a size off 16 bytes, NULL or misaligned buffers
-    before any device work (the context check comes after them)."""
+    """pcp_hbm_stream rejects a bad kind or shape, a size off 16 bytes, NULL or misaligned
+    buffers before any device work (the context check comes after them)."""
     L = _lib.lib()
-    assert L.pcp_hbm_stream(None, 4, 0, 0x1000, 0x2000, 0x3000, 1 << 20, None) == -1
+    assert L.pcp_hbm_stream(None, 4, 0, 1, 0x1000, 0x2000, 0x3000, 1 << 20, None) == -1
     assert "kind" in L.pcp_last_error(None).decode()
-    assert L.pcp_hbm_stream(None, 2, 0, 0x1000, None, 0x3000, 1000, None) == -1
-    assert L.pcp_hbm_stream(None, 3, 1, 0x1000, None, 0x3000, 1 << 20, None) == -1
+    assert L.pcp_hbm_stream(None, 2, 0, 3, 0x1000, None, 0x3000, 1 << 20, None) == -1
+    assert "vectors_per_lane" in L.pcp_last_error(None).decode()
+    assert L.pcp_hbm_stream(None, 2, 0, 1, 0x1000, None, 0x3000, 1000, None) == -1
+    assert L.pcp_hbm_stream(None, 3, 1, 1, 0x1000, None, 0x3000, 1 << 20, None) == -1
     assert "NULL" in L.pcp_last_error(None).decode()
-    assert L.pcp_hbm_stream(None, 2, 0, 0x1008, None, 0x3000, 1 << 20, None) == -1
-    assert L.pcp_hbm_stream(None, 0, 0, 0x1000, None, None, 1 << 20, None) == -1
-    assert L.pcp_hbm_stream(None, 1, 0, None, None, 0x3000, 1 << 20, None) == -1
+    assert L.pcp_hbm_stream(None, 2, 0, 1, 0x1008, None, 0x3000, 1 << 20, None) == -1
+    assert L.pcp_hbm_stream(None, 0, 0, 1, 0x1000, None, None, 1 << 20, None) == -1
+    assert L.pcp_hbm_stream(None, 1, 0, 8, None, None, 0x3000, 1 << 20, None) == -1
     assert "context is NULL" in L.pcp_last_error(None).decode()
