@@ -284,6 +284,11 @@ int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
  * vocab_chunk, PCP_FLAG_EXACT_BF16, or a backward workspace above 16 GiB, the backward
  * recomputes the logit tiles per vocab chunk instead (dlogits = the f32 value rounded
  * once), in memory bounded by the chunk.
+ * The live-token count never leaves the device: with PCP_FLAG_ASYNC the call only
+ * enqueues work, and it can be captured in a HIP graph. A captured graph uses the
+ * context's work buffers as they were at capture: make one uncaptured call of the same
+ * (or larger) sizes first, and re-capture after any call on the context that needed
+ * larger buffers (growing them frees the old ones).
  */
 typedef struct pcp_lmhead_args {
   int64_t n_seq;              /* sequences                                                */
