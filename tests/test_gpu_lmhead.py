@@ -645,8 +645,35 @@ def test_lmhead_qwen_vocab_vs_oracle():
 
 # ---- configuration 5 at full size against torch fp32 ------------------------------------------
 
-def _torch_reference(inp, coef=None, chunk=2048):
-    """fp32 logp / lse per token, and with coef the gradients and their bounds."""
+def _clip_kl_coef(lp, lr, old, adv, mask, cfg, lse):
+    """Per-token clip + KL coefficients c from reference log-probs lp / lr (float64 [N]),
+    formed by the oracle: the two-entry row [x, 0] with x = -log(expm1(-lp)) has
+    log-softmax lp at its first entry, so oracle_grpo_rows on such rows (float64
+    storage) computes c exactly as on the full rows. Also each token's coef_floor, what
+    the 1e-5 * max(1, |lse|) log-prob bar allows in c."""
+    S, T = mask.shape
+    w = mask.reshape(-1).astype(np.float32)
+    live = w != 0
+    lpd = np.minimum(np.where(live, lp, -1.0), -1e-30)
+    lrd = np.minimum(np.where(live, lr, -1.0), -1e-30)
+    rows = lambda v: np.ascontiguousarray(np.stack([-np.log(np.expm1(-v)), np.zeros_like(v)], 1))
+    L = np.maximum(mask.astype(np.float64).sum(1), 1.0).astype(np.float32)
+    Ltok, Atok = np.repeat(L, T), np.repeat(adv, T)
+    old = old.reshape(-1).astype(np.float32)
+    r = orc.grpo_rows(rows(lpd), np.zeros(S * T, np.int64), w, Atok, Ltok, float(S), ref_logits=rows(lrd),
+                      old_logp=old, loss_mode=orc.CLIP_KL, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta,
+                      dtype=orc.F64, want_dlogits=False)
+    assert np.abs(r.lp[live] - lpd[live]).max() <= 1e-12 * np.abs(lpd[live]).max()
+    tscale = np.maximum(1.0, np.abs(lse))
+    fl = coef_floor(r.coef, r.lp, r.lr, w.astype(np.float64), Atok.astype(np.float64), Ltok.astype(np.float64),
+                    float(S), old.astype(np.float64), False, cfg.kl_beta, cfg.clip_eps, tscale)
+    return r.coef, fl
+
+
+def _torch_reference(inp, coef=None, chunk=2048, floor=None):
+    """fp32 logp / lse per token, and with coef the gradients and their bounds; floor
+    (per token) is the error c itself may carry (clip + KL: coef_floor), else c is
+    exact up to f32 rounding (REINFORCE)."""
     h, W, ids = inp["hidden"], inp["weight"], inp["ids"].reshape(-1)
     Wf = W.float()
     N = h.shape[0]
@@ -672,9 +699,16 @@ def _torch_reference(inp, coef=None, chunk=2048):
             D = -P * cc[:, None]
             D.scatter_add_(1, idc[:, None], cc[:, None])
             E = (2.0 ** -8 + 1e-4) * D.abs()
-            # c is exact up to f32 rounding here (REINFORCE), so the softmax term carries
-            # only the log-prob error: |c| * 1e-5 * max(1, |lse|) * p.
-            E += (cc.abs() * 1e-5 * l.abs().clamp(min=1.0))[:, None] * P
+            if floor is None:
+                # c is exact up to f32 rounding (REINFORCE), so the softmax term carries
+                # only the log-prob error: |c| * 1e-5 * max(1, |lse|) * p.
+                E += (cc.abs() * 1e-5 * l.abs().clamp(min=1.0))[:, None] * P
+            else:
+                # The device's c and this one each lie within floor of the exact c:
+                # 2 floor (onehot + p), as in grad_bounds.
+                fc = 2.0 * floor[n0:n0 + chunk]
+                E += fc[:, None] * P
+                E.scatter_add_(1, idc[:, None], fc[:, None])
             # The default backward's f16 softmax cache (cache_error, in torch).
             V = Lc.shape[1]
             nb = (V + 127) // 128
@@ -703,8 +737,7 @@ def test_config5_full_size():
         print(f"config 5 full size: device mode={int(mode)}", flush=True)
         out = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"],
                                   ref_weight=inp["ref_weight"], rewards=inp["rewards"], group_size=cfg.group,
-                                  old_logp=old, loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta,
-                                  want_grads=mode == LossMode.REINFORCE)
+                                  old_logp=old, loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta)
         torch.cuda.synchronize()
         m = inp["mask"].reshape(-1) != 0
         sc = lse_ref.abs().clamp(min=1.0)
@@ -729,11 +762,29 @@ def test_config5_full_size():
             _, _, dh, tol_dh, dw, tol_dw = _torch_reference(inp, coef.float().reshape(-1))
             bad_h = ((out.dhidden - dh).abs() > tol_dh + 1e-6 * tol_dh.max()).sum().item()
             bad_w = ((out.dweight - dw).abs() > tol_dw + 1e-6 * tol_dw.max()).sum().item()
+            used_h = float(((out.dhidden - dh).abs() / (tol_dh + 1e-30)).max())
+            used_w = float(((out.dweight - dw).abs() / (tol_dw + 1e-30)).max())
+            print(f"  REINFORCE gradients: largest error / bound: dhidden {used_h:.3f}, dW {used_w:.3f}", flush=True)
             assert bad_h == 0 and bad_w == 0, (bad_h, bad_w)
             del dh, tol_dh, dw, tol_dw
         else:
-            lr_ref = _torch_reference({**inp, "weight": inp["ref_weight"]})[0]
+            lr_ref, rlse_ref = _torch_reference({**inp, "weight": inp["ref_weight"]})[:2]
             err = (out.ref_logp.reshape(-1) - lr_ref).abs()
             assert bool((err[m] <= 1e-5 * sc[m] + 1e-5).all()), float(err[m].max())
+            # clip + KL (the benchmark's mode): c from the fp32 reference log-probs through
+            # the oracle, each token's coef_floor in the bound.
+            print("config 5 full size: clip-KL reference gradients", flush=True)
+            scale = torch.maximum(lse_ref.abs(), rlse_ref.abs()).double().cpu().numpy()
+            coef, fl = _clip_kl_coef(lp_ref.double().cpu().numpy(), lr_ref.double().cpu().numpy(),
+                                     old.cpu().numpy(), adv, inp["mask"].cpu().numpy(), cfg, scale)
+            _, _, dh, tol_dh, dw, tol_dw = _torch_reference(inp, torch.from_numpy(coef).float().to(DEV),
+                                                            floor=torch.from_numpy(fl).float().to(DEV))
+            bad_h = ((out.dhidden - dh).abs() > tol_dh + 1e-6 * tol_dh.max()).sum().item()
+            bad_w = ((out.dweight - dw).abs() > tol_dw + 1e-6 * tol_dw.max()).sum().item()
+            used_h = float(((out.dhidden - dh).abs() / (tol_dh + 1e-30)).max())
+            used_w = float(((out.dweight - dw).abs() / (tol_dw + 1e-30)).max())
+            print(f"  clip-KL gradients: largest error / bound: dhidden {used_h:.3f}, dW {used_w:.3f}", flush=True)
+            assert bad_h == 0 and bad_w == 0, (bad_h, bad_w)
+            del dh, tol_dh, dw, tol_dw
         del out
         torch.cuda.empty_cache()
