@@ -550,6 +550,53 @@ def bench_hbm_roof(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+MFMA_FLOPS_PER_CLK_SIMD = 1024   # bf16 dense: 2.5 PFLOP/s = 256 CUs x 4 SIMDs x 2.4 GHz x 1024 (v_mfma_f32_32x32x16_bf16:
+                                 # 32768 flops in 32 cycles)
+
+
+def bench_mfma_roof(args) -> None:
+    """The practical MFMA roof (pcp_mfma_peak): register-resident v_mfma_f32_32x32x16_bf16
+    on one workgroup of eight waves per CU (the LM-head tile kernel's occupancy), no
+    memory traffic. Short and long launches (--mfma-iters rounds per wave, and a tenth of
+    that), since the clock under sustained MFMA load settles lower. The implied clock is
+    the rate over the CUs' 4 SIMDs x 1024 flops per cycle: the shader clock if the MFMA
+    pipes never idle, a lower bound on it otherwise."""
+    import torch
+
+    from pcp_amd._lib import check, lib
+    from pcp_amd.grpo import default_context
+
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    ctx = default_context(0)
+    stream = torch.cuda.current_stream().cuda_stream or None
+    out = torch.empty(8192, dtype=torch.float32, device=dev)
+    res = {}
+    for iters in (max(2, args.mfma_iters // 10 // 2 * 2), args.mfma_iters // 2 * 2):
+        call = lambda: check(lib().pcp_mfma_peak(ctx.handle, cus, iters, 1, out.data_ptr(), None, stream), ctx.handle)
+        for _ in range(args.warmup):
+            call()
+        torch.cuda.synchronize()
+        ms, _ = _timed_calls(ctx, args.steps, call)
+        tf = cus * 8 * iters * 8 * 32768 / (ms / 1e3) / 1e12
+        res[f"iters{iters}"] = {"kernel_ms": ms, "tflops": tf,
+                                "implied_clock_ghz": tf * 1e12 / (cus * 4 * MFMA_FLOPS_PER_CLK_SIMD) / 1e9}
+    long = res[f"iters{args.mfma_iters // 2 * 2}"]
+    line = {
+        "metric": "bf16 MFMA rate, register-resident v_mfma_f32_32x32x16_bf16, 8 waves per CU",
+        "value": long["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": long["kernel_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "pseudo-random bf16 operands in [-1, 1), register-resident",
+        "config": {"workload": f"pcp_mfma_peak: {cus} workgroups x 8 waves, {args.mfma_iters} rounds of 8 MFMAs",
+                   "cus": cus},
+        "roofline": {"bound": "mfma", "achieved": long["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": long["tflops"] / MFMA_BF16_PEAK_TFLOPS, "traffic": None, "kernel": "mfma_peak_kernel",
+                     "kernel_ms": long["kernel_ms"]},
+        "launches": res,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def bench_logprob(args) -> None:
     """Forward-only log-probs (pcp_grpo_logprob_fwd: log-softmax + sampled-token gather
     of the policy rows, and of the reference rows unless --policy-only) over the
@@ -710,13 +757,18 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--workload", choices=["loss", "logprob", "execute", "nesterov", "sample", "b64", "hbm_roof"],
+    ap.add_argument("--workload", choices=["loss", "logprob", "execute", "nesterov", "sample", "b64", "hbm_roof",
+                                           "mfma_roof"],
                     default="loss",
                     help="loss: the GRPO loss head of --config (the headline metric); logprob: forward-only "
                          "log-probs of --config's rows; execute: the host-bytes boundary (PCIe-inclusive); nesterov: the "
                          "optimizer step over Qwen2.5-0.5B's parameters; sample: the rollout sampler; "
-                         "b64: the UPDATE_WEIGHTS payload codec; hbm_roof: the practical HBM roof (stream probes)")
+                         "b64: the UPDATE_WEIGHTS payload codec; hbm_roof: the practical HBM roof (stream probes); "
+                         "mfma_roof: the practical bf16 MFMA roof and clock (register-resident probe)")
     ap.add_argument("--roof-gib", type=float, default=4.0, help="hbm_roof workload: bytes per buffer, in GiB")
+    ap.add_argument("--mfma-iters", type=int, default=40000,
+                    help="mfma_roof workload: rounds of 8 MFMAs per wave in the long launch (the short one runs "
+                         "a tenth)")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
     ap.add_argument("--no-zero-fill", action="store_true",
@@ -766,6 +818,9 @@ def main() -> None:
         return
     if args.workload == "hbm_roof":
         bench_hbm_roof(args)
+        return
+    if args.workload == "mfma_roof":
+        bench_mfma_roof(args)
         return
     if args.workload == "logprob":
         bench_logprob(args)

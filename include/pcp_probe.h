@@ -1,10 +1,11 @@
 /*
- * pcp_probe.h — HBM stream probes: the practical bandwidth roof of this device.
+ * pcp_probe.h — HBM stream and MFMA probes: the practical roofs of this device.
  *
  * No counterpart in the reference (it runs the loss head inside its compiled VMFB and
  * measures nothing of the kind). Measurement infrastructure for the roofline figures:
  * the bandwidth plain streaming kernels reach for the access mixes of the library's
- * HBM-bound kernels, beside the 8 TB/s spec figure.
+ * HBM-bound kernels, beside the 8 TB/s spec figure, and the bf16 MFMA rate and clock
+ * reached without memory traffic, beside the 2.5 PFLOP/s spec figure.
  */
 #ifndef PCP_PROBE_H
 #define PCP_PROBE_H
@@ -29,6 +30,21 @@ struct pcp_ctx;
  * points. */
 int pcp_hbm_stream(struct pcp_ctx* ctx, int kind, int nontemporal, int vectors_per_lane, const void* a,
                    const void* b, void* c, int64_t bytes, void* stream);
+
+/* The MFMA probe: `workgroups` workgroups of 8 waves (two per SIMD, the LM-head tile
+ * kernel's occupancy), each wave running `iters` (even, >= 2) rounds of eight independent
+ * v_mfma_f32_32x32x16_bf16 (32768 flops each) on register-resident operands: two sets of
+ * pseudo-random bf16 in [-1, 1) derived from `seed`, taken alternately, the same on every
+ * wave. Flops: workgroups x 8 x iters x 8 x 32768. No memory traffic inside the loop.
+ *   out:    [8192] f32 (4-byte aligned), the accumulators of workgroup 0's wave 0:
+ *           out[((i * 2 + j) * 16 + r) * 64 + lane] is element r of block (i, j) of `lane`
+ *           (column lane % 32, row 8 * (r / 4) + 4 * (lane / 32) + r % 4 of the 32 x 32
+ *           product of A fragment i and B fragment j)
+ *   clocks: NULL or [workgroups][4] u64 (8-byte aligned): wave 0's s_memtime and
+ *           s_memrealtime before and after its loop (start, end, start, end)
+ * Asynchronous on `stream`; timed by pcp_profile_start / pcp_profile_stop. */
+int pcp_mfma_peak(struct pcp_ctx* ctx, int workgroups, int iters, uint32_t seed, float* out, uint64_t* clocks,
+                  void* stream);
 
 #ifdef __cplusplus
 }

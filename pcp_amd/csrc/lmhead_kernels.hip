@@ -5,11 +5,14 @@
 // (forward), and dlogits = c_n * (onehot - softmax) (backward). The tile kernel
 // computes a 256 x 256 logits tile on v_mfma_f32_32x32x16_bf16 and reduces it in
 // its epilogue, so full logits never exist in HBM:
-//   kFwd  -> per (token, vocab tile) partial (max, sum 2^(x*log2e - max)) and the
-//            target logit when the target falls in the tile; with ECACHE also every
-//            term 2^(x*log2e - max) as f16 (the softmax cache of the backward);
-//   kBwd  -> dlogits for one vocab chunk in bf16, for the dhidden / dW GEMMs (the
-//            backward without the cache recomputes the logits this way).
+//   kLmFwd  -> per (token, kLmPart vocab entries) partial (max, sum 2^(x*log2e - max))
+//              and the target logit when the target falls in the tile, for the policy
+//              and (n_model = 2) the reference model in one launch; with ECACHE also
+//              every policy term 2^(x*log2e - max) as f16 (the softmax cache);
+//   kLmBwd  -> dlogits for one vocab chunk in bf16, for the dhidden / dW products (the
+//              backward without the cache recomputes the logits this way);
+//   kLmGemm -> up to two plain products C = B * A^T on K-contiguous or K-major
+//              operands (dhidden and dW from the cached dlogits and their transpose).
 //
 // Reference: the LM head and loss of tools/export_qwen_forward.py:146-163
 // (self.model.lm_head(hidden) then F.cross_entropy), and matmulVJP

@@ -13,6 +13,13 @@
 // vectors, VPT = 1, 2, 4 or 8 per lane. One vector per lane writes fastest (6.8 TB/s
 // against 5.6-5.8 TB/s for a grid of 32 workgroups per CU striding 8 per lane), so the
 // benchmark reports the best shape of each kind.
+//
+// MFMA probe (pcp_mfma_peak): the bf16 matrix rate that register-resident
+// v_mfma_f32_32x32x16_bf16 reaches with the tile kernel's wave shape and occupancy
+// (eight waves per workgroup, two per SIMD, a 128 x 64 block of accumulators per wave),
+// no memory traffic at all. The spec's 2.5 PFLOP/s assumes 2.4 GHz; under sustained
+// MFMA load the clock is held lower by the power limit, and this probe measures where
+// the rate settles.
 
 #include <hip/hip_runtime.h>
 
@@ -88,6 +95,90 @@ hipError_t launch_vpt(int vpt, const void* a, const void* b, void* c, int64_t n1
   }
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMfmaWaves = 8;
+
+// Pseudo-random bf16 in [-1, 1): element idx of the probe's operands (the same on every
+// wave), a murmur3-style mix of (seed, idx) mapped to a float and truncated to bf16.
+__device__ __forceinline__ __bf16 probe_bf16(uint32_t seed, uint32_t idx) {
+  uint32_t x = seed ^ (idx * 0x9E3779B9u);
+  x ^= x >> 16;
+  x *= 0x85EBCA6Bu;
+  x ^= x >> 13;
+  x *= 0xC2B2AE35u;
+  x ^= x >> 16;
+  const float f = static_cast<float>(static_cast<int32_t>(x >> 8) - (1 << 23)) * (1.f / (1 << 23));
+  return __builtin_bit_cast(__bf16, static_cast<uint16_t>(__builtin_bit_cast(uint32_t, f) >> 16));
+}
+
+// Each wave: operand sets s = 0, 1 of 4 A fragments (element idx ((s*4 + i)*64 + lane)*8
+// + e) and 2 B fragments (4096 + ((s*2 + j)*64 + lane)*8 + e), then `iters` rounds of the
+// 8 products acc[i][j] += A_s[i] B_s[j], s alternating (iters even).
+__global__ void __launch_bounds__(64 * kMfmaWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+mfma_peak_kernel(int iters, uint32_t seed, float* out, uint64_t* clocks) {
+  const int lane = threadIdx.x & 63;
+  bf16x8 a[2][4], b[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[s][i][e] = probe_bf16(seed, ((s * 4 + i) * 64 + lane) * 8 + e);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[s][j][e] = probe_bf16(seed, 4096 + ((s * 2 + j) * 64 + lane) * 8 + e);
+    }
+  }
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  __builtin_amdgcn_sched_barrier(0);
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_sched_barrier(0);
+  for (int it = 0; it < iters; it += 2) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s][i], b[s][j], acc[i][j], 0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_sched_barrier(0);
+  if (blockIdx.x == 0 && threadIdx.x < 64) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) out[((i * 2 + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+  } else {
+    // Every other wave keeps its products by a store that only a NaN sum makes.
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sum += acc[i][j][r];
+    if (sum != sum) out[lane] = sum;
+  }
+  if (clocks && threadIdx.x == 0) {
+    uint64_t* c = clocks + 4 * static_cast<int64_t>(blockIdx.x);
+    c[0] = t0;
+    c[1] = t1;
+    c[2] = r0;
+    c[3] = r1;
+  }
+}
+
 }  // namespace
 }  // namespace pcp
 
@@ -121,5 +212,25 @@ extern "C" int pcp_hbm_stream(pcp_ctx* ctx, int kind, int nontemporal, int vecto
   }
   prof_end(ctx, st, timed);
   if (e != hipSuccess) return hip_fail(ctx, e, "pcp_hbm_stream launch");
+  return PCP_OK;
+}
+
+extern "C" int pcp_mfma_peak(pcp_ctx* ctx, int workgroups, int iters, uint32_t seed, float* out, uint64_t* clocks,
+                             void* stream) {
+  using namespace pcp;
+  if (workgroups < 1 || workgroups > (1 << 20) || iters < 2 || iters % 2 != 0)
+    return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_mfma_peak: workgroups must be in [1, 2^20] and iters even and >= 2");
+  if (!out || (reinterpret_cast<uintptr_t>(out) & 3u) || (reinterpret_cast<uintptr_t>(clocks) & 7u))
+    return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_mfma_peak: out is NULL or a buffer is misaligned");
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool timed = prof_begin(ctx, st);
+  mfma_peak_kernel<<<dim3(static_cast<unsigned>(workgroups)), dim3(64 * kMfmaWaves), 0, st>>>(iters, seed, out,
+                                                                                             clocks);
+  e = hipGetLastError();
+  prof_end(ctx, st, timed);
+  if (e != hipSuccess) return hip_fail(ctx, e, "pcp_mfma_peak launch");
   return PCP_OK;
 }

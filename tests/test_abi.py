@@ -446,3 +446,19 @@ def test_hbm_stream_argument_errors_without_device():
     assert L.pcp_hbm_stream(None, 0, 0, 1, 0x1000, None, None, 1 << 20, None) == -1
     assert L.pcp_hbm_stream(None, 1, 0, 8, None, None, 0x3000, 1 << 20, None) == -1
     assert "context is NULL" in L.pcp_last_error(None).decode()
+
+
+def test_mfma_peak_argument_errors_without_device():
+    """pcp_mfma_peak rejects a bad grid, odd or too few rounds, a NULL or misaligned
+    buffer before any device work (the context check comes after them)."""
+    L = _lib.lib()
+    assert L.pcp_mfma_peak(None, 0, 2, 0, 0x1000, None, None) == -1
+    assert "workgroups" in L.pcp_last_error(None).decode()
+    assert L.pcp_mfma_peak(None, 1, 3, 0, 0x1000, None, None) == -1
+    assert L.pcp_mfma_peak(None, 1, 0, 0, 0x1000, None, None) == -1
+    assert L.pcp_mfma_peak(None, 1, 2, 0, None, None, None) == -1
+    assert "NULL" in L.pcp_last_error(None).decode()
+    assert L.pcp_mfma_peak(None, 1, 2, 0, 0x1002, None, None) == -1
+    assert L.pcp_mfma_peak(None, 1, 2, 0, 0x1000, 0x2004, None) == -1
+    assert L.pcp_mfma_peak(None, 1, 2, 0, 0x1000, 0x2000, None) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()
