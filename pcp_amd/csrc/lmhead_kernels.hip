@@ -12,7 +12,9 @@
 //   kLmBwd  -> dlogits for one vocab chunk in bf16, for the dhidden / dW products (the
 //              backward without the cache recomputes the logits this way);
 //   kLmGemm -> up to two plain products C = B * A^T on K-contiguous or K-major
-//              operands (dhidden and dW from the cached dlogits and their transpose).
+//              operands (dhidden and dW from the cached dlogits and their transpose);
+//              with FRAG the token-role operand A is stored fragment-major (written by
+//              lm_transpose_frag_kernel) and read straight into registers.
 //
 // Reference: the LM head and loss of tools/export_qwen_forward.py:146-163
 // (self.model.lm_head(hidden) then F.cross_entropy), and matmulVJP
@@ -144,11 +146,14 @@ __device__ __forceinline__ void lm_barrier() {
 // through two stages of BK hidden columns.
 // ATR (kLmGemm): the token-role operand is stored K-major and its fragments are read
 // with ds_read_b64_tr_b16 (see below).
+// FRAG (kLmGemm): the token-role operand is stored fragment-major and loaded straight
+// into VGPRs; only the vocab-role operand goes through LDS (see below).
 // ECACHE (kLmFwd): the epilogue of model 0 also stores the softmax terms (see there).
 // Tile p of product prod (kLmGemm), or of model prod (kLmFwd), called by lm_tile_kernel.
-template <int MODE, bool ATR, bool ECACHE>
+template <int MODE, bool ATR, bool ECACHE, bool FRAG>
 __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, char* smem) {
   using namespace lm;
+  static_assert(!FRAG || (MODE == kLmGemm && !ATR), "fragment-major operands: kLmGemm, K-contiguous roles");
 
   // The product: the loss-head modes read rows of H elements of hidden (A) and W (B);
   // kLmGemm takes one of its (up to) two products.
@@ -234,6 +239,19 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
       dofh[q] = static_cast<uint32_t>(row) * hbytes + c16;
     }
   }
+  // Fragment-major token operand (FRAG): the 1 KB MFMA B fragment of rows 32 b + [0, 32)
+  // and k 16 s + [0, 16) lies at byte 1024 (b lda/16 + s) (lane l's 16 bytes at 16 l:
+  // row 32 b + l % 32, k 16 s + 8 (l / 32) + 0..7), so a wave loads each of its
+  // fragments with one fully coalesced 1 KB load. Blocks past the tile's rows fall
+  // outside the descriptor and read 0; the writer zero-fills rows past N in a block.
+  const __amdgpu_buffer_rsrc_t rt =
+      FRAG ? row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0 / 32) * (lda / 16) * 1024,
+                      static_cast<uint32_t>((rows_h + 31) / 32) * static_cast<uint32_t>(lda / 16) * 1024u)
+           : rh;
+  uint32_t roff[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    roff[j] = static_cast<uint32_t>((wt * NJ + j) * (lda / 16)) * 1024u + 16u * static_cast<uint32_t>(lane);
   auto issue = [&](int st, int buf) {
     char* base = smem + buf * kStageBytes;
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
@@ -241,8 +259,9 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
 #pragma unroll
     for (int q = 0; q < QN; ++q) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (QN * wave + q) * 1024), 16, dofw[q] + koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (QN * wave + q) * 1024), 16, dofh[q] + kofh,
-                                               0, 0, 0);
+      if constexpr (!FRAG)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (QN * wave + q) * 1024), 16,
+                                                 dofh[q] + kofh, 0, 0, 0);
     }
   };
 
@@ -285,7 +304,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
             (__attribute__((address_space(3))) v4i16*)LM_LDS(tb + offBt[j] + 4 * 512));
         bfr[set][j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
-    } else {
+    } else if constexpr (!FRAG) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) bfr[set][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 32 * ROWB);
     }
@@ -319,6 +338,75 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   // behind it whenever the memory pipeline pushed back; one load (or fragment read)
   // between consecutive MFMAs measured 6% faster on config 5.
   const int nk = K / BK;
+  if constexpr (FRAG) {
+    // The token operand's fragments for one stage sit in a ring of registers: k-step kk
+    // of stage kb reads slot kk, and right after its MFMAs the slot is reloaded with
+    // k-step kk of stage kb + 1, about one stage ahead of its use. Only the vocab-role
+    // operand goes through LDS, so the stage barrier waits for its direct-to-LDS loads
+    // alone (the ring loads issued after them may still be in flight). Measured at
+    // configuration 5 against the same products with both operands through LDS,
+    // interleaved on one box: products launch 19.93-19.96 -> 18.35-18.46 ms, step
+    // 41.82-41.89 -> 40.29-40.40 ms. The forward gained nothing from the same scheme
+    // (18.5-19.2 against 19.0-19.9 ms over two boxes, within the spread), so it keeps
+    // both operands in LDS.
+    bf16x8 ring[4][NJ];
+    auto ring_load = [&](int kk, int st) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        ring[kk][j] =
+            __builtin_bit_cast(bf16x8, buf_ld16<false>(rt, roff[j] + static_cast<uint32_t>(4 * st + kk) * 1024u));
+    };
+    // k-step kk's MFMAs, j-major so slot (kk, 0) is free after the first four.
+    auto mf = [&](int set, int kk) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], ring[kk][j], acc[i][j], 0, 0, 0);
+    };
+    // Per k-step: the stage's direct-to-LDS loads (first k-step), then the 4 fragment
+    // reads of the next k-step between the first MFMAs, then the ring reloads.
+    auto sched_f = [&](bool dma) {
+      if (dma) __builtin_amdgcn_sched_group_barrier(0x020, QN, 0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * NJ - 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, NJ, 0);
+    };
+    issue(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) ring_load(kk, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    lm_barrier();
+    fload(0, 0, 0);
+    for (int kb = 0; kb < nk; ++kb) {
+      const int nx = min(kb + 1, nk - 1);   // past the end: reloads of the last stage, unused
+      issue(nx, (kb + 1) & 1);
+      fload(1, kb, 1);
+      mf(0, 0);
+      ring_load(0, nx);
+      sched_f(true);
+      fload(0, kb, 2);
+      mf(1, 1);
+      ring_load(1, nx);
+      sched_f(false);
+      fload(1, kb, 3);
+      mf(0, 2);
+      ring_load(2, nx);
+      sched_f(false);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(wait_vm(3 * NJ));   // stage kb+1's LDS loads landed
+      lm_barrier();
+      fload(0, nx, 0);
+      mf(1, 3);
+      ring_load(3, nx);
+      sched_f(false);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  } else {
   issue(0, 0);
   __builtin_amdgcn_s_waitcnt(kWaitStage);
   lm_barrier();
@@ -372,6 +460,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   }
   // Drain the trailing loads before any LDS reuse (the backward epilogue).
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  }
 
   const int vw = v0 + wv * 128;                 // first vocab row of this wave
   const int half = lane >> 5;
@@ -593,7 +682,7 @@ __device__ __forceinline__ int lm_total_tiles(const LmTileArgs& a, int prod) {
 // per-XCD atomic queues: 43.5 against 43.9 ms of kernel time per step (the queue's
 // per-tile barriers and atomic cost more than these early exits), and against a
 // persistent static split, 46.2 ms.
-template <int MODE, bool ATR = false, bool ECACHE = false>
+template <int MODE, bool ATR = false, bool ECACHE = false, bool FRAG = false>
 __global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(lm::WPE, lm::WPE)))
 lm_tile_kernel(LmTileArgs a) {
   extern __shared__ __align__(16) char smem[];
@@ -606,7 +695,7 @@ lm_tile_kernel(LmTileArgs a) {
     const int per = (tt + 7) / 8;
     const int p = xcd * per + i;
     if (i >= per || p >= tt) return;
-    lm_tile<MODE, ATR, ECACHE>(a, p % nm, p / nm, smem);
+    lm_tile<MODE, ATR, ECACHE, FRAG>(a, p % nm, p / nm, smem);
     return;
   }
   const int t0 = lm_total_tiles<MODE>(a, 0);
@@ -616,7 +705,7 @@ lm_tile_kernel(LmTileArgs a) {
   const int prod = i < per0 ? 0 : 1;
   const int p = prod == 0 ? xcd * per0 + i : xcd * per1 + (i - per0);
   if (p >= (prod == 0 ? t0 : t1)) return;
-  lm_tile<MODE, ATR, ECACHE>(a, prod, p, smem);
+  lm_tile<MODE, ATR, ECACHE, FRAG>(a, prod, p, smem);
 }
 
 // 64 x 64 bf16 tiles staged in LDS for a transpose: rows of 66 elements (33 words),
@@ -860,6 +949,39 @@ __global__ void __launch_bounds__(256) lm_transpose_kernel(LmTransposeArgs a) {
   }
 }
 
+// The same transpose into the fragment-major layout of the tile kernel's FRAG operand
+// (the MFMA B fragment of destination rows 32 b + [0, 32) and k 16 s + [0, 16) at
+// fragment b ld_dst/16 + s, lane l holding row 32 b + l % 32 and k 16 s + 8 (l / 32) +
+// 0..7): destination rows are source columns, k runs over source rows. Each block's
+// 64 x 64 tile is eight whole fragments, written as 1 KB runs; k from R up to R
+// rounded to 64 is zero, and k past that is not written.
+__global__ void __launch_bounds__(256) lm_transpose_frag_kernel(LmTransposeArgs a) {
+  __shared__ uint16_t t[64 * kTilePitch];
+  const int R = a.rcount ? min(a.R, *a.rcount) : a.R;
+  const int64_t rend = min(a.ld_dst, (static_cast<int64_t>(R) + 63) / 64 * 64);
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  if (r0 >= rend) return;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int rr = it * 32 + (tid >> 3), cc = (tid & 7) * 8;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r0 + rr < R && c0 + cc < a.C)
+      v = *reinterpret_cast<const u32x4*>(a.src + static_cast<int64_t>(r0 + rr) * a.ld_src + c0 + cc);
+    tile_put8(t, rr, cc, v);
+  }
+  __syncthreads();
+  u32x4* dst = reinterpret_cast<u32x4*>(a.dst);
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int idx = tid + 256 * it, f = idx >> 6, l = idx & 63;   // fragment f of the 8, lane l
+    const int bl = f >> 2, sl = f & 3;
+    const int c = 32 * bl + (l & 31), r = 16 * sl + 8 * (l >> 5);
+    if (c0 + c < a.C && r0 + r < rend)
+      dst[(static_cast<int64_t>(c0 / 32 + bl) * (a.ld_dst / 16) + r0 / 16 + sl) * 64 + l] = tile_col8(t, r, c);
+  }
+}
+
 __global__ void __launch_bounds__(256) lm_zero_kernel(float* dst, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
     dst[i] = 0.f;
@@ -870,14 +992,14 @@ __global__ void __launch_bounds__(256) lm_zero_kernel(float* dst, int64_t n) {
 // ---------------------------------------------------------------------------
 size_t lm_tile_smem_bytes() { return lm::kSmem; }
 
-template <int MODE, bool EC = false, bool kAtr = MODE == kLmGemm>
+template <int MODE, bool EC = false, bool kAtr = MODE == kLmGemm, bool kFrag = false>
 hipError_t launch_tiles_mode(const LmTileArgs& a, int max_tiles, hipStream_t st) {
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE, kAtr, EC>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_kernel<MODE, kAtr, EC, kFrag>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
   if (e != hipSuccess) return e;
   // Items per XCD at the largest sizes: each product rounds its share up separately.
   const int grid = 8 * ((max_tiles + 7) / 8 + (MODE == kLmGemm && a.n_gemm > 1 ? 1 : 0));
-  lm_tile_kernel<MODE, kAtr, EC><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
+  lm_tile_kernel<MODE, kAtr, EC, kFrag><<<dim3(grid), dim3(lm::NTHR), lm::kSmem, st>>>(a);
   return hipGetLastError();
 }
 
@@ -901,6 +1023,10 @@ hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, bool k_major_a
     grid += g[p].ntt * g[p].nvt;
   }
   if (grid <= 0) return hipSuccess;
+  const bool frag = a.n_gemm > 0 && a.gemm[0].a_frag;
+  if (a.n_gemm > 1 && (a.gemm[1].a_frag != 0) != frag) return hipErrorInvalidValue;   // one layout per launch
+  if (frag && k_major_a) return hipErrorInvalidValue;
+  if (frag) return launch_tiles_mode<kLmGemm, false, false, true>(a, grid, st);
   if (!k_major_a) return launch_tiles_mode<kLmGemm, false, false>(a, grid, st);
   return launch_tiles_mode<kLmGemm>(a, grid, st);
 }
@@ -909,6 +1035,13 @@ hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st) {
   if (a.C <= 0 || a.ld_dst <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>((a.ld_dst + 63) / 64));
   lm_transpose_kernel<<<grid, dim3(256), 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_transpose_frag(const LmTransposeArgs& a, hipStream_t st) {
+  if (a.C <= 0 || a.ld_dst <= 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>((a.ld_dst + 63) / 64));
+  lm_transpose_frag_kernel<<<grid, dim3(256), 0, st>>>(a);
   return hipGetLastError();
 }
 

@@ -54,6 +54,8 @@ struct LmTileArgs {
     int N, V, K;        // K % 64 == 0, K <= ldb
     int lda, ldb;       // row strides in elements (lda >= N rounded up to 8)
     int krows_a;        // K-major A: rows that exist; rows [krows_a, K) read as 0
+    int a_frag;         // A stored fragment-major (launch_lm_transpose_frag, K extent lda): read
+                        //   straight into registers; both products of a launch alike
     const int* vcount;  // or nullptr: V = *vcount (<= V; tiles past it exit)
     const int* kcount;  // or nullptr: K = *kcount rounded up to 64 (<= K), krows_a = *kcount
     float* C;           // f32 result: row v, column t at C[v * ldc + t], or at
@@ -164,6 +166,9 @@ hipError_t launch_lm_tiles(int mode, const LmTileArgs& a, hipStream_t st);
 // ([N, lda], krows_a unused).
 hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, bool k_major_a, hipStream_t st);
 hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st);
+// The same transpose written in the fragment-major layout of Gemm::a_frag operands
+// (dst rows = C, padded to 32; k extent ld_dst, a multiple of 64).
+hipError_t launch_lm_transpose_frag(const LmTransposeArgs& a, hipStream_t st);
 hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st);
 hipError_t launch_lm_dcache(const LmDcacheArgs& a, hipStream_t st);
 hipError_t launch_lm_terms(const RowArgs& ra, const LmTermsArgs& a, hipStream_t st);

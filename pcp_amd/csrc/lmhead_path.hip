@@ -295,12 +295,10 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   if (bwd) {
     char* dbuf = static_cast<char*>(ctx->lm_dbuf);
     float* dhc = want_dy ? F(o_dhc) : nullptr;
-    if (a->dweight) {
-      // hidden^T [H, ldt]: the dW product's token operand, zero past the live tokens.
-      const LmTransposeArgs tr{reinterpret_cast<const uint16_t*>(sp + o_hid), H, static_cast<int>(N),
-                               static_cast<int>(H), reinterpret_cast<uint16_t*>(sp + o_ht), ldt, cnt};
-      if ((e = launch_lm_transpose(tr, st)) != hipSuccess) return hip_fail(ctx, e, "transposing hidden rows");
-    }
+    // hidden^T [H, ldt], zero past the live tokens: an operand of dW (fragment-major
+    // when it is the products' token operand on the cached path).
+    const LmTransposeArgs tr{reinterpret_cast<const uint16_t*>(sp + o_hid), H, static_cast<int>(N),
+                             static_cast<int>(H), reinterpret_cast<uint16_t*>(sp + o_ht), ldt, cnt};
     // Chunked backward: the products of one vocab range [vc0, vc0 + w) of D
     // (token-major rows of ldd columns at dbuf), in one launch (they are independent):
     // the longer one (dhidden, K = the range, over fewer tiles) first, so the shorter
@@ -354,20 +352,24 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     if (cached) {
       // D and D^T over the whole vocabulary from the cache, W^T, then both products in
       // one launch on K-contiguous operands (K = the vocabulary for dhidden, the live
-      // tokens for dW; dhidden's 608 long tiles at configuration 5 go first).
+      // tokens for dW; dhidden's 608 long tiles at configuration 5 go first). The token
+      // operands (W^T, hidden^T) are written fragment-major and loaded straight into
+      // registers; D and D^T go through LDS.
       uint16_t* dt = a->dweight ? reinterpret_cast<uint16_t*>(dbuf + o_dt) : nullptr;
       uint16_t* wt = want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_wt) : nullptr;
       const LmDcacheArgs dc{reinterpret_cast<uint16_t*>(dbuf), ldv, cnt, dt, ldt, V, part, npart,
                             F(o_l2), F(o_coef), F(o_tgt), I(o_idsc)};
       if ((e = launch_lm_dcache(dc, st)) != hipSuccess) return hip_fail(ctx, e, "dlogits from the softmax cache");
+      if (a->dweight && (e = launch_lm_transpose_frag(tr, st)) != hipSuccess)
+        return hip_fail(ctx, e, "transposing hidden rows");
       LmTileArgs::Gemm g[2];
       int ng = 0;
       std::memset(g, 0, sizeof(g));
       if (want_dy) {
-        // W^T [H, ldv], zero past V.
+        // W^T [H, ldv] (fragment-major), zero past V.
         const LmTransposeArgs tw{static_cast<const uint16_t*>(a->weight), H, static_cast<int>(V), static_cast<int>(H),
                                  wt, ldv, nullptr};
-        if ((e = launch_lm_transpose(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
+        if ((e = launch_lm_transpose_frag(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
         // dhidden_c[t][h] = sum_v D[t][v] * W^T[h][v].
         LmTileArgs::Gemm& d = g[ng++];
         d.B = dbuf;
@@ -375,6 +377,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         d.V = static_cast<int>(N);
         d.vcount = cnt;
         d.A = wt;
+        d.a_frag = 1;
         d.lda = static_cast<int>(ldv);
         d.N = static_cast<int>(H);
         d.K = static_cast<int>(ldv);
@@ -390,6 +393,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         d.ldb = static_cast<int>(ldt);
         d.V = static_cast<int>(V);
         d.A = sp + o_ht;
+        d.a_frag = 1;
         d.lda = static_cast<int>(ldt);
         d.N = static_cast<int>(H);
         d.K = static_cast<int>(ldt);
@@ -407,6 +411,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       if (timed && (e = hipEventRecord(ctx->prof_stop[ctx->prof_used++], st)) != hipSuccess)
         return hip_fail(ctx, e, "hipEventRecord");
     } else {
+      if (a->dweight && (e = launch_lm_transpose(tr, st)) != hipSuccess)
+        return hip_fail(ctx, e, "transposing hidden rows");
       ta.B = a->weight;
       ta.lse2 = F(o_l2);
       ta.coef = F(o_coef);
