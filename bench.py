@@ -555,12 +555,13 @@ MFMA_FLOPS_PER_CLK_SIMD = 1024   # bf16 dense: 2.5 PFLOP/s = 256 CUs x 4 SIMDs x
 
 
 def bench_mfma_roof(args) -> None:
-    """The practical MFMA roof (pcp_mfma_peak): register-resident v_mfma_f32_32x32x16_bf16
-    on one workgroup of eight waves per CU (the LM-head tile kernel's occupancy), no
-    memory traffic. Short and long launches (--mfma-iters rounds per wave, and a tenth of
+    """The practical MFMA roof (pcp_mfma_peak): register-resident bf16 MFMAs, both shapes
+    (v_mfma_f32_32x32x16_bf16 and v_mfma_f32_16x16x32_bf16), on one workgroup of eight
+    waves per CU (the LM-head tile kernel's occupancy), no memory traffic. Short and long
+    launches per shape (--mfma-iters rounds of 32x32x16 work per wave, and a tenth of
     that), since the clock under sustained MFMA load settles lower. The implied clock is
     the rate over the CUs' 4 SIMDs x 1024 flops per cycle: the shader clock if the MFMA
-    pipes never idle, a lower bound on it otherwise."""
+    pipes never idle, a lower bound on it otherwise. `value` is the best long-launch rate."""
     import torch
 
     from pcp_amd._lib import check, lib
@@ -572,26 +573,33 @@ def bench_mfma_roof(args) -> None:
     stream = torch.cuda.current_stream().cuda_stream or None
     out = torch.empty(8192, dtype=torch.float32, device=dev)
     res = {}
-    for iters in (max(2, args.mfma_iters // 10 // 2 * 2), args.mfma_iters // 2 * 2):
-        call = lambda: check(lib().pcp_mfma_peak(ctx.handle, cus, iters, 1, out.data_ptr(), None, stream), ctx.handle)
-        for _ in range(args.warmup):
-            call()
-        torch.cuda.synchronize()
-        ms, _ = _timed_calls(ctx, args.steps, call)
-        tf = cus * 8 * iters * 8 * 32768 / (ms / 1e3) / 1e12
-        res[f"iters{iters}"] = {"kernel_ms": ms, "tflops": tf,
-                                "implied_clock_ghz": tf * 1e12 / (cus * 4 * MFMA_FLOPS_PER_CLK_SIMD) / 1e9}
-    long = res[f"iters{args.mfma_iters // 2 * 2}"]
+    # Flops per round and wave: 8 x 32768 (32x32x16) or 32 x 16384 (16x16x32); the
+    # 16x16x32 launches run half the rounds, so both shapes do the same work.
+    for shape, name, per_round in ((0, "32x32x16", 8 * 32768), (1, "16x16x32", 32 * 16384)):
+        long_iters = max(2, args.mfma_iters * 8 * 32768 // per_round // 2 * 2)
+        for iters in (max(2, long_iters // 10 // 2 * 2), long_iters):
+            call = lambda: check(lib().pcp_mfma_peak(ctx.handle, shape, cus, iters, 1, out.data_ptr(), None, stream),
+                                 ctx.handle)
+            for _ in range(args.warmup):
+                call()
+            torch.cuda.synchronize()
+            ms, _ = _timed_calls(ctx, args.steps, call)
+            tf = cus * 8 * iters * per_round / (ms / 1e3) / 1e12
+            res[f"{name}_iters{iters}"] = {"shape": name, "rounds": iters, "kernel_ms": ms, "tflops": tf,
+                                           "implied_clock_ghz": tf * 1e12 / (cus * 4 * MFMA_FLOPS_PER_CLK_SIMD) / 1e9,
+                                           "long": iters == long_iters}
+    best = max((v for v in res.values() if v["long"]), key=lambda v: v["tflops"])
     line = {
-        "metric": "bf16 MFMA rate, register-resident v_mfma_f32_32x32x16_bf16, 8 waves per CU",
-        "value": long["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": long["kernel_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "metric": "bf16 MFMA rate, register-resident, 8 waves per CU (best of v_mfma_f32_32x32x16_bf16 and "
+                  "v_mfma_f32_16x16x32_bf16)",
+        "value": best["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": best["kernel_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "pseudo-random bf16 operands in [-1, 1), register-resident",
-        "config": {"workload": f"pcp_mfma_peak: {cus} workgroups x 8 waves, {args.mfma_iters} rounds of 8 MFMAs",
-                   "cus": cus},
-        "roofline": {"bound": "mfma", "achieved": long["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": long["tflops"] / MFMA_BF16_PEAK_TFLOPS, "traffic": None, "kernel": "mfma_peak_kernel",
-                     "kernel_ms": long["kernel_ms"]},
+        "config": {"workload": f"pcp_mfma_peak: {cus} workgroups x 8 waves, {args.mfma_iters} rounds of "
+                               f"32x32x16 work per wave (long launches)", "cus": cus},
+        "roofline": {"bound": "mfma", "achieved": best["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": best["tflops"] / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                     "kernel": f"mfma_peak_kernel ({best['shape']})", "kernel_ms": best["kernel_ms"]},
         "launches": res,
     }
     print(json.dumps(line), flush=True)
@@ -767,8 +775,8 @@ def main() -> None:
                          "mfma_roof: the practical bf16 MFMA roof and clock (register-resident probe)")
     ap.add_argument("--roof-gib", type=float, default=4.0, help="hbm_roof workload: bytes per buffer, in GiB")
     ap.add_argument("--mfma-iters", type=int, default=40000,
-                    help="mfma_roof workload: rounds of 8 MFMAs per wave in the long launch (the short one runs "
-                         "a tenth)")
+                    help="mfma_roof workload: rounds of 8 32x32x16 MFMAs (or the same work in 16x16x32 ones) per "
+                         "wave in the long launch (the short one runs a tenth)")
     ap.add_argument("--mode", choices=["clip_kl", "reinforce"], default="clip_kl")
     ap.add_argument("--force-streaming", action="store_true")
     ap.add_argument("--no-zero-fill", action="store_true",

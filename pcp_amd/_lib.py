@@ -159,7 +159,7 @@ SIGNATURES = {
     "pcp_synth_sample_tokens": (_I, [_VP, _I, _I64, _I64, _U64, _VP, _VP]),
     "pcp_synth_lmhead_tokens": (_I, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _U64, _VP, _VP]),
     "pcp_hbm_stream": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _I64, _VP]),
-    "pcp_mfma_peak": (_I, [_VP, _I, _I, ctypes.c_uint32, _VP, _VP, _VP]),
+    "pcp_mfma_peak": (_I, [_VP, _I, _I, _I, ctypes.c_uint32, _VP, _VP, _VP]),
     "pcp_pack_rollouts": (_I, [_VP, _VP, _I64, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP]),
     "pcp_grad_stats_compute": (_I, [_VP, _VP, _I64, _I, ctypes.POINTER(GradStats), _VP]),
     "pcp_nesterov_create": (_I, [_VP, _F, _F, _I, _I, ctypes.POINTER(_I64), ctypes.POINTER(_VP)]),

@@ -24,6 +24,7 @@
 #include <stdint.h>
 
 #include <cstring>
+#include <type_traits>
 
 #include "grpo_device.hpp"
 #include "lmhead_launch.hpp"
@@ -659,6 +660,181 @@ __global__ void __launch_bounds__(256) lm_reduce_kernel(LmReduceArgs a) {
   if (lane == 0) a.lse2[n] = m + log2f(s);
 }
 
+#ifndef LM_MI16
+#define LM_MI16 1
+#endif
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+namespace lm {
+constexpr int NI16 = 8;         // 16-row vocab blocks per wave (its 128 rows)
+constexpr int NJ16 = TW / 16;   // 16-column token blocks per wave
+constexpr int KS16 = BK / 32;   // 32-deep k-steps per stage
+}  // namespace lm
+
+// The products' tile (kLmGemm, fragment-major token operand) on
+// v_mfma_f32_16x16x32_bf16. Same tile, waves, stages and operand paths as lm_tile's
+// FRAG instances; each wave's 128 x 64 block is 8 x 4 products of 16 x 16 (128
+// accumulators), two 32-deep k-steps per stage. Under the power limit this shape runs
+// the pipes at a higher clock than 32x32x16 for the same work (the register-resident
+// probe: 1.98 against 1.80 GHz at the same MFMA occupancy), as each instruction
+// reduces twice as deep per accumulator update.
+// Fragment layouts (pinned by the MFMA probe's test): an operand lane holds row
+// lane % 16 at k = 8 (lane / 16) + 0..7; the result lane holds column lane % 16 at rows
+// 4 (lane / 16) + 0..3.
+template <int MODE>
+__device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, char* smem) {
+  using namespace lm;
+  static_assert(MODE == kLmGemm, "16x16x32 tiles: the fragment-major products");
+  const LmTileArgs::Gemm& g = a.gemm[prod];
+  int V = g.V, K = g.K, nvt = g.nvt;
+  const int N = g.N, lda = g.lda, ldb = g.ldb, ldc = g.ldc, accumulate = g.accumulate;
+  if (g.vcount) {
+    V = min(V, *g.vcount);
+    nvt = (V + BV - 1) / BV;
+  }
+  if (g.kcount) K = min(K, (min(K, *g.kcount) + BK - 1) / BK * BK);
+  int tm, tn;
+  lm_tile_of(p, g.ntt, nvt, g.group_m, tm, tn);
+  const int m0 = tm * BT, v0 = tn * BV;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wv = wave / WT, wt = wave % WT;
+
+  // Vocab-role operand (B, K-contiguous rows) through LDS as in lm_tile, one 32 KB
+  // buffer per stage.
+  const uint32_t wbytes = static_cast<uint32_t>(ldb) * 2u;
+  const int rows_w = min(BV, V - v0), rows_h = min(BT, N - m0);
+  const __amdgpu_buffer_rsrc_t rw =
+      row_rsrc(reinterpret_cast<const char*>(g.B) + static_cast<int64_t>(v0) * wbytes, rows_w * wbytes);
+  uint32_t dofw[QN];
+#pragma unroll
+  for (int q = 0; q < QN; ++q) {
+    const int row = 8 * (QN * wave + q) + (lane >> 3);
+    dofw[q] = static_cast<uint32_t>(row) * wbytes + 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
+  }
+  auto issue = [&](int st, int buf) {
+    char* base = smem + buf * kOpBytes;
+    const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
+#pragma unroll
+    for (int q = 0; q < QN; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (QN * wave + q) * 1024), 16, dofw[q] + koff, 0, 0,
+                                               0);
+  };
+  // Token-role operand (A), fragment-major in 16 x 32 fragments: fragment (b, s) at byte
+  // 1024 (b lda/32 + s), lane l's 16 bytes at 16 l (row 16 b + l % 16, k 32 s + 8 (l / 16)
+  // + 0..7). Blocks past the tile's rows fall outside the descriptor and read 0.
+  const __amdgpu_buffer_rsrc_t rt =
+      row_rsrc(reinterpret_cast<const char*>(g.A) + static_cast<int64_t>(m0 / 16) * (lda / 32) * 1024,
+               static_cast<uint32_t>((rows_h + 15) / 16) * static_cast<uint32_t>(lda / 32) * 1024u);
+  uint32_t roff[NJ16];
+#pragma unroll
+  for (int j = 0; j < NJ16; ++j)
+    roff[j] = static_cast<uint32_t>((wt * NJ16 + j) * (lda / 32)) * 1024u + 16u * static_cast<uint32_t>(lane);
+
+  // A-side fragment reads from LDS: row wv*128 + 16 i + lane % 16, 16-byte chunk
+  // 4 kk + lane / 16 of the row's 8; the swizzle depends on lane % 16 only.
+  const int sw = lm_swz(lane & 15);
+  int fo[KS16];
+#pragma unroll
+  for (int kk = 0; kk < KS16; ++kk) fo[kk] = 16 * ((4 * kk + (lane >> 4)) ^ sw);
+  const int offA = (wv * 128 + (lane & 15)) * ROWB;
+  bf16x8 af[2][NI16], ring[KS16][NJ16];
+  auto fload = [&](int set, int st, int kk) {
+    const char* base = smem + (st % NST) * kOpBytes + offA + fo[kk];
+#pragma unroll
+    for (int i = 0; i < NI16; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(base + i * 16 * ROWB);
+  };
+  auto ring_load = [&](int kk, int st) {
+#pragma unroll
+    for (int j = 0; j < NJ16; ++j)
+      ring[kk][j] = __builtin_bit_cast(bf16x8, buf_ld16<false>(rt, roff[j] + static_cast<uint32_t>(KS16 * st + kk) * 1024u));
+  };
+  f32x4 acc[NI16][NJ16];
+#pragma unroll
+  for (int i = 0; i < NI16; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ16; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
+  // j-major, so ring slot (kk, j) is free after its 8 MFMAs.
+  auto mf = [&](int set, int kk) {
+#pragma unroll
+    for (int j = 0; j < NJ16; ++j)
+#pragma unroll
+      for (int i = 0; i < NI16; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[set][i], ring[kk][j], acc[i][j], 0, 0, 0);
+  };
+  constexpr int kMf16 = NI16 * NJ16;
+  // Per k-step: the next k-step's 8 fragment reads between the first MFMAs (and the
+  // stage's direct-to-LDS loads after them when the k-step starts a buffer), the ring
+  // reloads after the last.
+  auto sched16 = [&](auto dma) {
+    constexpr int nd = decltype(dma)::value ? QN : 0;
+#pragma unroll
+    for (int q = 0; q < NI16; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < nd; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kMf16 - NI16 - nd, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, NJ16, 0);
+  };
+
+  // Pipeline: LDS buffer kb % 2 holds stage kb; the DMA of stage kb + 2 goes into it
+  // once every wave has issued its last read of stage kb (the barrier), one stage ahead
+  // of its use. The ring's slot kk is reloaded with stage kb + 1 after k-step kk's MFMAs.
+  // At the barrier of iteration kb the loads issued after stage kb + 1's DMA are the ring
+  // reloads of (kb, 1) and (kb + 1, 0): vmcnt(2 NJ16) leaves only those in flight.
+  const int nk = K / BK;
+  issue(0, 0);
+  ring_load(0, 0);
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  lm_barrier();
+  issue(min(1, nk - 1), 1);
+  ring_load(1, 0);
+  fload(0, 0, 0);
+  for (int kb = 0; kb < nk; ++kb) {
+    const int n1 = min(kb + 1, nk - 1);   // past the end: reloads of the last stage, unused
+    fload(1, kb, 1);
+    mf(0, 0);
+    ring_load(0, n1);
+    sched16(std::false_type{});
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(wait_vm(2 * NJ16));   // stage kb+1's LDS loads landed
+    lm_barrier();
+    issue(min(kb + 2, nk - 1), kb & 1);
+    fload(0, n1, 0);
+    mf(1, 1);
+    ring_load(1, n1);
+    sched16(std::true_type{});
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+
+  // C[v][t] (+)= the tile; rows past V and columns past N are not stored. For fixed
+  // (i, r) each 16-lane group writes 16 consecutive floats of one row.
+  float* C = g.C;
+  const int vw = v0 + wv * 128;
+#pragma unroll
+  for (int j = 0; j < NJ16; ++j) {
+    const int n = m0 + wt * TW + 16 * j + (lane & 15);
+    if (n >= N) continue;
+#pragma unroll
+    for (int i = 0; i < NI16; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int vr = vw + 16 * i + 4 * (lane >> 4) + r;
+        if (vr < V) {
+          float* pc = C + static_cast<int64_t>(vr) * ldc + n;
+          *pc = accumulate ? *pc + acc[i][j][r] : acc[i][j][r];
+        }
+      }
+  }
+}
+
 // Tiles of product prod at this launch's live sizes (the kLmGemm row / K counts and
 // the loss-head modes' token count are read from device memory).
 template <int MODE>
@@ -705,7 +881,10 @@ lm_tile_kernel(LmTileArgs a) {
   const int prod = i < per0 ? 0 : 1;
   const int p = prod == 0 ? xcd * per0 + i : xcd * per1 + (i - per0);
   if (p >= (prod == 0 ? t0 : t1)) return;
-  lm_tile<MODE, ATR, ECACHE, FRAG>(a, prod, p, smem);
+  if constexpr (FRAG && LM_MI16)
+    lm_tile16<MODE>(a, prod, p, smem);
+  else
+    lm_tile<MODE, ATR, ECACHE, FRAG>(a, prod, p, smem);
 }
 
 // 64 x 64 bf16 tiles staged in LDS for a transpose: rows of 66 elements (33 words),
@@ -950,11 +1129,11 @@ __global__ void __launch_bounds__(256) lm_transpose_kernel(LmTransposeArgs a) {
 }
 
 // The same transpose into the fragment-major layout of the tile kernel's FRAG operand
-// (the MFMA B fragment of destination rows 32 b + [0, 32) and k 16 s + [0, 16) at
-// fragment b ld_dst/16 + s, lane l holding row 32 b + l % 32 and k 16 s + 8 (l / 32) +
-// 0..7): destination rows are source columns, k runs over source rows. Each block's
-// 64 x 64 tile is eight whole fragments, written as 1 KB runs; k from R up to R
-// rounded to 64 is zero, and k past that is not written.
+// (the MFMA B fragment of destination rows FM b + [0, FM) and k FK s + [0, FK) at
+// fragment b ld_dst/FK + s, lane l holding row FM b + l % FM and k FK s + 8 (l / FM) +
+// 0..7; FM x FK = 16 x 32): destination rows are source columns, k runs over source
+// rows. Each block's 64 x 64 tile is eight whole fragments, written as 1 KB runs; k from
+// R up to R rounded to 64 is zero, and k past that is not written.
 __global__ void __launch_bounds__(256) lm_transpose_frag_kernel(LmTransposeArgs a) {
   __shared__ uint16_t t[64 * kTilePitch];
   const int R = a.rcount ? min(a.R, *a.rcount) : a.R;
@@ -972,13 +1151,15 @@ __global__ void __launch_bounds__(256) lm_transpose_frag_kernel(LmTransposeArgs 
   }
   __syncthreads();
   u32x4* dst = reinterpret_cast<u32x4*>(a.dst);
+  // Fragments of FM rows x FK k: FM = 16, FK = 32 for the 16x16x32 products, else 32 x 16.
+  constexpr int FM = LM_MI16 ? 16 : 32, FK = 512 / FM;
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int idx = tid + 256 * it, f = idx >> 6, l = idx & 63;   // fragment f of the 8, lane l
-    const int bl = f >> 2, sl = f & 3;
-    const int c = 32 * bl + (l & 31), r = 16 * sl + 8 * (l >> 5);
+    const int bl = f / (64 / FK), sl = f % (64 / FK);
+    const int c = FM * bl + l % FM, r = FK * sl + 8 * (l / FM);
     if (c0 + c < a.C && r0 + r < rend)
-      dst[(static_cast<int64_t>(c0 / 32 + bl) * (a.ld_dst / 16) + r0 / 16 + sl) * 64 + l] = tile_col8(t, r, c);
+      dst[(static_cast<int64_t>(c0 / FM + bl) * (a.ld_dst / FK) + r0 / FK + sl) * 64 + l] = tile_col8(t, r, c);
   }
 }
 

@@ -15,11 +15,11 @@
 // benchmark reports the best shape of each kind.
 //
 // MFMA probe (pcp_mfma_peak): the bf16 matrix rate that register-resident
-// v_mfma_f32_32x32x16_bf16 reaches with the tile kernel's wave shape and occupancy
-// (eight waves per workgroup, two per SIMD, a 128 x 64 block of accumulators per wave),
-// no memory traffic at all. The spec's 2.5 PFLOP/s assumes 2.4 GHz; under sustained
-// MFMA load the clock is held lower by the power limit, and this probe measures where
-// the rate settles.
+// v_mfma_f32_32x32x16_bf16 or v_mfma_f32_16x16x32_bf16 reaches with the tile kernel's
+// wave shape and occupancy (eight waves per workgroup, two per SIMD, a 128 x 64 block
+// of accumulators per wave), no memory traffic at all. The spec's 2.5 PFLOP/s assumes
+// 2.4 GHz; under sustained MFMA load the clock is held lower by the power limit, and
+// this probe measures where the rate settles for each shape.
 
 #include <hip/hip_runtime.h>
 
@@ -97,6 +97,7 @@ hipError_t launch_vpt(int vpt, const void* a, const void* b, void* c, int64_t n1
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaWaves = 8;
 
@@ -179,6 +180,72 @@ mfma_peak_kernel(int iters, uint32_t seed, float* out, uint64_t* clocks) {
   }
 }
 
+// The same with v_mfma_f32_16x16x32_bf16 (16384 flops each): operand sets s = 0, 1 of 8 A
+// fragments (element ((s*8 + i)*64 + lane)*8 + e) and 4 B fragments (8192 + ((s*4 + j)*64
+// + lane)*8 + e), 32 products acc[i][j] += A_s[i] B_s[j] per round (twice the flops of a
+// 32x32x16 round).
+__global__ void __launch_bounds__(64 * kMfmaWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+mfma_peak16_kernel(int iters, uint32_t seed, float* out, uint64_t* clocks) {
+  const int lane = threadIdx.x & 63;
+  bf16x8 a[2][8], b[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[s][i][e] = probe_bf16(seed, ((s * 8 + i) * 64 + lane) * 8 + e);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[s][j][e] = probe_bf16(seed, 8192 + ((s * 4 + j) * 64 + lane) * 8 + e);
+    }
+  }
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
+  __builtin_amdgcn_sched_barrier(0);
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_sched_barrier(0);
+  for (int it = 0; it < iters; it += 2) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s][i], b[s][j], acc[i][j], 0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_sched_barrier(0);
+  if (blockIdx.x == 0 && threadIdx.x < 64) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) out[((i * 4 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+  } else {
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum += acc[i][j][r];
+    if (sum != sum) out[lane] = sum;
+  }
+  if (clocks && threadIdx.x == 0) {
+    uint64_t* c = clocks + 4 * static_cast<int64_t>(blockIdx.x);
+    c[0] = t0;
+    c[1] = t1;
+    c[2] = r0;
+    c[3] = r1;
+  }
+}
+
 }  // namespace
 }  // namespace pcp
 
@@ -215,9 +282,11 @@ extern "C" int pcp_hbm_stream(pcp_ctx* ctx, int kind, int nontemporal, int vecto
   return PCP_OK;
 }
 
-extern "C" int pcp_mfma_peak(pcp_ctx* ctx, int workgroups, int iters, uint32_t seed, float* out, uint64_t* clocks,
-                             void* stream) {
+extern "C" int pcp_mfma_peak(pcp_ctx* ctx, int shape, int workgroups, int iters, uint32_t seed, float* out,
+                             uint64_t* clocks, void* stream) {
   using namespace pcp;
+  if (shape != 0 && shape != 1)
+    return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_mfma_peak: shape must be 0 (32x32x16) or 1 (16x16x32)");
   if (workgroups < 1 || workgroups > (1 << 20) || iters < 2 || iters % 2 != 0)
     return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_mfma_peak: workgroups must be in [1, 2^20] and iters even and >= 2");
   if (!out || (reinterpret_cast<uintptr_t>(out) & 3u) || (reinterpret_cast<uintptr_t>(clocks) & 7u))
@@ -227,8 +296,12 @@ extern "C" int pcp_mfma_peak(pcp_ctx* ctx, int workgroups, int iters, uint32_t s
   if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool timed = prof_begin(ctx, st);
-  mfma_peak_kernel<<<dim3(static_cast<unsigned>(workgroups)), dim3(64 * kMfmaWaves), 0, st>>>(iters, seed, out,
-                                                                                             clocks);
+  if (shape == 0)
+    mfma_peak_kernel<<<dim3(static_cast<unsigned>(workgroups)), dim3(64 * kMfmaWaves), 0, st>>>(iters, seed, out,
+                                                                                               clocks);
+  else
+    mfma_peak16_kernel<<<dim3(static_cast<unsigned>(workgroups)), dim3(64 * kMfmaWaves), 0, st>>>(iters, seed, out,
+                                                                                                 clocks);
   e = hipGetLastError();
   prof_end(ctx, st, timed);
   if (e != hipSuccess) return hip_fail(ctx, e, "pcp_mfma_peak launch");

@@ -449,16 +449,18 @@ def test_hbm_stream_argument_errors_without_device():
 
 
 def test_mfma_peak_argument_errors_without_device():
-    """pcp_mfma_peak rejects a bad grid, odd or too few rounds, a NULL or misaligned
-    buffer before any device work (the context check comes after them)."""
+    """pcp_mfma_peak rejects a bad shape or grid, odd or too few rounds, a NULL or
+    misaligned buffer before any device work (the context check comes after them)."""
     L = _lib.lib()
-    assert L.pcp_mfma_peak(None, 0, 2, 0, 0x1000, None, None) == -1
+    assert L.pcp_mfma_peak(None, 2, 1, 2, 0, 0x1000, None, None) == -1
+    assert "shape" in L.pcp_last_error(None).decode()
+    assert L.pcp_mfma_peak(None, 0, 0, 2, 0, 0x1000, None, None) == -1
     assert "workgroups" in L.pcp_last_error(None).decode()
-    assert L.pcp_mfma_peak(None, 1, 3, 0, 0x1000, None, None) == -1
-    assert L.pcp_mfma_peak(None, 1, 0, 0, 0x1000, None, None) == -1
-    assert L.pcp_mfma_peak(None, 1, 2, 0, None, None, None) == -1
+    assert L.pcp_mfma_peak(None, 1, 1, 3, 0, 0x1000, None, None) == -1
+    assert L.pcp_mfma_peak(None, 0, 1, 0, 0, 0x1000, None, None) == -1
+    assert L.pcp_mfma_peak(None, 0, 1, 2, 0, None, None, None) == -1
     assert "NULL" in L.pcp_last_error(None).decode()
-    assert L.pcp_mfma_peak(None, 1, 2, 0, 0x1002, None, None) == -1
-    assert L.pcp_mfma_peak(None, 1, 2, 0, 0x1000, 0x2004, None) == -1
-    assert L.pcp_mfma_peak(None, 1, 2, 0, 0x1000, 0x2000, None) == -1
+    assert L.pcp_mfma_peak(None, 1, 1, 2, 0, 0x1002, None, None) == -1
+    assert L.pcp_mfma_peak(None, 0, 1, 2, 0, 0x1000, 0x2004, None) == -1
+    assert L.pcp_mfma_peak(None, 1, 1, 2, 0, 0x1000, 0x2000, None) == -1
     assert "context is NULL" in L.pcp_last_error(None).decode()

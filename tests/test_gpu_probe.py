@@ -70,31 +70,40 @@ def _probe_bf16(seed: int, idx: np.ndarray) -> np.ndarray:
     return ((f.view(np.uint32) >> np.uint32(16)) << np.uint32(16)).view(np.float32).astype(np.float64)
 
 
-def test_mfma_peak_products_and_clocks():
-    """Workgroup 0's wave 0 accumulators equal iters/2 x (A_0 B_0^T + A_1 B_1^T) per 32 x 32
-    block, with A fragment lane l holding row l % 32 at k = 8 (l / 32) + e and the result
-    lane l column l % 32 at rows 8 (r / 4) + 4 (l / 32) + r % 4; the clocks advance."""
+@pytest.mark.parametrize("shape", [0, 1], ids=["32x32x16", "16x16x32"])
+def test_mfma_peak_products_and_clocks(shape):
+    """Workgroup 0's wave 0 accumulators equal iters/2 x (A_0 B_0^T + A_1 B_1^T) per block,
+    with the documented fragment layouts: an A (B) fragment lane holds row (column)
+    lane % M at k = 8 (lane / M) + e, and the result lane column lane % M at rows
+    8 (r / 4) + 4 (lane / 32) + r % 4 (M = 32) or 4 (lane / 16) + r (M = 16). The
+    LM-head tile kernel relies on the same layouts. The clocks advance."""
     ctx = default_context(0)
     wg, iters, seed = 3, 64, 12345
+    M, K = (32, 16) if shape == 0 else (16, 32)
+    NI, NJ, NR = (4, 2, 16) if shape == 0 else (8, 4, 4)
     out = torch.full((8192,), float("nan"), dtype=torch.float32, device=DEV)
     clocks = torch.zeros((wg, 4), dtype=torch.int64, device=DEV)
-    print(f"mfma probe: workgroups={wg} iters={iters}", flush=True)
-    check(lib().pcp_mfma_peak(ctx.handle, wg, iters, seed, out.data_ptr(), clocks.data_ptr(), None), ctx.handle)
+    print(f"mfma probe: shape={shape} workgroups={wg} iters={iters}", flush=True)
+    check(lib().pcp_mfma_peak(ctx.handle, shape, wg, iters, seed, out.data_ptr(), clocks.data_ptr(), None),
+          ctx.handle)
     torch.cuda.synchronize()
-    got = out.cpu().numpy().astype(np.float64).reshape(4, 2, 16, 64)
+    got = out.cpu().numpy().astype(np.float64).reshape(NI, NJ, NR, 64)
     lane, e = np.arange(64)[:, None], np.arange(8)[None, :]
-    k = 8 * (lane // 32) + e                                     # [64, 8]
-    exp = np.zeros((4, 2, 32, 32))
+    k = 8 * (lane // M) + e                                      # [64, 8]
+    rows = np.broadcast_to(lane % M, k.shape)
+    boff = 4096 if shape == 0 else 8192
+    exp = np.zeros((NI, NJ, M, M))
     for s in range(2):
-        for i in range(4):
-            A = np.zeros((32, 16))
-            A[np.broadcast_to(lane % 32, k.shape), k] = _probe_bf16(seed, ((s * 4 + i) * 64 + lane) * 8 + e)
-            for j in range(2):
-                B = np.zeros((32, 16))
-                B[np.broadcast_to(lane % 32, k.shape), k] = _probe_bf16(seed, 4096 + ((s * 2 + j) * 64 + lane) * 8 + e)
+        for i in range(NI):
+            A = np.zeros((M, K))
+            A[rows, k] = _probe_bf16(seed, ((s * NI + i) * 64 + lane) * 8 + e)
+            for j in range(NJ):
+                B = np.zeros((M, K))
+                B[rows, k] = _probe_bf16(seed, boff + ((s * NJ + j) * 64 + lane) * 8 + e)
                 exp[i, j] += (iters // 2) * (A @ B.T)
-    r, ln = np.arange(16)[:, None], np.arange(64)[None, :]
-    want = exp[:, :, 8 * (r // 4) + 4 * (ln // 32) + r % 4, ln % 32]   # [4, 2, 16, 64]
+    r, ln = np.arange(NR)[:, None], np.arange(64)[None, :]
+    rrow = 8 * (r // 4) + 4 * (ln // 32) + r % 4 if shape == 0 else 4 * (ln // 16) + r
+    want = exp[:, :, rrow, ln % M]                               # [NI, NJ, NR, 64]
     err = np.abs(got - want).max()
     assert err <= 1e-4 * np.abs(want).max(), err
     c = clocks.cpu().numpy()
@@ -105,5 +114,5 @@ def test_mfma_peak_rejects_odd_iters_on_device():
     ctx = default_context(0)
     out = torch.zeros(8192, dtype=torch.float32, device=DEV)
     with pytest.raises(PcpError) as e:
-        check(lib().pcp_mfma_peak(ctx.handle, 1, 3, 0, out.data_ptr(), None, None), ctx.handle)
+        check(lib().pcp_mfma_peak(ctx.handle, 1, 1, 3, 0, out.data_ptr(), None, None), ctx.handle)
     assert e.value.code == -1 and "iters" in str(e.value)
