@@ -671,83 +671,122 @@ constexpr int NJ16 = TW / 16;   // 16-column token blocks per wave
 constexpr int KS16 = BK / 32;   // 32-deep k-steps per stage
 }  // namespace lm
 
-// The products' tile (kLmGemm, fragment-major token operand) on
-// v_mfma_f32_16x16x32_bf16. Same tile, waves, stages and operand paths as lm_tile's
-// FRAG instances; each wave's 128 x 64 block is 8 x 4 products of 16 x 16 (128
-// accumulators), two 32-deep k-steps per stage. Under the power limit this shape runs
-// the pipes at a higher clock than 32x32x16 for the same work (the register-resident
-// probe: 1.98 against 1.80 GHz at the same MFMA occupancy), as each instruction
-// reduces twice as deep per accumulator update.
+// A tile on v_mfma_f32_16x16x32_bf16: the forward (kLmFwd, both operands through LDS)
+// and the products (kLmGemm with a fragment-major token operand). Same tile, waves,
+// stages and operand paths as lm_tile; each wave's 128 x 64 block is 8 x 4 products of
+// 16 x 16 (128 accumulators), two 32-deep k-steps per stage. Under the power limit this
+// shape runs the pipes at a higher clock than 32x32x16 for the same work (the
+// register-resident probe: 1.93-1.98 against 1.72-1.80 GHz at the same MFMA occupancy),
+// as each instruction reduces twice as deep per accumulator update.
 // Fragment layouts (pinned by the MFMA probe's test): an operand lane holds row
 // lane % 16 at k = 8 (lane / 16) + 0..7; the result lane holds column lane % 16 at rows
 // 4 (lane / 16) + 0..3.
-template <int MODE>
+template <int MODE, bool ECACHE>
 __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, char* smem) {
   using namespace lm;
-  static_assert(MODE == kLmGemm, "16x16x32 tiles: the fragment-major products");
-  const LmTileArgs::Gemm& g = a.gemm[prod];
-  int V = g.V, K = g.K, nvt = g.nvt;
-  const int N = g.N, lda = g.lda, ldb = g.ldb, ldc = g.ldc, accumulate = g.accumulate;
-  if (g.vcount) {
-    V = min(V, *g.vcount);
-    nvt = (V + BV - 1) / BV;
+  static_assert(MODE == kLmGemm || MODE == kLmFwd, "16x16x32 tiles: the forward and the fragment-major products");
+  constexpr bool FWD = MODE == kLmFwd;
+  const LmTileArgs::Gemm& g = a.gemm[FWD ? 0 : prod];
+  const void* opA = FWD ? a.A : g.A;
+  const void* opB = FWD ? (prod == 1 ? a.B2 : a.B) : g.B;
+  int N, V, K, nvt, ntt, gm, lda, ldb, vt0 = 0;
+  if constexpr (FWD) {
+    // Tiles over the live tokens only (the grid covers all N).
+    N = min(a.N, *a.count);
+    V = a.V;
+    K = lda = ldb = a.H;
+    ntt = (N + BT - 1) / BT;
+    nvt = a.nvt;
+    gm = lm_group_m(MODE, ntt);
+    vt0 = a.vt0;
+  } else {
+    N = g.N;
+    V = g.V;
+    K = g.K;
+    lda = g.lda;
+    ldb = g.ldb;
+    nvt = g.nvt;
+    ntt = g.ntt;
+    gm = g.group_m;
+    if (g.vcount) {
+      V = min(V, *g.vcount);
+      nvt = (V + BV - 1) / BV;
+    }
+    if (g.kcount) K = min(K, (min(K, *g.kcount) + BK - 1) / BK * BK);
   }
-  if (g.kcount) K = min(K, (min(K, *g.kcount) + BK - 1) / BK * BK);
   int tm, tn;
-  lm_tile_of(p, g.ntt, nvt, g.group_m, tm, tn);
-  const int m0 = tm * BT, v0 = tn * BV;
+  lm_tile_of(p, ntt, nvt, gm, tm, tn);
+  const int m0 = tm * BT, v0 = (vt0 + tn) * BV;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wv = wave / WT, wt = wave % WT;
 
-  // Vocab-role operand (B, K-contiguous rows) through LDS as in lm_tile, one 32 KB
-  // buffer per stage.
-  const uint32_t wbytes = static_cast<uint32_t>(ldb) * 2u;
+  // Operands through LDS as in lm_tile: the vocab role (B) always, the token role (A)
+  // for the forward. A stage buffer holds one operand (products) or both (forward).
+  constexpr int kBuf = FWD ? kStageBytes : kOpBytes;
+  const uint32_t wbytes = static_cast<uint32_t>(ldb) * 2u, hbytes = static_cast<uint32_t>(lda) * 2u;
   const int rows_w = min(BV, V - v0), rows_h = min(BT, N - m0);
   const __amdgpu_buffer_rsrc_t rw =
-      row_rsrc(reinterpret_cast<const char*>(g.B) + static_cast<int64_t>(v0) * wbytes, rows_w * wbytes);
-  uint32_t dofw[QN];
+      row_rsrc(reinterpret_cast<const char*>(opB) + static_cast<int64_t>(v0) * wbytes, rows_w * wbytes);
+  const __amdgpu_buffer_rsrc_t rh =
+      row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0) * hbytes, FWD ? rows_h * hbytes : 0u);
+  uint32_t dofw[QN], dofh[QN];
 #pragma unroll
   for (int q = 0; q < QN; ++q) {
     const int row = 8 * (QN * wave + q) + (lane >> 3);
-    dofw[q] = static_cast<uint32_t>(row) * wbytes + 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
+    const uint32_t c16 = 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
+    dofw[q] = static_cast<uint32_t>(row) * wbytes + c16;
+    dofh[q] = static_cast<uint32_t>(row) * hbytes + c16;
   }
   auto issue = [&](int st, int buf) {
-    char* base = smem + buf * kOpBytes;
+    char* base = smem + buf * kBuf;
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
 #pragma unroll
-    for (int q = 0; q < QN; ++q)
+    for (int q = 0; q < QN; ++q) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (QN * wave + q) * 1024), 16, dofw[q] + koff, 0, 0,
                                                0);
+      if constexpr (FWD)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (QN * wave + q) * 1024), 16,
+                                                 dofh[q] + koff, 0, 0, 0);
+    }
   };
-  // Token-role operand (A), fragment-major in 16 x 32 fragments: fragment (b, s) at byte
-  // 1024 (b lda/32 + s), lane l's 16 bytes at 16 l (row 16 b + l % 16, k 32 s + 8 (l / 16)
-  // + 0..7). Blocks past the tile's rows fall outside the descriptor and read 0.
+  // Products: the token-role operand fragment-major in 16 x 32 fragments: fragment (b, s)
+  // at byte 1024 (b lda/32 + s), lane l's 16 bytes at 16 l (row 16 b + l % 16, k 32 s +
+  // 8 (l / 16) + 0..7). Blocks past the tile's rows fall outside the descriptor and read 0.
   const __amdgpu_buffer_rsrc_t rt =
-      row_rsrc(reinterpret_cast<const char*>(g.A) + static_cast<int64_t>(m0 / 16) * (lda / 32) * 1024,
-               static_cast<uint32_t>((rows_h + 15) / 16) * static_cast<uint32_t>(lda / 32) * 1024u);
+      row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0 / 16) * (lda / 32) * 1024,
+               FWD ? 0u : static_cast<uint32_t>((rows_h + 15) / 16) * static_cast<uint32_t>(lda / 32) * 1024u);
   uint32_t roff[NJ16];
 #pragma unroll
   for (int j = 0; j < NJ16; ++j)
     roff[j] = static_cast<uint32_t>((wt * NJ16 + j) * (lda / 32)) * 1024u + 16u * static_cast<uint32_t>(lane);
 
-  // A-side fragment reads from LDS: row wv*128 + 16 i + lane % 16, 16-byte chunk
+  // Fragment reads from LDS: row (wv*128 | wt*64) + 16 i + lane % 16, 16-byte chunk
   // 4 kk + lane / 16 of the row's 8; the swizzle depends on lane % 16 only.
   const int sw = lm_swz(lane & 15);
   int fo[KS16];
 #pragma unroll
   for (int kk = 0; kk < KS16; ++kk) fo[kk] = 16 * ((4 * kk + (lane >> 4)) ^ sw);
-  const int offA = (wv * 128 + (lane & 15)) * ROWB;
-  bf16x8 af[2][NI16], ring[KS16][NJ16];
+  const int offA = (wv * 128 + (lane & 15)) * ROWB, offB = kOpBytes + (wt * TW + (lane & 15)) * ROWB;
+  // af: vocab-role fragments; bt: token-role fragments (from LDS for the forward, the
+  // register ring for the products; slot kk holds k-step kk of the current stage).
+  bf16x8 af[2][NI16], bt[KS16][NJ16];
   auto fload = [&](int set, int st, int kk) {
-    const char* base = smem + (st % NST) * kOpBytes + offA + fo[kk];
+    const char* base = smem + (st % NST) * kBuf + fo[kk];
 #pragma unroll
-    for (int i = 0; i < NI16; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(base + i * 16 * ROWB);
+    for (int i = 0; i < NI16; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(base + offA + i * 16 * ROWB);
+    if constexpr (FWD) {
+#pragma unroll
+      for (int j = 0; j < NJ16; ++j) bt[kk][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 16 * ROWB);
+    }
   };
   auto ring_load = [&](int kk, int st) {
+    if constexpr (!FWD) {
 #pragma unroll
-    for (int j = 0; j < NJ16; ++j)
-      ring[kk][j] = __builtin_bit_cast(bf16x8, buf_ld16<false>(rt, roff[j] + static_cast<uint32_t>(KS16 * st + kk) * 1024u));
+      for (int j = 0; j < NJ16; ++j)
+        bt[kk][j] =
+            __builtin_bit_cast(bf16x8, buf_ld16<false>(rt, roff[j] + static_cast<uint32_t>(KS16 * st + kk) * 1024u));
+    }
   };
   f32x4 acc[NI16][NJ16];
 #pragma unroll
@@ -756,22 +795,24 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
     for (int j = 0; j < NJ16; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
-  // j-major, so ring slot (kk, j) is free after its 8 MFMAs.
+  // j-major, so token slot (kk, j) is free after its 8 MFMAs.
   auto mf = [&](int set, int kk) {
 #pragma unroll
     for (int j = 0; j < NJ16; ++j)
 #pragma unroll
       for (int i = 0; i < NI16; ++i)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[set][i], ring[kk][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[set][i], bt[kk][j], acc[i][j], 0, 0, 0);
   };
   constexpr int kMf16 = NI16 * NJ16;
-  // Per k-step: the next k-step's 8 fragment reads between the first MFMAs (and the
+  constexpr int kRd16 = NI16 + (FWD ? NJ16 : 0);     // fragment reads per k-step
+  constexpr int kLd16 = FWD ? 2 * QN : QN;          // direct-to-LDS loads per stage
+  // Per k-step: the next k-step's fragment reads between the first MFMAs (and the
   // stage's direct-to-LDS loads after them when the k-step starts a buffer), the ring
   // reloads after the last.
   auto sched16 = [&](auto dma) {
-    constexpr int nd = decltype(dma)::value ? QN : 0;
+    constexpr int nd = decltype(dma)::value ? kLd16 : 0;
 #pragma unroll
-    for (int q = 0; q < NI16; ++q) {
+    for (int q = 0; q < kRd16; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
@@ -780,15 +821,17 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, kMf16 - NI16 - nd, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, NJ16, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, kMf16 - kRd16 - nd, 0);
+    if constexpr (!FWD) __builtin_amdgcn_sched_group_barrier(0x020, NJ16, 0);
   };
+  static_assert(kRd16 + kLd16 <= kMf16, "schedule");
 
   // Pipeline: LDS buffer kb % 2 holds stage kb; the DMA of stage kb + 2 goes into it
   // once every wave has issued its last read of stage kb (the barrier), one stage ahead
-  // of its use. The ring's slot kk is reloaded with stage kb + 1 after k-step kk's MFMAs.
-  // At the barrier of iteration kb the loads issued after stage kb + 1's DMA are the ring
-  // reloads of (kb, 1) and (kb + 1, 0): vmcnt(2 NJ16) leaves only those in flight.
+  // of its use. The products reload ring slot kk with stage kb + 1 after k-step kk's
+  // MFMAs. At the barrier of iteration kb the loads issued after stage kb + 1's DMA are
+  // the ring reloads of (kb, 1) and (kb + 1, 0) (none in the forward): vmcnt(2 NJ16),
+  // or vmcnt(0), leaves only those in flight.
   const int nk = K / BK;
   issue(0, 0);
   ring_load(0, 0);
@@ -804,34 +847,131 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
     ring_load(0, n1);
     sched16(std::false_type{});
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(wait_vm(2 * NJ16));   // stage kb+1's LDS loads landed
+    __builtin_amdgcn_s_waitcnt(FWD ? kWaitVm0 : wait_vm(2 * NJ16));   // stage kb+1's LDS loads landed
     lm_barrier();
-    issue(min(kb + 2, nk - 1), kb & 1);
-    fload(0, n1, 0);
+    // The forward's 8 direct-to-LDS loads go between the k-step's MFMAs after its
+    // fragment reads; the products issue their 4 first (measured faster each way).
+    if constexpr (FWD) {
+      fload(0, n1, 0);
+      issue(min(kb + 2, nk - 1), kb & 1);
+    } else {
+      issue(min(kb + 2, nk - 1), kb & 1);
+      fload(0, n1, 0);
+    }
     mf(1, 1);
     ring_load(1, n1);
     sched16(std::true_type{});
   }
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
-  // C[v][t] (+)= the tile; rows past V and columns past N are not stored. For fixed
-  // (i, r) each 16-lane group writes 16 consecutive floats of one row.
-  float* C = g.C;
-  const int vw = v0 + wv * 128;
+  const int vw = v0 + wv * 128;   // first vocab row of this wave
+  const int grp = lane >> 4;      // the lane's 4-row group of each 16-row block
+  if constexpr (FWD) {
+    // Per token column: (max * log2e, sum 2^(x*log2e - max*log2e)) over this wave's
+    // 128 vocab rows (32 in-lane, the rest in lanes l ^ 16, l ^ 32, l ^ 48), and the
+    // target logit. Vocab rows past V (last tile only) become -inf, whose term is 0.
+    const bool any_v = vw < a.V;
+    const int vlim = a.V - vw;
+    if (vw + 128 > V) {
 #pragma unroll
-  for (int j = 0; j < NJ16; ++j) {
-    const int n = m0 + wt * TW + 16 * j + (lane & 15);
-    if (n >= N) continue;
+      for (int i = 0; i < NI16; ++i)
 #pragma unroll
-    for (int i = 0; i < NI16; ++i)
+        for (int j = 0; j < NJ16; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int vr = vw + 16 * i + 4 * (lane >> 4) + r;
-        if (vr < V) {
-          float* pc = C + static_cast<int64_t>(vr) * ldc + n;
-          *pc = accumulate ? *pc + acc[i][j][r] : acc[i][j][r];
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = 16 * i + 4 * grp + r < vlim ? acc[i][j][r] : kNegInf;
+    }
+    float ref[NJ16];
+#pragma unroll
+    for (int j = 0; j < NJ16; ++j) {
+      float mx = kNegInf;
+#pragma unroll
+      for (int i = 0; i < NI16; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, acc[i][j][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      ref[j] = mx * kLog2e;   // the block's max * log2e; ms_ref maps -inf to 0 below
+    }
+    // Two token blocks at a time, so each pair's accumulators die before the next.
+#pragma unroll
+    for (int jj = 0; jj < NJ16; jj += 2) {
+      float sum[2] = {0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < NI16; ++i) {
+        uint32_t pk[2][2];
+#pragma unroll
+        for (int jo = 0; jo < 2; ++jo) {
+          float ev[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            ev[r] = hw_exp2(fmaf(acc[i][jj + jo][r], kLog2e, -ms_ref(ref[jj + jo])));
+            sum[jo] += ev[r];
+          }
+          pk[jo][0] = pack2<F16T>(ev[0], ev[1]);
+          pk[jo][1] = pack2<F16T>(ev[2], ev[3]);
+        }
+        if (ECACHE && prod == 0) {
+          // Softmax cache: ecache[n][v] = f16(2^(x*log2e - ref)), token-major rows of lde
+          // (vocab past V holds 0). The lane's terms of block (i, j) are vocab rows
+          // 16 i + 4 grp + 0..3 of token column 16 j + lane % 16. One v_permlane16_swap
+          // per register trades the odd groups' block-jj terms with the even groups'
+          // block-(jj+1) terms, after which lanes of an even group hold 8 consecutive rows
+          // (16 i + 8 (grp / 2) + 0..7) of token 16 jj + lane % 16, and of an odd group the
+          // same rows of token 16 (jj + 1) + lane % 16: one 16-byte store each.
+          const auto lo = __builtin_amdgcn_permlane16_swap(pk[0][0], pk[1][0], false, false);
+          const auto hi = __builtin_amdgcn_permlane16_swap(pk[0][1], pk[1][1], false, false);
+          const int n = m0 + wt * TW + 16 * (jj + (grp & 1)) + (lane & 15);
+          const int64_t c = vw + 16 * i + 8 * (grp >> 1);
+          if (n < N && c < a.lde) {
+            const u32x4 w = {lo[0], hi[0], lo[1], hi[1]};
+            *reinterpret_cast<u32x4*>(a.ecache + static_cast<int64_t>(n) * a.lde + c) = w;
+          }
         }
       }
+#pragma unroll
+      for (int jo = 0; jo < 2; ++jo) {
+        const int j = jj + jo;
+        float s = sum[jo];
+        s += __shfl_xor(s, 16);
+        s += __shfl_xor(s, 32);
+        const int n = m0 + wt * TW + 16 * j + (lane & 15);
+        if (n < N && any_v) {
+          if (grp == 0)
+            (prod ? a.part2 : a.part)[static_cast<int64_t>(n) * a.ldp + vw / kPart] = make_float2(ref[j], s);
+          const int64_t rel = lm_id(a, n) - vw;
+          if (rel >= 0 && rel < 128) {
+            const int isel = static_cast<int>(rel) >> 4, gsel = (static_cast<int>(rel) >> 2) & 3;
+            const int rsel = static_cast<int>(rel) & 3;
+            float val = 0.f;
+#pragma unroll
+            for (int i = 0; i < NI16; ++i)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) val = (i == isel && r == rsel) ? acc[i][j][r] : val;
+            if (grp == gsel) (prod ? a.tgt2 : a.tgt)[n] = val;
+          }
+        }
+      }
+    }
+  } else {
+    // C[v][t] (+)= the tile; rows past V and columns past N are not stored. For fixed
+    // (i, r) each 16-lane group writes 16 consecutive floats of one row.
+    float* C = g.C;
+    const int ldc = g.ldc, accumulate = g.accumulate;
+#pragma unroll
+    for (int j = 0; j < NJ16; ++j) {
+      const int n = m0 + wt * TW + 16 * j + (lane & 15);
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < NI16; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int vr = vw + 16 * i + 4 * grp + r;
+          if (vr < V) {
+            float* pc = C + static_cast<int64_t>(vr) * ldc + n;
+            *pc = accumulate ? *pc + acc[i][j][r] : acc[i][j][r];
+          }
+        }
+    }
   }
 }
 
@@ -871,7 +1011,10 @@ lm_tile_kernel(LmTileArgs a) {
     const int per = (tt + 7) / 8;
     const int p = xcd * per + i;
     if (i >= per || p >= tt) return;
-    lm_tile<MODE, ATR, ECACHE, FRAG>(a, p % nm, p / nm, smem);
+    if constexpr (LM_MI16)
+      lm_tile16<MODE, ECACHE>(a, p % nm, p / nm, smem);
+    else
+      lm_tile<MODE, ATR, ECACHE, FRAG>(a, p % nm, p / nm, smem);
     return;
   }
   const int t0 = lm_total_tiles<MODE>(a, 0);
@@ -882,7 +1025,7 @@ lm_tile_kernel(LmTileArgs a) {
   const int p = prod == 0 ? xcd * per0 + i : xcd * per1 + (i - per0);
   if (p >= (prod == 0 ? t0 : t1)) return;
   if constexpr (FRAG && LM_MI16)
-    lm_tile16<MODE>(a, prod, p, smem);
+    lm_tile16<MODE, false>(a, prod, p, smem);
   else
     lm_tile<MODE, ATR, ECACHE, FRAG>(a, prod, p, smem);
 }
