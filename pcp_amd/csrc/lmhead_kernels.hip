@@ -3,8 +3,8 @@
 // logits[n, v] = sum_h hidden[n, h] * W[v, h] is a dense contraction; the loss
 // head only needs, per token, the log-sum-exp over v and the logit of its target
 // (forward), and dlogits = c_n * (onehot - softmax) (backward). The tile kernel
-// computes a 256 x 256 logits tile on v_mfma_f32_32x32x16_bf16 and reduces it in
-// its epilogue, so full logits never exist in HBM:
+// computes a 256 x 256 logits tile on bf16 MFMAs and reduces it in its epilogue, so
+// full logits never exist in HBM:
 //   kLmFwd  -> per (token, kLmPart vocab entries) partial (max, sum 2^(x*log2e - max))
 //              and the target logit when the target falls in the tile, for the policy
 //              and (n_model = 2) the reference model in one launch; with ECACHE also
@@ -15,6 +15,8 @@
 //              operands (dhidden and dW from the cached dlogits and their transpose);
 //              with FRAG the token-role operand A is stored fragment-major (written by
 //              lm_transpose_frag_kernel) and read straight into registers.
+// The forward and the FRAG products run on v_mfma_f32_16x16x32_bf16 (lm_tile16), the
+// backward recompute and the other products on v_mfma_f32_32x32x16_bf16 (lm_tile).
 //
 // Reference: the LM head and loss of tools/export_qwen_forward.py:146-163
 // (self.model.lm_head(hidden) then F.cross_entropy), and matmulVJP
@@ -145,21 +147,22 @@ __device__ __forceinline__ void lm_barrier() {
 // lane l holds token column l%32 and vocab rows 8*(r/4) + 4*(l/32) + r%4, r < 16.
 // Operands stream global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging)
 // through two stages of BK hidden columns.
+// This 32x32x16 tile serves the chunked backward (kLmBwd recompute tiles and their
+// products, whose token operand may be K-major) and the plain products; the forward
+// and the cached backward's products run on lm_tile16 below.
 // ATR (kLmGemm): the token-role operand is stored K-major and its fragments are read
 // with ds_read_b64_tr_b16 (see below).
-// FRAG (kLmGemm): the token-role operand is stored fragment-major and loaded straight
-// into VGPRs; only the vocab-role operand goes through LDS (see below).
-// ECACHE (kLmFwd): the epilogue of model 0 also stores the softmax terms (see there).
-// Tile p of product prod (kLmGemm), or of model prod (kLmFwd), called by lm_tile_kernel.
-template <int MODE, bool ATR, bool ECACHE, bool FRAG>
+// Tile p of product prod (kLmGemm), or of the vocab chunk (kLmBwd), called by
+// lm_tile_kernel.
+template <int MODE, bool ATR>
 __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, char* smem) {
   using namespace lm;
-  static_assert(!FRAG || (MODE == kLmGemm && !ATR), "fragment-major operands: kLmGemm, K-contiguous roles");
+  static_assert(MODE == kLmBwd || MODE == kLmGemm, "32x32x16 tiles: the backward recompute and plain products");
 
   // The product: the loss-head modes read rows of H elements of hidden (A) and W (B);
   // kLmGemm takes one of its (up to) two products.
   const void* opA = a.A;
-  const void* opB = MODE == kLmFwd && prod == 1 ? a.B2 : a.B;
+  const void* opB = a.B;
   int N = a.N, V = a.V, K = a.H, lda = a.H, ldb = a.H, ntt = a.ntt, nvt = a.nvt, gm = 1, vt0 = a.vt0;
   float* C = nullptr;
   int ldc = 0, accumulate = 0, transpose_c = 0, krows_a = 0;
@@ -240,19 +243,6 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
       dofh[q] = static_cast<uint32_t>(row) * hbytes + c16;
     }
   }
-  // Fragment-major token operand (FRAG): the 1 KB MFMA B fragment of rows 32 b + [0, 32)
-  // and k 16 s + [0, 16) lies at byte 1024 (b lda/16 + s) (lane l's 16 bytes at 16 l:
-  // row 32 b + l % 32, k 16 s + 8 (l / 32) + 0..7), so a wave loads each of its
-  // fragments with one fully coalesced 1 KB load. Blocks past the tile's rows fall
-  // outside the descriptor and read 0; the writer zero-fills rows past N in a block.
-  const __amdgpu_buffer_rsrc_t rt =
-      FRAG ? row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0 / 32) * (lda / 16) * 1024,
-                      static_cast<uint32_t>((rows_h + 31) / 32) * static_cast<uint32_t>(lda / 16) * 1024u)
-           : rh;
-  uint32_t roff[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j)
-    roff[j] = static_cast<uint32_t>((wt * NJ + j) * (lda / 16)) * 1024u + 16u * static_cast<uint32_t>(lane);
   auto issue = [&](int st, int buf) {
     char* base = smem + buf * kStageBytes;
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
@@ -260,9 +250,8 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
 #pragma unroll
     for (int q = 0; q < QN; ++q) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (QN * wave + q) * 1024), 16, dofw[q] + koff, 0, 0, 0);
-      if constexpr (!FRAG)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (QN * wave + q) * 1024), 16,
-                                                 dofh[q] + kofh, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (QN * wave + q) * 1024), 16, dofh[q] + kofh,
+                                               0, 0, 0);
     }
   };
 
@@ -305,7 +294,7 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
             (__attribute__((address_space(3))) v4i16*)LM_LDS(tb + offBt[j] + 4 * 512));
         bfr[set][j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
-    } else if constexpr (!FRAG) {
+    } else {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) bfr[set][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 32 * ROWB);
     }
@@ -339,75 +328,6 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   // behind it whenever the memory pipeline pushed back; one load (or fragment read)
   // between consecutive MFMAs measured 6% faster on config 5.
   const int nk = K / BK;
-  if constexpr (FRAG) {
-    // The token operand's fragments for one stage sit in a ring of registers: k-step kk
-    // of stage kb reads slot kk, and right after its MFMAs the slot is reloaded with
-    // k-step kk of stage kb + 1, about one stage ahead of its use. Only the vocab-role
-    // operand goes through LDS, so the stage barrier waits for its direct-to-LDS loads
-    // alone (the ring loads issued after them may still be in flight). Measured at
-    // configuration 5 against the same products with both operands through LDS,
-    // interleaved on one box: products launch 19.93-19.96 -> 18.35-18.46 ms, step
-    // 41.82-41.89 -> 40.29-40.40 ms. The forward gained nothing from the same scheme
-    // (18.5-19.2 against 19.0-19.9 ms over two boxes, within the spread), so it keeps
-    // both operands in LDS.
-    bf16x8 ring[4][NJ];
-    auto ring_load = [&](int kk, int st) {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        ring[kk][j] =
-            __builtin_bit_cast(bf16x8, buf_ld16<false>(rt, roff[j] + static_cast<uint32_t>(4 * st + kk) * 1024u));
-    };
-    // k-step kk's MFMAs, j-major so slot (kk, 0) is free after the first four.
-    auto mf = [&](int set, int kk) {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], ring[kk][j], acc[i][j], 0, 0, 0);
-    };
-    // Per k-step: the stage's direct-to-LDS loads (first k-step), then the 4 fragment
-    // reads of the next k-step between the first MFMAs, then the ring reloads.
-    auto sched_f = [&](bool dma) {
-      if (dma) __builtin_amdgcn_sched_group_barrier(0x020, QN, 0);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4 * NJ - 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, NJ, 0);
-    };
-    issue(0, 0);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) ring_load(kk, 0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    lm_barrier();
-    fload(0, 0, 0);
-    for (int kb = 0; kb < nk; ++kb) {
-      const int nx = min(kb + 1, nk - 1);   // past the end: reloads of the last stage, unused
-      issue(nx, (kb + 1) & 1);
-      fload(1, kb, 1);
-      mf(0, 0);
-      ring_load(0, nx);
-      sched_f(true);
-      fload(0, kb, 2);
-      mf(1, 1);
-      ring_load(1, nx);
-      sched_f(false);
-      fload(1, kb, 3);
-      mf(0, 2);
-      ring_load(2, nx);
-      sched_f(false);
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(wait_vm(3 * NJ));   // stage kb+1's LDS loads landed
-      lm_barrier();
-      fload(0, nx, 0);
-      mf(1, 3);
-      ring_load(3, nx);
-      sched_f(false);
-    }
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-  } else {
   issue(0, 0);
   __builtin_amdgcn_s_waitcnt(kWaitStage);
   lm_barrier();
@@ -461,91 +381,13 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
   }
   // Drain the trailing loads before any LDS reuse (the backward epilogue).
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
-  }
 
   const int vw = v0 + wv * 128;                 // first vocab row of this wave
   const int half = lane >> 5;
-  const bool full_v = vw + 128 <= V;
   // Vocab row of acc[i][*][r] relative to vw.
   auto vrow = [&](int i, int r) { return 32 * i + 8 * (r >> 2) + 4 * half + (r & 3); };
 
-  if constexpr (MODE == kLmFwd) {
-    // Per token column: (max * log2e, sum 2^(x*log2e - max*log2e)) over this wave's
-    // 128 vocab rows (64 in-lane + the partner lane l^32), and the target logit.
-    const bool any_v = vw < a.V;
-    // Vocab rows past V (last tile only) take no part: their logits become -inf,
-    // whose 2^(...) term is 0. Branch-free selects; full tiles skip them.
-    const int vlim = a.V - vw;
-    if (!full_v) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] = vrow(i, r) < vlim ? acc[i][j][r] : kNegInf;
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int n = m0 + wt * TW + 32 * j + (lane & 31);
-      float mx = kNegInf;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[i][j][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m2 = mx * kLog2e;
-      const float ref = ms_ref(m2);
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float ev[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          ev[r] = hw_exp2(fmaf(acc[i][j][r], kLog2e, -ref));
-          s += ev[r];
-        }
-        if (ECACHE && prod == 0) {
-          // Softmax cache: ecache[n][v] = f16(2^(x*log2e - ref)), token-major rows of lde
-          // (vocab past V holds 0). The lane's 16 terms are vocab rows 8q + 4*half + 0..3
-          // (q < 4) of this 32-row block; one v_permlane32_swap per register pair trades
-          // groups with the partner lane l^32, after which the lane holds 8 consecutive
-          // rows (16p + 8*half + 0..7 for pair p) and writes them as one 16-byte store.
-          uint32_t g[8];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            g[2 * q] = pack2<F16T>(ev[4 * q], ev[4 * q + 1]);
-            g[2 * q + 1] = pack2<F16T>(ev[4 * q + 2], ev[4 * q + 3]);
-          }
-#pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            // Lanes 32-63 of the first operand trade with lanes 0-31 of the second.
-            const auto lo = __builtin_amdgcn_permlane32_swap(g[4 * p], g[4 * p + 2], false, false);
-            const auto hi = __builtin_amdgcn_permlane32_swap(g[4 * p + 1], g[4 * p + 3], false, false);
-            const int64_t c = vw + 32 * i + 16 * p + 8 * half;
-            if (n < N && c < a.lde) {
-              const u32x4 w = {lo[0], hi[0], lo[1], hi[1]};
-              *reinterpret_cast<u32x4*>(a.ecache + static_cast<int64_t>(n) * a.lde + c) = w;
-            }
-          }
-        }
-      }
-      s += __shfl_xor(s, 32);
-      if (n < N && any_v) {
-        if (half == 0) (prod ? a.part2 : a.part)[static_cast<int64_t>(n) * a.ldp + vw / kPart] = make_float2(m2, s);
-        const int64_t rel = lm_id(a, n) - vw;
-        if (rel >= 0 && rel < 128) {
-          const int rr = static_cast<int>(rel) & 31, isel = static_cast<int>(rel) >> 5;
-          const int rsel = (rr >> 3) * 4 + (rr & 3);
-          float val = 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) val = (i == isel && r == rsel) ? acc[i][j][r] : val;
-          if (((rr >> 2) & 1) == half) (prod ? a.tgt2 : a.tgt)[n] = val;
-        }
-      }
-    }
-  } else if constexpr (MODE == kLmGemm) {
+  if constexpr (MODE == kLmGemm) {
     // C[v][t] (+)= the tile; rows past V and columns past N are not stored. For fixed
     // (i, r) lanes 0-31 and 32-63 each write 32 consecutive floats of one row. With
     // transpose_c the lane's 4 consecutive rows of a column are one 16-byte store.
@@ -660,9 +502,6 @@ __global__ void __launch_bounds__(256) lm_reduce_kernel(LmReduceArgs a) {
   if (lane == 0) a.lse2[n] = m + log2f(s);
 }
 
-#ifndef LM_MI16
-#define LM_MI16 1
-#endif
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace lm {
@@ -998,6 +837,9 @@ __device__ __forceinline__ int lm_total_tiles(const LmTileArgs& a, int prod) {
 // per-XCD atomic queues: 43.5 against 43.9 ms of kernel time per step (the queue's
 // per-tile barriers and atomic cost more than these early exits), and against a
 // persistent static split, 46.2 ms.
+// ECACHE (kLmFwd): the policy's tiles also store the softmax terms. FRAG (kLmGemm): the
+// token-role operands are fragment-major (the 16x16x32 tile); otherwise the products
+// and the backward recompute run on the 32x32x16 tile, ATR with a K-major token operand.
 template <int MODE, bool ATR = false, bool ECACHE = false, bool FRAG = false>
 __global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(lm::WPE, lm::WPE)))
 lm_tile_kernel(LmTileArgs a) {
@@ -1011,23 +853,20 @@ lm_tile_kernel(LmTileArgs a) {
     const int per = (tt + 7) / 8;
     const int p = xcd * per + i;
     if (i >= per || p >= tt) return;
-    if constexpr (LM_MI16)
-      lm_tile16<MODE, ECACHE>(a, p % nm, p / nm, smem);
+    lm_tile16<MODE, ECACHE>(a, p % nm, p / nm, smem);
+  } else {
+    const int t0 = lm_total_tiles<MODE>(a, 0);
+    const int t1 = (MODE == kLmGemm && a.n_gemm > 1) ? lm_total_tiles<MODE>(a, 1) : 0;
+    const int per0 = (t0 + 7) / 8, per1 = (t1 + 7) / 8;
+    if (i >= per0 + per1) return;
+    const int prod = i < per0 ? 0 : 1;
+    const int p = prod == 0 ? xcd * per0 + i : xcd * per1 + (i - per0);
+    if (p >= (prod == 0 ? t0 : t1)) return;
+    if constexpr (FRAG)
+      lm_tile16<MODE, false>(a, prod, p, smem);
     else
-      lm_tile<MODE, ATR, ECACHE, FRAG>(a, p % nm, p / nm, smem);
-    return;
+      lm_tile<MODE, ATR>(a, prod, p, smem);
   }
-  const int t0 = lm_total_tiles<MODE>(a, 0);
-  const int t1 = (MODE == kLmGemm && a.n_gemm > 1) ? lm_total_tiles<MODE>(a, 1) : 0;
-  const int per0 = (t0 + 7) / 8, per1 = (t1 + 7) / 8;
-  if (i >= per0 + per1) return;
-  const int prod = i < per0 ? 0 : 1;
-  const int p = prod == 0 ? xcd * per0 + i : xcd * per1 + (i - per0);
-  if (p >= (prod == 0 ? t0 : t1)) return;
-  if constexpr (FRAG && LM_MI16)
-    lm_tile16<MODE, false>(a, prod, p, smem);
-  else
-    lm_tile<MODE, ATR, ECACHE, FRAG>(a, prod, p, smem);
 }
 
 // 64 x 64 bf16 tiles staged in LDS for a transpose: rows of 66 elements (33 words),
@@ -1294,8 +1133,7 @@ __global__ void __launch_bounds__(256) lm_transpose_frag_kernel(LmTransposeArgs 
   }
   __syncthreads();
   u32x4* dst = reinterpret_cast<u32x4*>(a.dst);
-  // Fragments of FM rows x FK k: FM = 16, FK = 32 for the 16x16x32 products, else 32 x 16.
-  constexpr int FM = LM_MI16 ? 16 : 32, FK = 512 / FM;
+  constexpr int FM = 16, FK = 32;   // the 16x16x32 MFMA B fragment
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int idx = tid + 256 * it, f = idx >> 6, l = idx & 63;   // fragment f of the 8, lane l
