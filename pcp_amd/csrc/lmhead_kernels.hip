@@ -793,24 +793,25 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
     }
   } else {
     // C[v][t] (+)= the tile; rows past V and columns past N are not stored. For fixed
-    // (i, r) each 16-lane group writes 16 consecutive floats of one row.
+    // (i, r) each 16-lane group writes 16 consecutive floats of one row per token block,
+    // and the wave's four token blocks follow each other, so each row's 256 bytes are
+    // written by four consecutive stores (whole cache lines before any eviction).
     float* C = g.C;
     const int ldc = g.ldc, accumulate = g.accumulate;
+    const int n0 = m0 + wt * TW + (lane & 15);
 #pragma unroll
-    for (int j = 0; j < NJ16; ++j) {
-      const int n = m0 + wt * TW + 16 * j + (lane & 15);
-      if (n >= N) continue;
+    for (int i = 0; i < NI16; ++i)
 #pragma unroll
-      for (int i = 0; i < NI16; ++i)
+      for (int r = 0; r < 4; ++r) {
+        const int vr = vw + 16 * i + 4 * grp + r;
+        if (vr >= V) continue;
+        float* row = C + static_cast<int64_t>(vr) * ldc;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int vr = vw + 16 * i + 4 * grp + r;
-          if (vr < V) {
-            float* pc = C + static_cast<int64_t>(vr) * ldc + n;
-            *pc = accumulate ? *pc + acc[i][j][r] : acc[i][j][r];
-          }
+        for (int j = 0; j < NJ16; ++j) {
+          const int n = n0 + 16 * j;
+          if (n < N) row[n] = accumulate ? row[n] + acc[i][j][r] : acc[i][j][r];
         }
-    }
+      }
   }
 }
 
