@@ -281,7 +281,7 @@ int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
  * bf16 dlogits and runs dhidden = dlogits * weight and dweight = dlogits^T *
  * hidden_states (fp32) over the whole vocabulary. The f16 term adds at most 2^-11 of
  * |c * softmax| to an off-target dlogit before its bf16 rounding. With an explicit
- * vocab_chunk, PCP_FLAG_EXACT_BF16, or a backward workspace above 16 GiB, the backward
+ * vocab_chunk, PCP_FLAG_EXACT_BF16, or a backward workspace above 64 GiB, the backward
  * recomputes the logit tiles per vocab chunk instead (dlogits = the f32 value rounded
  * once), in memory bounded by the chunk.
  * The live-token count never leaves the device: with PCP_FLAG_ASYNC the call only

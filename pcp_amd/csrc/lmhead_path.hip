@@ -37,9 +37,12 @@ namespace pcp {
 namespace {
 
 constexpr int64_t kDefaultChunk = 16384;
-// Largest backward workspace (softmax cache, D^T, W^T) the default path allocates:
-// 7.1 GB at configuration 5 (9,603 live tokens, V = 151,936, H = 4,096).
-constexpr size_t kCacheBudget = size_t{16} << 30;
+// Largest backward workspace (softmax cache, D^T, W^T; sized for all N tokens) the
+// default path allocates: 11.2 GB at configuration 5 (16,384 tokens, V = 151,936,
+// H = 4,096). 64 GiB, under a quarter of the device's 288 GB, holds it up to about
+// 110,000 tokens at that vocabulary; beyond that, or when the allocation fails, the
+// backward runs chunked.
+constexpr size_t kCacheBudget = size_t{64} << 30;
 
 inline size_t r256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 

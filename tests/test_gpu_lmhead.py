@@ -788,3 +788,34 @@ def test_config5_full_size():
             del dh, tol_dh, dw, tol_dw
         del out
         torch.cuda.empty_cache()
+
+
+def test_lmhead_large_batch_cached_matches_chunked():
+    """A batch whose backward workspace (about 26 GB at 40,960 tokens, V = 151,936,
+    H = 4,096) is past the old 16 GiB cap takes the cached path and agrees with the
+    chunked path on the same inputs: identical log-probs and loss terms (the same
+    forward tiles), gradients within the f16 term's rounding (a misplaced tile or row
+    would be off by O(1)), and not bit-identical (so the cache path did run)."""
+    from dataclasses import replace
+    cfg = replace(synth.LMHEAD, prompts=10)
+    inp = synth.make_lmhead_inputs(cfg, DEV)
+    print(f"lmhead large batch: {cfg.S * cfg.T} tokens", flush=True)
+    kw = dict(ref_weight=inp["ref_weight"], rewards=inp["rewards"], group_size=cfg.group,
+              loss_mode=LossMode.GRPO_CLIP_KL, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta)
+    first = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], want_grads=False, **kw)
+    old = (first.logp + inp["old_shift"]).contiguous()
+    del first
+    cached = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], old_logp=old, **kw)
+    torch.cuda.synchronize()
+    chunked = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], old_logp=old,
+                                  vocab_chunk=16384, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(cached.logp, chunked.logp) and torch.equal(cached.ref_logp, chunked.ref_logp)
+    assert torch.equal(cached.token_loss, chunked.token_loss) and float(cached.loss) == float(chunked.loss)
+    for name in ("dhidden", "dweight"):
+        a, b = getattr(cached, name), getattr(chunked, name)
+        rel = float((a - b).norm() / b.norm())
+        worst = float((a - b).abs().max() / b.abs().max())
+        print(f"  {name}: relative Frobenius difference {rel:.2e}, largest {worst:.2e}", flush=True)
+        assert bool(torch.isfinite(a).all()) and rel < 2 ** -8 and worst < 2 ** -6, (name, rel, worst)
+    assert not torch.equal(cached.dweight, chunked.dweight)
