@@ -365,8 +365,9 @@ def test_execute_reference_signature():
 
 
 C_HOST = r"""
-/* A C caller of the host-bytes boundary, as INTEGRATION.md's Zig binding compiles:
- * pcp_init -> pcp_execute("grpo_loss_fwd_bwd") -> pcp_free -> pcp_destroy.
+/* A C caller of the host-bytes boundary, making the calls a Zig binding of the
+ * reference's WorkerBackend would: pcp_init -> pcp_execute("grpo_loss_fwd_bwd") ->
+ * pcp_free -> pcp_destroy.
  * argv: S T V dir; reads dir/{logits,ids,mask,adv}.bin, writes dir/{loss,dlogits}.bin. */
 #include <stdio.h>
 #include <stdlib.h>
@@ -414,7 +415,7 @@ int main(int argc, char** argv) {
 
 
 def test_c_host_execute_end_to_end(tmp_path):
-    """INTEGRATION.md's call sequence from a compiled C host on the golden case
+    """The binding's call sequence (init, execute, free, destroy) from a compiled C host on the golden case
     v64_shifted (the reference's shifted layout): the loss and dlogits it writes match the
     torch float64 fixture at the golden bars."""
     import subprocess
