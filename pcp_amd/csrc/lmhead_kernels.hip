@@ -113,8 +113,9 @@ __device__ __forceinline__ void lm_tile_of(int p, int ntt, int nvt, int group_m,
 // (step 55.3 ms against 55.6 with 8; 2 matched 4, 1 and 38 were slower), and so did
 // the whole-vocabulary products of the cached backward (dhidden / dW groups of 4 / 4:
 // step 42.19-42.25 ms; 4 / 8 42.28, 4 / 2 42.43, 4 / 16 42.65, 8 / 16 42.75, 2 / 16
-// 43.0, 16 / 16 43.1). The forward computes its group in the kernel from the live
-// token count.
+// 43.0, 16 / 16 43.1); on the 16x16x32 products, 4 again (products launch 17.13-17.15
+// ms against 17.28-17.32 with 8, 17.57-17.62 with 2, 17.97-18.00 with 16). The forward
+// computes its group in the kernel from the live token count.
 constexpr int kLmBwdGroup = 4;
 
 __host__ __device__ inline int lm_group_m(int mode, int ntt) {
