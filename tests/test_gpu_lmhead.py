@@ -627,16 +627,18 @@ def test_lmhead_final_norm_partial_gradients_and_errors():
 
 # ---- real hidden and vocabulary sizes, few tokens, against the float64 oracle ---------------
 
-def test_lmhead_qwen_vocab_vs_oracle():
-    """Config 5's hidden size and vocabulary, 205 live tokens: the default (softmax-cache)
-    backward and the recomputing one (PCP_FLAG_EXACT_BF16, 16384-wide chunks) against the
-    float64 oracle, each under its own bound."""
+@pytest.mark.parametrize("H", [4096, 896], ids=["H4096", "H896"])
+def test_lmhead_qwen_vocab_vs_oracle(H):
+    """The Qwen vocabulary with config 5's hidden size (4096) and Qwen2.5-0.5B's (896: 14
+    stages, a half-filled last tile of the products' H side), 205 live tokens: the default
+    (softmax-cache) backward and the recomputing one (PCP_FLAG_EXACT_BF16, 16384-wide
+    chunks) against the float64 oracle, each under its own bound."""
     cfg = synth.LMHEAD
-    c = make_case(2, 128, cfg.H, cfg.V, 2, seed=17, lengths=[128, 77], logit_std=cfg.std_w * np.sqrt(cfg.H))
+    c = make_case(2, 128, H, cfg.V, 2, seed=17 + H, lengths=[128, 77], logit_std=cfg.std_w * np.sqrt(H))
     L, lse, rlse, old, r = oracle_case(c, LossMode.GRPO_CLIP_KL)
     bounds = {cached: grad_bounds(c, L, lse, r, LossMode.GRPO_CLIP_KL, old, cached=cached) for cached in (True, False)}
     for exact in (False, True):
-        print(f"lmhead qwen-vocab N=256 H=4096 V=151936 exact={exact}", flush=True)
+        print(f"lmhead qwen-vocab N=256 H={H} V=151936 exact={exact}", flush=True)
         out = run_device(c, LossMode.GRPO_CLIP_KL, old, exact_bf16=exact)
         torch.cuda.synchronize()
         check_forward(c, out, L, lse, rlse, r, LossMode.GRPO_CLIP_KL)
