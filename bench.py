@@ -234,7 +234,8 @@ def bench_lmhead(args) -> None:
     torch.cuda.synchronize()
     t_setup = time.perf_counter() - t_setup
     kw = dict(ref_weight=inp["ref_weight"] if clip else None, rewards=inp["rewards"], group_size=cfg.group,
-              old_logp=inp["old_logp"], loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, ctx=ctx)
+              old_logp=inp["old_logp"], loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta,
+              exact_bf16=args.exact_bf16, vocab_chunk=args.vocab_chunk, ctx=ctx)
     if args.final_norm:
         # The decoder's final RMSNorm fused in: hidden is the last layer's output before it.
         g = torch.Generator(device=dev).manual_seed(5)
@@ -268,8 +269,13 @@ def bench_lmhead(args) -> None:
     # dominant kernel: dhidden and dW in one launch of the MFMA tile kernel.
     products = (2 if clip else 1) + 2
     step_flops = products * 2.0 * live * H * V
-    tile_flops = 2 * 2.0 * live * H * V
+    # With the chunked backward (--vocab-chunk) the library times the forward launch
+    # instead: one product per model.
+    chunked = args.vocab_chunk > 0
+    tile_flops = (products - 2 if chunked else 2) * 2.0 * live * H * V
     achieved = tile_flops / (kernel_ms / 1e3) / 1e12
+    tile_kernel = ("lm_tile_kernel<kLmFwd> (policy and reference logits, one launch)" if chunked
+                   else "lm_tile_kernel<kLmGemm> (dhidden + dW products, one launch)")
     line = {
         "metric": "GRPO fused LM-head + loss fwd+bwd tokens/s, H=4096, V=151936 bf16",
         "value": live / (ms_step / 1e3),
@@ -285,18 +291,21 @@ def bench_lmhead(args) -> None:
         "data": "synthetic (seeded Philox/PCG64 inputs of the configuration)",
         "config": {"workload": f"config5 {cfg.name}: {cfg.prompts} prompts x G={cfg.group}, T={cfg.T}, "
                                f"hidden {H}, V={V}, bf16 hidden/weights, loss={args.mode}"
-                               + (", final RMSNorm fused" if args.final_norm else ""),
+                               + (", final RMSNorm fused" if args.final_norm else "")
+                               + (", exact bf16 dlogits (f32 softmax terms)" if args.exact_bf16 else "")
+                               + (f", recomputing backward in {args.vocab_chunk}-wide vocab chunks"
+                                  if args.vocab_chunk else ""),
                    "tokens": N, "valid_tokens": live, "global_batch": cfg.S, "seq_len": cfg.T},
         "step_tflops": step_flops / (ms_step / 1e3) / 1e12,
         "dense_equivalent_tflops": products * 2.0 * N * H * V / (ms_step / 1e3) / 1e12,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
-                     "kernel": "lm_tile_kernel<kLmGemm> (dhidden + dW products, one launch)", "kernel_ms": kernel_ms,
+                     "kernel": tile_kernel, "kernel_ms": kernel_ms,
                      "algorithmic_flops": tile_flops},
         "setup_s": t_setup,
     }
     tfile = os.path.join(ROOT, "profiles", f"traffic_config5_{args.mode}.json")
-    if os.path.exists(tfile):
+    if os.path.exists(tfile) and not args.exact_bf16 and not chunked:   # measured on the default path
         with open(tfile) as f:
             line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
     if not args.no_cpu_baseline:
@@ -783,7 +792,11 @@ def main() -> None:
                     help="loss workload: leave the dlogits rows of masked and pad tokens unwritten "
                          "(PCP_FLAG_NO_ZERO_FILL); algorithmic bytes then count live rows only")
     ap.add_argument("--exact-bf16", action="store_true",
-                    help="loss workload: PCP_FLAG_EXACT_BF16 (no f16 softmax terms in the bf16 dlogits pass)")
+                    help="loss workload: PCP_FLAG_EXACT_BF16 (no f16 softmax terms in the bf16 dlogits pass); "
+                         "config 5: the same flag (the forward keeps f32 softmax terms)")
+    ap.add_argument("--vocab-chunk", type=int, default=0,
+                    help="config 5: the recomputing backward's vocab chunk (a multiple of 256; 0: the forward's "
+                         "softmax terms)")
     ap.add_argument("--policy-only", action="store_true", help="logprob workload: the policy rows only")
     ap.add_argument("--rows", type=int, default=64,
                     help="sample workload: rows per call (64: a decoding step of config 2; 1: the reference's "

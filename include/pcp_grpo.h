@@ -100,8 +100,9 @@ typedef enum pcp_loss_mode {
  * even. By default the resident kernel keeps the softmax terms of the sum pass as f16
  * (unit roundoff 2^-11) and scales them into dlogits, which saves one exponential per
  * element (3-5% of the step at configs 2-4) and adds up to 2^-11 of |dlogit| before
- * the bf16 rounding. On pcp_grpo_lmhead_fwd_bwd it selects the recomputing backward,
- * whose bf16 dlogits operand is likewise the f32 value rounded once. */
+ * the bf16 rounding. On pcp_grpo_lmhead_fwd_bwd the forward keeps its softmax terms as
+ * f32 instead of f16, so the bf16 dlogits operand of the backward is likewise the f32
+ * value rounded once (about twice the backward workspace). */
 #define PCP_FLAG_EXACT_BF16 0x8u
 
 /* The token id that contributes nothing (F.cross_entropy ignore_index; the
@@ -280,10 +281,11 @@ int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
  * as f16 (one 2-byte term per live token and vocab entry), the backward turns them into
  * bf16 dlogits and runs dhidden = dlogits * weight and dweight = dlogits^T *
  * hidden_states (fp32) over the whole vocabulary. The f16 term adds at most 2^-11 of
- * |c * softmax| to an off-target dlogit before its bf16 rounding. With an explicit
- * vocab_chunk, PCP_FLAG_EXACT_BF16, or a backward workspace above 64 GiB, the backward
- * recomputes the logit tiles per vocab chunk instead (dlogits = the f32 value rounded
- * once), in memory bounded by the chunk.
+ * |c * softmax| to an off-target dlogit before its bf16 rounding; PCP_FLAG_EXACT_BF16
+ * keeps the terms as f32 (4 bytes per live token and vocab entry), so each dlogit is
+ * the f32 value rounded once. With an explicit vocab_chunk, or a backward workspace
+ * above 64 GiB, the backward recomputes the logit tiles per vocab chunk instead
+ * (dlogits = the f32 value rounded once), in memory bounded by the chunk.
  * The live-token count never leaves the device: with PCP_FLAG_ASYNC the call only
  * enqueues work, and it can be captured in a HIP graph. A captured graph uses the
  * context's work buffers as they were at capture: make one uncaptured call of the same

@@ -521,7 +521,8 @@ constexpr int KS16 = BK / 32;   // 32-deep k-steps per stage
 // Fragment layouts (pinned by the MFMA probe's test): an operand lane holds row
 // lane % 16 at k = 8 (lane / 16) + 0..7; the result lane holds column lane % 16 at rows
 // 4 (lane / 16) + 0..3.
-template <int MODE, bool ECACHE>
+// E32 (with ECACHE): the softmax terms are stored as f32 (a.ecache32) in place of f16.
+template <int MODE, bool ECACHE, bool E32 = false>
 __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, char* smem) {
   using namespace lm;
   static_assert(MODE == kLmGemm || MODE == kLmFwd, "16x16x32 tiles: the forward and the fragment-major products");
@@ -738,19 +739,38 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
       float sum[2] = {0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < NI16; ++i) {
+        float ev[2][4];
         uint32_t pk[2][2];
 #pragma unroll
         for (int jo = 0; jo < 2; ++jo) {
-          float ev[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            ev[r] = hw_exp2(fmaf(acc[i][jj + jo][r], kLog2e, -ms_ref(ref[jj + jo])));
-            sum[jo] += ev[r];
+            ev[jo][r] = hw_exp2(fmaf(acc[i][jj + jo][r], kLog2e, -ms_ref(ref[jj + jo])));
+            sum[jo] += ev[jo][r];
           }
-          pk[jo][0] = pack2<F16T>(ev[0], ev[1]);
-          pk[jo][1] = pack2<F16T>(ev[2], ev[3]);
+          pk[jo][0] = pack2<F16T>(ev[jo][0], ev[jo][1]);
+          pk[jo][1] = pack2<F16T>(ev[jo][2], ev[jo][3]);
         }
-        if (ECACHE && prod == 0) {
+        if (ECACHE && E32 && prod == 0) {
+          // f32 terms: the same exchange per register (rows 4 grp + r), after which the
+          // lane holds rows 16 i + 8 (grp / 2) + 0..3 in w0 and + 4..7 in w1: two 16-byte
+          // stores.
+          u32x4 w0, w1;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(ev[0][r]), __float_as_uint(ev[1][r]),
+                                                             false, false);
+            w0[r] = sw[0];
+            w1[r] = sw[1];
+          }
+          const int n = m0 + wt * TW + 16 * (jj + (grp & 1)) + (lane & 15);
+          const int64_t c = vw + 16 * i + 8 * (grp >> 1);
+          if (n < N && c < a.lde) {
+            u32x4* dst = reinterpret_cast<u32x4*>(a.ecache32 + static_cast<int64_t>(n) * a.lde + c);
+            dst[0] = w0;
+            dst[1] = w1;
+          }
+        } else if (ECACHE && prod == 0) {
           // Softmax cache: ecache[n][v] = f16(2^(x*log2e - ref)), token-major rows of lde
           // (vocab past V holds 0). The lane's terms of block (i, j) are vocab rows
           // 16 i + 4 grp + 0..3 of token column 16 j + lane % 16. One v_permlane16_swap
@@ -831,6 +851,20 @@ __device__ __forceinline__ int lm_total_tiles(const LmTileArgs& a, int prod) {
   }
 }
 
+// One kLmFwd work item (lm_tile_kernel's order). Both models' tiles of one (token,
+// vocab) pair are consecutive items, so they run side by side on one XCD and read each
+// hidden slab from its L2 once.
+template <bool ECACHE, bool E32>
+__device__ __forceinline__ void lm_fwd_item(const LmTileArgs& a, char* smem) {
+  const int xcd = blockIdx.x % 8, i = blockIdx.x / 8;
+  const int nm = a.n_model > 1 ? 2 : 1;
+  const int tt = lm_total_tiles<kLmFwd>(a, 0) * nm;
+  const int per = (tt + 7) / 8;
+  const int p = xcd * per + i;
+  if (i >= per || p >= tt) return;
+  lm_tile16<kLmFwd, ECACHE, E32>(a, p % nm, p / nm, smem);
+}
+
 // One workgroup per tile. Workgroup ids are dealt round-robin to the 8 XCDs, so
 // workgroup b runs on XCD b % 8 and takes item b / 8 of that XCD's contiguous eighth of
 // every product's tiles (products in order). The grid is sized for every token and
@@ -846,17 +880,10 @@ template <int MODE, bool ATR = false, bool ECACHE = false, bool FRAG = false>
 __global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(lm::WPE, lm::WPE)))
 lm_tile_kernel(LmTileArgs a) {
   extern __shared__ __align__(16) char smem[];
-  const int xcd = blockIdx.x % 8, i = blockIdx.x / 8;
   if constexpr (MODE == kLmFwd) {
-    // Both models' tiles of one (token, vocab) pair are consecutive items, so they run
-    // side by side on one XCD and read each hidden slab from its L2 once.
-    const int nm = a.n_model > 1 ? 2 : 1;
-    const int tt = lm_total_tiles<MODE>(a, 0) * nm;
-    const int per = (tt + 7) / 8;
-    const int p = xcd * per + i;
-    if (i >= per || p >= tt) return;
-    lm_tile16<MODE, ECACHE>(a, p % nm, p / nm, smem);
+    lm_fwd_item<ECACHE, false>(a, smem);
   } else {
+    const int xcd = blockIdx.x % 8, i = blockIdx.x / 8;
     const int t0 = lm_total_tiles<MODE>(a, 0);
     const int t1 = (MODE == kLmGemm && a.n_gemm > 1) ? lm_total_tiles<MODE>(a, 1) : 0;
     const int per0 = (t0 + 7) / 8, per1 = (t1 + 7) / 8;
@@ -869,6 +896,14 @@ lm_tile_kernel(LmTileArgs a) {
     else
       lm_tile<MODE, ATR>(a, prod, p, smem);
   }
+}
+
+// The kLmFwd launch that keeps the policy's softmax terms as f32 (a.ecache32), for
+// the exact-rounding backward (PCP_FLAG_EXACT_BF16).
+__global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(lm::WPE, lm::WPE)))
+lm_tile_fwd32_kernel(LmTileArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  lm_fwd_item<true, true>(a, smem);
 }
 
 // 64 x 64 bf16 tiles staged in LDS for a transpose: rows of 66 elements (33 words),
@@ -909,7 +944,10 @@ constexpr int kDcacheVocabTiles = 4;
 // nontemporal accesses: each byte is touched once here and read back only by the next
 // launch, so keeping the lines in L2 only delays other traffic (config 5, kernel
 // traces: 2.07 -> 1.85 ms; the same hint on the forward's cache stores cost 0.5 ms).
-__global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
+// F32: the terms are f32 at a.src32 (the exact-rounding forward) and D goes to a.d
+// beside them, not in place.
+template <bool F32>
+__device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
   __shared__ uint16_t t[64 * kTilePitch];    // [token][vocab] bf16
   const int tid = threadIdx.x;
   const int64_t n = *a.count;
@@ -922,13 +960,13 @@ __global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
     const int cc = (tid & 7) * 8;
     const int64_t c0 = v0 + cc;
     // Both rows' loads first (one round trip): the f16 terms and the row's scalars.
-    u32x4 w[2];
+    u32x4 w[2], w2[2];
     float cf[2], l2[2], m2[2], tg[2];
     int id[2];
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
       const int64_t row = r0 + (tid >> 3) + 32 * it;
-      w[it] = u32x4{0u, 0u, 0u, 0u};
+      w[it] = w2[it] = u32x4{0u, 0u, 0u, 0u};
       cf[it] = 0.f;
       l2[it] = m2[it] = tg[it] = 0.f;
       id[it] = -1;
@@ -938,7 +976,13 @@ __global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
         id[it] = a.ids[row];
         tg[it] = a.tgt[row];
         if (c0 < a.V) {
-          w[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.d + row * a.ld + c0));
+          if constexpr (F32) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(a.src32 + row * a.ld + c0);
+            w[it] = __builtin_nontemporal_load(src);
+            w2[it] = __builtin_nontemporal_load(src + 1);
+          } else {
+            w[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.d + row * a.ld + c0));
+          }
           m2[it] = a.part[row * a.ldp + c0 / kLmPart].x;
         }
       }
@@ -954,7 +998,10 @@ __global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
         const int64_t rel = static_cast<int64_t>(id[it]) - c0;
         float d[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) d[k] = c0 + k < a.V ? f * F16T::unpack(ww, k) : 0.f;
+        for (int k = 0; k < 8; ++k) {
+          const float e = F32 ? __uint_as_float(k < 4 ? w[it][k] : w2[it][k - 4]) : F16T::unpack(ww, k);
+          d[k] = c0 + k < a.V ? f * e : 0.f;
+        }
         if (rel >= 0 && rel < 8) {
           const float pt = hw_exp2(fmaf(tg[it], kLog2e, -l2[it]));
 #pragma unroll
@@ -976,6 +1023,9 @@ __global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
     __syncthreads();
   }
 }
+
+__global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) { lm_dcache_body<false>(a); }
+__global__ void __launch_bounds__(256) lm_dcache32_kernel(LmDcacheArgs a) { lm_dcache_body<true>(a); }
 
 // GRPO terms per token from logp / ref logp (token_terms); also masks logp for
 // dead tokens and keeps the policy lse (base 2) and the coefficient for the backward.
@@ -1174,6 +1224,13 @@ hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {
   LmTileArgs a = args;
   const int grid = a.ntt * a.nvt * (mode == kLmFwd && a.n_model > 1 ? 2 : 1);   // tiles at the largest token count
   if (grid <= 0) return hipSuccess;
+  if (mode == kLmFwd && a.ecache32) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_fwd32_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));
+    if (e != hipSuccess) return e;
+    lm_tile_fwd32_kernel<<<dim3(8 * ((grid + 7) / 8)), dim3(lm::NTHR), lm::kSmem, st>>>(a);
+    return hipGetLastError();
+  }
   if (mode == kLmFwd)
     return a.ecache ? launch_tiles_mode<kLmFwd, true>(a, grid, st) : launch_tiles_mode<kLmFwd>(a, grid, st);
   return launch_tiles_mode<kLmBwd>(a, grid, st);
@@ -1226,7 +1283,10 @@ hipError_t launch_lm_dcache(const LmDcacheArgs& a, hipStream_t st) {
   const int64_t ntile = a.ldt / 64;
   const int64_t vblocks = (a.ld / 64 + kDcacheVocabTiles - 1) / kDcacheVocabTiles;
   const dim3 grid(static_cast<unsigned>(ntile < 65535 ? ntile : 65535), static_cast<unsigned>(vblocks));
-  lm_dcache_kernel<<<grid, dim3(256), 0, st>>>(a);
+  if (a.src32)
+    lm_dcache32_kernel<<<grid, dim3(256), 0, st>>>(a);
+  else
+    lm_dcache_kernel<<<grid, dim3(256), 0, st>>>(a);
   return hipGetLastError();
 }
 

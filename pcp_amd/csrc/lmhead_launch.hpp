@@ -38,6 +38,7 @@ struct LmTileArgs {
   float* tgt2;
   uint16_t* ecache;     // or nullptr: [N, lde] f16 softmax terms 2^(x*log2e - ref) of the
   int64_t lde;          //   partial's reference ref (lde % 64 == 0, >= V; 0 past V)
+  float* ecache32;      // or nullptr: the same terms as f32 (ecache then nullptr)
   // kLmBwd
   const float* lse2;    // [N] base-2 log-sum-exp
   const float* coef;    // [N] d loss / d logp
@@ -82,7 +83,8 @@ struct LmTransposeArgs {
 // and the same values transposed into dt[v][n], zero for *count <= n < *count rounded
 // up to 64 (columns past that are not written).
 struct LmDcacheArgs {
-  uint16_t* d;            // [ldt, ld]
+  uint16_t* d;            // [ldt, ld] bf16 D, written over the f16 terms there (src32 nullptr)
+  const float* src32;     // or [ldt, ld] f32 terms, read in place of d's
   int64_t ld;             // multiple of 64, >= V
   const int* count;       // [1] live tokens (device)
   uint16_t* dt;           // [ld, ldt] or nullptr

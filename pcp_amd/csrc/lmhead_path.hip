@@ -169,17 +169,20 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   // device). By default: the whole-vocabulary softmax cache [N, ldv] (the policy forward
   // stores its f16 terms there; a pass rewrites them as dlogits D and writes D^T
   // [ldv, ldt] beside it) and W^T [H, ldv], so both products read K-contiguous
-  // operands. With an explicit vocab_chunk, PCP_FLAG_EXACT_BF16, more than kCacheBudget
-  // bytes, or no memory for them: one dlogits chunk [N, chunk] that the backward refills
-  // by recomputing the logits.
+  // operands. With PCP_FLAG_EXACT_BF16 the terms are f32 [N, ldv] and D follows them
+  // (D is then the f32 value rounded once). With an explicit vocab_chunk, more than
+  // kCacheBudget bytes, or no memory for them: one dlogits chunk [N, chunk] that the
+  // backward refills by recomputing the logits.
+  const bool exact = (a->flags & PCP_FLAG_EXACT_BF16) != 0;
   const int64_t ldv = (V + 63) / 64 * 64;
   const int64_t ldt = ldt_max;
-  const size_t o_dt = 2 * static_cast<size_t>(ldt) * ldv;
+  const size_t o_d = exact ? 4 * static_cast<size_t>(ldt) * ldv : 0;
+  const size_t o_dt = o_d + 2 * static_cast<size_t>(ldt) * ldv;
   const size_t o_wt = o_dt + (a->dweight ? 2 * static_cast<size_t>(ldv) * ldt : 0);
   const size_t cache_bytes = o_wt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
   bool cached = false;
   if (bwd) {
-    if (a->vocab_chunk == 0 && !(a->flags & PCP_FLAG_EXACT_BF16) && cache_bytes <= kCacheBudget) {
+    if (a->vocab_chunk == 0 && cache_bytes <= kCacheBudget) {
       e = grow_dbuf(ctx, cache_bytes);
       if (e == hipSuccess) cached = true;
       else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the softmax cache");
@@ -241,7 +244,8 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   // for both), then one merge per model.
   ta.B = a->weight;
   ta.tgt = F(o_tgt);
-  ta.ecache = cached ? static_cast<uint16_t*>(ctx->lm_dbuf) : nullptr;
+  ta.ecache = cached && !exact ? static_cast<uint16_t*>(ctx->lm_dbuf) : nullptr;
+  ta.ecache32 = cached && exact ? static_cast<float*>(ctx->lm_dbuf) : nullptr;
   ta.lde = ldv;
   ta.n_model = ref ? 2 : 1;
   if (ref) {
@@ -360,8 +364,9 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       // registers; D and D^T go through LDS.
       uint16_t* dt = a->dweight ? reinterpret_cast<uint16_t*>(dbuf + o_dt) : nullptr;
       uint16_t* wt = want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_wt) : nullptr;
-      const LmDcacheArgs dc{reinterpret_cast<uint16_t*>(dbuf), ldv, cnt, dt, ldt, V, part, npart,
-                            F(o_l2), F(o_coef), F(o_tgt), I(o_idsc)};
+      uint16_t* dd = reinterpret_cast<uint16_t*>(dbuf + o_d);
+      const LmDcacheArgs dc{dd, exact ? reinterpret_cast<const float*>(dbuf) : nullptr, ldv, cnt, dt, ldt, V,
+                            part, npart, F(o_l2), F(o_coef), F(o_tgt), I(o_idsc)};
       if ((e = launch_lm_dcache(dc, st)) != hipSuccess) return hip_fail(ctx, e, "dlogits from the softmax cache");
       if (a->dweight && (e = launch_lm_transpose_frag(tr, st)) != hipSuccess)
         return hip_fail(ctx, e, "transposing hidden rows");
@@ -375,7 +380,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         if ((e = launch_lm_transpose_frag(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
         // dhidden_c[t][h] = sum_v D[t][v] * W^T[h][v].
         LmTileArgs::Gemm& d = g[ng++];
-        d.B = dbuf;
+        d.B = dd;
         d.ldb = static_cast<int>(ldv);
         d.V = static_cast<int>(N);
         d.vcount = cnt;

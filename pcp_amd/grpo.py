@@ -228,9 +228,10 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
     weight / ref_weight [V, H] bf16, ids / mask / old_logp [S, T]. With norm_weight
     (f32 [H]) the decoder's final RMSNorm is fused in: hidden is the last layer's
     output before the norm, and dhidden / dnorm_weight are the gradients there.
-    vocab_chunk 0 lets the library keep the forward's softmax terms (f16) for the
-    backward; a chunk width, or exact_bf16 (PCP_FLAG_EXACT_BF16), recomputes the
-    logits per chunk instead."""
+    vocab_chunk 0 lets the library keep the forward's softmax terms for the backward:
+    f16 by default, f32 with exact_bf16 (PCP_FLAG_EXACT_BF16; the bf16 dlogits are then
+    the f32 value rounded once); a chunk width recomputes the logits per chunk
+    instead."""
     ctx = ctx or default_context(hidden.device.index or 0)
     if ids.dim() != 2:
         raise PcpError(-1, "ids must be [S, T]")

@@ -346,36 +346,86 @@ def test_execute_lmhead_final_norm_shifted():
     assert np.array_equal(np.frombuffer(outs[6], np.float32), ref.dnorm_weight.cpu().numpy())
 
 
-@pytest.mark.parametrize("chunk", [512, 0], ids=["chunked", "cached"])
-def test_lmhead_deterministic(chunk):
+@pytest.mark.parametrize("chunk, exact", [(512, False), (0, False), (0, True)], ids=["chunked", "cached", "exact"])
+def test_lmhead_deterministic(chunk, exact):
     c = make_case(2, 70, 128, 900, 2, seed=5, lengths=[70, 33])
     old = np.full((2, 70), -7.0, np.float32)
-    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk)
-    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk)
+    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk, exact_bf16=exact)
+    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk, exact_bf16=exact)
     torch.cuda.synchronize()
     for f in ("loss", "logp", "ref_logp", "token_loss", "dhidden", "dweight"):
         assert torch.equal(getattr(a, f), getattr(b, f)), f
 
 
-def test_lmhead_exact_flag_recomputes():
-    """PCP_FLAG_EXACT_BF16 with the default vocab_chunk takes the recomputing backward:
-    bit for bit the result of an explicit 16384-wide chunk, inside the bound without the
-    cache term. The default (cached) backward meets its own bound, and its forward
-    outputs are those of the exact call."""
+def test_lmhead_exact_flag():
+    """PCP_FLAG_EXACT_BF16 keeps the forward's softmax terms as f32, so the backward's
+    bf16 dlogits are the f32 value rounded once: inside the bound without the cache
+    term, as the recomputing backward (an explicit chunk) is. With an explicit chunk the
+    flag changes nothing, bit for bit. The forward outputs of the default, exact and
+    chunked calls are identical; the default backward meets its own bound."""
     c = make_case(3, 90, 192, 2500, 3, seed=31, lengths=[90, 61, 12])
     mode = LossMode.GRPO_CLIP_KL
     L, lse, rlse, old, r = oracle_case(c, mode)
     ex = run_device(c, mode, old, exact_bf16=True)
     ch = run_device(c, mode, old, vocab_chunk=16384)
+    chx = run_device(c, mode, old, vocab_chunk=16384, exact_bf16=True)
     ca = run_device(c, mode, old)
     torch.cuda.synchronize()
     for f in ("loss", "logp", "ref_logp", "token_loss", "dhidden", "dweight"):
-        assert torch.equal(getattr(ex, f), getattr(ch, f)), f
+        assert torch.equal(getattr(chx, f), getattr(ch, f)), f
     for f in ("loss", "logp", "ref_logp", "token_loss"):
         assert torch.equal(getattr(ca, f), getattr(ex, f)), f
+        assert torch.equal(getattr(ch, f), getattr(ex, f)), f
     check_forward(c, ex, L, lse, rlse, r, mode)
-    check_grads(ex, *grad_bounds(c, L, lse, r, mode, old, cached=False))
+    exact_bounds = grad_bounds(c, L, lse, r, mode, old, cached=False)
+    check_grads(ex, *exact_bounds)
+    check_grads(ch, *exact_bounds)
     check_grads(ca, *grad_bounds(c, L, lse, r, mode, old, cached=True))
+
+
+@pytest.mark.parametrize("variant", ["exact", "chunked", "cached"])
+def test_lmhead_dlogits_rounded_once(variant):
+    """The bf16 dlogits operand itself. With one live token the dW product has K = 1, so
+    dW[v, k] = D_v * h_k exactly (a product of two bf16 values is exact in f32) and
+    D_v = dW[v, k0] / h_k0 exactly in float64. With PCP_FLAG_EXACT_BF16 (f32 softmax
+    terms) and with the recomputing backward (an explicit chunk), every D_v is the
+    float64 D = c (onehot - softmax) rounded to nearest even, except where D lies within
+    1e-4 of a rounding midpoint relative to |D| (the f32 logits, exponentials and c stay
+    far inside that). The default f16 terms (2^-11 relative) fail the same check on a
+    share of the elements, which shows that the check tells the two apart."""
+    T, H, V = 16, 256, 5000
+    c = make_case(1, T, H, V, 1, seed=61, lengths=[T], logit_std=3.0)
+    L = orc.lmhead_logits(c["hb"], c["wb"])
+    h = orc.bf16_to_f32(c["hb"]).astype(np.float64)
+    adv = 0.75
+    kw = {"exact": dict(exact_bf16=True), "chunked": dict(vocab_chunk=1024), "cached": {}}[variant]
+    bf16 = lambda x: orc.bf16_from_f32(np.asarray(x, np.float64).astype(np.float32))
+    checked = wrong = 0
+    for t in np.random.default_rng(62).choice(T, 4, replace=False):
+        mask = np.zeros((1, T), np.float32)
+        mask[0, t] = 1.0
+        print(f"dlogits rounded once: {variant}, live token {t}", flush=True)
+        out = grpo.lmhead_fwd_bwd(dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), dev(mask),
+                                  rewards=dev(np.ones(1, np.float32)), advantages=dev(np.full(1, adv, np.float32)), **kw)
+        torch.cuda.synchronize()
+        dw = out.dweight.cpu().numpy().astype(np.float64)
+        k0 = int(np.argmax(np.abs(h[t])))
+        d_dev = dw[:, k0] / h[t, k0]
+        assert np.array_equal(orc.bf16_to_f32(bf16(d_dev)).astype(np.float64), d_dev), "D is not a bf16 value"
+        # REINFORCE, one sequence of one live token: d loss / d logp = -adv.
+        coef = -adv
+        x = L[t]
+        p = np.exp(x - (x.max() + np.log(np.exp(x - x.max()).sum())))
+        d = -coef * p
+        d[c["ids"][0, t]] += coef
+        clear = bf16(d * (1 + 1e-4)) == bf16(d * (1 - 1e-4))
+        checked += int(clear.sum())
+        wrong += int((bf16(d_dev) != bf16(d))[clear].sum())
+    assert checked > 0.9 * 4 * V, checked
+    if variant == "cached":
+        assert wrong > 0, "the check does not tell f16 terms from exact rounding"
+    else:
+        assert wrong == 0, f"{wrong} of {checked} dlogits are not the exact value rounded once"
 
 
 def test_lmhead_async_does_not_wait():
@@ -406,8 +456,8 @@ def test_lmhead_async_does_not_wait():
         assert torch.equal(getattr(got, f), getattr(want, f)), f
 
 
-@pytest.mark.parametrize("chunk", [0, 512], ids=["cached", "chunked"])
-def test_lmhead_graph_capture_replays(chunk):
+@pytest.mark.parametrize("chunk, exact", [(0, False), (512, False), (0, True)], ids=["cached", "chunked", "exact"])
+def test_lmhead_graph_capture_replays(chunk, exact):
     """The call captured in a HIP graph (asynchronous, no host read): three replays with
     eager work between them (outputs overwritten with NaN) each equal an eager call bit
     for bit."""
@@ -415,7 +465,7 @@ def test_lmhead_graph_capture_replays(chunk):
     old = np.full((2, 70), -7.0, np.float32)
     args = (dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), dev(c["mask"]))
     kw = dict(ref_weight=dev(c["rb"]), rewards=dev(c["rewards"]), group_size=2, old_logp=dev(old),
-              loss_mode=LossMode.GRPO_CLIP_KL, vocab_chunk=chunk)
+              loss_mode=LossMode.GRPO_CLIP_KL, vocab_chunk=chunk, exact_bf16=exact)
     want = grpo.lmhead_fwd_bwd(*args, **kw)
     out = grpo.lmhead_fwd_bwd(*args, **kw)     # the graph's outputs; buffers already grown
     ctx = grpo.default_context(0)
@@ -429,7 +479,7 @@ def test_lmhead_graph_capture_replays(chunk):
         for f in fields:
             getattr(out, f).fill_(float("nan"))
         torch.cuda.synchronize()
-        print(f"graph replay {rep} ({'cached' if chunk == 0 else 'chunked'})", flush=True)
+        print(f"graph replay {rep} ({'chunked' if chunk else 'exact' if exact else 'cached'})", flush=True)
         g.replay()
         torch.cuda.synchronize()
         for f in fields:
@@ -631,18 +681,19 @@ def test_lmhead_final_norm_partial_gradients_and_errors():
 def test_lmhead_qwen_vocab_vs_oracle(H):
     """The Qwen vocabulary with config 5's hidden size (4096) and Qwen2.5-0.5B's (896: 14
     stages, a half-filled last tile of the products' H side), 205 live tokens: the default
-    (softmax-cache) backward and the recomputing one (PCP_FLAG_EXACT_BF16, 16384-wide
-    chunks) against the float64 oracle, each under its own bound."""
+    (f16 softmax terms) backward, the exact one (PCP_FLAG_EXACT_BF16, f32 terms) and the
+    recomputing one (16384-wide chunks) against the float64 oracle, each under its own
+    bound."""
     cfg = synth.LMHEAD
     c = make_case(2, 128, H, cfg.V, 2, seed=17 + H, lengths=[128, 77], logit_std=cfg.std_w * np.sqrt(H))
     L, lse, rlse, old, r = oracle_case(c, LossMode.GRPO_CLIP_KL)
     bounds = {cached: grad_bounds(c, L, lse, r, LossMode.GRPO_CLIP_KL, old, cached=cached) for cached in (True, False)}
-    for exact in (False, True):
-        print(f"lmhead qwen-vocab N=256 H={H} V=151936 exact={exact}", flush=True)
-        out = run_device(c, LossMode.GRPO_CLIP_KL, old, exact_bf16=exact)
+    for name, kw in (("cached", {}), ("exact", dict(exact_bf16=True)), ("chunked", dict(vocab_chunk=16384))):
+        print(f"lmhead qwen-vocab N=256 H={H} V=151936 {name}", flush=True)
+        out = run_device(c, LossMode.GRPO_CLIP_KL, old, **kw)
         torch.cuda.synchronize()
         check_forward(c, out, L, lse, rlse, r, LossMode.GRPO_CLIP_KL)
-        check_grads(out, *bounds[not exact])
+        check_grads(out, *bounds[name == "cached"])
 
 
 # ---- configuration 5 at full size against torch fp32 ------------------------------------------
