@@ -203,6 +203,21 @@ def test_lmhead_small_vs_oracle(shape, mode):
     check_grads(out, *grad_bounds(c, L, lse, r, mode, old, cached=chunk == 0))
 
 
+@pytest.mark.parametrize("shape", SMALL, ids=lambda s: f"S{s[0]}T{s[1]}H{s[2]}V{s[3]}")
+def test_lmhead_small_exact_vs_oracle(shape):
+    """PCP_FLAG_EXACT_BF16 (f32 softmax terms) at the same ragged shapes, the shape's
+    chunk ignored: under the bound without the cache term."""
+    S, T, H, V, G, _, lengths = shape
+    c = make_case(S, T, H, V, G, seed=S * 1000 + V + 7, lengths=lengths)
+    mode = LossMode.GRPO_CLIP_KL
+    L, lse, rlse, old, r = oracle_case(c, mode)
+    print(f"lmhead small exact S={S} T={T} H={H} V={V}", flush=True)
+    out = run_device(c, mode, old, exact_bf16=True)
+    torch.cuda.synchronize()
+    check_forward(c, out, L, lse, rlse, r, mode)
+    check_grads(out, *grad_bounds(c, L, lse, r, mode, old, cached=False))
+
+
 def test_lmhead_ignore_index_int32_bool_mask_and_no_grads():
     c = make_case(2, 40, 128, 700, 2, seed=11, lengths=[40, 25])
     c["ids"][0, 3] = -100          # live by mask, ignored by id: no loss, no gradient, no error
@@ -220,15 +235,15 @@ def test_lmhead_ignore_index_int32_bool_mask_and_no_grads():
 
 
 def test_lmhead_all_masked_and_no_mask():
-    """No live token: the loss, log-probs and every gradient are 0 on the cached and the
-    chunked backward (the live count stays on the device; the products run with no
+    """No live token: the loss, log-probs and every gradient are 0 on the cached (f16 and
+    f32 terms) and the chunked backward (the live count stays on the device; the products run with no
     token tiles / an empty K), with and without the fused final norm; outputs are
     pre-filled with NaN so that a skipped write shows. Then mask = NULL."""
     c = make_case(2, 20, 64, 500, 2, seed=9, lengths=[20, 20])
     old = np.full((2, 20), -6.0, np.float32)
     zero = torch.zeros((2, 20), dtype=torch.float32, device=DEV)
     nan = float("nan")
-    for chunk in (0, 256):
+    for chunk, exact in ((0, False), (256, False), (0, True)):
         outs = grpo.LmheadOutputs(loss=torch.full((), nan, device=DEV), logp=torch.full((2, 20), nan, device=DEV),
                                   ref_logp=torch.full((2, 20), nan, device=DEV),
                                   token_loss=torch.full((2, 20), nan, device=DEV),
@@ -236,7 +251,7 @@ def test_lmhead_all_masked_and_no_mask():
                                   dhidden=torch.full((40, 64), nan, device=DEV), dweight=torch.full((500, 64), nan, device=DEV))
         out = grpo.lmhead_fwd_bwd(dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), zero, ref_weight=dev(c["rb"]),
                                   rewards=dev(c["rewards"]), group_size=2, old_logp=dev(old),
-                                  loss_mode=LossMode.GRPO_CLIP_KL, vocab_chunk=chunk, outputs=outs)
+                                  loss_mode=LossMode.GRPO_CLIP_KL, vocab_chunk=chunk, exact_bf16=exact, outputs=outs)
         torch.cuda.synchronize()
         assert float(out.loss) == 0.0 and not out.logp.any() and not out.token_loss.any()
         assert not out.dhidden.any() and not out.dweight.any()
@@ -247,7 +262,8 @@ def test_lmhead_all_masked_and_no_mask():
                                   dhidden=torch.full((40, 64), nan, device=DEV), dweight=torch.full((500, 64), nan, device=DEV),
                                   dnorm_weight=torch.full((64,), nan, device=DEV))
         out = grpo.lmhead_fwd_bwd(dev(cn["h"]), dev(cn["wb"]), dev(cn["ids"]), zero, rewards=dev(cn["rewards"]),
-                                  group_size=2, vocab_chunk=chunk, norm_weight=dev(cn["gamma"]), outputs=outs)
+                                  group_size=2, vocab_chunk=chunk, exact_bf16=exact, norm_weight=dev(cn["gamma"]),
+                                  outputs=outs)
         torch.cuda.synchronize()
         assert float(out.loss) == 0.0 and not out.logp.any()
         assert not out.dhidden.any() and not out.dweight.any() and not out.dnorm_weight.any()
