@@ -95,7 +95,10 @@ typedef enum pcp_loss_mode {
 #define PCP_FLAG_ASYNC 0x1u            /* return after enqueueing; errors surface in pcp_sync */
 #define PCP_FLAG_NO_ZERO_FILL 0x2u     /* leave dlogits rows of masked / pad tokens untouched */
 #define PCP_FLAG_FORCE_STREAMING 0x4u  /* use the two-read streaming kernel even when the
-                                          register-resident one fits (testing / comparison)  */
+                                          register-resident one fits (testing / comparison);
+                                          on pcp_grpo_lmhead_fwd_bwd with a vocab_chunk: the
+                                          chunked backward's low-memory form (K-major
+                                          operands, no transposed copies)                    */
 /* bf16 logits -> bf16 dlogits: every output is the f32 result rounded once to nearest
  * even. By default the resident kernel keeps the softmax terms of the sum pass as f16
  * (unit roundoff 2^-11) and scales them into dlogits, which saves one exponential per
@@ -285,7 +288,9 @@ int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
  * keeps the terms as f32 (4 bytes per live token and vocab entry), so each dlogit is
  * the f32 value rounded once. With an explicit vocab_chunk, or a backward workspace
  * above 64 GiB, the backward recomputes the logit tiles per vocab chunk instead
- * (dlogits = the f32 value rounded once), in memory bounded by the chunk.
+ * (dlogits = the f32 value rounded once): with a transposed copy of the chunk and of
+ * the weight (2 * (2 * tokens * chunk + hidden * vocab) bytes), or, when that does not
+ * fit, in memory bounded by the chunk alone.
  * The live-token count never leaves the device: with PCP_FLAG_ASYNC the call only
  * enqueues work, and it can be captured in a HIP graph. A captured graph uses the
  * context's work buffers as they were at capture: make one uncaptured call of the same

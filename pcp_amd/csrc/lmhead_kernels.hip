@@ -8,15 +8,17 @@
 //   kLmFwd  -> per (token, kLmPart vocab entries) partial (max, sum 2^(x*log2e - max))
 //              and the target logit when the target falls in the tile, for the policy
 //              and (n_model = 2) the reference model in one launch; with ECACHE also
-//              every policy term 2^(x*log2e - max) as f16 (the softmax cache);
+//              every policy term 2^(x*log2e - max) as f16 (the softmax cache), or as f32
+//              (lm_tile_fwd32_kernel, the exact-rounding backward);
 //   kLmBwd  -> dlogits for one vocab chunk in bf16, for the dhidden / dW products (the
 //              backward without the cache recomputes the logits this way);
 //   kLmGemm -> up to two plain products C = B * A^T on K-contiguous or K-major
-//              operands (dhidden and dW from the cached dlogits and their transpose);
+//              operands (dhidden and dW from the dlogits and their transpose);
 //              with FRAG the token-role operand A is stored fragment-major (written by
 //              lm_transpose_frag_kernel) and read straight into registers.
-// The forward and the FRAG products run on v_mfma_f32_16x16x32_bf16 (lm_tile16), the
-// backward recompute and the other products on v_mfma_f32_32x32x16_bf16 (lm_tile).
+// The logit tiles (kLmFwd, kLmBwd) and the FRAG products run on
+// v_mfma_f32_16x16x32_bf16 (lm_tile16), the K-major and plain products on
+// v_mfma_f32_32x32x16_bf16 (lm_tile).
 //
 // Reference: the LM head and loss of tools/export_qwen_forward.py:146-163
 // (self.model.lm_head(hidden) then F.cross_entropy), and matmulVJP
@@ -59,9 +61,7 @@ constexpr int WT = NW / 2;        // waves along the tokens
 constexpr int TW = 256 / WT;      // token columns per wave
 constexpr int NJ = TW / 32;       // 32-column token blocks per wave
 constexpr int QN = 32 / NW;       // direct-to-LDS loads per wave per operand per stage
-constexpr int LDD = BV + 8;       // bf16 dlogits row in the backward epilogue (528 B, 16-B aligned)
-constexpr size_t kSmemEpi = (BT / 2) * LDD * sizeof(__bf16);   // half the token columns at a time
-constexpr size_t kSmem = kSmemGemm > kSmemEpi ? kSmemGemm : kSmemEpi;
+constexpr size_t kSmem = kSmemGemm;
 constexpr int kPart = 128;        // vocab entries per log-sum-exp partial (one wave's rows)
 
 // s_waitcnt immediate for vmcnt(n), expcnt and lgkmcnt left at their maxima: vmcnt
@@ -148,17 +148,15 @@ __device__ __forceinline__ void lm_barrier() {
 // lane l holds token column l%32 and vocab rows 8*(r/4) + 4*(l/32) + r%4, r < 16.
 // Operands stream global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging)
 // through two stages of BK hidden columns.
-// This 32x32x16 tile serves the chunked backward (kLmBwd recompute tiles and their
-// products, whose token operand may be K-major) and the plain products; the forward
-// and the cached backward's products run on lm_tile16 below.
-// ATR (kLmGemm): the token-role operand is stored K-major and its fragments are read
-// with ds_read_b64_tr_b16 (see below).
-// Tile p of product prod (kLmGemm), or of the vocab chunk (kLmBwd), called by
-// lm_tile_kernel.
+// This 32x32x16 tile serves the products of the chunked backward's low-memory form
+// (ATR: the token-role operand stored K-major, its fragments read with
+// ds_read_b64_tr_b16, see below) and the plain products; the logit tiles and the
+// other products run on lm_tile16 below.
+// Tile p of product prod, called by lm_tile_kernel.
 template <int MODE, bool ATR>
 __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, char* smem) {
   using namespace lm;
-  static_assert(MODE == kLmBwd || MODE == kLmGemm, "32x32x16 tiles: the backward recompute and plain products");
+  static_assert(MODE == kLmGemm, "32x32x16 tiles: the K-major and plain products");
 
   // The product: the loss-head modes read rows of H elements of hidden (A) and W (B);
   // kLmGemm takes one of its (up to) two products.
@@ -193,11 +191,6 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
       krows_a = min(K, *g.kcount);
       K = min(K, (krows_a + BK - 1) / BK * BK);
     }
-  } else {
-    // Tiles over the live tokens only (the grid covers all N).
-    N = min(N, *a.count);
-    ntt = (N + BT - 1) / BT;
-    gm = lm_group_m(MODE, ntt);
   }
   int tm, tn;
   lm_tile_of(p, ntt, nvt, gm, tm, tn);
@@ -428,58 +421,6 @@ __device__ __forceinline__ void lm_tile(const LmTileArgs& a, int prod, int p, ch
           }
       }
     }
-  } else {
-    // dlogits[t][v] = coef_t * (onehot - 2^(x*log2e - lse2_t)) in bf16, staged as a
-    // token-major tile in LDS (one half of the token columns at a time), then
-    // written with 16-byte row-contiguous stores. Columns are relative to the chunk
-    // start; vocab past V is written as 0.
-    uint16_t* Ds = reinterpret_cast<uint16_t*>(smem);      // [BT / 2][LDD]
-    const int vlim = a.V - vw;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      __syncthreads();   // the pipeline's (or the previous half's) LDS reads are done
-      if ((wt * TW) / 128 == h) {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int tcol = (wt * TW) % 128 + 32 * j + (lane & 31);        // column within this half
-          const int n = m0 + h * 128 + tcol;
-          float cf = 0.f, l2 = 0.f;
-          int64_t rel = -1;
-          if (n < N) {
-            cf = a.coef[n];
-            l2 = a.lse2[n];
-            rel = lm_id(a, n) - vw;
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float d[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int vr = vrow(i, 4 * q + e);
-                const float x = -cf * hw_exp2(fmaf(acc[i][j][4 * q + e], kLog2e, -l2)) + (vr == rel ? cf : 0.f);
-                d[e] = (cf != 0.f && vr < vlim) ? x : 0.f;
-              }
-              const uint32_t lo = pack2<BF16T>(d[0], d[1]), hi = pack2<BF16T>(d[2], d[3]);
-              *reinterpret_cast<uint2*>(Ds + tcol * LDD + wv * 128 + vrow(i, 4 * q)) = make_uint2(lo, hi);
-            }
-        }
-      }
-      __syncthreads();
-      // 32 lanes per token row (512 B), eight rows per step over the workgroup.
-      const int cidx = tid & 31;
-      const int col0 = v0 - a.vc0 + cidx * 8;
-#pragma unroll 4
-      for (int it = 0; it < BT / 2 / (NTHR / 32); ++it) {
-        const int t = it * (NTHR / 32) + (tid >> 5);
-        const int n = m0 + h * 128 + t;
-        if (n < N && col0 < a.ldd) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(Ds + t * LDD + cidx * 8);
-          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.dchunk) + static_cast<int64_t>(n) * a.ldd + col0) = w;
-        }
-      }
-    }
   }
 }
 
@@ -511,8 +452,8 @@ constexpr int NJ16 = TW / 16;   // 16-column token blocks per wave
 constexpr int KS16 = BK / 32;   // 32-deep k-steps per stage
 }  // namespace lm
 
-// A tile on v_mfma_f32_16x16x32_bf16: the forward (kLmFwd, both operands through LDS)
-// and the products (kLmGemm with a fragment-major token operand). Same tile, waves,
+// A tile on v_mfma_f32_16x16x32_bf16: the logit tiles (kLmFwd, kLmBwd: both operands
+// through LDS) and the products (kLmGemm with a fragment-major token operand). Same tile, waves,
 // stages and operand paths as lm_tile; each wave's 128 x 64 block is 8 x 4 products of
 // 16 x 16 (128 accumulators), two 32-deep k-steps per stage. Under the power limit this
 // shape runs the pipes at a higher clock than 32x32x16 for the same work (the
@@ -525,13 +466,13 @@ constexpr int KS16 = BK / 32;   // 32-deep k-steps per stage
 template <int MODE, bool ECACHE, bool E32 = false>
 __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, char* smem) {
   using namespace lm;
-  static_assert(MODE == kLmGemm || MODE == kLmFwd, "16x16x32 tiles: the forward and the fragment-major products");
-  constexpr bool FWD = MODE == kLmFwd;
+  constexpr bool FWD = MODE == kLmFwd, BWD = MODE == kLmBwd;
+  constexpr bool TL = FWD || BWD;   // the token operand through LDS too (the logit tiles)
   const LmTileArgs::Gemm& g = a.gemm[FWD ? 0 : prod];
-  const void* opA = FWD ? a.A : g.A;
-  const void* opB = FWD ? (prod == 1 ? a.B2 : a.B) : g.B;
+  const void* opA = TL ? a.A : g.A;
+  const void* opB = TL ? (prod == 1 ? a.B2 : a.B) : g.B;
   int N, V, K, nvt, ntt, gm, lda, ldb, vt0 = 0;
-  if constexpr (FWD) {
+  if constexpr (TL) {
     // Tiles over the live tokens only (the grid covers all N).
     N = min(a.N, *a.count);
     V = a.V;
@@ -564,13 +505,13 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
 
   // Operands through LDS as in lm_tile: the vocab role (B) always, the token role (A)
   // for the forward. A stage buffer holds one operand (products) or both (forward).
-  constexpr int kBuf = FWD ? kStageBytes : kOpBytes;
+  constexpr int kBuf = TL ? kStageBytes : kOpBytes;
   const uint32_t wbytes = static_cast<uint32_t>(ldb) * 2u, hbytes = static_cast<uint32_t>(lda) * 2u;
   const int rows_w = min(BV, V - v0), rows_h = min(BT, N - m0);
   const __amdgpu_buffer_rsrc_t rw =
       row_rsrc(reinterpret_cast<const char*>(opB) + static_cast<int64_t>(v0) * wbytes, rows_w * wbytes);
   const __amdgpu_buffer_rsrc_t rh =
-      row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0) * hbytes, FWD ? rows_h * hbytes : 0u);
+      row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0) * hbytes, TL ? rows_h * hbytes : 0u);
   uint32_t dofw[QN], dofh[QN];
 #pragma unroll
   for (int q = 0; q < QN; ++q) {
@@ -586,7 +527,7 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
     for (int q = 0; q < QN; ++q) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (QN * wave + q) * 1024), 16, dofw[q] + koff, 0, 0,
                                                0);
-      if constexpr (FWD)
+      if constexpr (TL)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (QN * wave + q) * 1024), 16,
                                                  dofh[q] + koff, 0, 0, 0);
     }
@@ -616,13 +557,13 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
     const char* base = smem + (st % NST) * kBuf + fo[kk];
 #pragma unroll
     for (int i = 0; i < NI16; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(base + offA + i * 16 * ROWB);
-    if constexpr (FWD) {
+    if constexpr (TL) {
 #pragma unroll
       for (int j = 0; j < NJ16; ++j) bt[kk][j] = *reinterpret_cast<const bf16x8*>(base + offB + j * 16 * ROWB);
     }
   };
   auto ring_load = [&](int kk, int st) {
-    if constexpr (!FWD) {
+    if constexpr (!TL) {
 #pragma unroll
       for (int j = 0; j < NJ16; ++j)
         bt[kk][j] =
@@ -645,8 +586,8 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[set][i], bt[kk][j], acc[i][j], 0, 0, 0);
   };
   constexpr int kMf16 = NI16 * NJ16;
-  constexpr int kRd16 = NI16 + (FWD ? NJ16 : 0);     // fragment reads per k-step
-  constexpr int kLd16 = FWD ? 2 * QN : QN;          // direct-to-LDS loads per stage
+  constexpr int kRd16 = NI16 + (TL ? NJ16 : 0);     // fragment reads per k-step
+  constexpr int kLd16 = TL ? 2 * QN : QN;          // direct-to-LDS loads per stage
   // Per k-step: the next k-step's fragment reads between the first MFMAs (and the
   // stage's direct-to-LDS loads after them when the k-step starts a buffer), the ring
   // reloads after the last.
@@ -663,7 +604,7 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, kMf16 - kRd16 - nd, 0);
-    if constexpr (!FWD) __builtin_amdgcn_sched_group_barrier(0x020, NJ16, 0);
+    if constexpr (!TL) __builtin_amdgcn_sched_group_barrier(0x020, NJ16, 0);
   };
   static_assert(kRd16 + kLd16 <= kMf16, "schedule");
 
@@ -688,11 +629,11 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
     ring_load(0, n1);
     sched16(std::false_type{});
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(FWD ? kWaitVm0 : wait_vm(2 * NJ16));   // stage kb+1's LDS loads landed
+    __builtin_amdgcn_s_waitcnt(TL ? kWaitVm0 : wait_vm(2 * NJ16));   // stage kb+1's LDS loads landed
     lm_barrier();
     // The forward's 8 direct-to-LDS loads go between the k-step's MFMAs after its
     // fragment reads; the products issue their 4 first (measured faster each way).
-    if constexpr (FWD) {
+    if constexpr (TL) {
       fload(0, n1, 0);
       issue(min(kb + 2, nk - 1), kb & 1);
     } else {
@@ -812,6 +753,52 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
         }
       }
     }
+  } else if constexpr (BWD) {
+    // dlogits[t][v] = coef_t * (onehot - 2^(x*log2e - lse2_t)) in bf16 into the chunk
+    // buffer (columns relative to the chunk start; vocab past V is written as 0), with
+    // the forward's exchange: after one v_permlane16_swap per register pair each lane
+    // holds 8 consecutive vocab rows of one token, one 16-byte store.
+    const int vlim = a.V - vw;
+#pragma unroll
+    for (int jj = 0; jj < NJ16; jj += 2) {
+      float cf[2], l2[2];
+      int rel[2];
+#pragma unroll
+      for (int jo = 0; jo < 2; ++jo) {
+        const int n = m0 + wt * TW + 16 * (jj + jo) + (lane & 15);
+        cf[jo] = l2[jo] = 0.f;
+        rel[jo] = -1;
+        if (n < N) {
+          cf[jo] = a.coef[n];
+          l2[jo] = a.lse2[n];
+          rel[jo] = static_cast<int>(lm_id(a, n) - vw);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NI16; ++i) {
+        uint32_t pk[2][2];
+#pragma unroll
+        for (int jo = 0; jo < 2; ++jo) {
+          float d[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int vr = 16 * i + 4 * grp + r;
+            const float x = -cf[jo] * hw_exp2(fmaf(acc[i][jj + jo][r], kLog2e, -l2[jo])) + (vr == rel[jo] ? cf[jo] : 0.f);
+            d[r] = (cf[jo] != 0.f && vr < vlim) ? x : 0.f;
+          }
+          pk[jo][0] = pack2<BF16T>(d[0], d[1]);
+          pk[jo][1] = pack2<BF16T>(d[2], d[3]);
+        }
+        const auto lo = __builtin_amdgcn_permlane16_swap(pk[0][0], pk[1][0], false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap(pk[0][1], pk[1][1], false, false);
+        const int n = m0 + wt * TW + 16 * (jj + (grp & 1)) + (lane & 15);
+        const int col = vw - a.vc0 + 16 * i + 8 * (grp >> 1);
+        if (n < N) {
+          const u32x4 w = {lo[0], hi[0], lo[1], hi[1]};
+          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.dchunk) + static_cast<int64_t>(n) * a.ldd + col) = w;
+        }
+      }
+    }
   } else {
     // C[v][t] (+)= the tile; rows past V and columns past N are not stored. For fixed
     // (i, r) each 16-lane group writes 16 consecutive floats of one row per token block,
@@ -874,8 +861,8 @@ __device__ __forceinline__ void lm_fwd_item(const LmTileArgs& a, char* smem) {
 // per-tile barriers and atomic cost more than these early exits), and against a
 // persistent static split, 46.2 ms.
 // ECACHE (kLmFwd): the policy's tiles also store the softmax terms. FRAG (kLmGemm): the
-// token-role operands are fragment-major (the 16x16x32 tile); otherwise the products
-// and the backward recompute run on the 32x32x16 tile, ATR with a K-major token operand.
+// token-role operands are fragment-major (the 16x16x32 tile, as the logit tiles);
+// otherwise the products run on the 32x32x16 tile, ATR with a K-major token operand.
 template <int MODE, bool ATR = false, bool ECACHE = false, bool FRAG = false>
 __global__ void __launch_bounds__(lm::NTHR) __attribute__((amdgpu_waves_per_eu(lm::WPE, lm::WPE)))
 lm_tile_kernel(LmTileArgs a) {
@@ -891,7 +878,7 @@ lm_tile_kernel(LmTileArgs a) {
     const int prod = i < per0 ? 0 : 1;
     const int p = prod == 0 ? xcd * per0 + i : xcd * per1 + (i - per0);
     if (p >= (prod == 0 ? t0 : t1)) return;
-    if constexpr (FRAG)
+    if constexpr (FRAG || MODE == kLmBwd)
       lm_tile16<MODE, false>(a, prod, p, smem);
     else
       lm_tile<MODE, ATR>(a, prod, p, smem);

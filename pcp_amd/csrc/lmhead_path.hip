@@ -180,14 +180,26 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_dt = o_d + 2 * static_cast<size_t>(ldt) * ldv;
   const size_t o_wt = o_dt + (a->dweight ? 2 * static_cast<size_t>(ldv) * ldt : 0);
   const size_t cache_bytes = o_wt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
-  bool cached = false;
+  const size_t o_cdt = 2 * static_cast<size_t>(ldt) * chunk;
+  const size_t o_cwt = o_cdt + (a->dweight ? 2 * static_cast<size_t>(chunk) * ldt : 0);
+  const size_t chunk_frag_bytes = o_cwt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
+  bool cached = false, chunk_frag = false;
   if (bwd) {
     if (a->vocab_chunk == 0 && cache_bytes <= kCacheBudget) {
       e = grow_dbuf(ctx, cache_bytes);
       if (e == hipSuccess) cached = true;
       else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the softmax cache");
     }
-    if (!cached && (e = grow_dbuf(ctx, 2 * static_cast<size_t>(N) * chunk)) != hipSuccess) {
+    // Chunked: the dlogits chunk [ldt, chunk], with room for its transpose [chunk, ldt] and
+    // W^T [H, ldv] (fragment-major, once per call) the products run as on the cached
+    // path; in less memory (or with PCP_FLAG_FORCE_STREAMING), with K-major operands and
+    // no transposed copies.
+    if (!cached && !(a->flags & PCP_FLAG_FORCE_STREAMING)) {
+      e = grow_dbuf(ctx, chunk_frag_bytes);
+      if (e == hipSuccess) chunk_frag = true;
+      else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the dlogits chunk");
+    }
+    if (!cached && !chunk_frag && (e = grow_dbuf(ctx, 2 * static_cast<size_t>(N) * chunk)) != hipSuccess) {
       if (e == hipErrorOutOfMemory)
         return fail(ctx, PCP_ERR_OOM, "hipMalloc of the %lld x %lld dlogits chunk failed", (long long)N,
                     (long long)chunk);
@@ -419,8 +431,56 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       if (timed && (e = hipEventRecord(ctx->prof_stop[ctx->prof_used++], st)) != hipSuccess)
         return hip_fail(ctx, e, "hipEventRecord");
     } else {
-      if (a->dweight && (e = launch_lm_transpose(tr, st)) != hipSuccess)
+      if (a->dweight && (e = chunk_frag ? launch_lm_transpose_frag(tr, st) : launch_lm_transpose(tr, st)) != hipSuccess)
         return hip_fail(ctx, e, "transposing hidden rows");
+      uint16_t* cdt = chunk_frag && a->dweight ? reinterpret_cast<uint16_t*>(dbuf + o_cdt) : nullptr;
+      uint16_t* cwt = chunk_frag && want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_cwt) : nullptr;
+      if (cwt) {
+        const LmTransposeArgs tw{static_cast<const uint16_t*>(a->weight), H, static_cast<int>(V), static_cast<int>(H),
+                                 cwt, ldv, nullptr};
+        if ((e = launch_lm_transpose_frag(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
+      }
+      // The cached path's products over one chunk [vc0, vc0 + w): D_c token-major (rows of
+      // chunk entries) with W^T's fragments of that range, and D_c^T with hidden^T.
+      auto products_frag = [&](int64_t vc0, int64_t w) -> hipError_t {
+        LmTileArgs::Gemm g[2];
+        int ng = 0;
+        std::memset(g, 0, sizeof(g));
+        if (want_dy) {
+          LmTileArgs::Gemm& d = g[ng++];
+          d.B = dbuf;
+          d.ldb = static_cast<int>(chunk);
+          d.V = static_cast<int>(N);
+          d.vcount = cnt;
+          d.A = cwt + 16 * vc0;   // fragment column vc0 / 32 (1 KB = 512 elements each)
+          d.a_frag = 1;
+          d.lda = static_cast<int>(ldv);
+          d.N = static_cast<int>(H);
+          d.K = static_cast<int>((w + 63) / 64 * 64);
+          d.nvt = ntl;
+          d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
+          d.C = dhc;
+          d.ldc = static_cast<int>(H);
+          d.accumulate = vc0 > 0;
+        }
+        if (a->dweight) {
+          LmTileArgs::Gemm& d = g[ng++];
+          d.B = cdt;
+          d.ldb = static_cast<int>(ldt);
+          d.V = static_cast<int>(w);
+          d.A = sp + o_ht;
+          d.a_frag = 1;
+          d.lda = static_cast<int>(ldt);
+          d.N = static_cast<int>(H);
+          d.K = static_cast<int>(ldt);
+          d.kcount = cnt;
+          d.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
+          d.ntt = static_cast<int>((H + kLmTileT - 1) / kLmTileT);
+          d.C = a->dweight + vc0 * H;
+          d.ldc = static_cast<int>(H);
+        }
+        return launch_lm_gemms(g, ng, false, st);
+      };
       ta.B = a->weight;
       ta.lse2 = F(o_l2);
       ta.coef = F(o_coef);
@@ -433,7 +493,14 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         ta.vt0 = static_cast<int>(vc0 / kLmTileV);
         ta.nvt = static_cast<int>((w + kLmTileV - 1) / kLmTileV);
         if ((e = launch_lm_tiles(kLmBwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head backward tiles");
-        if ((e = products(vc0, w, chunk)) != hipSuccess) return hip_fail(ctx, e, "dhidden / dweight products");
+        if (cdt) {
+          // D_c^T [w, ldt], zero past the live tokens.
+          const LmTransposeArgs td{reinterpret_cast<const uint16_t*>(dbuf), chunk, static_cast<int>(N),
+                                   static_cast<int>(w), cdt, ldt, cnt};
+          if ((e = launch_lm_transpose(td, st)) != hipSuccess) return hip_fail(ctx, e, "transposing dlogits");
+        }
+        if ((e = chunk_frag ? products_frag(vc0, w) : products(vc0, w, chunk)) != hipSuccess)
+          return hip_fail(ctx, e, "dhidden / dweight products");
       }
     }
     if (norm && want_dy) {

@@ -222,6 +222,7 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
                    loss_mode: int = LossMode.REINFORCE, clip_eps: float = 0.2, kl_beta: float = 0.04,
                    loss_norm: float = 0.0, std_eps: float = 1e-8, want_grads: bool = True, vocab_chunk: int = 0,
                    norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6, exact_bf16: bool = False,
+                   low_memory_chunks: bool = False,
                    outputs: LmheadOutputs | None = None, sync: bool = True, stream=None,
                    ctx: Context | None = None) -> LmheadOutputs:
     """Fused LM-head + GRPO loss (pcp_grpo_lmhead_fwd_bwd). hidden [S*T, H] bf16,
@@ -231,7 +232,8 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
     vocab_chunk 0 lets the library keep the forward's softmax terms for the backward:
     f16 by default, f32 with exact_bf16 (PCP_FLAG_EXACT_BF16; the bf16 dlogits are then
     the f32 value rounded once); a chunk width recomputes the logits per chunk
-    instead."""
+    instead, and low_memory_chunks (PCP_FLAG_FORCE_STREAMING) selects that backward's
+    form without transposed copies (which it takes by itself when they do not fit)."""
     ctx = ctx or default_context(hidden.device.index or 0)
     if ids.dim() != 2:
         raise PcpError(-1, "ids must be [S, T]")
@@ -273,7 +275,8 @@ def lmhead_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, ids: torch.Tensor
     a.norm_weight, a.dnorm_weight, a.norm_eps = _ptr(norm_weight), _ptr(outputs.dnorm_weight), norm_eps
     a.loss_mode = int(loss_mode)
     a.clip_eps, a.kl_beta, a.std_eps, a.loss_norm = clip_eps, kl_beta, std_eps, loss_norm
-    a.flags = (0 if sync else _lib.FLAG_ASYNC) | (_lib.FLAG_EXACT_BF16 if exact_bf16 else 0)
+    a.flags = ((0 if sync else _lib.FLAG_ASYNC) | (_lib.FLAG_EXACT_BF16 if exact_bf16 else 0)
+               | (_lib.FLAG_FORCE_STREAMING if low_memory_chunks else 0))
     a.stream = _stream_handle(stream)
     check(lib().pcp_grpo_lmhead_fwd_bwd(ctx.handle, ctypes.byref(a)), ctx.handle)
     return outputs

@@ -77,12 +77,12 @@ def oracle_case(c, mode, clip_eps=0.2, kl_beta=0.04):
 
 
 def run_device(c, mode, old, *, vocab_chunk=0, want_grads=True, ids=None, mask=None, clip_eps=0.2, kl_beta=0.04,
-               exact_bf16=False):
+               exact_bf16=False, low_memory=False):
     return grpo.lmhead_fwd_bwd(dev(c["hb"]), dev(c["wb"]), dev(c["ids"]) if ids is None else ids,
                                dev(c["mask"]) if mask is None else mask, ref_weight=dev(c["rb"]),
                                rewards=dev(c["rewards"]), group_size=c["G"], old_logp=dev(old), loss_mode=mode,
                                clip_eps=clip_eps, kl_beta=kl_beta, vocab_chunk=vocab_chunk, want_grads=want_grads,
-                               exact_bf16=exact_bf16)
+                               exact_bf16=exact_bf16, low_memory_chunks=low_memory)
 
 
 def cache_error(L, lse, coef, ids):
@@ -201,6 +201,25 @@ def test_lmhead_small_vs_oracle(shape, mode):
     torch.cuda.synchronize()
     check_forward(c, out, L, lse, rlse, r, mode)
     check_grads(out, *grad_bounds(c, L, lse, r, mode, old, cached=chunk == 0))
+
+
+@pytest.mark.parametrize("shape", [s for s in SMALL if s[5] > 0], ids=lambda s: f"S{s[0]}T{s[1]}H{s[2]}V{s[3]}c{s[5]}")
+def test_lmhead_small_low_memory_chunks_vs_oracle(shape):
+    """The chunked backward's low-memory form (K-major operands read with LDS transpose
+    loads, no transposed copies), which it takes when the copies do not fit: the same
+    shapes against the oracle, and the same forward as the default chunked form."""
+    S, T, H, V, G, chunk, lengths = shape
+    c = make_case(S, T, H, V, G, seed=S * 1000 + V, lengths=lengths)
+    mode = LossMode.GRPO_CLIP_KL
+    L, lse, rlse, old, r = oracle_case(c, mode)
+    print(f"lmhead small low-memory chunks S={S} T={T} H={H} V={V} chunk={chunk}", flush=True)
+    lo = run_device(c, mode, old, vocab_chunk=chunk, low_memory=True)
+    hi = run_device(c, mode, old, vocab_chunk=chunk)
+    torch.cuda.synchronize()
+    check_forward(c, lo, L, lse, rlse, r, mode)
+    check_grads(lo, *grad_bounds(c, L, lse, r, mode, old, cached=False))
+    for f in ("loss", "logp", "ref_logp", "token_loss"):
+        assert torch.equal(getattr(lo, f), getattr(hi, f)), f
 
 
 @pytest.mark.parametrize("shape", SMALL, ids=lambda s: f"S{s[0]}T{s[1]}H{s[2]}V{s[3]}")
@@ -362,12 +381,13 @@ def test_execute_lmhead_final_norm_shifted():
     assert np.array_equal(np.frombuffer(outs[6], np.float32), ref.dnorm_weight.cpu().numpy())
 
 
-@pytest.mark.parametrize("chunk, exact", [(512, False), (0, False), (0, True)], ids=["chunked", "cached", "exact"])
-def test_lmhead_deterministic(chunk, exact):
+@pytest.mark.parametrize("chunk, exact, low", [(512, False, False), (512, False, True), (0, False, False),
+                                              (0, True, False)], ids=["chunked", "chunked-low-memory", "cached", "exact"])
+def test_lmhead_deterministic(chunk, exact, low):
     c = make_case(2, 70, 128, 900, 2, seed=5, lengths=[70, 33])
     old = np.full((2, 70), -7.0, np.float32)
-    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk, exact_bf16=exact)
-    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk, exact_bf16=exact)
+    a = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk, exact_bf16=exact, low_memory=low)
+    b = run_device(c, LossMode.GRPO_CLIP_KL, old, vocab_chunk=chunk, exact_bf16=exact, low_memory=low)
     torch.cuda.synchronize()
     for f in ("loss", "logp", "ref_logp", "token_loss", "dhidden", "dweight"):
         assert torch.equal(getattr(a, f), getattr(b, f)), f
