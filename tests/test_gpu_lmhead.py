@@ -237,6 +237,50 @@ def test_lmhead_small_exact_vs_oracle(shape):
     check_grads(out, *grad_bounds(c, L, lse, r, mode, old, cached=False))
 
 
+def _variant_shapes(n, seed=2024):
+    # Seeded shapes for all four backward forms: up to 8 sequences of up to 700 tokens
+    # (empty ones included), hidden sizes of 1 to 16 stages, vocabularies up to 40,000
+    # and chunk widths below and past them, capped so the float64 oracle stays quick.
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        S = int(rng.integers(1, 9))
+        T = int(rng.integers(3, 700))
+        H = int(rng.choice([64, 128, 192, 256, 448, 640, 1024]))
+        V = int(rng.integers(1, 40000))
+        G = int(rng.choice([d for d in range(1, S + 1) if S % d == 0]))
+        lengths = [int(x) for x in rng.integers(0, T + 1, size=S)]
+        chunk = int(rng.choice([256, 512, 1024, 4096, 16384]))
+        std = float(rng.choice([1.0, 2.0, 4.0]))
+        mode = LossMode.GRPO_CLIP_KL if rng.random() < 0.7 else LossMode.REINFORCE
+        if S * T * V * H <= 3e9:
+            out.append((S, T, H, V, G, chunk, lengths, std, mode))
+    return out
+
+
+@pytest.mark.parametrize("case", _variant_shapes(12), ids=lambda s: f"S{s[0]}T{s[1]}H{s[2]}V{s[3]}c{s[5]}")
+def test_lmhead_random_variants_vs_oracle(case):
+    """Each backward form on the same seeded random inputs: the default (f16 softmax
+    terms), PCP_FLAG_EXACT_BF16 (f32 terms), the chunked recompute with transposed
+    copies and in its low-memory form, each under its bound; the forward outputs of
+    all four are identical."""
+    S, T, H, V, G, chunk, lengths, std, mode = case
+    c = make_case(S, T, H, V, G, seed=S * 7919 + V, lengths=lengths, logit_std=std)
+    L, lse, rlse, old, r = oracle_case(c, mode)
+    first = None
+    for name, kw in (("cached", {}), ("exact", dict(exact_bf16=True)), ("chunked", dict(vocab_chunk=chunk)),
+                     ("low-memory", dict(vocab_chunk=chunk, low_memory=True))):
+        print(f"lmhead random S={S} T={T} H={H} V={V} chunk={chunk} mode={int(mode)} {name}", flush=True)
+        out = run_device(c, mode, old, **kw)
+        torch.cuda.synchronize()
+        check_forward(c, out, L, lse, rlse, r, mode)
+        check_grads(out, *grad_bounds(c, L, lse, r, mode, old, cached=name == "cached"))
+        if first is None:
+            first = out
+        for f in ("loss", "logp", "token_loss"):
+            assert torch.equal(getattr(out, f), getattr(first, f)), (name, f)
+
+
 def test_lmhead_ignore_index_int32_bool_mask_and_no_grads():
     c = make_case(2, 40, 128, 700, 2, seed=11, lengths=[40, 25])
     c["ids"][0, 3] = -100          # live by mask, ignored by id: no loss, no gradient, no error
