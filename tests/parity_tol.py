@@ -119,18 +119,22 @@ BF16_CACHED_REL = 2.0 ** -8 + 2.0 ** -11 + 1.3e-5
 BF16_EXACT_REL = 2.0 ** -8 + 1.1e-5
 
 
-def assert_dlogits(got, want, floor_rows, bf16_out, exact=False):
+def assert_dlogits(got, want, floor_rows, bf16_out, exact=False, f16_out=False):
     """floor_rows: per-row absolute floor (coef_floor), broadcast over the vocabulary.
     bf16_out: a 16-bit output (bf16 or f16). exact: the output is the f32 result rounded
-    once (PCP_FLAG_EXACT_BF16, or a path without the f16 softmax cache)."""
+    once (PCP_FLAG_EXACT_BF16, or a path without the f16 softmax cache). f16_out: the
+    output is f16, whose values below 2^-14 are subnormal with a fixed spacing of 2^-24,
+    so a correctly rounded one is off by up to 2^-25 absolutely, whatever its size (rows
+    whose coefficient nearly cancels reach that range)."""
     got = got.astype(np.float64)
     want = want.astype(np.float64)
     fl = np.asarray(floor_rows, np.float64)[..., None]
     err = np.abs(got - want)
+    sub = 2.0 ** -25 if f16_out else 0.0
     if bf16_out and exact:
-        tol = BF16_EXACT_REL * np.abs(want) + (1 + 2.0 ** -7) * fl
+        tol = BF16_EXACT_REL * np.abs(want) + (1 + 2.0 ** -7) * fl + sub
     elif bf16_out:
-        tol = BF16_CACHED_REL * np.abs(want) + (1 + 2.0 ** -6) * fl
+        tol = BF16_CACHED_REL * np.abs(want) + (1 + 2.0 ** -6) * fl + sub
     else:
         tol = 1e-5 * np.abs(want) + fl
         assert err.max() <= 1e-4

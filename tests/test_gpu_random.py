@@ -1,7 +1,9 @@
 """Seeded random sweep of the loss head (pcp_grpo_loss_fwd_bwd) against the CPU oracle:
 vocabulary sizes from 1 to 151,936, f32 / bf16 / f16 logits, the aligned and the
 reference's shifted layout, ignored (-100) ids, empty sequences, both loss modes, and
-the resident and streaming kernels. The bars are those of tests/parity_tol.py."""
+the resident and streaming kernels. The bars are those of tests/parity_tol.py.
+A one-off run of the same generator over seeds 16-175 (both kernels, all passing with
+the f16 subnormal term of assert_dlogits) found the cases that term covers."""
 import numpy as np
 import pytest
 import torch
@@ -53,7 +55,9 @@ def make_case(k):
 
 
 @pytest.mark.parametrize("streaming", [False, True])
-@pytest.mark.parametrize("k", range(len(VOCABS)))
+# Three passes over the vocabularies with other seeds, and two seeds whose clip-KL rows
+# have coefficients near 1e-5, which puts their f16 dlogits among f16's subnormals.
+@pytest.mark.parametrize("k", list(range(3 * len(VOCABS))) + [77, 125])
 def test_random_case_vs_oracle(k, streaming):
     c = make_case(k)
     S, T, V, rows, off = c["S"], c["T"], c["V"], c["rows"], c["off"]
@@ -86,7 +90,7 @@ def test_random_case_vs_oracle(k, streaming):
     floor = tok_to_rows(full_floor(want, c["mask"], c["old"], S, reinforce, 0.04, 0.2, scale), rows, off, T)
     got = host_bits(out.dlogits)
     got = orc.bf16_to_f32(got) if c["dt"] == "bf16" else got.astype(np.float32)
-    assert_dlogits(got, want.dlogits, floor, c["dt"] != "f32")
+    assert_dlogits(got, want.dlogits, floor, c["dt"] != "f32", f16_out=c["dt"] == "f16")
     # rows without a live token (masked, ignored, pad) are exactly zero
     d = host_bits(out.dlogits)
     for s in range(S):
