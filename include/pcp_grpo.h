@@ -289,8 +289,8 @@ int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
  * the f32 value rounded once. With an explicit vocab_chunk, or a backward workspace
  * above 64 GiB, the backward recomputes the logit tiles per vocab chunk instead
  * (dlogits = the f32 value rounded once): with a transposed copy of the chunk and of
- * the weight (2 * (2 * tokens * chunk + hidden * vocab) bytes), or, when that does not
- * fit, in memory bounded by the chunk alone.
+ * the weight (2 * (2 * tokens * chunk + hidden * vocab) bytes, up to 64 GiB), or, when
+ * that does not fit, in memory bounded by the chunk alone (2 * tokens * chunk bytes).
  * The live-token count never leaves the device: with PCP_FLAG_ASYNC the call only
  * enqueues work, and it can be captured in a HIP graph. A captured graph uses the
  * context's work buffers as they were at capture: make one uncaptured call of the same

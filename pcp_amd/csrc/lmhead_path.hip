@@ -192,9 +192,9 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     }
     // Chunked: the dlogits chunk [ldt, chunk], with room for its transpose [chunk, ldt] and
     // W^T [H, ldv] (fragment-major, once per call) the products run as on the cached
-    // path; in less memory (or with PCP_FLAG_FORCE_STREAMING), with K-major operands and
-    // no transposed copies.
-    if (!cached && !(a->flags & PCP_FLAG_FORCE_STREAMING)) {
+    // path; past kCacheBudget, in less memory, or with PCP_FLAG_FORCE_STREAMING, with
+    // K-major operands and no transposed copies.
+    if (!cached && !(a->flags & PCP_FLAG_FORCE_STREAMING) && chunk_frag_bytes <= kCacheBudget) {
       e = grow_dbuf(ctx, chunk_frag_bytes);
       if (e == hipSuccess) chunk_frag = true;
       else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the dlogits chunk");
