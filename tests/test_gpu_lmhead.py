@@ -803,10 +803,13 @@ def _clip_kl_coef(lp, lr, old, adv, mask, cfg, lse):
     return r.coef, fl
 
 
-def _torch_reference(inp, coef=None, chunk=2048, floor=None):
+def _torch_reference(inp, coef=None, chunk=2048, floor=None, cache_terms=None):
     """fp32 logp / lse per token, and with coef the gradients and their bounds; floor
     (per token) is the error c itself may carry (clip + KL: coef_floor), else c is
-    exact up to f32 rounding (REINFORCE)."""
+    exact up to f32 rounding (REINFORCE). The bounds include the f16 softmax terms'
+    error, unless cache_terms (a dict) is given: that part of the bounds then goes to
+    cache_terms["dh"] and cache_terms["dw"] (the bounds returned are those of dlogits
+    rounded once, PCP_FLAG_EXACT_BF16)."""
     h, W, ids = inp["hidden"], inp["weight"], inp["ids"].reshape(-1)
     Wf = W.float()
     N = h.shape[0]
@@ -819,6 +822,9 @@ def _torch_reference(inp, coef=None, chunk=2048, floor=None):
         dw = torch.zeros_like(Wf)
         tol_dw = torch.zeros_like(Wf)
         Wa = Wf.abs()
+        if cache_terms is not None:
+            cache_terms["dh"] = torch.empty_like(dh)
+            cache_terms["dw"] = torch.zeros_like(Wf)
     for n0 in range(0, N, chunk):
         hc = h[n0:n0 + chunk].float()
         Lc = hc @ Wf.T
@@ -849,7 +855,11 @@ def _torch_reference(inp, coef=None, chunk=2048, floor=None):
             X = torch.exp(blk - l[:, None]).repeat_interleave(128, dim=1)[:, :V]
             X = (1 + 2.0 ** -7) * cc.abs()[:, None] * (2.0 ** -11 * P + 2.0 ** -25 * X)
             X.scatter_(1, idc[:, None], 0.0)
-            E += X
+            if cache_terms is None:
+                E += X
+            else:
+                cache_terms["dh"][n0:n0 + chunk] = X @ Wa
+                cache_terms["dw"] += X.T @ hc.abs()
             del P, X, blk, Lc
             dh[n0:n0 + chunk] = D @ Wf
             tol_dh[n0:n0 + chunk] = E @ Wa
@@ -892,14 +902,25 @@ def test_config5_full_size():
             # a reference independent of the device's forward.
             coef = (-torch.from_numpy(adv).to(DEV).double()[:, None] * inp["mask"].double() / (L[:, None] * S))
             print("config 5 full size: reference gradients", flush=True)
-            _, _, dh, tol_dh, dw, tol_dw = _torch_reference(inp, coef.float().reshape(-1))
-            bad_h = ((out.dhidden - dh).abs() > tol_dh + 1e-6 * tol_dh.max()).sum().item()
-            bad_w = ((out.dweight - dw).abs() > tol_dw + 1e-6 * tol_dw.max()).sum().item()
-            used_h = float(((out.dhidden - dh).abs() / (tol_dh + 1e-30)).max())
-            used_w = float(((out.dweight - dw).abs() / (tol_dw + 1e-30)).max())
-            print(f"  REINFORCE gradients: largest error / bound: dhidden {used_h:.3f}, dW {used_w:.3f}", flush=True)
-            assert bad_h == 0 and bad_w == 0, (bad_h, bad_w)
-            del dh, tol_dh, dw, tol_dw
+            cache = {}
+            _, _, dh, tol_dh, dw, tol_dw = _torch_reference(inp, coef.float().reshape(-1), cache_terms=cache)
+            # The default backward (f16 softmax terms) under the bound with their term, and
+            # PCP_FLAG_EXACT_BF16 (f32 terms) under the bound of dlogits rounded once.
+            exact = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"],
+                                        ref_weight=inp["ref_weight"], rewards=inp["rewards"], group_size=cfg.group,
+                                        old_logp=old, loss_mode=mode, exact_bf16=True)
+            torch.cuda.synchronize()
+            assert torch.equal(exact.logp, out.logp) and torch.equal(exact.loss, out.loss)
+            for name, res, th, tw in (("default", out, tol_dh + cache["dh"], tol_dw + cache["dw"]),
+                                      ("exact", exact, tol_dh, tol_dw)):
+                bad_h = ((res.dhidden - dh).abs() > th + 1e-6 * th.max()).sum().item()
+                bad_w = ((res.dweight - dw).abs() > tw + 1e-6 * tw.max()).sum().item()
+                used_h = float(((res.dhidden - dh).abs() / (th + 1e-30)).max())
+                used_w = float(((res.dweight - dw).abs() / (tw + 1e-30)).max())
+                print(f"  REINFORCE gradients, {name}: largest error / bound: dhidden {used_h:.3f}, dW {used_w:.3f}",
+                      flush=True)
+                assert bad_h == 0 and bad_w == 0, (name, bad_h, bad_w)
+            del dh, tol_dh, dw, tol_dw, cache, exact
         else:
             lr_ref, rlse_ref = _torch_reference({**inp, "weight": inp["ref_weight"]})[:2]
             err = (out.ref_logp.reshape(-1) - lr_ref).abs()
