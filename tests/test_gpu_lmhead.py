@@ -973,3 +973,18 @@ def test_lmhead_large_batch_cached_matches_chunked():
         print(f"  {name}: relative Frobenius difference {rel:.2e}, largest {worst:.2e}", flush=True)
         assert bool(torch.isfinite(a).all()) and rel < 2 ** -8 and worst < 2 ** -6, (name, rel, worst)
     assert not torch.equal(cached.dweight, chunked.dweight)
+    # The chunked backward's low-memory form (K-major operands on the 32x32x16 tile, 32-bit
+    # offsets within each 40,960 x 16,384 chunk): the same D as the chunked form. (Measured
+    # bit-identical, both MFMA shapes adding the k products in the same order; the bar
+    # leaves room for a different one.)
+    del cached
+    low = grpo.lmhead_fwd_bwd(inp["hidden"], inp["weight"], inp["ids"], inp["mask"], old_logp=old,
+                              vocab_chunk=16384, low_memory_chunks=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(low.logp, chunked.logp) and float(low.loss) == float(chunked.loss)
+    for name in ("dhidden", "dweight"):
+        a, b = getattr(low, name), getattr(chunked, name)
+        rel = float((a - b).norm() / b.norm())
+        worst = float((a - b).abs().max() / b.abs().max())
+        print(f"  low-memory {name}: relative Frobenius difference {rel:.2e}, largest {worst:.2e}", flush=True)
+        assert bool(torch.isfinite(a).all()) and rel < 2 ** -16 and worst < 2 ** -12, (name, rel, worst)
