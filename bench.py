@@ -297,7 +297,6 @@ def bench_lmhead(args) -> None:
                                   if args.vocab_chunk else ""),
                    "tokens": N, "valid_tokens": live, "global_batch": cfg.S, "seq_len": cfg.T},
         "step_tflops": step_flops / (ms_step / 1e3) / 1e12,
-        "dense_equivalent_tflops": products * 2.0 * N * H * V / (ms_step / 1e3) / 1e12,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
                      "kernel": tile_kernel, "kernel_ms": kernel_ms,

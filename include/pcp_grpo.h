@@ -102,10 +102,11 @@ typedef enum pcp_loss_mode {
 /* bf16 logits -> bf16 dlogits: every output is the f32 result rounded once to nearest
  * even. By default the resident kernel keeps the softmax terms of the sum pass as f16
  * (unit roundoff 2^-11) and scales them into dlogits, which saves one exponential per
- * element (3-5% of the step at configs 2-4) and adds up to 2^-11 of |dlogit| before
- * the bf16 rounding. On pcp_grpo_lmhead_fwd_bwd the forward keeps its softmax terms as
- * f32 instead of f16, so the bf16 dlogits operand of the backward is likewise the f32
- * value rounded once (about twice the backward workspace). */
+ * element (3-5% of the step at configs 2-4) and adds, before the bf16 rounding, up to
+ * 2^-11 of |dlogit| plus 2^-25 * |c| (terms below f16's normal range). On
+ * pcp_grpo_lmhead_fwd_bwd the forward keeps its softmax terms as f32 instead of f16,
+ * so the bf16 dlogits operand of the backward is likewise the f32 value rounded once
+ * (about twice the backward workspace). */
 #define PCP_FLAG_EXACT_BF16 0x8u
 
 /* The token id that contributes nothing (F.cross_entropy ignore_index; the
@@ -187,6 +188,15 @@ int pcp_get_backend_type(const pcp_ctx* ctx);
 const char* pcp_last_error(const pcp_ctx* ctx);
 /* Wait for work enqueued with PCP_FLAG_ASYNC; returns the first device-side error. */
 int pcp_sync(pcp_ctx* ctx);
+/* Free the context's grow-only device work buffers: the per-call scratch and the
+ * LM-head backward workspace (the softmax cache: 11.2 GB at 16,384 tokens, V =
+ * 151,936, H = 4,096; 21.2 GB with PCP_FLAG_EXACT_BF16), which otherwise stay held
+ * until pcp_destroy. Synchronises the device first (every stream: calls enqueued with
+ * PCP_FLAG_ASYNC may still use the buffers). The next call allocates again. No
+ * counterpart in the reference (IREE holds its own device pools). */
+int pcp_release_workspace(pcp_ctx* ctx);
+/* Bytes of device work buffers the context holds now (0 for NULL). */
+size_t pcp_workspace_bytes(const pcp_ctx* ctx);
 
 /*
  * Host-bytes path. ~ WorkerBackend.executeFunction (worker_backend.zig:27-33),
@@ -283,14 +293,21 @@ int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
  * stored. By default (vocab_chunk 0) the policy forward also keeps its softmax terms
  * as f16 (one 2-byte term per live token and vocab entry), the backward turns them into
  * bf16 dlogits and runs dhidden = dlogits * weight and dweight = dlogits^T *
- * hidden_states (fp32) over the whole vocabulary. The f16 term adds at most 2^-11 of
- * |c * softmax| to an off-target dlogit before its bf16 rounding; PCP_FLAG_EXACT_BF16
- * keeps the terms as f32 (4 bytes per live token and vocab entry), so each dlogit is
- * the f32 value rounded once. With an explicit vocab_chunk, or a backward workspace
- * above 64 GiB, the backward recomputes the logit tiles per vocab chunk instead
- * (dlogits = the f32 value rounded once): with a transposed copy of the chunk and of
- * the weight (2 * (2 * tokens * chunk + hidden * vocab) bytes, up to 64 GiB), or, when
- * that does not fit, in memory bounded by the chunk alone (2 * tokens * chunk bytes).
+ * hidden_states (fp32) over the whole vocabulary. The f16 term adds to an off-target
+ * dlogit, before its bf16 rounding, at most 2^-11 of |c * softmax| (terms in f16's
+ * normal range) plus 2^-25 * |c| * 2^(m_b - lse) (terms below it; m_b = the largest
+ * logit of the entry's 128-entry block): PCP_FLAG_EXACT_BF16 keeps the terms as f32
+ * (4 bytes per live token and vocab entry), so each dlogit is the f32 value rounded
+ * once. The backward workspace (softmax cache, dlogits^T, weight^T; 11.2 GB at 16,384
+ * tokens, V = 151,936, H = 4,096) is allocated when it fits the budget: at most 64 GiB
+ * and at most half of the device memory free at the call plus what the context holds.
+ * It stays held until pcp_release_workspace or pcp_destroy; growing it synchronises
+ * the device (PCP_FLAG_ASYNC calls included) before freeing the smaller buffer. With an
+ * explicit vocab_chunk, or a workspace above the budget, the backward recomputes the
+ * logit tiles per vocab chunk instead (dlogits = the f32 value rounded once): with a
+ * transposed copy of the chunk and of the weight (2 * (2 * tokens * chunk + hidden *
+ * vocab) bytes, within the same budget), or, when that does not fit, in memory
+ * bounded by the chunk alone (2 * tokens * chunk bytes).
  * The live-token count never leaves the device: with PCP_FLAG_ASYNC the call only
  * enqueues work, and it can be captured in a HIP graph. A captured graph uses the
  * context's work buffers as they were at capture: make one uncaptured call of the same

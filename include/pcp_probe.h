@@ -19,13 +19,16 @@ extern "C" {
 struct pcp_ctx;
 
 /* One stream over `bytes` (a positive multiple of 16; buffers 16-byte aligned):
- *   kind 0 read:  reads a                      (c: a 16-byte word written only if the
- *                                                  XOR of all of a is all ones)
+ *   kind 0 read:  reads a                      (c: a 16-byte word written only by a lane
+ *                                                  whose XOR over its own vectors is all
+ *                                                  ones, which keeps the loads live)
  *   kind 1 write: writes c
  *   kind 2 copy:  c = a
  *   kind 3 mix:   c = a ^ b                    (two reads per write)
  * nontemporal != 0 uses nontemporal loads and stores. The grid is flat: each 256-lane
- * workgroup moves 256 x vectors_per_lane (1, 2, 4 or 8) 16-byte vectors. Asynchronous
+ * workgroup moves 256 x vectors_per_lane (1, 2, 4 or 8) 16-byte vectors, and the grid
+ * must stay under 2^32 lanes (bytes / (16 * vectors_per_lane), rounded up to 256,
+ * < 2^32; else PCP_ERR_INVALID_ARG). Asynchronous
  * on `stream`; timed by pcp_profile_start / pcp_profile_stop like the other entry
  * points. */
 int pcp_hbm_stream(struct pcp_ctx* ctx, int kind, int nontemporal, int vectors_per_lane, const void* a,

@@ -139,6 +139,8 @@ SIGNATURES = {
     "pcp_get_backend_type": (_I, [_VP]),
     "pcp_last_error": (ctypes.c_char_p, [_VP]),
     "pcp_sync": (_I, [_VP]),
+    "pcp_release_workspace": (_I, [_VP]),
+    "pcp_workspace_bytes": (ctypes.c_size_t, [_VP]),
     "pcp_execute": (_I, [_VP, ctypes.c_char_p, _I, ctypes.POINTER(_VP), ctypes.POINTER(ctypes.c_size_t),
                          ctypes.POINTER(ctypes.POINTER(_I64)), ctypes.POINTER(_I), ctypes.POINTER(_I),
                          ctypes.POINTER(_I), ctypes.POINTER(ctypes.POINTER(_VP)),

@@ -435,6 +435,22 @@ void pcp_destroy(pcp_ctx* ctx) {
   delete ctx;
 }
 
+int pcp_release_workspace(pcp_ctx* ctx) {
+  if (!ctx) return fail(nullptr, PCP_ERR_INVALID_ARG, "context is NULL");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  if (!ctx->scratch && !ctx->lm_dbuf) return PCP_OK;
+  // Earlier calls (PCP_FLAG_ASYNC ones included) may still use the buffers.
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(ctx, e, "hipDeviceSynchronize");
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->lm_dbuf) (void)hipFree(ctx->lm_dbuf);
+  ctx->scratch = ctx->lm_dbuf = nullptr;
+  ctx->scratch_bytes = ctx->lm_dbuf_bytes = 0;
+  return PCP_OK;
+}
+
+size_t pcp_workspace_bytes(const pcp_ctx* ctx) { return ctx ? ctx->scratch_bytes + ctx->lm_dbuf_bytes : 0; }
+
 int pcp_get_backend_type(const pcp_ctx* ctx) { return ctx ? ctx->backend : PCP_ERR_INVALID_ARG; }
 
 const char* pcp_last_error(const pcp_ctx* ctx) {

@@ -167,7 +167,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   //    policy sum for chunks [kb, kb + RB) runs in the same step as reference batch
   //    kb, so its exponentials overlap reference loads in flight instead of leaving
   //    the CU's memory idle. For bf16 -> bf16 the policy terms e = 2^(x*log2e - m2)
-  //    are also kept, as f16 in place of the row (e <= 1: 2^-12 relative, 2^-25
+  //    are also kept, as f16 in place of the row (e <= 1: 2^-11 relative, 2^-25
   //    absolute below the f16 normal range), and dlogits become a multiple of them.
   constexpr int NB = (NCH + RB - 1) / RB;
   constexpr int PD = kPrefetch;
@@ -804,8 +804,10 @@ namespace {
 
 template <typename TI, typename TO, int BLOCK, int NCH, bool EDGE, bool CACHE>
 hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
-  // RB = 2: the largest reference batch that needs no register spill next to a
-  // 19-chunk resident row at 128 VGPRs (4 spills 9 VGPRs and measured ~1% slower).
+  // RB = 2: reference batches of two chunks next to a 19-chunk resident row at 128
+  // VGPRs. The headline instance (bf16 -> bf16, cache) then spills 2 VGPRs and 42
+  // SGPRs (12 bytes of scratch per lane); RB = 4 spills 9 VGPRs and measured ~1%
+  // slower.
   constexpr int RB = 2;
   // One workgroup per resident slot of the device (the kernel's occupancy times the
   // CU count), at most one per row. Only a successful query is cached.

@@ -9,15 +9,17 @@
 // per-(token, vocab tile) log-sum-exp partials and the target logit; one wave per
 // token merges the partials. Then the GRPO terms per token and the loss reduction
 // (the same kernels as the logits-input path).
-// Backward, by default: the policy forward also stored its softmax terms (f16); one
-// pass turns them into bf16 dlogits D in place and writes D^T, W is transposed once,
-// and one launch of the MFMA tile kernel (kLmGemm, both operands K-contiguous) runs
+// Backward, by default: the policy forward also stored its softmax terms (f16, or f32
+// with PCP_FLAG_EXACT_BF16); one pass turns them into bf16 dlogits D (in place over
+// f16 terms, beside f32 ones) and writes D^T, W is transposed once, and one launch of
+// the MFMA tile kernel (kLmGemm, both operands K-contiguous) runs
 //   dhidden = D * W      over the whole vocabulary (rows: live tokens), and
 //   dW      = D^T * hidden over the live tokens (rows: vocab).
-// Chunked backward (an explicit vocab_chunk, PCP_FLAG_EXACT_BF16, or a workspace
-// past kCacheBudget): per vocab chunk, logits tiles recomputed into bf16 D, then the
-// same two products with one operand read K-major through LDS transpose loads,
-// dhidden accumulating over the chunks.
+// Chunked backward (an explicit vocab_chunk, or a workspace past cache_budget):
+// per vocab chunk, logits tiles recomputed into bf16 D, then the same two products
+// (on transposed copies of the chunk and of W when they fit the budget, else with one
+// operand read K-major through LDS transpose loads), dhidden accumulating over the
+// chunks.
 // Either way the compact dhidden rows are scattered back (zero rows for dead tokens).
 // This mirrors the LM head's VJP (src/autodiff/vjp_rules.zig:426-497, matmulVJP).
 
@@ -37,12 +39,25 @@ namespace pcp {
 namespace {
 
 constexpr int64_t kDefaultChunk = 16384;
-// Largest backward workspace (softmax cache, D^T, W^T; sized for all N tokens) the
+// Cap on the backward workspace (softmax cache, D^T, W^T; sized for all N tokens) the
 // default path allocates: 11.2 GB at configuration 5 (16,384 tokens, V = 151,936,
-// H = 4,096). 64 GiB, under a quarter of the device's 288 GB, holds it up to about
-// 110,000 tokens at that vocabulary; beyond that, or when the allocation fails, the
-// backward runs chunked.
-constexpr size_t kCacheBudget = size_t{64} << 30;
+// H = 4,096). 64 GiB holds it up to about 110,000 tokens at that vocabulary.
+constexpr size_t kCacheBudgetCap = size_t{64} << 30;
+
+// Bytes the backward workspace may occupy on this call: the cap, and at most half of
+// the device memory that is free now plus what the context already holds, so a
+// training loop sharing the GPU keeps the other half. A workspace larger than this
+// budget is not allocated: the backward then runs chunked, in less memory.
+size_t cache_budget(pcp_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->lm_dbuf_bytes) return ctx->lm_dbuf_bytes;   // already held
+  size_t free_b = 0, total_b = 0;
+  if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const size_t avail = (free_b + ctx->lm_dbuf_bytes) / 2;
+  return avail < kCacheBudgetCap ? avail : kCacheBudgetCap;
+}
 
 inline size_t r256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
@@ -171,7 +186,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   // [ldv, ldt] beside it) and W^T [H, ldv], so both products read K-contiguous
   // operands. With PCP_FLAG_EXACT_BF16 the terms are f32 [N, ldv] and D follows them
   // (D is then the f32 value rounded once). With an explicit vocab_chunk, more than
-  // kCacheBudget bytes, or no memory for them: one dlogits chunk [N, chunk] that the
+  // cache_budget bytes, or no memory for them: one dlogits chunk [N, chunk] that the
   // backward refills by recomputing the logits.
   const bool exact = (a->flags & PCP_FLAG_EXACT_BF16) != 0;
   const int64_t ldv = (V + 63) / 64 * 64;
@@ -185,16 +200,17 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t chunk_frag_bytes = o_cwt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
   bool cached = false, chunk_frag = false;
   if (bwd) {
-    if (a->vocab_chunk == 0 && cache_bytes <= kCacheBudget) {
+    if (a->vocab_chunk == 0 && cache_bytes <= cache_budget(ctx, cache_bytes)) {
       e = grow_dbuf(ctx, cache_bytes);
       if (e == hipSuccess) cached = true;
       else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the softmax cache");
     }
     // Chunked: the dlogits chunk [ldt, chunk], with room for its transpose [chunk, ldt] and
     // W^T [H, ldv] (fragment-major, once per call) the products run as on the cached
-    // path; past kCacheBudget, in less memory, or with PCP_FLAG_FORCE_STREAMING, with
+    // path; past the budget, in less memory, or with PCP_FLAG_FORCE_STREAMING, with
     // K-major operands and no transposed copies.
-    if (!cached && !(a->flags & PCP_FLAG_FORCE_STREAMING) && chunk_frag_bytes <= kCacheBudget) {
+    if (!cached && !(a->flags & PCP_FLAG_FORCE_STREAMING) &&
+        chunk_frag_bytes <= cache_budget(ctx, chunk_frag_bytes)) {
       e = grow_dbuf(ctx, chunk_frag_bytes);
       if (e == hipSuccess) chunk_frag = true;
       else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the dlogits chunk");

@@ -72,7 +72,9 @@ __global__ void __launch_bounds__(kThreads) hbm_stream_kernel(const u32x4* a, co
       if constexpr (KIND == 3) st<NT>(c + i, x[k] ^ y[k]);
     }
   }
-  // The read kernel keeps its loads by a store that only an all-ones XOR would make.
+  // The read kernel keeps its loads by a store that a lane makes only when the XOR of
+  // its own vectors is all ones (never for the probes' data; several lanes may store
+  // then, all to the same word).
   if constexpr (KIND == 0)
     if (acc[0] == 0xFFFFFFFFu && acc[1] == 0xFFFFFFFFu && acc[2] == 0xFFFFFFFFu && acc[3] == 0xFFFFFFFFu) *sink = acc;
 }
@@ -260,6 +262,11 @@ extern "C" int pcp_hbm_stream(pcp_ctx* ctx, int kind, int nontemporal, int vecto
   const int vpt = vectors_per_lane;
   if (vpt != 1 && vpt != 2 && vpt != 4 && vpt != 8)
     return fail(ctx, PCP_ERR_INVALID_ARG, "pcp_hbm_stream: vectors_per_lane must be 1, 2, 4 or 8");
+  // The flat grid launches one lane per vpt vectors: at most 2^32 - 1 lanes.
+  if ((bytes / 16 + kThreads * vpt - 1) / (kThreads * vpt) * kThreads >= (int64_t{1} << 32))
+    return fail(ctx, PCP_ERR_INVALID_ARG,
+                "pcp_hbm_stream: %lld bytes at vectors_per_lane %d need 2^32 lanes or more: raise vectors_per_lane",
+                (long long)bytes, vpt);
   const bool need_a = kind != 1, need_b = kind == 3, need_c = kind != 0;
   if ((need_a && !a) || (need_b && !b) || (need_c && !c) || (kind == 0 && !c) ||
       ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c)) & 15u))

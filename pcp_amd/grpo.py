@@ -58,6 +58,15 @@ class Context:
     def sync(self) -> None:
         check(lib().pcp_sync(self.handle), self.handle)
 
+    def release_workspace(self) -> None:
+        """Free the context's device work buffers (the LM-head softmax cache among them);
+        synchronises the device first. The next call allocates again."""
+        check(lib().pcp_release_workspace(self.handle), self.handle)
+
+    def workspace_bytes(self) -> int:
+        """Bytes of device work buffers the context holds now."""
+        return int(lib().pcp_workspace_bytes(self.handle))
+
 
 _default_ctx: dict[int, Context] = {}
 

@@ -181,6 +181,29 @@ def test_noalloc_rejects_oversized_requests_without_device():
     assert rc == -1 and b"context is NULL" in _lib.lib().pcp_last_error(None)
 
 
+def test_noalloc_rejects_an_oversized_live_row_list_without_device():
+    # Without zero-fill the live-row list (4 bytes per logits row) also lives in the
+    # array: with the per-token losses passed in, 2^20 + 1 rows of list alone do not fit,
+    # while the same request with zero-fill (no list) passes the size check.
+    a = _valid_args()
+    a.n_seq, a.rows, a.group_size = 1, (1 << 20) + 1, 1
+    a.dlogits, a.token_loss = 0x4000, 0x5000
+    a.flags = _lib.FLAG_NO_ZERO_FILL
+    rc = _lib.lib().pcp_grpo_loss_fwd_bwd_noalloc(None, ctypes.byref(a))
+    assert rc == -9
+    assert b"allocation-free" in _lib.lib().pcp_last_error(None)
+    a.flags = 0
+    rc = _lib.lib().pcp_grpo_loss_fwd_bwd_noalloc(None, ctypes.byref(a))
+    assert rc == -1 and b"context is NULL" in _lib.lib().pcp_last_error(None)
+
+
+def test_workspace_calls_without_device():
+    L = _lib.lib()
+    assert L.pcp_release_workspace(None) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()
+    assert L.pcp_workspace_bytes(None) == 0
+
+
 def test_valid_args_then_null_context():
     L = _lib.lib()
     a = _valid_args()
@@ -445,6 +468,12 @@ def test_hbm_stream_argument_errors_without_device():
     assert L.pcp_hbm_stream(None, 2, 0, 1, 0x1008, None, 0x3000, 1 << 20, None) == -1
     assert L.pcp_hbm_stream(None, 0, 0, 1, 0x1000, None, None, 1 << 20, None) == -1
     assert L.pcp_hbm_stream(None, 1, 0, 8, None, None, 0x3000, 1 << 20, None) == -1
+    assert "context is NULL" in L.pcp_last_error(None).decode()
+    # 64 GiB at one vector per lane is 2^32 lanes: rejected before any launch; at two
+    # vectors per lane the same size passes the checks (and stops at the NULL context).
+    assert L.pcp_hbm_stream(None, 1, 0, 1, None, None, 0x3000, 1 << 36, None) == -1
+    assert "2^32 lanes" in L.pcp_last_error(None).decode()
+    assert L.pcp_hbm_stream(None, 1, 0, 2, None, None, 0x3000, 1 << 36, None) == -1
     assert "context is NULL" in L.pcp_last_error(None).decode()
 
 

@@ -22,12 +22,12 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def make_case(seed, S, T, V, G, mode):
+def make_case(seed, S, T, V, G, mode, max_len=None):
     rng = np.random.default_rng(seed)
     pol = (rng.standard_normal((S, T, V), dtype=np.float32) * 3).astype(np.float32)
     ref = pol + rng.standard_normal((S, T, V), dtype=np.float32) * 0.1
     ids = rng.integers(0, V, size=(S, T)).astype(np.int64)
-    lengths = rng.integers(1, T + 1, size=S)
+    lengths = rng.integers(1, (max_len or T) + 1, size=S)
     mask = (np.arange(T)[None] < lengths[:, None]).astype(np.float32)
     rewards = rng.random(S).astype(np.float32)
     old = (rng.standard_normal((S, T)) * 0.01 - np.log(V)).astype(np.float32)
@@ -39,9 +39,10 @@ def bf16_dev(h):
     return torch.from_numpy(h.view(np.int16)).to(DEV).view(torch.bfloat16)
 
 
-def run(c, noalloc, token_loss_out):
+def run(c, noalloc, token_loss_out, flags=0):
     """One call through the C ABI; token_loss_out False leaves token_loss NULL so the
-    library keeps the per-token losses in its work buffers."""
+    library keeps the per-token losses in its work buffers. dlogits start as 7.0, so
+    rows a PCP_FLAG_NO_ZERO_FILL call leaves untouched keep that value."""
     S, T, V = c["S"], c["T"], c["V"]
     pol, ref = bf16_dev(c["pol"]), bf16_dev(c["ref"])
     ids = torch.from_numpy(c["ids"]).to(DEV)
@@ -66,6 +67,7 @@ def run(c, noalloc, token_loss_out):
     a.token_loss = tl.data_ptr() if tl is not None else None
     a.advantages_out, a.loss = adv.data_ptr(), loss.data_ptr()
     a.loss_mode = int(c["mode"])
+    a.flags = flags
     a.stream = torch.cuda.current_stream().cuda_stream or None
     ctx = grpo.default_context(0)
     fn = lib().pcp_grpo_loss_fwd_bwd_noalloc if noalloc else lib().pcp_grpo_loss_fwd_bwd
@@ -98,6 +100,30 @@ def test_noalloc_matches_allocating_entry_point_two_calls(token_loss_out):
                             old_logp=c["old"], loss_mode=int(c["mode"]), dtype=orc.BF16)
         # The f32 log-prob bar (1e-5 of the row scale, here |lse| < 20) through the loss's
         # linear aggregation: at most 1e-5 * 20 * mean_s |A_s| * (|rho| + beta) per sequence.
+        scale = 20.0 * float(np.abs(exp.adv).mean() * 1.5 + 0.04) + abs(exp.loss)
+        assert abs(float(got["loss"]) - exp.loss) <= 1e-5 * scale, (got["loss"], exp.loss)
+
+
+def test_noalloc_without_zero_fill_walks_the_listed_rows():
+    """PCP_FLAG_NO_ZERO_FILL keeps the live-row list and its count in the static array.
+    With under half the rows live the row kernel visits the listed rows only; the
+    results equal the allocating call's bit for bit, dead rows keep their 7.0 fill, and
+    a second, smaller call on the shared array does the same."""
+    big = make_case(3, S=8, T=96, V=5003, G=4, mode=LossMode.GRPO_CLIP_KL, max_len=30)
+    small = make_case(4, S=4, T=40, V=3000, G=2, mode=LossMode.REINFORCE, max_len=12)
+    print("noalloc no-zero-fill: big S=8 T=96 V=5003 then small S=4 T=40 V=3000", flush=True)
+    seven = np.array([7.0], np.float32).view(np.uint32)[0] >> 16
+    for c in (big, small):
+        assert 2 * int(c["mask"].sum()) < c["mask"].size, "the case must leave under half the rows live"
+        got = run(c, True, False, _lib.FLAG_NO_ZERO_FILL)
+        want = run(c, False, False, _lib.FLAG_NO_ZERO_FILL)
+        assert_same(got, want)
+        dead = c["mask"] == 0
+        assert (got["dl"][dead].view(np.uint16) == seven).all(), "a dead row was written"
+        assert not (got["dl"][~dead].view(np.uint16) == seven).all(axis=-1).any(), "a live row was not written"
+        exp = orc.grpo_full(c["pol"], c["ids"], c["mask"], rows=c["T"], rewards=c["rewards"], group_size=c["G"],
+                            ref_logits=c["ref"] if c["mode"] == LossMode.GRPO_CLIP_KL else None,
+                            old_logp=c["old"], loss_mode=int(c["mode"]), dtype=orc.BF16)
         scale = 20.0 * float(np.abs(exp.adv).mean() * 1.5 + 0.04) + abs(exp.loss)
         assert abs(float(got["loss"]) - exp.loss) <= 1e-5 * scale, (got["loss"], exp.loss)
 
