@@ -27,15 +27,15 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 
 
-def algorithmic_bytes(cfg, lengths, mode_clip_kl: bool, zero_fill: bool = True) -> dict:
+def algorithmic_bytes(cfg, lengths, mode_clip_kl: bool, zero_fill: bool = True, s_out: int | None = None) -> dict:
     """Bytes the fused row kernel must move: per live row one read of the policy row,
-    one of the reference row (clip-KL mode) and one write of dlogits; per masked row
-    the zero-fill write; per row 28 B of token scalars (id 8, mask 4, old logp 4,
-    logp 4, ref logp 4, token loss 4)."""
+    one of the reference row (clip-KL mode) and one write of dlogits (s_out bytes per
+    element; by default the logits' size); per masked row the zero-fill write; per row
+    28 B of token scalars (id 8, mask 4, old logp 4, logp 4, ref logp 4, token loss 4)."""
     import numpy as np
 
     s_in = 2 if cfg.dtype == "bf16" else 4
-    s_out = s_in
+    s_out = s_in if s_out is None else s_out
     V = cfg.V
     live = int(np.minimum(lengths, cfg.T).sum())
     rows = cfg.S * cfg.T
@@ -793,6 +793,8 @@ def main() -> None:
     ap.add_argument("--exact-bf16", action="store_true",
                     help="loss workload: PCP_FLAG_EXACT_BF16 (no f16 softmax terms in the bf16 dlogits pass); "
                          "config 5: the same flag (the forward keeps f32 softmax terms)")
+    ap.add_argument("--dlogits-f32", action="store_true",
+                    help="loss workload: f32 dlogits from the configuration's bf16 logits")
     ap.add_argument("--vocab-chunk", type=int, default=0,
                     help="config 5: the recomputing backward's vocab chunk (a multiple of 256; 0: the forward's "
                          "softmax terms)")
@@ -863,7 +865,9 @@ def main() -> None:
               old_logp=inp["old_logp"], loss_mode=mode, clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta,
               force_streaming=args.force_streaming, zero_fill=not args.no_zero_fill,
               exact_bf16=args.exact_bf16, ctx=ctx)
-    out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], **kw)  # allocates outputs
+    d_dtype = torch.float32 if args.dlogits_f32 else None
+    out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], dlogits_dtype=d_dtype,
+                                 **kw)  # allocates outputs
     for _ in range(args.warmup):
         grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], outputs=out, sync=False, **kw)
     ctx.sync()
@@ -882,7 +886,8 @@ def main() -> None:
     check(lib().pcp_profile_stop(ctx.handle, ctypes.byref(n_l), ctypes.byref(tot)), ctx.handle)
     kernel_ms = tot.value / max(n_l.value, 1)
 
-    ab = algorithmic_bytes(cfg, inp["lengths"], clip, zero_fill=not args.no_zero_fill)
+    ab = algorithmic_bytes(cfg, inp["lengths"], clip, zero_fill=not args.no_zero_fill,
+                           s_out=4 if args.dlogits_f32 else None)
     ms_step = elapsed * 1e3 / args.steps
     value = ab["live_rows"] / (ms_step / 1e3)
     achieved = ab["bytes"] / (kernel_ms / 1e3) / 1e9
@@ -903,7 +908,8 @@ def main() -> None:
                                f"V={cfg.V}, {cfg.dtype} logits, loss={args.mode}"
                                + (", dlogits of masked rows left unwritten (no zero-fill)" if args.no_zero_fill
                                   else "")
-                               + (", bf16 dlogits rounded once from f32 (exact mode)" if args.exact_bf16 else ""),
+                               + (", bf16 dlogits rounded once from f32 (exact mode)" if args.exact_bf16 else "")
+                               + (", f32 dlogits" if args.dlogits_f32 else ""),
                    "rows": ab["rows"], "valid_rows": ab["live_rows"], "global_batch": cfg.S, "seq_len": cfg.T,
                    "zero_fill": not args.no_zero_fill},
         "step_gbs": ab["bytes"] / (ms_step / 1e3) / 1e9,
@@ -915,7 +921,10 @@ def main() -> None:
         "setup_s": t_setup,
     }
     tfile = os.path.join(ROOT, "profiles", f"traffic_config{cfg.key}_{args.mode}"
-                                           f"{'_no_zero_fill' if args.no_zero_fill else ''}.json")
+                                           f"{'_no_zero_fill' if args.no_zero_fill else ''}"
+                                           f"{'_exact' if args.exact_bf16 else ''}"
+                                           f"{'_f32_out' if args.dlogits_f32 else ''}"
+                                           f"{'_streaming' if args.force_streaming else ''}.json")
     if os.path.exists(tfile):
         with open(tfile) as f:
             line["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")

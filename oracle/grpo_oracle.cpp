@@ -323,6 +323,61 @@ int oracle_grpo_rows(const oracle_rows_args* a) {
   return 0;
 }
 
+// Element-wise check of a device's dlogits rows against the exact (float64) rows
+// c * (onehot - softmax) of kExact above, without materialising the exact rows: per
+// row the log-sum-exp is recomputed in double, then every element's error against the
+// bar  tol = rel * |d| + kfloor * floor[n] + sub  is reduced to per-row statistics.
+typedef struct oracle_check_args {
+  int64_t nrows, vocab;
+  int32_t dtype;             // logits storage (pcp_dtype codes 0..3)
+  const void* logits;        // [nrows, V]
+  const int64_t* ids;        // [nrows] targets (live rows only: 0 <= id < V)
+  const double* coef;        // [nrows] exact coefficient d loss / d lp (oracle_grpo_rows, kExact)
+  const double* floor_row;   // [nrows] absolute error floor of the row
+  int32_t got_dtype;         // the device's dlogits: 0 f16, 1 bf16, 2 f32
+  const void* got;           // [nrows, V]
+  double rel, kfloor, sub;   // the bar's relative, floor and absolute terms
+  double rel_min;            // max_rel counts elements with |d| >= rel_min * |coef|
+  int32_t nthreads;
+  double* max_usage;         // [nrows] max err / tol
+  double* max_abs;           // [nrows] max err
+  double* max_rel;           // [nrows] max err / |d| over |d| >= rel_min * |coef| (0 if none)
+  int64_t* n_bad;            // [nrows] elements with err > tol
+} oracle_check_args;
+
+int oracle_check_dlogits(const oracle_check_args* a) {
+  if (!a || a->nrows < 0 || a->vocab < 1 || !a->logits || !a->ids || !a->coef || !a->floor_row || !a->got ||
+      !a->max_usage || !a->max_abs || !a->max_rel || !a->n_bad)
+    return -1;
+  if (a->got_dtype != kF16 && a->got_dtype != kBF16 && a->got_dtype != kF32) return -1;
+  if (a->nthreads > 0) omp_set_num_threads(a->nthreads);
+  const int64_t V = a->vocab;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t n = 0; n < a->nrows; ++n) {
+    const int64_t base = n * V, id = a->ids[n];
+    const RowLse<double> p = row_lse<double>(a->logits, a->dtype, base, V);
+    const double c = a->coef[n], fl = a->kfloor * a->floor_row[n] + a->sub, thr = a->rel_min * std::fabs(c);
+    double mu = 0.0, ma = 0.0, mr = 0.0;
+    int64_t bad = 0;
+    for (int64_t v = 0; v < V; ++v) {
+      const double d = c * ((v == id ? 1.0 : 0.0) - std::exp(loadd(a->logits, a->dtype, base + v) - p.lse));
+      const double g = loadd(a->got, a->got_dtype, base + v);
+      const double err = std::fabs(g - d), ad = std::fabs(d);
+      const double tol = a->rel * ad + fl;
+      if (!(err <= tol)) ++bad;
+      const double u = tol > 0.0 ? err / tol : (err > 0.0 ? INFINITY : 0.0);
+      if (!(u <= mu)) mu = u;
+      if (!(err <= ma)) ma = err;
+      if (ad > 0.0 && ad >= thr && !(err / ad <= mr)) mr = err / ad;
+    }
+    a->max_usage[n] = mu;
+    a->max_abs[n] = ma;
+    a->max_rel[n] = mr;
+    a->n_bad[n] = bad;
+  }
+  return 0;
+}
+
 int oracle_max_threads(void) { return omp_get_max_threads(); }
 
 }  // extern "C"

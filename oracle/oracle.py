@@ -12,6 +12,7 @@ What each function restates (reference file:line):
                cited in grpo_oracle.cpp) and the clipped-ratio + k3-KL loss
   grpo_full    the whole loss head over [S, T, V] with the kernels' row layout
                (seq lengths = clamp(mask.sum(1), min=1), export_qwen_forward.py:160)
+  check_dlogits  grpo_rows' exact dlogits compared in place with a device's rows
   lmhead_*     export_qwen_forward.py:147 (lm_head) and matmulVJP, vjp_rules.zig:426-497
   rmsnorm_*    the final norm before lm_head (export_qwen_forward.py:112, model.norm =
                Qwen2RMSNorm of transformers' modeling_qwen2) and its VJP
@@ -56,6 +57,18 @@ class _RowsArgs(ctypes.Structure):
     ]
 
 
+class _CheckArgs(ctypes.Structure):
+    _fields_ = [
+        ("nrows", ctypes.c_int64), ("vocab", ctypes.c_int64), ("dtype", ctypes.c_int32),
+        ("logits", ctypes.c_void_p), ("ids", ctypes.c_void_p), ("coef", ctypes.c_void_p),
+        ("floor_row", ctypes.c_void_p), ("got_dtype", ctypes.c_int32), ("got", ctypes.c_void_p),
+        ("rel", ctypes.c_double), ("kfloor", ctypes.c_double), ("sub", ctypes.c_double),
+        ("rel_min", ctypes.c_double), ("nthreads", ctypes.c_int32),
+        ("max_usage", ctypes.c_void_p), ("max_abs", ctypes.c_void_p), ("max_rel", ctypes.c_void_p),
+        ("n_bad", ctypes.c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -74,6 +87,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_grpo_rows.argtypes = [ctypes.POINTER(_RowsArgs)]
         L.oracle_grpo_rows.restype = ctypes.c_int
         L.oracle_max_threads.restype = ctypes.c_int
+        L.oracle_check_dlogits.argtypes = [ctypes.POINTER(_CheckArgs)]
+        L.oracle_check_dlogits.restype = ctypes.c_int
         _VP, _I64 = ctypes.c_void_p, ctypes.c_int64
         L.oracle_nesterov.argtypes = [_VP, _VP, _VP, _I64, ctypes.c_float, ctypes.c_float, ctypes.c_int]
         L.oracle_nesterov.restype = None
@@ -254,6 +269,40 @@ def grpo_rows(logits: np.ndarray, ids: np.ndarray, w: np.ndarray, adv: np.ndarra
     rc = lib().oracle_grpo_rows(ctypes.byref(a))
     if rc != 0:
         raise ValueError("oracle_grpo_rows rejected its arguments")
+    return res
+
+
+@dataclass
+class CheckResult:
+    max_usage: np.ndarray   # per row: max err / tol
+    max_abs: np.ndarray     # per row: max |got - exact|
+    max_rel: np.ndarray     # per row: max err / |exact| over |exact| >= rel_min * |coef|
+    n_bad: np.ndarray       # per row: elements with err > tol
+
+
+def check_dlogits(logits: np.ndarray, ids: np.ndarray, coef: np.ndarray, floor_row: np.ndarray, got: np.ndarray,
+                  got_dtype: int, rel: float, kfloor: float, sub: float = 0.0, rel_min: float = 2.0 ** -14,
+                  dtype: int | None = None, nthreads: int = 0) -> CheckResult:
+    """Compare a device's dlogits rows (storage form: uint16 bf16 / float16 / float32)
+    with the exact float64 rows coef * (onehot(ids) - softmax(logits)), element by
+    element against tol = rel * |exact| + kfloor * floor_row + sub, without holding the
+    exact rows in memory. coef: the oracle's exact coefficients (grpo_rows). Rows must be
+    live (0 <= id < V)."""
+    x = np.ascontiguousarray(logits)
+    dt = storage_dtype_code(x) if dtype is None else dtype
+    N, V = x.shape
+    g = np.ascontiguousarray(got)
+    assert g.shape == (N, V)
+    ids64 = np.ascontiguousarray(ids, dtype=np.int64).reshape(N)
+    assert ((ids64 >= 0) & (ids64 < V)).all()
+    cf = np.ascontiguousarray(coef, dtype=np.float64).reshape(N)
+    fl = np.ascontiguousarray(floor_row, dtype=np.float64).reshape(N)
+    res = CheckResult(np.empty(N), np.empty(N), np.empty(N), np.empty(N, np.int64))
+    a = _CheckArgs(N, V, dt, _ptr(x), _ptr(ids64), _ptr(cf), _ptr(fl), int(got_dtype), _ptr(g), float(rel),
+                   float(kfloor), float(sub), float(rel_min), nthreads, _ptr(res.max_usage), _ptr(res.max_abs),
+                   _ptr(res.max_rel), _ptr(res.n_bad))
+    if lib().oracle_check_dlogits(ctypes.byref(a)) != 0:
+        raise ValueError("oracle_check_dlogits rejected its arguments")
     return res
 
 

@@ -800,7 +800,7 @@ def _clip_kl_coef(lp, lr, old, adv, mask, cfg, lse):
     tscale = np.maximum(1.0, np.abs(lse))
     fl = coef_floor(r.coef, r.lp, r.lr, w.astype(np.float64), Atok.astype(np.float64), Ltok.astype(np.float64),
                     float(S), old.astype(np.float64), False, cfg.kl_beta, cfg.clip_eps, tscale)
-    return r.coef, fl
+    return r.coef, fl, r.token_loss
 
 
 def _torch_reference(inp, coef=None, chunk=2048, floor=None, cache_terms=None):
@@ -886,6 +886,7 @@ def test_config5_full_size():
         sc = lse_ref.abs().clamp(min=1.0)
         err = (out.logp.reshape(-1) - lp_ref).abs()
         assert bool((err[m] <= 1e-5 * sc[m]).all()), float(err[m].max())
+        e_lp = float((err / sc)[m].max())
         assert bool((out.logp.reshape(-1)[~m] == 0).all())
         # The loss is the masked sequence mean of the device's own token losses.
         L = inp["mask"].double().sum(1).clamp(min=1.0)
@@ -911,6 +912,10 @@ def test_config5_full_size():
                                         old_logp=old, loss_mode=mode, exact_bf16=True)
             torch.cuda.synchronize()
             assert torch.equal(exact.logp, out.logp) and torch.equal(exact.loss, out.loss)
+            # The loss from the fp32 reference log-probs: -A * sum_t m lp / L, averaged.
+            seq_ref = -(inp["mask"].double() * lp_ref.double().reshape(S, T)).sum(1) / L
+            loss_ref = float((seq_ref * torch.from_numpy(adv).to(DEV).double()).sum() / S)
+            e_loss = abs(float(out.loss) - loss_ref) / max(abs(loss_ref), 1e-30)
             for name, res, th, tw in (("default", out, tol_dh + cache["dh"], tol_dw + cache["dw"]),
                                       ("exact", exact, tol_dh, tol_dw)):
                 bad_h = ((res.dhidden - dh).abs() > th + 1e-6 * th.max()).sum().item()
@@ -919,6 +924,10 @@ def test_config5_full_size():
                 used_w = float(((res.dweight - dw).abs() / (tw + 1e-30)).max())
                 print(f"  REINFORCE gradients, {name}: largest error / bound: dhidden {used_h:.3f}, dW {used_w:.3f}",
                       flush=True)
+                print(f"PARITY-TABLE config5 reinforce {name}: |dlogp|/max(1,|lse|) {e_lp:.2e} (bar 1e-5); loss rel "
+                      f"{e_loss:.2e} (vs fp32 torch); dhidden max abs {float((res.dhidden - dh).abs().max()):.2e} "
+                      f"({used_h:.3f} of its bound); dW max abs {float((res.dweight - dw).abs().max()):.2e} "
+                      f"({used_w:.3f} of its bound)", flush=True)
                 assert bad_h == 0 and bad_w == 0, (name, bad_h, bad_w)
             del dh, tol_dh, dw, tol_dw, cache, exact
         else:
@@ -929,8 +938,12 @@ def test_config5_full_size():
             # the oracle, each token's coef_floor in the bound.
             print("config 5 full size: clip-KL reference gradients", flush=True)
             scale = torch.maximum(lse_ref.abs(), rlse_ref.abs()).double().cpu().numpy()
-            coef, fl = _clip_kl_coef(lp_ref.double().cpu().numpy(), lr_ref.double().cpu().numpy(),
-                                     old.cpu().numpy(), adv, inp["mask"].cpu().numpy(), cfg, scale)
+            coef, fl, tl_ref = _clip_kl_coef(lp_ref.double().cpu().numpy(), lr_ref.double().cpu().numpy(),
+                                             old.cpu().numpy(), adv, inp["mask"].cpu().numpy(), cfg, scale)
+            Lh = L.cpu().numpy()
+            loss_ref = float((tl_ref.reshape(S, T).sum(1) / Lh).sum() / S)
+            e_loss = abs(float(out.loss) - loss_ref) / max(abs(loss_ref), 1e-30)
+            e_lr = float(((out.ref_logp.reshape(-1) - lr_ref).abs() / rlse_ref.abs().clamp(min=1.0))[m].max())
             _, _, dh, tol_dh, dw, tol_dw = _torch_reference(inp, torch.from_numpy(coef).float().to(DEV),
                                                             floor=torch.from_numpy(fl).float().to(DEV))
             bad_h = ((out.dhidden - dh).abs() > tol_dh + 1e-6 * tol_dh.max()).sum().item()
@@ -938,6 +951,10 @@ def test_config5_full_size():
             used_h = float(((out.dhidden - dh).abs() / (tol_dh + 1e-30)).max())
             used_w = float(((out.dweight - dw).abs() / (tol_dw + 1e-30)).max())
             print(f"  clip-KL gradients: largest error / bound: dhidden {used_h:.3f}, dW {used_w:.3f}", flush=True)
+            print(f"PARITY-TABLE config5 clip_kl default: |dlogp|/max(1,|lse|) {e_lp:.2e} (bar 1e-5); ref {e_lr:.2e}; "
+                  f"loss rel {e_loss:.2e} (vs fp32 torch); dhidden max abs {float((out.dhidden - dh).abs().max()):.2e} "
+                  f"({used_h:.3f} of its bound); dW max abs {float((out.dweight - dw).abs().max()):.2e} "
+                  f"({used_w:.3f} of its bound)", flush=True)
             assert bad_h == 0 and bad_w == 0, (bad_h, bad_w)
             del dh, tol_dh, dw, tol_dw
         del out

@@ -247,6 +247,57 @@ def test_finite_differences_tiny(orc):
     np.testing.assert_allclose(g, fd, rtol=2e-3, atol=2e-4)
 
 
+def test_check_dlogits_agrees_with_numpy_and_catches_planted_mistakes(orc):
+    """check_dlogits (the in-place element-wise comparison the full-size GPU tests use)
+    against the same statistics computed in numpy from grpo_rows' materialised exact
+    rows, on bf16 and f32 device-like outputs; then planted mistakes in the compared
+    rows (a sign, a shifted index, a dropped onehot term, one element off by two bf16
+    ulps) are counted."""
+    rng = np.random.default_rng(11)
+    N, V = 12, 777
+    x = orc.bf16_from_f32((rng.standard_normal((N, V)) * 3).astype(np.float32))
+    ids = rng.integers(0, V, N)
+    A = rng.standard_normal(N).astype(np.float32)
+    r = orc.grpo_rows(x, ids, np.ones(N), A, np.full(N, 5.0), 2.0, dtype=orc.BF16)
+    exact = orc.grpo_rows(x, ids, np.ones(N), A, np.full(N, 5.0), 2.0, dtype=orc.BF16).dlogits
+    # grpo_rows stores f32; recompute the float64 rows for the numpy side.
+    xd = orc.bf16_to_f32(x).astype(np.float64)
+    lse = np.log(np.exp(xd - xd.max(1, keepdims=True)).sum(1)) + xd.max(1)
+    d = -np.exp(xd - lse[:, None]) * r.coef[:, None]
+    d[np.arange(N), ids] += r.coef
+    np.testing.assert_allclose(exact, d.astype(np.float32), rtol=0, atol=0)
+    fl = 1e-5 * np.abs(r.coef)
+    rel, kf = 2.0 ** -8 + 1.1e-5, 1 + 2.0 ** -7
+    for dt, got in ((orc.BF16, orc.bf16_from_f32(d.astype(np.float32))), (orc.F32, d.astype(np.float32))):
+        res = orc.check_dlogits(x, ids, r.coef, fl, got, dt, rel, kf, dtype=orc.BF16)
+        g = orc.bf16_to_f32(got).astype(np.float64) if dt == orc.BF16 else got.astype(np.float64)
+        err = np.abs(g - d)
+        tol = rel * np.abs(d) + kf * fl[:, None]
+        # The two log-sum-exps differ in summation order (~1e-16 relative), which moves
+        # the tiny f32 errors by ~1e-17 absolute.
+        np.testing.assert_allclose(res.max_abs, err.max(1), rtol=1e-6, atol=1e-15)
+        np.testing.assert_allclose(res.max_usage, (err / tol).max(1), rtol=1e-6, atol=1e-9)
+        big = np.abs(d) >= 2.0 ** -14 * np.abs(r.coef)[:, None]
+        np.testing.assert_allclose(res.max_rel, np.where(big, err / np.where(big, np.abs(d), 1), 0).max(1),
+                                   rtol=1e-6, atol=1e-12)
+        assert (res.n_bad == 0).all() and res.max_usage.max() <= 1.0
+        if dt == orc.BF16:
+            assert res.max_rel.max() <= 2.0 ** -8 and res.max_rel.max() > 2.0 ** -10   # RNE rounding is seen
+    good = orc.bf16_from_f32(d.astype(np.float32))
+
+    def bad_rows(g):
+        return int((orc.check_dlogits(x, ids, r.coef, fl, g, orc.BF16, rel, kf, dtype=orc.BF16).n_bad > 0).sum())
+
+    assert bad_rows(orc.bf16_from_f32(-d.astype(np.float32))) == N            # sign of the coefficient
+    assert bad_rows(np.ascontiguousarray(np.roll(good, 1, axis=1))) == N      # off-by-one vocabulary index
+    no_onehot = d.copy()
+    no_onehot[np.arange(N), ids] -= r.coef
+    assert bad_rows(orc.bf16_from_f32(no_onehot.astype(np.float32))) == N     # dropped onehot term
+    one = good.copy()
+    one[3, ids[3]] = one[3, ids[3]] + 2 if abs(d[3, ids[3]]) > 0 else one[3, ids[3]]   # two ulps at the target
+    assert bad_rows(one) == 1
+
+
 # ---- mutation tests: plausible mistakes in the oracle are caught -----------------
 
 def test_checks_catch_planted_mistakes(orc):
