@@ -196,8 +196,8 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
     return rc;
   }
 
-  // Scratch: adv | seq_len | seq_scale | seq_val | loss | row counter, live-row count |
-  // token_loss | live-row list (without zero-fill).
+  // Scratch: adv | seq_len | seq_scale | seq_val | loss | row counter, live-row count,
+  // loss ticket | token_loss | live-row list (without zero-fill).
   const size_t sv = round256(sizeof(float) * g.n_seq);
   const bool need_tl = (op == kLoss) && a->token_loss == nullptr;
   const size_t tl_bytes = need_tl ? round256(sizeof(float) * g.n_seq * g.tstride) : 0;
@@ -223,11 +223,13 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   float* s_scale = reinterpret_cast<float*>(sp + 2 * sv);
   float* s_val = reinterpret_cast<float*>(sp + 3 * sv);
   float* s_loss = reinterpret_cast<float*>(sp + 4 * sv);
-  // The persistent row kernel's counter: a one-thread kernel zeroes it before each
-  // launch. The allocation-free path keeps it in the shared array, the other path in
-  // the context's own allocation.
+  // The persistent row kernel's counter, zeroed before each launch (by step_prep_kernel
+  // on the loss path). The allocation-free path keeps it in the shared array, the other
+  // path in the context's own allocation. The loss ticket of loss_reduce_kernel and the
+  // live-row count sit in the scratch.
   int* s_next = noalloc ? reinterpret_cast<int*>(sp + 4 * sv + 256) : ctx->d_next_row;
   int* s_count = reinterpret_cast<int*>(sp + 4 * sv + 256 + 64);
+  int* s_done = reinterpret_cast<int*>(sp + 4 * sv + 256 + 128);
   float* s_tl = need_tl ? reinterpret_cast<float*>(sp + 4 * sv + 512) : a->token_loss;
   int* s_list = need_list ? reinterpret_cast<int*>(sp + 4 * sv + 512 + tl_bytes) : nullptr;
 
@@ -253,19 +255,32 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   ra.ref_logp = a->ref_logp;
 
   if (op == kLoss) {
-    const float* adv = a->advantages;
-    if (!adv) {
-      e = launch_advantages(a->rewards, g.n_seq, g.group, a->std_eps, s_adv, st);
-      if (e != hipSuccess) return hip_fail(ctx, e, "advantages launch");
-      adv = s_adv;
-    }
-    if (a->advantages_out && a->advantages_out != adv) {
-      e = hipMemcpyAsync(a->advantages_out, adv, sizeof(float) * g.n_seq, hipMemcpyDeviceToDevice, st);
-      if (e != hipSuccess) return hip_fail(ctx, e, "copying advantages");
-    }
-    e = launch_seq_prep(a->mask, ra.mask_u8, g.n_seq, g.rows, g.tstride, g.toff, g.loss_norm, s_len,
-                        s_scale, st);
-    if (e != hipSuccess) return hip_fail(ctx, e, "seq_prep launch");
+    // One launch: advantages (or the copy of the given ones), per-sequence lengths, and
+    // the row kernel's and the loss ticket's counters zeroed.
+    const float* adv = a->advantages ? a->advantages : s_adv;
+    StepPrepArgs pa;
+    std::memset(&pa, 0, sizeof(pa));
+    pa.mask = a->mask;
+    pa.mask_u8 = ra.mask_u8;
+    pa.n_seq = g.n_seq;
+    pa.rows = g.rows;
+    pa.tok_stride = g.tstride;
+    pa.tok_offset = g.toff;
+    pa.loss_norm = g.loss_norm;
+    pa.seq_len = s_len;
+    pa.seq_scale = s_scale;
+    pa.rewards = a->advantages ? nullptr : a->rewards;
+    pa.adv_in = a->advantages;
+    pa.group = g.group;
+    pa.std_eps = a->std_eps;
+    pa.adv = s_adv;
+    pa.adv_out = a->advantages_out != adv ? a->advantages_out : nullptr;
+    pa.zero[0] = s_next;
+    pa.zero[1] = s_list ? s_count : nullptr;
+    pa.zero[2] = s_done;
+    e = launch_step_prep(pa, st);
+    if (e != hipSuccess) return hip_fail(ctx, e, "step prep launch");
+    ra.counters_zeroed = 1;
     ra.ref_logits = (a->loss_mode == PCP_LOSS_GRPO_CLIP_KL) ? a->ref_logits : nullptr;
     ra.old_logp = a->old_logp;
     ra.adv = adv;
@@ -302,9 +317,9 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   }
 
   if (op == kLoss) {
-    float* loss = a->loss ? a->loss : s_loss;
-    e = launch_loss_reduce(s_tl, g.n_seq, g.rows, g.tstride, g.toff, s_len, ra.adv,
-                           a->loss_mode == PCP_LOSS_REINFORCE, g.loss_norm, s_val, loss, st);
+    const LossReduceArgs la{s_tl, g.rows, g.tstride, g.toff, s_len, ra.adv, a->loss_mode == PCP_LOSS_REINFORCE,
+                            s_val, g.n_seq, g.loss_norm, s_done, a->loss ? a->loss : s_loss};
+    e = launch_loss_reduce_fused(la, st);
     if (e != hipSuccess) return hip_fail(ctx, e, "loss reduction launch");
   }
   return finish(ctx, a, st);

@@ -308,6 +308,7 @@ struct RowArgs {
   int32_t mask_u8;
   int32_t loss_mode;
   int32_t zero_fill;
+  int32_t counters_zeroed;  // next_row / row_count were zeroed earlier on the stream (step_prep_kernel)
   float clip_eps;
   float kl_beta;
 };

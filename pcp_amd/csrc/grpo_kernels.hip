@@ -748,13 +748,10 @@ seq_prep_kernel(const void* mask, int32_t mask_u8, int64_t rows, int64_t tok_str
 // which are compiled outside this scope), so the arithmetic is written with
 // plain operators under contract(off); fp32 '/' and sqrtf are correctly rounded
 // (hipcc's default -fhip-fp32-correctly-rounded-divide-sqrt).
-__global__ void __launch_bounds__(64)
-advantages_kernel(const float* r, int64_t n, int64_t group, float eps, float* adv) {
+// The group of rewards [i, e): adv[k] (and adv2[k] when adv2 is not null).
+__device__ __forceinline__ void group_advantages(const float* r, int64_t i, int64_t e, float eps, float* adv,
+                                                 float* adv2) {
 #pragma clang fp contract(off)
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
-  const int64_t i = g * group;
-  if (i >= n) return;
-  const int64_t e = (i + group < n) ? i + group : n;
   const float cnt = static_cast<float>(e - i);
   float sum = 0.f;
   for (int64_t k = i; k < e; ++k) sum = sum + r[k];
@@ -766,7 +763,19 @@ advantages_kernel(const float* r, int64_t n, int64_t group, float eps, float* ad
     ssd = ssd + d2;
   }
   const float sd = sqrtf(ssd / cnt) + eps;
-  for (int64_t k = i; k < e; ++k) adv[k] = (r[k] - mean) / sd;
+  for (int64_t k = i; k < e; ++k) {
+    const float v = (r[k] - mean) / sd;
+    adv[k] = v;
+    if (adv2) adv2[k] = v;
+  }
+}
+
+__global__ void __launch_bounds__(64)
+advantages_kernel(const float* r, int64_t n, int64_t group, float eps, float* adv) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+  const int64_t i = g * group;
+  if (i >= n) return;
+  group_advantages(r, i, (i + group < n) ? i + group : n, eps, adv, nullptr);
 }
 
 // seq_val[s] = (sum_t token_loss) / seq_len[s] (* adv[s] in REINFORCE mode):
@@ -795,6 +804,85 @@ loss_final_kernel(const float* seq_val, int64_t n_seq, float loss_norm, float* l
   for (int64_t s = threadIdx.x; s < n_seq; s += kFinalBlock) acc += seq_val[s];
   const float tot = block_sum<kFinalBlock>(acc, lds);
   if (threadIdx.x == 0) *loss = tot / loss_norm;
+}
+
+// The work before the row kernel in one launch, one workgroup per sequence s:
+//  * seq_len[s], seq_scale[s] as seq_prep_kernel (the same per-lane order and reduction);
+//  * with rewards: thread 0 of the first workgroup of each group computes the group's
+//    advantages as advantages_kernel (the same function, so the same bits), also into
+//    adv_out; without: adv_out[s] = adv_in[s] (when adv_out is set);
+//  * workgroup 0 zeroes the counters the row kernel and loss_reduce_kernel start from.
+__global__ void __launch_bounds__(kSmallBlock) step_prep_kernel(StepPrepArgs a) {
+  const int64_t s = blockIdx.x;
+  if (threadIdx.x == 0) {
+    if (s == 0) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        if (a.zero[k]) *a.zero[k] = 0;
+    }
+    if (a.rewards) {
+      if (s % a.group == 0) group_advantages(a.rewards, s, min(s + a.group, a.n_seq), a.std_eps, a.adv, a.adv_out);
+    } else if (a.adv_out) {
+      a.adv_out[s] = a.adv_in[s];
+    }
+  }
+  __shared__ float lds[kSmallBlock / 64];
+  float acc = 0.f;
+  const int64_t base = s * a.tok_stride + a.tok_offset;
+  for (int64_t t = threadIdx.x; t < a.rows; t += kSmallBlock) {
+    float m;
+    if (a.mask == nullptr) m = 1.f;
+    else if (a.mask_u8) m = static_cast<const uint8_t*>(a.mask)[base + t] ? 1.f : 0.f;
+    else m = static_cast<const float*>(a.mask)[base + t];
+    acc += m;
+  }
+  const float tot = block_sum<kSmallBlock>(acc, lds);
+  if (threadIdx.x == 0) {
+    const float L = fmaxf(tot, 1.f);
+    a.seq_len[s] = L;
+    a.seq_scale[s] = 1.f / (a.loss_norm * L);
+  }
+}
+
+// The loss in one launch, one workgroup per sequence: seq_val[s] as seq_loss_kernel;
+// the workgroup that finishes last (a ticket from *done, which step_prep_kernel zeroed)
+// then forms the loss in loss_final_kernel's order, lane for lane: the 16 waves of
+// that 1024-lane sum are taken four at a time by this workgroup's waves (lane l of
+// wave w adds seq_val[64 w + l], [64 w + l + 1024], ... and reduces by the same xor
+// butterfly), and the wave sums add in wave order. It leaves *done at 0.
+__global__ void __launch_bounds__(kSmallBlock) loss_reduce_kernel(LossReduceArgs a) {
+  __shared__ float lds[kFinalBlock / 64];
+  __shared__ int last;
+  const int64_t s = blockIdx.x;
+  const int64_t base = s * a.tok_stride + a.tok_offset;
+  float acc = 0.f;
+  for (int64_t t = threadIdx.x; t < a.rows; t += kSmallBlock) acc += a.token_loss[base + t];
+  const float tot = block_sum<kSmallBlock>(acc, lds);
+  if (threadIdx.x == 0) {
+    const float v = tot / a.seq_len[s];
+    a.seq_val[s] = a.reinforce ? v * a.adv[s] : v;
+    __threadfence();   // seq_val[s] visible before the ticket
+    last = atomicAdd(a.done, 1) == static_cast<int>(a.n_seq - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();     // every other workgroup's seq_val, past this CU's caches
+  const int lane = threadIdx.x & 63;
+  for (int w = threadIdx.x >> 6; w < kFinalBlock / 64; w += kSmallBlock / 64) {
+    float v = 0.f;
+    for (int64_t k = 64 * w + lane; k < a.n_seq; k += kFinalBlock) v += a.seq_val[k];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if (lane == 0) lds[w] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = lds[0];
+#pragma unroll
+    for (int w = 1; w < kFinalBlock / 64; ++w) v += lds[w];
+    *a.loss = v / a.loss_norm;
+    *a.done = 0;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -829,7 +917,7 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
   if (grid <= 0) return hipSuccess;
   const dim3 g(static_cast<unsigned>(grid)), b(BLOCK);
   if constexpr (kPersistentRows<TI, TO>) {
-    reset_counter_kernel<<<1, 1, 0, st>>>(a.next_row, a.row_list ? a.row_count : nullptr);
+    if (!a.counters_zeroed) reset_counter_kernel<<<1, 1, 0, st>>>(a.next_row, a.row_list ? a.row_count : nullptr);
     if (a.row_list) {
       live_rows_kernel<<<dim3(static_cast<unsigned>((nrows + 255) / 256)), dim3(256), 0, st>>>(a);
       grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE, CACHE, true><<<g, b, 0, st>>>(a);
@@ -982,6 +1070,16 @@ hipError_t launch_advantages(const float* r, int64_t n, int64_t group, float eps
   const int64_t ngroups = (n + group - 1) / group;
   const unsigned nb = static_cast<unsigned>((ngroups + 63) / 64);
   advantages_kernel<<<dim3(nb), dim3(64), 0, st>>>(r, n, group, eps, adv);
+  return hipGetLastError();
+}
+
+hipError_t launch_step_prep(const StepPrepArgs& a, hipStream_t st) {
+  step_prep_kernel<<<dim3(static_cast<unsigned>(a.n_seq)), dim3(kSmallBlock), 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_loss_reduce_fused(const LossReduceArgs& a, hipStream_t st) {
+  loss_reduce_kernel<<<dim3(static_cast<unsigned>(a.n_seq)), dim3(kSmallBlock), 0, st>>>(a);
   return hipGetLastError();
 }
 

@@ -36,4 +36,40 @@ hipError_t launch_loss_reduce(const float* token_loss, int64_t n_seq, int64_t ro
                               const float* adv, int reinforce, float loss_norm, float* seq_val,
                               float* loss, hipStream_t st);
 
+// One launch before the row kernel: per-sequence lengths and loss scales (as
+// launch_seq_prep), the group advantages (as launch_advantages, when rewards is set)
+// or a copy of the given ones into adv_out, and up to three counters zeroed.
+struct StepPrepArgs {
+  const void* mask;       // nullptr: all ones
+  int32_t mask_u8;
+  int64_t n_seq, rows, tok_stride, tok_offset;
+  float loss_norm;
+  float* seq_len;
+  float* seq_scale;
+  const float* rewards;   // nullptr: the advantages are given (adv_in)
+  const float* adv_in;
+  int64_t group;
+  float std_eps;
+  float* adv;             // the computed advantages (rewards set)
+  float* adv_out;         // optional copy of the advantages used
+  int* zero[3];           // optional counters set to 0
+};
+hipError_t launch_step_prep(const StepPrepArgs& a, hipStream_t st);
+
+// The loss in one launch (seq_loss_kernel + loss_final_kernel, the same summation
+// order): done must be 0 at the launch (step_prep_kernel zeroes it) and is left 0.
+struct LossReduceArgs {
+  const float* token_loss;
+  int64_t rows, tok_stride, tok_offset;
+  const float* seq_len;
+  const float* adv;
+  int32_t reinforce;
+  float* seq_val;         // [n_seq] work
+  int64_t n_seq;
+  float loss_norm;
+  int* done;
+  float* loss;
+};
+hipError_t launch_loss_reduce_fused(const LossReduceArgs& a, hipStream_t st);
+
 }  // namespace pcp

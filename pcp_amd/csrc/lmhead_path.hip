@@ -157,6 +157,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   size_t off = 0;
   auto take = [&](size_t bytes) { const size_t o = off; off += r256(bytes); return o; };
   const size_t o_adv = take(4 * S), o_len = take(4 * S), o_scale = take(4 * S), o_val = take(4 * S), o_loss = take(4);
+  const size_t o_done = take(4);
   const size_t o_tl = a->token_loss ? 0 : take(4 * N);
   const size_t o_live = take(4 * N), o_cidx = take(4 * N), o_idsc = take(4 * N), o_cnt = take(4);
   const size_t o_hid = take(2 * static_cast<size_t>(N) * H);
@@ -240,18 +241,30 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     return hip_fail(ctx, e, "gathering live hidden rows");
   }
 
-  // Advantages and per-sequence lengths.
-  const float* adv = a->advantages;
-  if (!adv) {
-    if ((e = launch_advantages(a->rewards, S, a->group_size, a->std_eps, F(o_adv), st)) != hipSuccess)
-      return hip_fail(ctx, e, "advantages launch");
-    adv = F(o_adv);
+  // Advantages (or the copy of the given ones), per-sequence lengths and the loss
+  // ticket's counter, in one launch.
+  const float* adv = a->advantages ? a->advantages : F(o_adv);
+  {
+    StepPrepArgs pa;
+    std::memset(&pa, 0, sizeof(pa));
+    pa.mask = a->mask;
+    pa.mask_u8 = mask_u8;
+    pa.n_seq = S;
+    pa.rows = T;
+    pa.tok_stride = T;
+    pa.tok_offset = 0;
+    pa.loss_norm = loss_norm;
+    pa.seq_len = F(o_len);
+    pa.seq_scale = F(o_scale);
+    pa.rewards = a->advantages ? nullptr : a->rewards;
+    pa.adv_in = a->advantages;
+    pa.group = a->group_size;
+    pa.std_eps = a->std_eps;
+    pa.adv = F(o_adv);
+    pa.adv_out = a->advantages_out != adv ? a->advantages_out : nullptr;
+    pa.zero[0] = I(o_done);
+    if ((e = launch_step_prep(pa, st)) != hipSuccess) return hip_fail(ctx, e, "step prep launch");
   }
-  if (a->advantages_out && a->advantages_out != adv &&
-      (e = hipMemcpyAsync(a->advantages_out, adv, 4 * S, hipMemcpyDeviceToDevice, st)) != hipSuccess)
-    return hip_fail(ctx, e, "copying advantages");
-  if ((e = launch_seq_prep(a->mask, mask_u8, S, T, T, 0, loss_norm, F(o_len), F(o_scale), st)) != hipSuccess)
-    return hip_fail(ctx, e, "seq_prep launch");
 
   // Forward, per model: tiles -> partials + target logit; merge -> lse2.
   LmTileArgs ta;
@@ -321,9 +334,11 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   ra.kl_beta = a->kl_beta;
   LmTermsArgs tma{N, I(o_cidx), F(o_tgt), F(o_l2), ref ? F(o_rtgt) : nullptr, ref ? F(o_rl2) : nullptr, F(o_coef)};
   if ((e = launch_lm_terms(ra, tma, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head terms");
-  if ((e = launch_loss_reduce(tl, S, T, T, 0, F(o_len), adv, a->loss_mode == PCP_LOSS_REINFORCE, loss_norm,
-                              F(o_val), a->loss ? a->loss : F(o_loss), st)) != hipSuccess)
-    return hip_fail(ctx, e, "loss reduction");
+  {
+    const LossReduceArgs la{tl, T, T, 0, F(o_len), adv, a->loss_mode == PCP_LOSS_REINFORCE, F(o_val), S, loss_norm,
+                            I(o_done), a->loss ? a->loss : F(o_loss)};
+    if ((e = launch_loss_reduce_fused(la, st)) != hipSuccess) return hip_fail(ctx, e, "loss reduction");
+  }
 
   // Backward over the live tokens. With none, the products have no tiles (dhidden) or
   // an empty K (dW: zero), and dead rows are written as zero, so every gradient is 0.

@@ -140,3 +140,38 @@ def assert_dlogits(got, want, floor_rows, bf16_out, exact=False, f16_out=False):
         assert err.max() <= 1e-4
     bad = err > tol
     assert not bad.any(), f"{bad.sum()} dlogits out of tolerance; worst {err.max():.3e}"
+
+
+def emulate_block_sum(x, block):
+    """float32 value of the device's fixed-order workgroup sum of x over `block` lanes:
+    lane j adds x[j], x[j + block], ... in order; each 64-lane wave then reduces by the
+    xor butterfly (every lane adds the value of lane ^ off, off = 32, 16, ..., 1); the
+    wave sums add in wave order."""
+    x = np.asarray(x, np.float32).reshape(-1)
+    acc = np.zeros(block, np.float32)
+    for k in range(0, len(x), block):
+        c = x[k:k + block]
+        acc[:len(c)] = acc[:len(c)] + c
+    w = acc.reshape(block // 64, 64)
+    lanes = np.arange(64)
+    for off in (32, 16, 8, 4, 2, 1):
+        w = w + w[:, lanes ^ off]
+    v = w[0, 0]
+    for i in range(1, block // 64):
+        v = np.float32(v + w[i, 0])
+    return np.float32(v)
+
+
+def emulate_loss(token_loss, mask, adv, reinforce, loss_norm):
+    """The loss the device's reduction forms from its own f32 token losses [S, T] (the
+    token-carrying columns) and 0/1 mask: per sequence the 256-lane sum over its tokens
+    divided by max(sum mask, 1) (times the advantage in REINFORCE), then the 1024-lane
+    sum of those over the sequences divided by loss_norm, every step in float32."""
+    tl = np.asarray(token_loss, np.float32)
+    S = tl.shape[0]
+    seq_len = np.maximum(np.asarray(mask, np.float32).sum(1, dtype=np.float32), np.float32(1))
+    vals = np.empty(S, np.float32)
+    for s in range(S):
+        v = np.float32(emulate_block_sum(tl[s], 256) / seq_len[s])
+        vals[s] = np.float32(v * np.float32(adv[s])) if reinforce else v
+    return np.float32(emulate_block_sum(vals, 1024) / np.float32(loss_norm))

@@ -916,6 +916,9 @@ def test_config5_full_size():
             seq_ref = -(inp["mask"].double() * lp_ref.double().reshape(S, T)).sum(1) / L
             loss_ref = float((seq_ref * torch.from_numpy(adv).to(DEV).double()).sum() / S)
             e_loss = abs(float(out.loss) - loss_ref) / max(abs(loss_ref), 1e-30)
+            terms = float(((inp["mask"].double() * lp_ref.double().reshape(S, T)).abs().sum(1) / L
+                           * torch.from_numpy(np.abs(adv)).to(DEV).double()).sum() / S)
+            e_terms = abs(float(out.loss) - loss_ref) / terms
             for name, res, th, tw in (("default", out, tol_dh + cache["dh"], tol_dw + cache["dw"]),
                                       ("exact", exact, tol_dh, tol_dw)):
                 bad_h = ((res.dhidden - dh).abs() > th + 1e-6 * th.max()).sum().item()
@@ -925,7 +928,8 @@ def test_config5_full_size():
                 print(f"  REINFORCE gradients, {name}: largest error / bound: dhidden {used_h:.3f}, dW {used_w:.3f}",
                       flush=True)
                 print(f"PARITY-TABLE config5 reinforce {name}: |dlogp|/max(1,|lse|) {e_lp:.2e} (bar 1e-5); loss rel "
-                      f"{e_loss:.2e} (vs fp32 torch); dhidden max abs {float((res.dhidden - dh).abs().max()):.2e} "
+                      f"{e_loss:.2e}, per sum of |terms| {e_terms:.2e} (vs fp32 torch); dhidden max abs "
+                      f"{float((res.dhidden - dh).abs().max()):.2e} "
                       f"({used_h:.3f} of its bound); dW max abs {float((res.dweight - dw).abs().max()):.2e} "
                       f"({used_w:.3f} of its bound)", flush=True)
                 assert bad_h == 0 and bad_w == 0, (name, bad_h, bad_w)
@@ -943,6 +947,7 @@ def test_config5_full_size():
             Lh = L.cpu().numpy()
             loss_ref = float((tl_ref.reshape(S, T).sum(1) / Lh).sum() / S)
             e_loss = abs(float(out.loss) - loss_ref) / max(abs(loss_ref), 1e-30)
+            e_terms = abs(float(out.loss) - loss_ref) / float((np.abs(tl_ref).reshape(S, T).sum(1) / Lh).sum() / S)
             e_lr = float(((out.ref_logp.reshape(-1) - lr_ref).abs() / rlse_ref.abs().clamp(min=1.0))[m].max())
             _, _, dh, tol_dh, dw, tol_dw = _torch_reference(inp, torch.from_numpy(coef).float().to(DEV),
                                                             floor=torch.from_numpy(fl).float().to(DEV))
@@ -952,7 +957,8 @@ def test_config5_full_size():
             used_w = float(((out.dweight - dw).abs() / (tol_dw + 1e-30)).max())
             print(f"  clip-KL gradients: largest error / bound: dhidden {used_h:.3f}, dW {used_w:.3f}", flush=True)
             print(f"PARITY-TABLE config5 clip_kl default: |dlogp|/max(1,|lse|) {e_lp:.2e} (bar 1e-5); ref {e_lr:.2e}; "
-                  f"loss rel {e_loss:.2e} (vs fp32 torch); dhidden max abs {float((out.dhidden - dh).abs().max()):.2e} "
+                  f"loss rel {e_loss:.2e}, per sum of |terms| {e_terms:.2e} (vs fp32 torch); dhidden max abs "
+                  f"{float((out.dhidden - dh).abs().max()):.2e} "
                   f"({used_h:.3f} of its bound); dW max abs {float((out.dweight - dw).abs().max()):.2e} "
                   f"({used_w:.3f} of its bound)", flush=True)
             assert bad_h == 0 and bad_w == 0, (bad_h, bad_w)

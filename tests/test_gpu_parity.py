@@ -27,8 +27,8 @@ from oracle import oracle as orc
 from pcp_amd import grpo, synth
 from pcp_amd._lib import DType, LossMode, PcpError
 from pcp_amd.backend import HipGrpoBackend
-from parity_tol import (BF16_CACHED_REL, BF16_EXACT_REL, assert_dlogits, coef_floor, dev, full_floor, full_loss_tol,
-                        host_bits, loss_tolerance, lse_scale, tok_to_rows, token_scale)
+from parity_tol import (BF16_CACHED_REL, BF16_EXACT_REL, assert_dlogits, coef_floor, dev, emulate_loss, full_floor,
+                        full_loss_tol, host_bits, loss_tolerance, lse_scale, tok_to_rows, token_scale)
 
 pytestmark = pytest.mark.gpu
 
@@ -172,10 +172,14 @@ def test_config1_full(mode):
     ltol = full_loss_tol(want, h["logits"], h["ids"], h["mask"], cfg.T, 0, orc.F32, mode == LossMode.REINFORCE,
                          cfg.kl_beta, cfg.S)
     e_loss = abs(float(out.loss.cpu()) - want.loss)
+    terms = np.abs(want.token_loss).sum(1) / want.seq_len.astype(np.float64)
+    if mode == LossMode.REINFORCE:
+        terms = terms * np.abs(want.adv.astype(np.float64))
     d_abs = np.abs(got_d.astype(np.float64) - want.dlogits.astype(np.float64))
     print(f"PARITY-TABLE config1 {'clip_kl' if mode == LossMode.GRPO_CLIP_KL else 'reinforce'}: live rows "
           f"{int(live.sum())} of {live.size}; |dlogp|/max(1,|lse|) {e_lp:.2e} (bar 1e-5); ref {e_lr:.2e}; token loss "
-          f"{e_tl:.2e}; loss rel {e_loss / max(abs(want.loss), 1e-30):.2e} ({e_loss / ltol:.2f} of its bar); f32 "
+          f"{e_tl:.2e}; loss rel {e_loss / max(abs(want.loss), 1e-30):.2e}, per sum of |terms| "
+          f"{e_loss / (terms.sum() / cfg.S):.2e} ({e_loss / ltol:.3f} of its bar); f32 "
           f"dlogits max abs {d_abs.max():.2e} (bar 1e-4)", flush=True)
 
 
@@ -560,6 +564,39 @@ def test_device_errors_are_reported_and_cleared():
     assert abs(float(out.loss.cpu()) - c["exp_loss"]) <= golden_loss_tol(c)
 
 
+@pytest.mark.parametrize("S,T", [(1, 5), (3, 300), (64, 512), (1500, 7), (2100, 3)])
+@pytest.mark.parametrize("mode", [LossMode.REINFORCE, LossMode.GRPO_CLIP_KL])
+def test_loss_reduction_order_bit_exact(S, T, mode):
+    """The one-launch loss reduction (per-sequence sums, then the last workgroup's sum
+    over the sequences) equals, bit for bit, a float32 emulation of its fixed summation
+    order applied to the device's own token losses: 256 lanes per sequence, 1024 lanes
+    over the sequences (S = 1500 and 2100 take the second and third pass of that sum).
+    The advantages it computes in the same launch as the lengths are the oracle's bits."""
+    print(f"loss reduction order S={S} T={T} mode={int(mode)}", flush=True)
+    rng = np.random.default_rng(S * 7 + T)
+    V, G = 8, (3 if S % 3 == 0 else (2 if S % 2 == 0 else 1))
+    x = torch.from_numpy(rng.standard_normal((S, T, V)).astype(np.float32) * 2).to(DEV)
+    ids = torch.from_numpy(rng.integers(0, V, (S, T))).to(DEV)
+    lengths = rng.integers(0, T + 1, S)
+    mask = torch.from_numpy((np.arange(T)[None] < lengths[:, None]).astype(np.float32)).to(DEV)
+    rewards = torch.from_numpy(rng.random(S).astype(np.float32)).to(DEV)
+    old = torch.from_numpy((rng.standard_normal((S, T)) * 0.1 - 2).astype(np.float32)).to(DEV)
+    ref = (x + 0.1 * torch.from_numpy(rng.standard_normal((S, T, V)).astype(np.float32)).to(DEV)).contiguous()
+    out = grpo.grpo_loss_fwd_bwd(x, ids, mask, rewards=rewards, group_size=G, ref_logits=ref, old_logp=old,
+                                 loss_mode=mode, want_dlogits=False)
+    torch.cuda.synchronize()
+    adv = orc.advantages(rewards.cpu().numpy(), G)
+    assert np.array_equal(out.advantages.cpu().numpy().view(np.uint32), adv.view(np.uint32))
+    want = emulate_loss(out.token_loss.cpu().numpy(), mask.cpu().numpy(), adv, mode == LossMode.REINFORCE, S)
+    got = out.loss.cpu().numpy().astype(np.float32)
+    assert got.view(np.uint32) == want.view(np.uint32), (float(got), float(want))
+    # and again on the same context: the reduction's ticket was left at zero
+    out2 = grpo.grpo_loss_fwd_bwd(x, ids, mask, rewards=rewards, group_size=G, ref_logits=ref, old_logp=old,
+                                  loss_mode=mode, want_dlogits=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out2.loss, out.loss)
+
+
 def test_deterministic_repeat():
     c = CASES["v1024_clip_kl"]
     a = run_case(c)
@@ -654,9 +691,13 @@ def _all_live_rows_check(cfg, inp, out, mode, exact, label, chunk=4096):
     assert abs(got_loss - loss_exact) <= tol, (label, got_loss, loss_exact, tol)
     st["loss_rel"] = abs(got_loss - loss_exact) / max(abs(loss_exact), 1e-30)
     st["loss_use"] = abs(got_loss - loss_exact) / tol
+    terms = np.abs(tl2).sum(1) / Ls.astype(np.float64)
+    if m == orc.REINFORCE:
+        terms = terms * np.abs(adv.astype(np.float64))
+    st["loss_rel_terms"] = abs(got_loss - loss_exact) / (terms.sum() / S)
     print(f"PARITY-TABLE {label}: live rows {len(live)} of {S * T}; |dlogp|/max(1,|lse|) {st['lp']:.2e}"
-          f" (bar 1e-5); ref {st['lr']:.2e}; token loss {st['tl']:.2e}; loss rel {st['loss_rel']:.2e}"
-          f" ({st['loss_use']:.2f} of its bar); bf16 dlogits max abs {st['abs']:.2e}, max rel (p >= 2^-14)"
+          f" (bar 1e-5); ref {st['lr']:.2e}; token loss {st['tl']:.2e}; loss rel {st['loss_rel']:.2e}, per sum of"
+          f" |terms| {st['loss_rel_terms']:.2e} ({st['loss_use']:.3f} of its bar); bf16 dlogits max abs {st['abs']:.2e}, max rel (p >= 2^-14)"
           f" {st['rel']:.3e} (2^-8 = 3.906e-03), bar used {st['usage']:.3f}", flush=True)
     return st
 
