@@ -390,9 +390,11 @@ def bench_sample(args) -> None:
     """The rollout sampler over f32 logits [R, 151936] in HBM (Sampler.sample,
     math.zig:21-58, at temperature 0.7, the reference's default, generation_engine.zig:163).
     R = 64 (--rows, default) is one decoding step of configuration 2's 64 rollouts; R = 1
-    is the reference's own call pattern, one row per generated token. Every call returns
-    with the tokens on the device (the library synchronises), so ms_per_step is the
-    latency of one call. The CPU baseline is the reference's path for the same rows: copy
+    is the reference's own call pattern, one row per generated token. By default every
+    call returns with the tokens on the device (the library synchronises), so
+    ms_per_step is the latency of one call; with --async-sample calls are only enqueued
+    (as a decode loop issues them behind its forward), so ms_per_step is the time per
+    call of a stream of them. The CPU baseline is the reference's path for the same rows: copy
     the logits to host memory (600 KB per row, generation_engine.zig:255-268), then the
     sequential sampler loop."""
     import numpy as np
@@ -407,10 +409,16 @@ def bench_sample(args) -> None:
     u = torch.rand(R, device=dev, generator=gen)
     ids = torch.empty(R, dtype=torch.int64, device=dev)
     from pcp_amd.grpo import default_context
+    ctx = default_context(0)
+    sync = not args.async_sample
+    stream = torch.cuda.current_stream().cuda_stream or None
+    call = lambda: step.sample_tokens(x, T, u, ids=ids, stream=stream, ctx=ctx, sync=sync)
     for _ in range(args.warmup):
-        step.sample_tokens(x, T, u, ids=ids)
+        call()
+    ctx.sync()
     torch.cuda.synchronize()
-    kernel_ms, elapsed = _timed_calls(default_context(0), args.steps, lambda: step.sample_tokens(x, T, u, ids=ids))
+    kernel_ms, elapsed = _timed_calls(ctx, args.steps, call)
+    ctx.sync()
     ms_step = elapsed * 1e3 / args.steps
     alg = R * V * 4 + R * 4 + R * 8
     line = {
@@ -418,8 +426,11 @@ def bench_sample(args) -> None:
         "value": R / (ms_step / 1e3), "unit": "sampled tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic (torch normal logits, uniform draws)",
-        "config": {"workload": f"Sampler.sample at T={T} over {R} rows of {V} f32 logits", "rows": R, "vocab": V,
-                   "latency_us_per_call": ms_step * 1e3},
+        "config": {"workload": f"Sampler.sample at T={T} over {R} rows of {V} f32 logits"
+                               + (", enqueued only (pcp_sample_tokens_async; back-to-back calls on one stream, "
+                                  "the host waits once at the end)" if args.async_sample else
+                                  ", each call synchronous"), "rows": R, "vocab": V,
+                   ("us_per_call_enqueued" if args.async_sample else "latency_us_per_call"): ms_step * 1e3},
         "roofline": {"bound": "hbm", "achieved": alg / (kernel_ms / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": alg / (kernel_ms / 1e3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
                      "kernel": "sampler kernels (one call)", "kernel_ms": kernel_ms, "algorithmic_bytes": alg},
@@ -802,6 +813,8 @@ def main() -> None:
     ap.add_argument("--rows", type=int, default=64,
                     help="sample workload: rows per call (64: a decoding step of config 2; 1: the reference's "
                          "one row per generated token)")
+    ap.add_argument("--async-sample", action="store_true",
+                    help="sample workload: enqueue each call without waiting (pcp_sample_tokens_async)")
     ap.add_argument("--final-norm", action="store_true",
                     help="config 5: fuse the decoder's final RMSNorm (hidden = the last layer's output)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -916,7 +929,8 @@ def main() -> None:
         "rows_per_s": ab["rows"] / (ms_step / 1e3),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "grpo_resident_kernel" if not args.force_streaming else "grpo_stream_kernel",
+                     "kernel": ("grpo_stream_kernel" if args.force_streaming or args.dlogits_f32
+                                else "grpo_resident_kernel"),
                      "kernel_ms": kernel_ms, "algorithmic_bytes": ab["bytes"]},
         "setup_s": t_setup,
     }

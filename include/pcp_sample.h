@@ -41,6 +41,15 @@ extern "C" {
 int pcp_sample_tokens(pcp_ctx* ctx, const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                       int64_t row_stride, float temperature, const float* uniforms, int64_t* ids,
                       void* stream);
+/* The same, enqueued only: one kernel launch on `stream` behind the work that produced
+ * the logits (a decode step's forward), the token ids left in device memory, no host
+ * synchronisation (as PCP_FLAG_ASYNC; pcp_sync waits for it). For the reference's one
+ * sampled row per generated token (generation_engine.zig:255-268) without its
+ * device-to-host copy of the row. Calls on one context use its per-row tickets: calls
+ * that may overlap on different streams need separate contexts. */
+int pcp_sample_tokens_async(pcp_ctx* ctx, const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                            int64_t row_stride, float temperature, const float* uniforms, int64_t* ids,
+                            void* stream);
 
 #ifdef __cplusplus
 }

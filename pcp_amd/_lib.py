@@ -173,6 +173,7 @@ SIGNATURES = {
     "pcp_nesterov_serialize": (_I, [_VP, _VP, ctypes.c_size_t]),
     "pcp_nesterov_deserialize": (_I, [_VP, _VP, ctypes.c_size_t]),
     "pcp_sample_tokens": (_I, [_VP, _VP, _I, _I64, _I64, _I64, _F, _VP, _VP, _VP]),
+    "pcp_sample_tokens_async": (_I, [_VP, _VP, _I, _I64, _I64, _I64, _F, _VP, _VP, _VP]),
     "pcp_prompts_load": (_I, [_VP, ctypes.c_char_p, _VP, _I64, _VP, _I64, ctypes.POINTER(_I64),
                               ctypes.POINTER(_I64)]),
     "pcp_weights_load": (_I, [_VP, ctypes.c_char_p, _I, ctypes.POINTER(_I64), _VP, _VP]),

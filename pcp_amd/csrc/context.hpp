@@ -33,6 +33,7 @@ struct pcp_ctx {
   bool prof_on = false;
   void* lm_dbuf = nullptr;        // LM-head backward operand (softmax cache / dlogits chunk), grown on demand
   size_t lm_dbuf_bytes = 0;
+  int* sample_ticket = nullptr;   // the sampler's per-row tickets (zero between launches)
   pcp::HostStager* stager = nullptr;  // pinned staging ring of the host-bytes path
   hipStream_t xs[3] = {};         // host-bytes path: upload, compute and download streams
 };

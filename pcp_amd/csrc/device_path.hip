@@ -300,7 +300,8 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   const bool edge_ok = !ra.dlogits || (a->dlogits_dtype == a->logits_dtype &&
                                        ((reinterpret_cast<uintptr_t>(a->logits) ^
                                          reinterpret_cast<uintptr_t>(ra.dlogits)) & 15u) == 0);
-  RowPlan plan = plan_rows(in_bytes, g.vocab, al, edge_ok, ra.dlogits == nullptr,
+  RowPlan plan = plan_rows(in_bytes, ra.dlogits ? dtype_bytes(a->dlogits_dtype) : in_bytes, g.vocab, al, edge_ok,
+                           ra.dlogits == nullptr,
                            (a->flags & PCP_FLAG_FORCE_STREAMING) != 0);
   plan.exact = (a->flags & PCP_FLAG_EXACT_BF16) ? 1 : 0;
   const int out_dt = ra.dlogits ? a->dlogits_dtype : a->logits_dtype;
@@ -442,6 +443,7 @@ void pcp_destroy(pcp_ctx* ctx) {
     release_profile_events(ctx);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->lm_dbuf) (void)hipFree(ctx->lm_dbuf);
+    if (ctx->sample_ticket) (void)hipFree(ctx->sample_ticket);
     destroy_stager(ctx);
     for (hipStream_t x : ctx->xs)
       if (x) (void)hipStreamDestroy(x);

@@ -867,13 +867,21 @@ __global__ void __launch_bounds__(kSmallBlock) loss_reduce_kernel(LossReduceArgs
   __syncthreads();
   if (!last) return;
   __threadfence();     // every other workgroup's seq_val, past this CU's caches
-  const int lane = threadIdx.x & 63;
-  for (int w = threadIdx.x >> 6; w < kFinalBlock / 64; w += kSmallBlock / 64) {
-    float v = 0.f;
-    for (int64_t k = 64 * w + lane; k < a.n_seq; k += kFinalBlock) v += a.seq_val[k];
+  const int lane = threadIdx.x & 63, w0 = threadIdx.x >> 6;
+  constexpr int kPer = kFinalBlock / kSmallBlock;   // the final sum's waves per wave here
+  float v[kPer];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    if (lane == 0) lds[w] = v;
+  for (int i = 0; i < kPer; ++i) {   // first terms of all of them in flight together
+    const int64_t k = 64 * (w0 + 4 * i) + lane;
+    v[i] = 0.f;
+    if (k < a.n_seq) v[i] += a.seq_val[k];   // 0 + x, as loss_final_kernel's first addition
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    for (int64_t k = 64 * (w0 + 4 * i) + lane + kFinalBlock; k < a.n_seq; k += kFinalBlock) v[i] += a.seq_val[k];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v[i] += __shfl_xor(v[i], off);
+    if (lane == 0) lds[w0 + 4 * i] = v[i];
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -1011,7 +1019,8 @@ hipError_t dispatch_rows(const RowPlan& p, const RowArgs& a, int64_t nrows, hipS
 
 }  // namespace
 
-RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool edge_ok, bool forward_only, bool force_stream) {
+RowPlan plan_rows(int in_bytes, int out_bytes, int64_t vocab, bool aligned16, bool edge_ok, bool forward_only,
+                  bool force_stream) {
   RowPlan p;
   const int epv = 16 / in_bytes;
   const bool vec = aligned16 && (vocab % epv == 0);
@@ -1033,6 +1042,11 @@ RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool edge_ok, boo
   // Rows off 16 bytes stay resident when dlogits rows share the logits rows' element
   // type and offset (the head and tail then line up); otherwise they stream.
   if (!vec && !edge_ok) return p;
+  // 16-bit logits with f32 dlogits stream: at configuration 2 (bf16 -> f32, clip-KL)
+  // the streaming kernel took 8.81 ms against 9.74 ms resident, whose 32-byte output
+  // per lane and chunk goes out as two 16-byte stores 32 bytes apart (28.5 GB written
+  // against 19.9 GB of dlogits).
+  if (in_bytes == 2 && out_bytes == 4) return p;
   const int64_t nv = vocab / epv;   // the interior of a row off 16 bytes has at most as many
   for (int i = 0; i < static_cast<int>(sizeof(kResCfgs) / sizeof(kResCfgs[0])); ++i) {
     if (static_cast<int64_t>(kResCfgs[i].block) * kResCfgs[i].nch >= nv) {

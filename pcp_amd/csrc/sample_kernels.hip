@@ -1,13 +1,13 @@
 // The rollout sampler on the GPU (pcp_sample.h): Sampler.sample
 // (src/core/math.zig:21-58) over rows of logits in HBM.
 //
-// A row is cut into blocks of 64 lanes x 16 bytes (256 f32 or 512 bf16 logits).
-// Pass 1 (`sample_part_kernel`, kBlocksPerWg blocks per workgroup, so a batch of rows
-// fills the chip): per block (max, sum 2^((x - max) * k)), k = log2(e) / T, or for
-// greedy rows the first maximum of each workgroup's span, into scratch. Pass 2
-// (`sample_select_kernel`, one wave per row): rescale the block sums to the row max,
-// find the block where the running sum reaches u * total, re-read that block alone
-// and scan it. HBM traffic: one read of the row + one block.
+// A row is cut into blocks of 64 lanes x 16 bytes (256 f32 or 512 bf16 logits). One
+// launch (`sample_kernel`, kBlocksPerWg blocks per workgroup, so a batch of rows fills
+// the chip): per block (max, sum 2^((x - max) * k)), k = log2(e) / T, or for greedy
+// rows the first maximum of each workgroup's span, into scratch; the workgroup that
+// finishes a row last (a per-row ticket) then selects with one wave: rescale the
+// block sums to the row max, find the block where the running sum reaches u * total,
+// re-read that block alone and scan it. HBM traffic: one read of the row + one block.
 
 #include <hip/hip_runtime.h>
 
@@ -36,6 +36,7 @@ struct SampleArgs {
   int64_t* ids;
   float2* part;                           // [n_rows, nb] block (max, sum); greedy: [n_rows, nwg]
   int64_t* part_idx;                      // greedy: [n_rows, nwg] first-maximum index
+  int* ticket;                            // [n_rows] workgroups done per row; 0 between launches
   int nb, nwg;
 };
 
@@ -102,15 +103,13 @@ __device__ __forceinline__ void wave_better(float& v, int64_t& i) {
   }
 }
 
-// Pass 1: workgroup (g, row) covers blocks [g*kBlocksPerWg, (g+1)*kBlocksPerWg).
+// Partials of workgroup (g, row): blocks [g*kBlocksPerWg, (g+1)*kBlocksPerWg).
 template <typename TI>
-__global__ void __launch_bounds__(64 * kWaves) sample_part_kernel(SampleArgs a) {
+__device__ __forceinline__ void sample_part(const SampleArgs& a, int64_t row, int g) {
   constexpr int EPL = 16 / TI::kBytes;
   constexpr int BLK = 64 * EPL;
   __shared__ float wv_max[kWaves];
   __shared__ int64_t wv_idx[kWaves];
-  const int64_t row = blockIdx.y;
-  const int g = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t V = a.vocab;
   const __amdgpu_buffer_rsrc_t r = row_buffer<TI>(a, row);
@@ -156,13 +155,11 @@ __global__ void __launch_bounds__(64 * kWaves) sample_part_kernel(SampleArgs a) 
   }
 }
 
-// Pass 2: one wave per row.
+// The selection of one row, by one wave, from every workgroup's partials.
 template <typename TI>
-__global__ void __launch_bounds__(64) sample_select_kernel(SampleArgs a) {
+__device__ __forceinline__ void sample_select(const SampleArgs& a, int64_t row, int lane) {
   constexpr int EPL = 16 / TI::kBytes;
   constexpr int BLK = 64 * EPL;
-  const int64_t row = blockIdx.x;
-  const int lane = threadIdx.x;
   const int64_t V = a.vocab;
   if (a.greedy) {
     float v = kNegInf;
@@ -289,13 +286,31 @@ __global__ void __launch_bounds__(64) sample_select_kernel(SampleArgs a) {
                        : min<int64_t>(V, static_cast<int64_t>(hb + 1) * BLK) - 1;   // rounding: the block's last
 }
 
+// One launch: workgroup (g, row) writes its partials, takes a ticket of its row, and
+// the row's last workgroup (every other one's partials visible past the fences) selects
+// with its first wave and returns the ticket to 0 for the next launch. A single-row
+// call (the reference's one row per generated token) thus costs one launch.
+template <typename TI>
+__global__ void __launch_bounds__(64 * kWaves) sample_kernel(SampleArgs a) {
+  __shared__ int last;
+  const int64_t row = blockIdx.y;
+  sample_part<TI>(a, row, blockIdx.x);
+  __syncthreads();   // every wave's partials stored (workgroup scope)
+  if (threadIdx.x == 0) {
+    __threadfence();   // ... and visible device-wide before the ticket
+    last = atomicAdd(a.ticket + row, 1) == a.nwg - 1;
+  }
+  __syncthreads();
+  if (!last || threadIdx.x >= 64) return;
+  __threadfence();     // the other workgroups' partials, past this CU's caches
+  sample_select<TI>(a, row, threadIdx.x);
+  if (threadIdx.x == 0) a.ticket[row] = 0;
+}
+
 template <typename TI>
 hipError_t launch_sample(const SampleArgs& a, hipStream_t st) {
-  sample_part_kernel<TI><<<dim3(static_cast<unsigned>(a.nwg), static_cast<unsigned>(a.n_rows)), dim3(64 * kWaves), 0,
-                           st>>>(a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  sample_select_kernel<TI><<<dim3(static_cast<unsigned>(a.n_rows)), dim3(64), 0, st>>>(a);
+  sample_kernel<TI><<<dim3(static_cast<unsigned>(a.nwg), static_cast<unsigned>(a.n_rows)), dim3(64 * kWaves), 0, st>>>(
+      a);
   return hipGetLastError();
 }
 
@@ -304,9 +319,10 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t st) {
 
 using namespace pcp;
 
-extern "C" int pcp_sample_tokens(pcp_ctx* ctx, const void* logits, int dtype, int64_t n_rows, int64_t vocab,
-                                 int64_t row_stride, float temperature, const float* uniforms, int64_t* ids,
-                                 void* stream) {
+namespace {
+
+int sample_tokens(pcp_ctx* ctx, const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                  float temperature, const float* uniforms, int64_t* ids, void* stream, bool async) {
   if (dtype != PCP_F32 && dtype != PCP_BF16) return fail(ctx, PCP_ERR_DTYPE, "logits must be f32 or bf16");
   if (n_rows < 1 || n_rows > 65535 || vocab < 1 || vocab > PCP_SAMPLE_MAX_VOCAB || row_stride < vocab)
     return fail(ctx, PCP_ERR_INVALID_ARG, "need 1 <= n_rows <= 65535, 1 <= vocab <= %d, row_stride >= vocab",
@@ -332,12 +348,38 @@ extern "C" int pcp_sample_tokens(pcp_ctx* ctx, const void* logits, int dtype, in
   int rc = ensure_scratch(ctx, o_idx + sizeof(int64_t) * static_cast<size_t>(n_rows) * nwg);
   if (rc != PCP_OK) return rc;
   char* sp = static_cast<char*>(ctx->scratch);
+  // The per-row tickets: allocated and zeroed on the context's first sampler call, then
+  // left at zero by every launch.
+  if (!ctx->sample_ticket) {
+    if ((e = hipMalloc(&ctx->sample_ticket, sizeof(int) * (PCP_SAMPLE_MAX_ROWS + 1))) != hipSuccess) {
+      ctx->sample_ticket = nullptr;
+      (void)hipGetLastError();
+      return fail(ctx, PCP_ERR_OOM, "hipMalloc of the sampler's row tickets failed");
+    }
+    if ((e = hipMemsetAsync(ctx->sample_ticket, 0, sizeof(int) * (PCP_SAMPLE_MAX_ROWS + 1), st)) != hipSuccess)
+      return hip_fail(ctx, e, "zeroing the sampler's row tickets");
+  }
   SampleArgs a{logits, n_rows, vocab, row_stride, greedy ? 0.f : kLog2e / temperature, greedy ? 1 : 0, uniforms, ids,
-               reinterpret_cast<float2*>(sp), reinterpret_cast<int64_t*>(sp + o_idx), nb, nwg};
+               reinterpret_cast<float2*>(sp), reinterpret_cast<int64_t*>(sp + o_idx), ctx->sample_ticket, nb, nwg};
   const bool timed = prof_begin(ctx, st);
   e = dtype == PCP_F32 ? launch_sample<F32T>(a, st) : launch_sample<BF16T>(a, st);
   prof_end(ctx, st, timed);
   if (e != hipSuccess) return hip_fail(ctx, e, "sampler launch");
+  if (async) return add_pending(ctx, st);
   if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
   return PCP_OK;
+}
+
+}  // namespace
+
+extern "C" int pcp_sample_tokens(pcp_ctx* ctx, const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                                 int64_t row_stride, float temperature, const float* uniforms, int64_t* ids,
+                                 void* stream) {
+  return sample_tokens(ctx, logits, dtype, n_rows, vocab, row_stride, temperature, uniforms, ids, stream, false);
+}
+
+extern "C" int pcp_sample_tokens_async(pcp_ctx* ctx, const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                                       int64_t row_stride, float temperature, const float* uniforms, int64_t* ids,
+                                       void* stream) {
+  return sample_tokens(ctx, logits, dtype, n_rows, vocab, row_stride, temperature, uniforms, ids, stream, true);
 }

@@ -120,10 +120,13 @@ def _f32(*ts):
 
 
 def sample_tokens(logits: torch.Tensor, temperature: float, uniforms: torch.Tensor | None = None, *,
-                  ids: torch.Tensor | None = None, stream=None, ctx: Context | None = None) -> torch.Tensor:
+                  ids: torch.Tensor | None = None, stream=None, ctx: Context | None = None,
+                  sync: bool = True) -> torch.Tensor:
     """Sampler.sample (src/core/math.zig:21-58) on every row of logits [R, V] (f32 or
     bf16, HBM): greedy when temperature < 1e-6, else inverse-transform sampling with
-    the caller's uniform draws (f32 [R] in [0, 1)). Returns int64 [R] token ids."""
+    the caller's uniform draws (f32 [R] in [0, 1)). Returns int64 [R] token ids.
+    sync=False only enqueues the launch on the stream (pcp_sample_tokens_async): the ids
+    are ready in stream order, and ctx.sync() waits for them."""
     from ._lib import DType
     if logits.dim() != 2:
         raise PcpError(-1, "logits must be [rows, vocab]")
@@ -138,7 +141,7 @@ def sample_tokens(logits: torch.Tensor, temperature: float, uniforms: torch.Tens
         ids = torch.empty(R, dtype=torch.int64, device=logits.device)
     if uniforms is not None and (uniforms.dtype != torch.float32 or uniforms.numel() != R):
         raise PcpError(-1, "uniforms must be f32 with one value per row")
-    check(lib().pcp_sample_tokens(ctx.handle, logits.data_ptr(), int(code), R, V, logits.stride(0),
-                                  float(temperature), _ptr(uniforms), _ptr(ids), _stream_handle(stream)),
-          ctx.handle)
+    fn = lib().pcp_sample_tokens if sync else lib().pcp_sample_tokens_async
+    check(fn(ctx.handle, logits.data_ptr(), int(code), R, V, logits.stride(0), float(temperature), _ptr(uniforms),
+             _ptr(ids), _stream_handle(stream)), ctx.handle)
     return ids

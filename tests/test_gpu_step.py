@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from pcp_amd import step
+from pcp_amd import grpo, step
 from pcp_amd._lib import NesterovMode, PcpError
 
 pytestmark = pytest.mark.gpu
@@ -322,6 +322,39 @@ def test_sampler_few_rows_match_batch(dtype, T):
         thr = float(u[r]) * c[-1]
         g = five[r]
         assert c[g] >= thr - 1e-6 * c[-1] and (g == 0 or c[g - 1] <= thr + 1e-6 * c[-1]), (r, g)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T", [0.0, 0.7])
+def test_sampler_async_enqueues_behind_the_producer(dtype, T):
+    """pcp_sample_tokens_async: a decode loop's pattern. On one stream, each step writes
+    a row of logits (a torch kernel standing for the forward), then the sampler is only
+    enqueued behind it; no host wait until the end. The tokens equal the synchronous
+    entry point's on the same rows, one row per call (the reference's pattern) and 64
+    rows per call, over consecutive calls (each launch leaves its row tickets at zero)."""
+    rng = np.random.default_rng(27)
+    V, steps = 151936, 12
+    base = torch.from_numpy((rng.standard_normal((steps, V)) * 2.5).astype(np.float32)).to(DEV).to(dtype)
+    u = torch.from_numpy(rng.random(steps).astype(np.float32)).to(DEV)
+    ctx = grpo.Context(0)
+    st = torch.cuda.Stream()
+    row = torch.empty((1, V), dtype=dtype, device=DEV)
+    out = torch.empty((steps, 1), dtype=torch.int64, device=DEV)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        for i in range(steps):
+            row.copy_(base[i:i + 1])              # the producer, on the same stream
+            step.sample_tokens(row, T, u[i:i + 1] if T > 0 else None, ids=out[i], stream=st.cuda_stream, ctx=ctx,
+                               sync=False)
+    ctx.sync()
+    torch.cuda.synchronize()
+    want = torch.stack([step.sample_tokens(base[i:i + 1], T, u[i:i + 1] if T > 0 else None, ctx=ctx)
+                        for i in range(steps)])
+    assert torch.equal(out, want)
+    many = step.sample_tokens(base, T, u if T > 0 else None, ctx=ctx, sync=False)
+    ctx.sync()
+    assert torch.equal(many.view(-1, 1), want)
+    ctx.close()
 
 
 def test_sampler_bf16_and_strided_rows():
