@@ -88,6 +88,9 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 def _stream_handle(stream) -> int | None:
+    """A torch stream, a raw hipStream_t handle (int) or None (torch's current stream)."""
+    if isinstance(stream, int):
+        return stream or None
     s = stream if stream is not None else torch.cuda.current_stream()
     return s.cuda_stream or None
 
