@@ -279,6 +279,24 @@ __device__ __forceinline__ void block_merge2(float& m1, float& s1, float& m2, fl
 // ---------------------------------------------------------------------------
 // Kernel argument block (passed by value) and per-row metadata.
 // ---------------------------------------------------------------------------
+// Handing values from one workgroup to another in the same launch (the last of a
+// group of workgroups, chosen by an atomic ticket, reads what the others wrote). A
+// device-scope release fence writes back the whole L2 of the XCD (buffer_wbl2), which
+// cost microseconds per workgroup here. Instead each value is stored through to the
+// device-coherent level (an agent-scope atomic store), the storing wave waits for its
+// stores to complete before the ticket, and the reader, after the ticket, invalidates
+// its caches' copies once (an agent-scope acquire fence: buffer_inv, no write-back) and
+// loads as usual, so its loads go out together. (Agent-scope atomic loads would each
+// wait for the one before.)
+template <typename T>
+__device__ __forceinline__ void store_coherent(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// This wave's stores complete (at the level they were issued to) before what follows.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Before reading what other workgroups stored with store_coherent (after the ticket).
+__device__ __forceinline__ void acquire_coherent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
 struct RowArgs {
   const void* logits;
   const void* ref_logits;  // nullptr => no reference pass

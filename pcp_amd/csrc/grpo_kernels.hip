@@ -860,13 +860,13 @@ __global__ void __launch_bounds__(kSmallBlock) loss_reduce_kernel(LossReduceArgs
   const float tot = block_sum<kSmallBlock>(acc, lds);
   if (threadIdx.x == 0) {
     const float v = tot / a.seq_len[s];
-    a.seq_val[s] = a.reinforce ? v * a.adv[s] : v;
-    __threadfence();   // seq_val[s] visible before the ticket
+    store_coherent(a.seq_val + s, a.reinforce ? v * a.adv[s] : v);
+    wait_stores();     // seq_val[s] at the coherent level before the ticket
     last = atomicAdd(a.done, 1) == static_cast<int>(a.n_seq - 1);
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();     // every other workgroup's seq_val, past this CU's caches
+  acquire_coherent();
   const int lane = threadIdx.x & 63, w0 = threadIdx.x >> 6;
   constexpr int kPer = kFinalBlock / kSmallBlock;   // the final sum's waves per wave here
   float v[kPer];

@@ -53,6 +53,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const SampleArgs& a
   return row_rsrc(row_ptr<TI>(a, row), static_cast<uint32_t>(a.vocab * TI::kBytes) & ~3u);
 }
 
+// A partial handed to the row's last workgroup (see store_coherent): one 8-byte
+// coherent store.
+__device__ __forceinline__ void put_part(float2* p, float2 v) {
+  store_coherent(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v));
+}
+
 // Lane `lane`'s EPL elements of 64-lane block b of a row (-inf past `vocab`).
 template <typename TI>
 __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, const void* row, int64_t vocab, int64_t b,
@@ -135,8 +141,8 @@ __device__ __forceinline__ void sample_part(const SampleArgs& a, int64_t row, in
       float v = kNegInf;
       int64_t i = V;
       for (int w = 0; w < kWaves; ++w) better(v, i, wv_max[w], wv_idx[w]);
-      a.part[row * a.nwg + g] = make_float2(v, 0.f);
-      a.part_idx[row * a.nwg + g] = i;
+      put_part(a.part + row * a.nwg + g, make_float2(v, 0.f));
+      store_coherent(a.part_idx + row * a.nwg + g, i);
     }
     return;
   }
@@ -151,7 +157,7 @@ __device__ __forceinline__ void sample_part(const SampleArgs& a, int64_t row, in
 #pragma unroll
     for (int j = 0; j < EPL; ++j) s += hw_exp2((x[u][j] - ref) * a.k);
     s = wave_sum(s);
-    if (lane == 0 && b0 + u < a.nb) a.part[row * a.nb + b0 + u] = make_float2(m, s);
+    if (lane == 0 && b0 + u < a.nb) put_part(a.part + row * a.nb + b0 + u, make_float2(m, s));
   }
 }
 
@@ -164,7 +170,8 @@ __device__ __forceinline__ void sample_select(const SampleArgs& a, int64_t row, 
   if (a.greedy) {
     float v = kNegInf;
     int64_t i = V;
-    for (int g = lane; g < a.nwg; g += 64) better(v, i, a.part[row * a.nwg + g].x, a.part_idx[row * a.nwg + g]);
+    for (int g = lane; g < a.nwg; g += 64)
+      better(v, i, a.part[row * a.nwg + g].x, a.part_idx[row * a.nwg + g]);
     wave_better(v, i);
     if (lane == 0) a.ids[row] = (i == V) ? 0 : i;
     return;
@@ -286,23 +293,21 @@ __device__ __forceinline__ void sample_select(const SampleArgs& a, int64_t row, 
                        : min<int64_t>(V, static_cast<int64_t>(hb + 1) * BLK) - 1;   // rounding: the block's last
 }
 
-// One launch: workgroup (g, row) writes its partials, takes a ticket of its row, and
-// the row's last workgroup (every other one's partials visible past the fences) selects
-// with its first wave and returns the ticket to 0 for the next launch. A single-row
-// call (the reference's one row per generated token) thus costs one launch.
+// One launch: workgroup (g, row) writes its partials (coherent stores, complete before
+// its ticket), takes a ticket of its row, and the row's last workgroup selects with its
+// first wave (after an acquire fence) and returns the ticket to 0 for the next launch. A single-row call (the reference's one row per generated token) thus costs
+// one launch.
 template <typename TI>
 __global__ void __launch_bounds__(64 * kWaves) sample_kernel(SampleArgs a) {
   __shared__ int last;
   const int64_t row = blockIdx.y;
   sample_part<TI>(a, row, blockIdx.x);
-  __syncthreads();   // every wave's partials stored (workgroup scope)
-  if (threadIdx.x == 0) {
-    __threadfence();   // ... and visible device-wide before the ticket
-    last = atomicAdd(a.ticket + row, 1) == a.nwg - 1;
-  }
+  wait_stores();     // this wave's partials at the coherent level
+  __syncthreads();   // ... every wave's, before the ticket
+  if (threadIdx.x == 0) last = atomicAdd(a.ticket + row, 1) == a.nwg - 1;
   __syncthreads();
   if (!last || threadIdx.x >= 64) return;
-  __threadfence();     // the other workgroups' partials, past this CU's caches
+  acquire_coherent();
   sample_select<TI>(a, row, threadIdx.x);
   if (threadIdx.x == 0) a.ticket[row] = 0;
 }
