@@ -410,9 +410,24 @@ def bench_sample(args) -> None:
     ids = torch.empty(R, dtype=torch.int64, device=dev)
     from pcp_amd.grpo import default_context
     ctx = default_context(0)
-    sync = not args.async_sample
     stream = torch.cuda.current_stream().cuda_stream or None
-    call = lambda: step.sample_tokens(x, T, u, ids=ids, stream=stream, ctx=ctx, sync=sync)
+    if args.async_sample:
+        # The enqueue-only entry point called through the C ABI with its arguments marshalled
+        # once, as a compiled decode loop calls it (the Python wrapper's per-call checks
+        # cost more than the kernel at one row).
+        import ctypes
+
+        from pcp_amd._lib import DType, PcpError, lib
+        fn = lib().pcp_sample_tokens_async
+        cargs = (ctx.handle, x.data_ptr(), int(DType.f32), R, V, x.stride(0), ctypes.c_float(T), u.data_ptr(),
+                 ids.data_ptr(), stream)
+
+        def call():
+            rc = fn(*cargs)
+            if rc != 0:
+                raise PcpError(rc, lib().pcp_last_error(ctx.handle).decode())
+    else:
+        call = lambda: step.sample_tokens(x, T, u, ids=ids, stream=stream, ctx=ctx)
     for _ in range(args.warmup):
         call()
     ctx.sync()
@@ -427,8 +442,8 @@ def bench_sample(args) -> None:
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic (torch normal logits, uniform draws)",
         "config": {"workload": f"Sampler.sample at T={T} over {R} rows of {V} f32 logits"
-                               + (", enqueued only (pcp_sample_tokens_async; back-to-back calls on one stream, "
-                                  "the host waits once at the end)" if args.async_sample else
+                               + (", enqueued only (pcp_sample_tokens_async through the C ABI; back-to-back "
+                                  "calls on one stream, the host waits once at the end)" if args.async_sample else
                                   ", each call synchronous"), "rows": R, "vocab": V,
                    ("us_per_call_enqueued" if args.async_sample else "latency_us_per_call"): ms_step * 1e3},
         "roofline": {"bound": "hbm", "achieved": alg / (kernel_ms / 1e3) / 1e9, "peak": HBM_PEAK_GBS,

@@ -917,12 +917,10 @@ __device__ __forceinline__ u32x4 tile_col8(const uint16_t* t, int r, int c) {
 }
 
 // Vocab tiles of 64 per lm_dcache_kernel block: fewer blocks, so fewer of them idle
-// past the live token count, and each thread's loads of all of them in flight at once.
+// past the live token count.
 constexpr int kDcacheVocabTiles = 4;
 
-// dlogits from the forward's softmax cache, per block of 64 tokens x kDcacheVocabTiles
-// 64-wide vocab tiles (each thread's loads of the whole block issued before its math,
-// one round trip; the tiles' transposes staged in LDS together, one barrier): D is
+// dlogits from the forward's softmax cache, per 64 x 64 tile (tokens x vocab): D is
 // written in place over the cache (f16 terms -> bf16, token-major, the dhidden
 // product's operand) and transposed through LDS into Dt [ldv, ldt] (vocab-major,
 // the dW product's operand; tokens past n are 0). D[n][v] = -c_n * e * 2^(ref -
@@ -937,97 +935,77 @@ constexpr int kDcacheVocabTiles = 4;
 // beside them, not in place.
 template <bool F32>
 __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
-  constexpr int NV = kDcacheVocabTiles;
-  __shared__ uint16_t t[NV][64 * kTilePitch];    // [vocab tile][token][vocab] bf16
+  __shared__ uint16_t t[64 * kTilePitch];    // [token][vocab] bf16
   const int tid = threadIdx.x;
   const int64_t n = *a.count;
   const int64_t ntile = (n + 63) / 64;     // token tiles that the dW product reads
-  const int cc = (tid & 7) * 8;
-  for (int64_t tb = blockIdx.x; tb < ntile; tb += gridDim.x) {
+  for (int64_t tb = blockIdx.x; tb < ntile; tb += gridDim.x)
+  for (int vs = 0; vs < kDcacheVocabTiles; ++vs) {
+    const int64_t v0 = (static_cast<int64_t>(blockIdx.y) * kDcacheVocabTiles + vs) * 64;
+    if (v0 >= a.ld) break;
     const int64_t r0 = tb * 64;
-    const int64_t vb = static_cast<int64_t>(blockIdx.y) * NV * 64;   // the block's first vocab entry
-    // Every load of the block first (its NV vocab tiles of both rows: one round trip),
-    // then the math, the D stores and the LDS tiles, one barrier, the D^T stores.
-    float cf[2], l2[2], tg[2];
+    const int cc = (tid & 7) * 8;
+    const int64_t c0 = v0 + cc;
+    // Both rows' loads first (one round trip): the f16 terms and the row's scalars.
+    u32x4 w[2], w2[2];
+    float cf[2], l2[2], m2[2], tg[2];
     int id[2];
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
       const int64_t row = r0 + (tid >> 3) + 32 * it;
-      cf[it] = l2[it] = tg[it] = 0.f;
+      w[it] = w2[it] = u32x4{0u, 0u, 0u, 0u};
+      cf[it] = 0.f;
+      l2[it] = m2[it] = tg[it] = 0.f;
       id[it] = -1;
       if (row < n) {
         cf[it] = a.coef[row];
         l2[it] = a.lse2[row];
         id[it] = a.ids[row];
         tg[it] = a.tgt[row];
-      }
-    }
-    u32x4 w[NV][2], w2[NV][2];
-    float m2[NV][2];
-#pragma unroll
-    for (int vs = 0; vs < NV; ++vs)
-#pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int64_t row = r0 + (tid >> 3) + 32 * it;
-        const int64_t c0 = vb + 64 * vs + cc;
-        w[vs][it] = w2[vs][it] = u32x4{0u, 0u, 0u, 0u};
-        m2[vs][it] = 0.f;
-        if (row < n && c0 < a.V) {
+        if (c0 < a.V) {
           if constexpr (F32) {
             const u32x4* src = reinterpret_cast<const u32x4*>(a.src32 + row * a.ld + c0);
-            w[vs][it] = __builtin_nontemporal_load(src);
-            w2[vs][it] = __builtin_nontemporal_load(src + 1);
+            w[it] = __builtin_nontemporal_load(src);
+            w2[it] = __builtin_nontemporal_load(src + 1);
           } else {
-            w[vs][it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.d + row * a.ld + c0));
+            w[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.d + row * a.ld + c0));
           }
-          m2[vs][it] = a.part[row * a.ldp + c0 / kLmPart].x;
+          m2[it] = a.part[row * a.ldp + c0 / kLmPart].x;
         }
-      }
-#pragma unroll
-    for (int vs = 0; vs < NV; ++vs) {
-      if (vb + 64 * vs >= a.ld) break;
-#pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int rr = (tid >> 3) + 32 * it;
-        const int64_t row = r0 + rr;
-        const int64_t c0 = vb + 64 * vs + cc;
-        u32x4 out = {0u, 0u, 0u, 0u};
-        if (row < n && cf[it] != 0.f && c0 < a.V) {
-          const float f = -cf[it] * hw_exp2(ms_ref(m2[vs][it]) - l2[it]);
-          const uint32_t ww[4] = {w[vs][it][0], w[vs][it][1], w[vs][it][2], w[vs][it][3]};
-          const int64_t rel = static_cast<int64_t>(id[it]) - c0;
-          float d[8];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const float e = F32 ? __uint_as_float(k < 4 ? w[vs][it][k] : w2[vs][it][k - 4]) : F16T::unpack(ww, k);
-            d[k] = c0 + k < a.V ? f * e : 0.f;
-          }
-          if (rel >= 0 && rel < 8) {
-            const float pt = hw_exp2(fmaf(tg[it], kLog2e, -l2[it]));
-#pragma unroll
-            for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf[it] * pt + cf[it] : d[k];
-          }
-          out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
-                      pack2<BF16T>(d[6], d[7])};
-        }
-        if (row < n) __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(a.d + row * a.ld + c0));
-        tile_put8(t[vs], rr, cc, out);
       }
     }
-    __syncthreads();
-    // Dt row v + c, tokens r0 + 8g .. +7: eight lanes write one row's 128 bytes.
-    if (a.dt) {
 #pragma unroll
-      for (int vs = 0; vs < NV; ++vs) {
-        const int64_t v0 = vb + 64 * vs;
-        if (v0 >= a.ld) break;
+    for (int it = 0; it < 2; ++it) {
+      const int rr = (tid >> 3) + 32 * it;
+      const int64_t row = r0 + rr;
+      u32x4 out = {0u, 0u, 0u, 0u};
+      if (row < n && cf[it] != 0.f && c0 < a.V) {
+        const float f = -cf[it] * hw_exp2(ms_ref(m2[it]) - l2[it]);
+        const uint32_t ww[4] = {w[it][0], w[it][1], w[it][2], w[it][3]};
+        const int64_t rel = static_cast<int64_t>(id[it]) - c0;
+        float d[8];
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-          const int c = (tid >> 3) + 32 * it, g = tid & 7;
-          __builtin_nontemporal_store(tile_col8(t[vs], 8 * g, c),
-                                      reinterpret_cast<u32x4*>(a.dt + (v0 + c) * a.ldt + r0 + 8 * g));
+        for (int k = 0; k < 8; ++k) {
+          const float e = F32 ? __uint_as_float(k < 4 ? w[it][k] : w2[it][k - 4]) : F16T::unpack(ww, k);
+          d[k] = c0 + k < a.V ? f * e : 0.f;
         }
+        if (rel >= 0 && rel < 8) {
+          const float pt = hw_exp2(fmaf(tg[it], kLog2e, -l2[it]));
+#pragma unroll
+          for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf[it] * pt + cf[it] : d[k];
+        }
+        out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
+                    pack2<BF16T>(d[6], d[7])};
       }
+      if (row < n) __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(a.d + row * a.ld + c0));
+      tile_put8(t, rr, cc, out);
+    }
+    __syncthreads();
+    // Dt row v0 + c, tokens r0 + 8g .. +7: eight lanes write one row's 128 bytes.
+#pragma unroll
+    for (int it = 0; it < 2 && a.dt; ++it) {
+      const int c = (tid >> 3) + 32 * it, g = tid & 7;
+      __builtin_nontemporal_store(tile_col8(t, 8 * g, c), reinterpret_cast<u32x4*>(a.dt + (v0 + c) * a.ldt + r0 + 8 * g));
     }
     __syncthreads();
   }
@@ -1178,49 +1156,33 @@ __global__ void __launch_bounds__(256) lm_transpose_kernel(LmTransposeArgs a) {
 // (the MFMA B fragment of destination rows FM b + [0, FM) and k FK s + [0, FK) at
 // fragment b ld_dst/FK + s, lane l holding row FM b + l % FM and k FK s + 8 (l / FM) +
 // 0..7; FM x FK = 16 x 32): destination rows are source columns, k runs over source
-// rows. A block takes kFragTiles 64 x 64 tiles down the source rows, every load of
-// them issued before the first store (one round trip), and writes each tile as eight
-// whole fragments, 1 KB runs; k from R up to R rounded to 64 is zero, and k past that
-// is not written.
-constexpr int kFragTiles = 4;
-
+// rows. Each block's 64 x 64 tile is eight whole fragments, written as 1 KB runs; k from
+// R up to R rounded to 64 is zero, and k past that is not written.
 __global__ void __launch_bounds__(256) lm_transpose_frag_kernel(LmTransposeArgs a) {
-  __shared__ uint16_t t[kFragTiles][64 * kTilePitch];
+  __shared__ uint16_t t[64 * kTilePitch];
   const int R = a.rcount ? min(a.R, *a.rcount) : a.R;
   const int64_t rend = min(a.ld_dst, (static_cast<int64_t>(R) + 63) / 64 * 64);
-  const int c0 = blockIdx.x * 64;
-  const int64_t rb = static_cast<int64_t>(blockIdx.y) * 64 * kFragTiles;
-  if (rb >= rend) return;
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  if (r0 >= rend) return;
   const int tid = threadIdx.x;
-  u32x4 v[kFragTiles][2];
 #pragma unroll
-  for (int j = 0; j < kFragTiles; ++j)
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int64_t r = rb + 64 * j + it * 32 + (tid >> 3);
-      const int cc = (tid & 7) * 8;
-      v[j][it] = u32x4{0u, 0u, 0u, 0u};
-      if (r < R && c0 + cc < a.C) v[j][it] = *reinterpret_cast<const u32x4*>(a.src + r * a.ld_src + c0 + cc);
-    }
-#pragma unroll
-  for (int j = 0; j < kFragTiles; ++j)
-#pragma unroll
-    for (int it = 0; it < 2; ++it) tile_put8(t[j], it * 32 + (tid >> 3), (tid & 7) * 8, v[j][it]);
+  for (int it = 0; it < 2; ++it) {
+    const int rr = it * 32 + (tid >> 3), cc = (tid & 7) * 8;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r0 + rr < R && c0 + cc < a.C)
+      v = *reinterpret_cast<const u32x4*>(a.src + static_cast<int64_t>(r0 + rr) * a.ld_src + c0 + cc);
+    tile_put8(t, rr, cc, v);
+  }
   __syncthreads();
   u32x4* dst = reinterpret_cast<u32x4*>(a.dst);
   constexpr int FM = 16, FK = 32;   // the 16x16x32 MFMA B fragment
 #pragma unroll
-  for (int j = 0; j < kFragTiles; ++j) {
-    const int64_t r0 = rb + 64 * j;
-    if (r0 >= rend) break;
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int idx = tid + 256 * it, f = idx >> 6, l = idx & 63;   // fragment f of the 8, lane l
-      const int bl = f / (64 / FK), sl = f % (64 / FK);
-      const int c = FM * bl + l % FM, r = FK * sl + 8 * (l / FM);
-      if (c0 + c < a.C && r0 + r < rend)
-        dst[(static_cast<int64_t>(c0 / FM + bl) * (a.ld_dst / FK) + r0 / FK + sl) * 64 + l] = tile_col8(t[j], r, c);
-    }
+  for (int it = 0; it < 2; ++it) {
+    const int idx = tid + 256 * it, f = idx >> 6, l = idx & 63;   // fragment f of the 8, lane l
+    const int bl = f / (64 / FK), sl = f % (64 / FK);
+    const int c = FM * bl + l % FM, r = FK * sl + 8 * (l / FM);
+    if (c0 + c < a.C && r0 + r < rend)
+      dst[(static_cast<int64_t>(c0 / FM + bl) * (a.ld_dst / FK) + r0 / FK + sl) * 64 + l] = tile_col8(t, r, c);
   }
 }
 
@@ -1289,8 +1251,7 @@ hipError_t launch_lm_transpose(const LmTransposeArgs& a, hipStream_t st) {
 
 hipError_t launch_lm_transpose_frag(const LmTransposeArgs& a, hipStream_t st) {
   if (a.C <= 0 || a.ld_dst <= 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((a.C + 63) / 64),
-                  static_cast<unsigned>((a.ld_dst + 64 * kFragTiles - 1) / (64 * kFragTiles)));
+  const dim3 grid(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>((a.ld_dst + 63) / 64));
   lm_transpose_frag_kernel<<<grid, dim3(256), 0, st>>>(a);
   return hipGetLastError();
 }
