@@ -140,6 +140,11 @@ __device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off
 }
 
 template <bool NT>
+__device__ __forceinline__ u32x2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, NT ? kBufNT : 0));
+}
+
+template <bool NT>
 __device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, u32x4 v, uint32_t off) {
   typedef int i32x4 __attribute__((ext_vector_type(4)));
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, off, 0, NT ? kBufNT : 0);

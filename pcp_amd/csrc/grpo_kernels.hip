@@ -119,8 +119,20 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   // scaled into dlogits, one exponential per element fewer. Other pairs recompute.
   constexpr bool kBf16Pair = __is_same(TI, BF16T) && __is_same(TO, BF16T);
   constexpr bool kCache = kBf16Pair && CACHE;
+  // 16-bit logits with f32 dlogits: a lane's chunk is two 8-byte halves 512 bytes apart
+  // in its wave's 1 KB of the chunk (elements 4 l + 0..3 and 256 + 4 l + 0..3 of the
+  // wave's 512), so each half's f32 output is one 16-byte store and each store
+  // instruction writes 1 KB contiguously (16-byte halves of 32-byte outputs, stride 32,
+  // leave every instruction writing half lines). Rows of this pair are never EDGE rows.
+  constexpr bool kSplit = TI::kBytes == 2 && TO::kBytes == 4;
+  static_assert(!(kSplit && EDGE), "16-bit -> f32 rows are not EDGE rows");
+
   constexpr int kPrefetch = PCP_RES_PREFETCH;   // reference batches in flight ahead of the math
   const int tid = threadIdx.x;
+  // kSplit: half h of chunk k of this lane is 4-element group
+  //   k * 2 * BLOCK + 128 * wave + 64 * h + lane,
+  // valid when below 2 * nv; its input at 8 bytes, its output at 16 bytes per group.
+  const uint32_t sgrp = kSplit ? static_cast<uint32_t>(128 * (tid >> 6) + (tid & 63)) : 0u;
   const RowMeta r = row_meta(a, row);
   const int64_t row_elem = row * a.vocab;
   const void* xrow = static_cast<const char*>(a.logits) + row_elem * TI::kBytes;
@@ -138,8 +150,16 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
       float z[EPV];
 #pragma unroll
       for (int j = 0; j < EPV; ++j) z[j] = 0.f;
+      if constexpr (kSplit) {
+        const float (&z4)[4] = reinterpret_cast<const float (&)[4]>(z);
 #pragma unroll
-      for (int k = 0; k < NCH; ++k) buf_store_vals<TO, EPV, true>(drow, (k * BLOCK + tid) * kOutVec, z);
+        for (int k = 0; k < NCH; ++k)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) buf_store_vals<TO, 4, true>(drow, (k * 2 * BLOCK + 64 * h + sgrp) * 16u, z4);
+      } else {
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) buf_store_vals<TO, EPV, true>(drow, (k * BLOCK + tid) * kOutVec, z);
+      }
       if (EDGE && ek >= 0) store1<TO>(a.dlogits, row_elem + ek, 0.f);
     }
     return;
@@ -158,8 +178,21 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xsp.vec, in_bytes);
   const uint32_t voff = tid * 16u;
   u32x4 xv[NCH];
+  if constexpr (kSplit) {
 #pragma unroll
-  for (int k = 0; k < NCH; ++k) xv[k] = buf_ld16<true>(xbuf, fresh_off(voff, k * kChunkBytes));
+    for (int k = 0; k < NCH; ++k) {
+      const u32x2 lo = buf_ld8<true>(xbuf, fresh_off(sgrp * 8u, k * kChunkBytes));
+      const u32x2 hi = buf_ld8<true>(xbuf, fresh_off(sgrp * 8u, k * kChunkBytes + 512u));
+      xv[k] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) xv[k] = buf_ld16<true>(xbuf, fresh_off(voff, k * kChunkBytes));
+  }
+  // kSplit: half h of chunk k of this lane holds row values (past the row end it read 0).
+  auto half_ok = [&](int k, int h) {
+    return static_cast<int64_t>(k) * 2 * BLOCK + 64 * h + sgrp < 2 * static_cast<int64_t>(nv);
+  };
   const float xe = (EDGE && ek >= 0) ? TI::load1(xrow, ek) : kNegInf;
 
   // 2. Per-lane (max, sum) of the resident policy values and online (max, sum) of
@@ -188,7 +221,23 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
     float mx = kNegInf;
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
-      if (k * BLOCK + tid < nv) {
+      if constexpr (kSplit) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (!half_ok(k, h)) continue;
+          if constexpr (__is_same(TI, BF16T)) {
+            // bf16 halves by byte permutes, as for the bf16 pair below.
+#pragma unroll
+            for (int q = 2 * h; q < 2 * h + 2; ++q)
+              mx = fmaxf(fmaxf(mx, __uint_as_float(__builtin_amdgcn_perm(w[q], 0u, 0x05040c0cu))),
+                         __uint_as_float(__builtin_amdgcn_perm(w[q], 0u, 0x07060c0cu)));
+          } else {
+#pragma unroll
+            for (int j = 4 * h; j < 4 * h + 4; ++j) mx = fmaxf(mx, TI::unpack(w, j));
+          }
+        }
+      } else if (k * BLOCK + tid < nv) {
         const uint32_t* w = reinterpret_cast<const uint32_t*>(&xv[k]);
         if constexpr (kBf16Pair) {
           // bf16 halves by byte permutes: the same values as unpack(), but not
@@ -224,7 +273,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
 #pragma unroll
     for (int q = 0; q < RB; ++q) {
       const int k = kb + q;
-      if (k >= NCH || k * BLOCK + tid >= nv) continue;
+      if (k >= NCH || (!kSplit && k * BLOCK + tid >= nv)) continue;
       uint32_t* w = reinterpret_cast<uint32_t*>(&xv[k]);
       if constexpr (kCache) {
 #pragma unroll
@@ -237,6 +286,13 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
           // Pin the pack here: left to itself the compiler sinks the packs into the
           // dlogits loop and keeps 152 f32 terms live across the merge.
           asm volatile("" ::"v"(w[h]));
+        }
+      } else if constexpr (kSplit) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (!half_ok(k, h)) continue;
+#pragma unroll
+          for (int j = 4 * h; j < 4 * h + 4; ++j) ps += hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -m2));
         }
       } else {
 #pragma unroll
@@ -305,7 +361,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
         o[2 * q] = f * static_cast<float>(h[0]);
         o[2 * q + 1] = f * static_cast<float>(h[1]);
       }
-    } else if constexpr (kBf16Pair) {
+    } else if constexpr (kBf16Pair || kSplit) {
       // The words pass through an opaque copy: otherwise the compiler reuses the sum
       // pass's unpacked values here and keeps all of them live across the merge.
       uint32_t u[4];
@@ -320,10 +376,23 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
 #pragma unroll
       for (int j = 0; j < EPV; ++j) o[j] = nc * hw_exp2(fmaf(TI::unpack(w, j), kLog2e, -lse2));
     }
-    buf_store_vals<TO, EPV, true>(drow, fresh_off(tid * kOutVec, k * BLOCK * kOutVec), o);
+    if constexpr (kSplit) {
+      // Groups past the row end sit past the descriptor: their stores are dropped.
+      const float (&o0)[4] = reinterpret_cast<const float (&)[4]>(o[0]);
+      const float (&o1)[4] = reinterpret_cast<const float (&)[4]>(o[4]);
+      buf_store_vals<TO, 4, true>(drow, fresh_off(sgrp * 16u, k * 2 * BLOCK * 16u), o0);
+      buf_store_vals<TO, 4, true>(drow, fresh_off(sgrp * 16u, k * 2 * BLOCK * 16u + 1024u), o1);
+    } else {
+      buf_store_vals<TO, EPV, true>(drow, fresh_off(tid * kOutVec, k * BLOCK * kOutVec), o);
+    }
   }
   const int64_t it = r.id - xsp.head;   // the target's index in the interior
-  if (it >= 0 && it < static_cast<int64_t>(nv) * EPV && tid == static_cast<int>((it / EPV) % BLOCK)) {
+  // The lane that stored the target's group (kSplit: group it / 4 at lane
+  // 64 (r / 128) + r % 64, r = (it / 4) % (2 BLOCK); else vector it / EPV at lane
+  // (it / EPV) % BLOCK).
+  const int t_lane = kSplit ? static_cast<int>(64 * (((it >> 2) % (2 * BLOCK)) >> 7) + ((it >> 2) & 63))
+                            : static_cast<int>((it / EPV) % BLOCK);
+  if (it >= 0 && it < static_cast<int64_t>(nv) * EPV && tid == t_lane) {
     const float dy = c - c * hw_exp2(fmaf(xy, kLog2e, -lse2));
     buf_store1<TO, true>(drow, static_cast<uint32_t>(it) * TO::kBytes, dy);
   }
@@ -343,10 +412,6 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
 // together. The index is double-buffered: thread 0 writes slot i & 1 at the top of
 // step i, while slot (i - 1) & 1 may still be read; the barrier at the end of step i
 // orders the reads of slot i & 1 before its next write, in step i + 2.
-// bf16 logits with f32 dlogits keep one row per workgroup: in the loop that pair
-// runs past 128 VGPRs (86 spilled at 19 chunks).
-template <typename TI, typename TO>
-constexpr bool kPersistentRows = !(__is_same(TI, BF16T) && __is_same(TO, F32T));
 
 // LIST: the instance for launches without zero-fill, which visit the live rows listed
 // by live_rows_kernel (a separate instance, so the zero-fill loop is compiled as before).
@@ -354,10 +419,6 @@ template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE, bool 
 __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
   __shared__ float lds[4 * (BLOCK / 64)];
   __shared__ int s_next[2];
-  if constexpr (!kPersistentRows<TI, TO>) {
-    resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>(a, blockIdx.x, lds);
-    return;
-  }
   if constexpr (LIST) {
     // Without zero-fill: live_rows_kernel listed the live rows and counted them earlier
     // on the stream. When fewer than half the rows are live the launch visits the listed
@@ -921,21 +982,15 @@ hipError_t launch_resident(const RowArgs& a, int64_t nrows, hipStream_t st) {
     slots = cus * (occ > 0 ? occ : 1);
     cached.store(slots, std::memory_order_relaxed);
   }
-  const int64_t grid = kPersistentRows<TI, TO> ? (nrows < slots ? nrows : slots) : nrows;
+  const int64_t grid = nrows < slots ? nrows : slots;
   if (grid <= 0) return hipSuccess;
   const dim3 g(static_cast<unsigned>(grid)), b(BLOCK);
-  if constexpr (kPersistentRows<TI, TO>) {
-    if (!a.counters_zeroed) reset_counter_kernel<<<1, 1, 0, st>>>(a.next_row, a.row_list ? a.row_count : nullptr);
-    if (a.row_list) {
-      live_rows_kernel<<<dim3(static_cast<unsigned>((nrows + 255) / 256)), dim3(256), 0, st>>>(a);
-      grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE, CACHE, true><<<g, b, 0, st>>>(a);
-    } else {
-      grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE, CACHE, false><<<g, b, 0, st>>>(a);
-    }
+  if (!a.counters_zeroed) reset_counter_kernel<<<1, 1, 0, st>>>(a.next_row, a.row_list ? a.row_count : nullptr);
+  if (a.row_list) {
+    live_rows_kernel<<<dim3(static_cast<unsigned>((nrows + 255) / 256)), dim3(256), 0, st>>>(a);
+    grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE, CACHE, true><<<g, b, 0, st>>>(a);
   } else {
-    RowArgs one = a;   // one workgroup per row: dead rows return at once
-    one.row_list = nullptr;
-    grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE, CACHE, false><<<g, b, 0, st>>>(one);
+    grpo_resident_kernel<TI, TO, BLOCK, NCH, RB, EDGE, CACHE, false><<<g, b, 0, st>>>(a);
   }
   return hipGetLastError();
 }
@@ -1042,11 +1097,7 @@ RowPlan plan_rows(int in_bytes, int out_bytes, int64_t vocab, bool aligned16, bo
   // Rows off 16 bytes stay resident when dlogits rows share the logits rows' element
   // type and offset (the head and tail then line up); otherwise they stream.
   if (!vec && !edge_ok) return p;
-  // 16-bit logits with f32 dlogits stream: at configuration 2 (bf16 -> f32, clip-KL)
-  // the streaming kernel took 8.81 ms against 9.74 ms resident, whose 32-byte output
-  // per lane and chunk goes out as two 16-byte stores 32 bytes apart (28.5 GB written
-  // against 19.9 GB of dlogits).
-  if (in_bytes == 2 && out_bytes == 4) return p;
+
   const int64_t nv = vocab / epv;   // the interior of a row off 16 bytes has at most as many
   for (int i = 0; i < static_cast<int>(sizeof(kResCfgs) / sizeof(kResCfgs[0])); ++i) {
     if (static_cast<int64_t>(kResCfgs[i].block) * kResCfgs[i].nch >= nv) {

@@ -610,7 +610,7 @@ BF16_CACHED_BAR = (BF16_CACHED_REL, 1 + 2.0 ** -6)
 BF16_EXACT_BAR = (BF16_EXACT_REL, 1 + 2.0 ** -7)
 
 
-def _all_live_rows_check(cfg, inp, out, mode, exact, label, chunk=4096):
+def _all_live_rows_check(cfg, inp, out, mode, exact, label, chunk=4096, f32_out=False):
     """Every live row of a full-size configuration against the oracle, in chunks of
     `chunk` rows: log-prob, reference log-prob and token loss of each against the f32
     bar, every dlogits element against the bf16 bar (oracle.check_dlogits compares the
@@ -632,7 +632,7 @@ def _all_live_rows_check(cfg, inp, out, mode, exact, label, chunk=4096):
     lr_all = out.ref_logp.view(-1).cpu().numpy() if out.ref_logp is not None else None
     tl_all = out.token_loss.view(-1).cpu().numpy()
     m = orc.CLIP_KL if mode == LossMode.GRPO_CLIP_KL else orc.REINFORCE
-    rel, kf = BF16_EXACT_BAR if exact else BF16_CACHED_BAR
+    rel, kf = (1e-5, 1.0) if f32_out else (BF16_EXACT_BAR if exact else BF16_CACHED_BAR)
     live = np.nonzero((w_all != 0) & (ids_all >= 0) & (ids_all < V))[0]
     st = dict(lp=0.0, lr=0.0, tl=0.0, usage=0.0, abs=0.0, rel=0.0)
     tl_exact = np.zeros(S * T)
@@ -666,8 +666,10 @@ def _all_live_rows_check(cfg, inp, out, mode, exact, label, chunk=4096):
         fl = coef_floor(want.coef, want.lp, want.lr, w, adv[seq].astype(np.float64), Ls[seq].astype(np.float64),
                         float(S), old_all[rows].astype(np.float64), m == orc.REINFORCE, cfg.kl_beta, cfg.clip_eps,
                         sc)
-        res = orc.check_dlogits(L, ids, want.coef, fl, D, orc.BF16, rel, kf, dtype=orc.BF16)
+        res = orc.check_dlogits(L, ids, want.coef, fl, D, orc.F32 if f32_out else orc.BF16, rel, kf, dtype=orc.BF16)
         assert int(res.n_bad.sum()) == 0, (label, int(res.n_bad.sum()), float(res.max_usage.max()))
+        if f32_out:
+            assert float(res.max_abs.max()) <= 1e-4, (label, float(res.max_abs.max()))
         st["lp"] = max(st["lp"], float(e_lp.max()))
         st["tl"] = max(st["tl"], float(e_tl.max()))
         st["usage"] = max(st["usage"], float(res.max_usage.max()))
@@ -697,23 +699,26 @@ def _all_live_rows_check(cfg, inp, out, mode, exact, label, chunk=4096):
     st["loss_rel_terms"] = abs(got_loss - loss_exact) / (terms.sum() / S)
     print(f"PARITY-TABLE {label}: live rows {len(live)} of {S * T}; |dlogp|/max(1,|lse|) {st['lp']:.2e}"
           f" (bar 1e-5); ref {st['lr']:.2e}; token loss {st['tl']:.2e}; loss rel {st['loss_rel']:.2e}, per sum of"
-          f" |terms| {st['loss_rel_terms']:.2e} ({st['loss_use']:.3f} of its bar); bf16 dlogits max abs {st['abs']:.2e}, max rel (p >= 2^-14)"
-          f" {st['rel']:.3e} (2^-8 = 3.906e-03), bar used {st['usage']:.3f}", flush=True)
+          f" |terms| {st['loss_rel_terms']:.2e} ({st['loss_use']:.3f} of its bar); {'f32' if f32_out else 'bf16'}"
+          f" dlogits max abs {st['abs']:.2e}{' (bar 1e-4)' if f32_out else ''}, max rel (p >= 2^-14) {st['rel']:.3e}"
+          f"{'' if f32_out else ' (2^-8 = 3.906e-03)'}, bar used {st['usage']:.3f}", flush=True)
     return st
 
 
-def _full_config(key, mode, exact=False, n_seq=None):
+def _full_config(key, mode, exact=False, n_seq=None, f32_out=False):
     cfg = synth.CONFIGS[key]
     inp = synth.make_device_inputs(cfg, DEV, n_seq=n_seq)
     S = inp["logits"].shape[0]
-    label = f"config{key} {'clip_kl' if mode == LossMode.GRPO_CLIP_KL else 'reinforce'}" + (" exact" if exact else "")
+    label = (f"config{key} {'clip_kl' if mode == LossMode.GRPO_CLIP_KL else 'reinforce'}" + (" exact" if exact else "")
+             + (f" f32 dlogits, {S} sequences" if f32_out else ""))
     print(f"full-size {label}", flush=True)
     out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], rewards=inp["rewards"], group_size=cfg.group,
                                  ref_logits=inp["ref_logits"], old_logp=inp["old_logp"], loss_mode=mode,
-                                 clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, exact_bf16=exact)
+                                 clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, exact_bf16=exact,
+                                 dlogits_dtype=torch.float32 if f32_out else None)
     torch.cuda.synchronize()
     T = cfg.T
-    _all_live_rows_check(cfg, inp, out, mode, exact, label)
+    _all_live_rows_check(cfg, inp, out, mode, exact, label, f32_out=f32_out)
     # every masked row of dlogits is exactly zero
     lengths = inp["lengths"]
     for s in range(S):
@@ -740,6 +745,13 @@ def _full_config(key, mode, exact=False, n_seq=None):
 @pytest.mark.parametrize("mode", [LossMode.GRPO_CLIP_KL, LossMode.REINFORCE])
 def test_config2_full_size(mode, exact):
     _full_config(2, mode, exact)
+
+
+def test_config2_rows_f32_dlogits():
+    """bf16 logits with f32 dlogits (the resident kernel's split-half instance) at
+    configuration 2's row shape, 8 of its sequences, every live row against the oracle
+    under the f32 bar (max-abs 1e-4)."""
+    _full_config(2, LossMode.GRPO_CLIP_KL, n_seq=8, f32_out=True)
 
 
 @pytest.mark.parametrize("exact", [False, True])

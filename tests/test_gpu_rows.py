@@ -100,6 +100,8 @@ ZF_CASES = [
     ("resident-f32", "f32", 3000, "f32", False, False, 0.7),
     ("resident-f32-sparse", "f32", 3000, "f32", False, True, 0.25),
     ("resident-bf16-to-f32", "bf16", 4096, "f32", False, True, 0.7),
+    ("resident-bf16-to-f32-qwen", "bf16", 151936, "f32", False, False, 0.7),
+    ("resident-bf16-to-f32-qwen-sparse", "bf16", 151936, "f32", False, True, 0.25),
     ("stream-vec", "bf16", 4096, "bf16", True, True, 0.7),
     ("stream-scalar", "bf16", 5003, "f32", False, False, 0.7),
 ]
