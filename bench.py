@@ -952,8 +952,7 @@ def main() -> None:
         "rows_per_s": ab["rows"] / (ms_step / 1e3),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": ("grpo_stream_kernel" if args.force_streaming or args.dlogits_f32
-                                else "grpo_resident_kernel"),
+                     "kernel": ("grpo_stream_kernel" if args.force_streaming else "grpo_resident_kernel"),
                      "kernel_ms": kernel_ms, "algorithmic_bytes": ab["bytes"]},
         "setup_s": t_setup,
     }

@@ -300,8 +300,7 @@ int run(pcp_ctx* ctx, const pcp_grpo_args* a, Op op, bool noalloc = false) {
   const bool edge_ok = !ra.dlogits || (a->dlogits_dtype == a->logits_dtype &&
                                        ((reinterpret_cast<uintptr_t>(a->logits) ^
                                          reinterpret_cast<uintptr_t>(ra.dlogits)) & 15u) == 0);
-  RowPlan plan = plan_rows(in_bytes, ra.dlogits ? dtype_bytes(a->dlogits_dtype) : in_bytes, g.vocab, al, edge_ok,
-                           ra.dlogits == nullptr,
+  RowPlan plan = plan_rows(in_bytes, g.vocab, al, edge_ok, ra.dlogits == nullptr,
                            (a->flags & PCP_FLAG_FORCE_STREAMING) != 0);
   plan.exact = (a->flags & PCP_FLAG_EXACT_BF16) ? 1 : 0;
   const int out_dt = ra.dlogits ? a->dlogits_dtype : a->logits_dtype;

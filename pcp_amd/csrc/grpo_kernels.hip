@@ -1074,8 +1074,7 @@ hipError_t dispatch_rows(const RowPlan& p, const RowArgs& a, int64_t nrows, hipS
 
 }  // namespace
 
-RowPlan plan_rows(int in_bytes, int out_bytes, int64_t vocab, bool aligned16, bool edge_ok, bool forward_only,
-                  bool force_stream) {
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool edge_ok, bool forward_only, bool force_stream) {
   RowPlan p;
   const int epv = 16 / in_bytes;
   const bool vec = aligned16 && (vocab % epv == 0);

@@ -19,11 +19,10 @@ struct RowPlan {
   int exact;  // bf16 -> bf16 resident rows without the f16 softmax cache (PCP_FLAG_EXACT_BF16)
 };
 
-// in_bytes / out_bytes: logits and dlogits element sizes; aligned16: every row base is
-// 16-byte aligned; edge_ok: dlogits (if any) have the logits' element type and the same
-// address mod 16, so rows off 16 bytes split alike; forward_only: no dlogits are written.
-RowPlan plan_rows(int in_bytes, int out_bytes, int64_t vocab, bool aligned16, bool edge_ok, bool forward_only,
-                  bool force_stream);
+// in_bytes: logits element size; aligned16: every row base is 16-byte aligned;
+// edge_ok: dlogits (if any) have the logits' element type and the same address mod 16,
+// so rows off 16 bytes split alike; forward_only: no dlogits are written.
+RowPlan plan_rows(int in_bytes, int64_t vocab, bool aligned16, bool edge_ok, bool forward_only, bool force_stream);
 
 hipError_t launch_rows(const RowPlan& p, int in_dtype, int out_dtype, const RowArgs& a,
                        int64_t nrows, hipStream_t st);
