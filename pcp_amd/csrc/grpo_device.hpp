@@ -27,6 +27,7 @@ constexpr int kErrTokenRange = 1;
 constexpr int kErrNonFinite = 2;
 constexpr int kErrBadRagged = 4;   // rollout packing: offsets decrease or run past the token array
 constexpr int kErrBadBase64 = 8;   // base64: a character outside the alphabet or misplaced padding
+constexpr int kErrListedRow = 16;  // a row listed live by live_rows_kernel was not live in the row kernel
 
 // v_exp_f32: 2^x. Used only for the per-element softmax terms, where results
 // below the fp32 normal range are irrelevant (they multiply a coefficient < 1).

@@ -110,8 +110,48 @@ __device__ __forceinline__ void edge_state(const void* p, const RowSpan& sp, int
 // stored as vectors, the head and tail (under EPV elements each) by threads 0..13 one
 // element each. dlogits == nullptr: forward only (log-probs).
 // ---------------------------------------------------------------------------
-template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE, bool CACHE>
-__device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row, float* lds) {
+// Chunk k of a row through its descriptor: 16 bytes at lane offset voff, or for kSplit
+// (16-bit logits, f32 dlogits) the two 8-byte halves of 4-element group sgrp, 512 bytes
+// apart (see resident_row).
+template <typename TI, typename TO, int BLOCK>
+__device__ __forceinline__ u32x4 load_chunk(const __amdgpu_buffer_rsrc_t buf, int k, uint32_t voff, uint32_t sgrp) {
+  constexpr uint32_t kChunkBytes = BLOCK * 16;
+  if constexpr (TI::kBytes == 2 && TO::kBytes == 4) {
+    const u32x2 lo = buf_ld8<true>(buf, fresh_off(sgrp * 8u, k * kChunkBytes));
+    const u32x2 hi = buf_ld8<true>(buf, fresh_off(sgrp * 8u, k * kChunkBytes + 512u));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  } else {
+    return buf_ld16<true>(buf, fresh_off(voff, k * kChunkBytes));
+  }
+}
+
+template <typename TI, typename TO, int BLOCK>
+__device__ __forceinline__ uint32_t split_group(int tid) {
+  return (TI::kBytes == 2 && TO::kBytes == 4) ? static_cast<uint32_t>(128 * (tid >> 6) + (tid & 63)) : 0u;
+}
+
+// The policy row's descriptor for rows without EDGE handling (aligned, V % EPV == 0);
+// row < 0 gives an empty descriptor, whose loads return 0 without a memory access.
+template <typename TI>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t policy_rsrc(const RowArgs& a, int64_t row) {
+  constexpr int EPV = 16 / TI::kBytes;
+  const bool ok = row >= 0;
+  const char* base = static_cast<const char*>(a.logits) + (ok ? row * a.vocab * TI::kBytes : 0);
+  return row_rsrc(base, ok ? static_cast<uint32_t>(a.vocab / EPV) * 16u : 0u);
+}
+
+// PF (listed live rows without EDGE handling): the policy row arrives in xv already
+// loaded (by the caller for the first row, by the previous row's dlogits pass after
+// that). Thread 0 passes the list entry of the row after this one (next_listed, valid
+// when next_ok), which reaches every thread through s_pub under the merge's barrier
+// (the select sits there too, so no wave waits for the entry's load before then); the
+// dlogits pass then loads that row's chunks into xv as it frees them, so the next
+// row's policy loads are in flight under this row's stores. Returns the next row (PF,
+// -1 for none) or -1.
+template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE, bool CACHE, bool PF = false>
+__device__ __forceinline__ int64_t resident_row(const RowArgs& a, const int64_t row, float* lds, u32x4 (&xv)[NCH],
+                                                int next_listed = -1, bool next_ok = false, int* s_pub = nullptr) {
+  static_assert(!(PF && EDGE), "prefetching rows are aligned rows");
   constexpr int EPV = 16 / TI::kBytes;
   constexpr uint32_t kChunkBytes = BLOCK * 16;          // one chunk: 16 bytes per lane
   constexpr uint32_t kOutVec = EPV * TO::kBytes;        // output bytes per input vector
@@ -132,7 +172,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   // kSplit: half h of chunk k of this lane is 4-element group
   //   k * 2 * BLOCK + 128 * wave + 64 * h + lane,
   // valid when below 2 * nv; its input at 8 bytes, its output at 16 bytes per group.
-  const uint32_t sgrp = kSplit ? static_cast<uint32_t>(128 * (tid >> 6) + (tid & 63)) : 0u;
+  const uint32_t sgrp = split_group<TI, TO, BLOCK>(tid);
   const RowMeta r = row_meta(a, row);
   const int64_t row_elem = row * a.vocab;
   const void* xrow = static_cast<const char*>(a.logits) + row_elem * TI::kBytes;
@@ -143,6 +183,8 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   const uint32_t out_bytes = static_cast<uint32_t>(nv) * kOutVec;
   const __amdgpu_buffer_rsrc_t drow =
       row_rsrc(static_cast<char*>(a.dlogits) + (row_elem + xsp.head) * TO::kBytes, out_bytes);
+
+  const uint32_t voff = tid * 16u;
 
   if (!r.live) {
     write_token_outputs(a, r, 0.f, 0.f, 0.f);
@@ -162,7 +204,14 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
       }
       if (EDGE && ek >= 0) store1<TO>(a.dlogits, row_elem + ek, 0.f);
     }
-    return;
+    if constexpr (PF) {
+      // live_rows_kernel listed this row as live from the same ids and mask, so the
+      // inputs changed under the launch. Fail loudly; this workgroup's claimed rows
+      // stay unprocessed. (Loading the next row here as well as in the live path's
+      // dlogits pass made hipcc spill 75-110 VGPRs.)
+      if (tid == 0) atomicOr(a.err, kErrListedRow);
+    }
+    return -1;
   }
 
   const bool has_ref = a.ref_logits != nullptr;
@@ -176,18 +225,9 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   // 1. Policy row -> registers: all NCH loads back to back through one row
   //    descriptor (lanes past the row end read 0 and are skipped below).
   const __amdgpu_buffer_rsrc_t xbuf = row_rsrc(xsp.vec, in_bytes);
-  const uint32_t voff = tid * 16u;
-  u32x4 xv[NCH];
-  if constexpr (kSplit) {
+  if constexpr (!PF) {
 #pragma unroll
-    for (int k = 0; k < NCH; ++k) {
-      const u32x2 lo = buf_ld8<true>(xbuf, fresh_off(sgrp * 8u, k * kChunkBytes));
-      const u32x2 hi = buf_ld8<true>(xbuf, fresh_off(sgrp * 8u, k * kChunkBytes + 512u));
-      xv[k] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < NCH; ++k) xv[k] = buf_ld16<true>(xbuf, fresh_off(voff, k * kChunkBytes));
+    for (int k = 0; k < NCH; ++k) xv[k] = load_chunk<TI, TO, BLOCK>(xbuf, k, voff, sgrp);
   }
   // kSplit: half h of chunk k of this lane holds row values (past the row end it read 0).
   auto half_ok = [&](int k, int h) {
@@ -331,6 +371,9 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
 
   // 3. Workgroup merge.
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (PF) {
+    if (tid == 0) s_pub[0] = next_ok ? next_listed : -1;
+  }
   block_merge2<BLOCK>(pm, ps, rm, rs, lds);
   const float lse2 = pm + log2f(ps);
   const float lse = lse2 * kLn2;
@@ -342,7 +385,11 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
   const float lr = ry - rlse;
   const TokenTerms tt = token_terms(a, r, lp, lr);
   write_token_outputs(a, r, lp, lr, tt.loss);
-  if (a.dlogits == nullptr) return;   // forward only (log-probs)
+  if constexpr (!PF) {   // PF launches always write dlogits
+    if (a.dlogits == nullptr) return -1;   // forward only (log-probs)
+  }
+  const int64_t nxt = PF ? s_pub[0] : -1;   // PF: the next row
+  const __amdgpu_buffer_rsrc_t nbuf = policy_rsrc<TI>(a, nxt);
 
   // 5. dlogits = c * (onehot - softmax) from the resident row; stores past the
   //    row end are dropped by the buffer range check. The target element,
@@ -385,6 +432,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
     } else {
       buf_store_vals<TO, EPV, true>(drow, fresh_off(tid * kOutVec, k * BLOCK * kOutVec), o);
     }
+    if constexpr (PF) xv[k] = load_chunk<TI, TO, BLOCK>(nbuf, k, voff, sgrp);
   }
   const int64_t it = r.id - xsp.head;   // the target's index in the interior
   // The lane that stored the target's group (kSplit: group it / 4 at lane
@@ -403,6 +451,7 @@ __device__ __forceinline__ void resident_row(const RowArgs& a, const int64_t row
       store1<TO>(a.dlogits, row_elem + ek, o);
     }
   }
+  return nxt;
 }
 
 // Persistent: a workgroup takes row blockIdx.x, then rows from the launch's counter
@@ -423,25 +472,62 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
     // Without zero-fill: live_rows_kernel listed the live rows and counted them earlier
     // on the stream. When fewer than half the rows are live the launch visits the listed
     // rows only; otherwise every row in order (dead rows return at once), which measured
-    // faster there (config 2, 57% live: 3.01-3.04 ms against 3.08-3.14 ms listed; config 4,
-    // 21% live: 2.25-2.28 ms listed against 2.62-2.66 ms).
+    // faster there (config 2, 57% live: 3.01-3.04 ms against 3.14-3.16 ms listed with the
+    // next-row prefetch below; config 4, 21% live: 2.25-2.28 ms listed without it against
+    // 2.62-2.66 ms).
     const int n = *a.row_count;
     if (2 * static_cast<int64_t>(n) < a.nrows) {
-      int64_t idx = blockIdx.x;
-      for (int i = 0; idx < n; ++i) {
-        if (threadIdx.x == 0) s_next[i & 1] = atomicAdd(a.next_row, 1) + static_cast<int>(gridDim.x);
-        resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>(a, a.row_list[idx], lds);
-        __syncthreads();   // s_next visible; this row's LDS reads done before the next row writes
-        idx = s_next[i & 1];
+      if (!EDGE && a.dlogits != nullptr) {
+        // Every listed row is live, so each row's dlogits pass loads the next row's
+        // policy chunks (resident_row, PF). List indices: blockIdx.x, then
+        // blockIdx.x + gridDim.x, then from the counter (+ 2 gridDim.x). At the top of
+        // each row thread 0 reads the list entry of the row after it (claim) and claims
+        // the index of the one after that; the entry goes to every thread at the
+        // row's merge, and the claimed index is used at the next row's top, so both
+        // loads complete under the current row. Rows are claimed dynamically: dealt
+        // statically (entries blockIdx.x + i gridDim.x, each row's successor known at
+        // its start) the same launch was 1.5-3% slower and varied more from run to run.
+        int idx = blockIdx.x;
+        if (idx >= n) return;
+        int64_t row = a.row_list[idx];
+        const uint32_t sgrp = split_group<TI, TO, BLOCK>(threadIdx.x);
+        u32x4 xv[NCH];
+        {
+          const __amdgpu_buffer_rsrc_t buf = policy_rsrc<TI>(a, row);
+#pragma unroll
+          for (int k = 0; k < NCH; ++k) xv[k] = load_chunk<TI, TO, BLOCK>(buf, k, threadIdx.x * 16u, sgrp);
+        }
+        int claim = idx + static_cast<int>(gridDim.x);
+        for (;;) {
+          int listed = -1, taken = 0;
+          if (threadIdx.x == 0) {
+            taken = atomicAdd(a.next_row, 1);
+            listed = a.row_list[min(claim, n - 1)];
+          }
+          row = resident_row<TI, TO, BLOCK, NCH, RB, false, CACHE, true>(a, row, lds, xv, listed, claim < n, s_next);
+          claim = taken + 2 * static_cast<int>(gridDim.x);
+          __syncthreads();   // every thread has read s_next before thread 0 writes it again
+          if (row < 0) return;
+        }
+      } else {
+        int64_t idx = blockIdx.x;
+        for (int i = 0; idx < n; ++i) {
+          if (threadIdx.x == 0) s_next[i & 1] = atomicAdd(a.next_row, 1) + static_cast<int>(gridDim.x);
+          u32x4 xv[NCH];
+          resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>(a, a.row_list[idx], lds, xv);
+          __syncthreads();   // s_next visible; this row's LDS reads done before the next row writes
+          idx = s_next[i & 1];
+        }
+        return;
       }
-      return;
     }
   }
   {
     int64_t row = blockIdx.x;
     for (int i = 0; row < a.nrows; ++i) {
       if (threadIdx.x == 0) s_next[i & 1] = atomicAdd(a.next_row, 1) + static_cast<int>(gridDim.x);
-      resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>(a, row, lds);
+      u32x4 xv[NCH];
+      resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>(a, row, lds, xv);
       __syncthreads();   // s_next visible; this row's LDS reads done before the next row writes
       row = s_next[i & 1];
     }

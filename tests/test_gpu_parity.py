@@ -705,26 +705,31 @@ def _all_live_rows_check(cfg, inp, out, mode, exact, label, chunk=4096, f32_out=
     return st
 
 
-def _full_config(key, mode, exact=False, n_seq=None, f32_out=False):
+def _full_config(key, mode, exact=False, n_seq=None, f32_out=False, zero_fill=True):
     cfg = synth.CONFIGS[key]
     inp = synth.make_device_inputs(cfg, DEV, n_seq=n_seq)
     S = inp["logits"].shape[0]
     label = (f"config{key} {'clip_kl' if mode == LossMode.GRPO_CLIP_KL else 'reinforce'}" + (" exact" if exact else "")
-             + (f" f32 dlogits, {S} sequences" if f32_out else ""))
+             + (f" f32 dlogits, {S} sequences" if f32_out else "") + ("" if zero_fill else " no zero-fill"))
     print(f"full-size {label}", flush=True)
+    sentinel = -3.5
+    dl = None if zero_fill else torch.full(inp["logits"].shape, sentinel, dtype=torch.bfloat16, device=DEV)
     out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], rewards=inp["rewards"], group_size=cfg.group,
                                  ref_logits=inp["ref_logits"], old_logp=inp["old_logp"], loss_mode=mode,
                                  clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, exact_bf16=exact,
-                                 dlogits_dtype=torch.float32 if f32_out else None)
+                                 dlogits_dtype=torch.float32 if f32_out else None, dlogits=dl, zero_fill=zero_fill)
     torch.cuda.synchronize()
     T = cfg.T
     _all_live_rows_check(cfg, inp, out, mode, exact, label, f32_out=f32_out)
-    # every masked row of dlogits is exactly zero
+    # every masked row of dlogits is exactly zero, or without zero-fill untouched
     lengths = inp["lengths"]
     for s in range(S):
         ln = int(lengths[s])
         if ln < T:
-            assert float(out.dlogits[s, ln:].abs().amax()) == 0.0
+            if zero_fill:
+                assert float(out.dlogits[s, ln:].abs().amax()) == 0.0
+            else:
+                assert bool((out.dlogits[s, ln:] == sentinel).all())
     # loss == the f64 aggregation of the kernel's own token losses (reduce kernels)
     tl = out.token_loss.double().cpu().numpy()
     Ls = orc.seq_lengths(inp["mask"].cpu().numpy(), T, 0).astype(np.float64)
@@ -762,6 +767,15 @@ def test_config3_full_size(exact):
 @pytest.mark.parametrize("exact", [False, True])
 def test_config4_full_size(exact):
     _full_config(4, LossMode.GRPO_CLIP_KL, exact)
+
+
+@pytest.mark.parametrize("key", [2, 4])
+def test_full_size_no_zero_fill(key):
+    """PCP_FLAG_NO_ZERO_FILL at full size. Config 4 (21% of rows live) takes the listed
+    path, where each workgroup runs about 53 live rows in turn and loads each next row's
+    policy chunks during the current row's dlogits pass; config 2 (57% live) visits
+    every row. Every live row against the oracle, dead rows untouched."""
+    _full_config(key, LossMode.GRPO_CLIP_KL, zero_fill=False)
 
 
 @pytest.mark.parametrize("V", [(1 << 29) - 4, (1 << 29) + 4])
