@@ -931,6 +931,12 @@ constexpr int kDcacheVocabTiles = 4;
 // nontemporal accesses: each byte is touched once here and read back only by the next
 // launch, so keeping the lines in L2 only delays other traffic (config 5, kernel
 // traces: 2.07 -> 1.85 ms; the same hint on the forward's cache stores cost 0.5 ms).
+// A block takes one 64-token tile and kDcacheVocabTiles vocab tiles in turn: the
+// rows' scalars are read once, and each vocab tile's loads are issued before the
+// previous tile's stores, so a wave's wait for them (vector-memory counts retire in
+// issue order) does not include those stores. All accesses go through per-tile
+// buffer descriptors with 32-bit offsets (the host checks ld and ldt), which keeps the
+// kernel at 64 VGPRs, eight waves per SIMD.
 // F32: the terms are f32 at a.src32 (the exact-rounding forward) and D goes to a.d
 // beside them, not in place.
 template <bool F32>
@@ -939,79 +945,103 @@ __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
   const int tid = threadIdx.x;
   const int64_t n = *a.count;
   const int64_t ntile = (n + 63) / 64;     // token tiles that the dW product reads
-  for (int64_t tb = blockIdx.x; tb < ntile; tb += gridDim.x)
-  for (int vs = 0; vs < kDcacheVocabTiles; ++vs) {
-    const int64_t v0 = (static_cast<int64_t>(blockIdx.y) * kDcacheVocabTiles + vs) * 64;
-    if (v0 >= a.ld) break;
+  const int cc = (tid & 7) * 8;            // the thread's 8 columns of a vocab tile
+  const int rq = tid >> 3;                 // and its rows rq, rq + 32 of the token tile
+  const uint32_t ld = static_cast<uint32_t>(a.ld), ldt = static_cast<uint32_t>(a.ldt);
+  const int64_t vbase = static_cast<int64_t>(blockIdx.y) * kDcacheVocabTiles * 64;
+  for (int64_t tb = blockIdx.x; tb < ntile; tb += gridDim.x) {
     const int64_t r0 = tb * 64;
-    const int cc = (tid & 7) * 8;
-    const int64_t c0 = v0 + cc;
-    // Both rows' loads first (one round trip): the f16 terms and the row's scalars.
-    u32x4 w[2], w2[2];
-    float cf[2], l2[2], m2[2], tg[2];
+    const uint32_t nr = static_cast<uint32_t>(min<int64_t>(64, n - r0));   // rows past n read 0, stores drop
+    const __amdgpu_buffer_rsrc_t rd = row_rsrc(a.d + r0 * a.ld, nr * ld * 2u);
+    const __amdgpu_buffer_rsrc_t rs = F32 ? row_rsrc(a.src32 + r0 * a.ld, nr * ld * 4u) : rd;
+    const __amdgpu_buffer_rsrc_t rp = row_rsrc(a.part + r0 * a.ldp, nr * static_cast<uint32_t>(a.ldp) * 8u);
+    float cf[2], l2[2], tg[2];
     int id[2];
+    {
+      const __amdgpu_buffer_rsrc_t rc = row_rsrc(a.coef + r0, nr * 4u), rl = row_rsrc(a.lse2 + r0, nr * 4u),
+                                   rt = row_rsrc(a.tgt + r0, nr * 4u), ri = row_rsrc(a.ids + r0, nr * 4u);
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int64_t row = r0 + (tid >> 3) + 32 * it;
-      w[it] = w2[it] = u32x4{0u, 0u, 0u, 0u};
-      cf[it] = 0.f;
-      l2[it] = m2[it] = tg[it] = 0.f;
-      id[it] = -1;
-      if (row < n) {
-        cf[it] = a.coef[row];
-        l2[it] = a.lse2[row];
-        id[it] = a.ids[row];
-        tg[it] = a.tgt[row];
-        if (c0 < a.V) {
-          if constexpr (F32) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(a.src32 + row * a.ld + c0);
-            w[it] = __builtin_nontemporal_load(src);
-            w2[it] = __builtin_nontemporal_load(src + 1);
-          } else {
-            w[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.d + row * a.ld + c0));
+      for (int it = 0; it < 2; ++it) {
+        const uint32_t off = static_cast<uint32_t>(rq + 32 * it) * 4u;
+        cf[it] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0));
+        l2[it] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rl, off, 0, 0));
+        tg[it] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rt, off, 0, 0));
+        id[it] = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(ri, off, 0, 0));
+      }
+    }
+    // Loads of vocab tile v0 into set q: the terms (16 or 32 bytes per row) and the
+    // exponent reference of the tile's 128-entry partial. Past the row's columns they
+    // read the next row's bytes (past the last row 0), never used.
+    u32x4 w[2][2], w2[2][2];
+    float m2[2][2];
+    auto load = [&](int q, int64_t v0) {
+      const uint32_t c0 = static_cast<uint32_t>(v0) + cc;
+      const uint32_t pi = min(c0 / kLmPart, static_cast<uint32_t>(a.ldp - 1));
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const uint32_t rr = static_cast<uint32_t>(rq + 32 * it);
+        if constexpr (F32) {
+          w[q][it] = buf_ld16<true>(rs, (rr * ld + c0) * 4u);
+          w2[q][it] = buf_ld16<true>(rs, (rr * ld + c0) * 4u + 16u);
+        } else {
+          w[q][it] = buf_ld16<true>(rd, (rr * ld + c0) * 2u);
+        }
+        m2[q][it] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rp, (rr * static_cast<uint32_t>(a.ldp) + pi) * 8u, 0, 0));
+      }
+    };
+    load(0, vbase);
+#pragma unroll
+    for (int vs = 0; vs < kDcacheVocabTiles; ++vs) {
+      const int64_t v0 = vbase + vs * 64;
+      if (v0 >= a.ld) break;
+      const int q = vs & 1;
+      if (vs + 1 < kDcacheVocabTiles) load(q ^ 1, v0 + 64);
+      const int64_t c0 = v0 + cc;
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int rr = rq + 32 * it;
+        u32x4 out = {0u, 0u, 0u, 0u};
+        if (cf[it] != 0.f && c0 < a.V) {
+          const float f = -cf[it] * hw_exp2(ms_ref(m2[q][it]) - l2[it]);
+          const uint32_t ww[4] = {w[q][it][0], w[q][it][1], w[q][it][2], w[q][it][3]};
+          const int64_t rel = static_cast<int64_t>(id[it]) - c0;
+          float d[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float e = F32 ? __uint_as_float(k < 4 ? w[q][it][k] : w2[q][it][k - 4]) : F16T::unpack(ww, k);
+            d[k] = c0 + k < a.V ? f * e : 0.f;
           }
-          m2[it] = a.part[row * a.ldp + c0 / kLmPart].x;
+          if (rel >= 0 && rel < 8) {
+            const float pt = hw_exp2(fmaf(tg[it], kLog2e, -l2[it]));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf[it] * pt + cf[it] : d[k];
+          }
+          out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
+                      pack2<BF16T>(d[6], d[7])};
+        }
+        buf_st16<true>(rd, out, (static_cast<uint32_t>(rr) * ld + static_cast<uint32_t>(c0)) * 2u);
+        tile_put8(t, rr, cc, out);
+      }
+      __syncthreads();
+      // Dt row v0 + c, tokens r0 + 8g .. +7: eight lanes write one row's 128 bytes.
+      if (a.dt) {
+        const __amdgpu_buffer_rsrc_t rdt = row_rsrc(a.dt + v0 * a.ldt, 64u * ldt * 2u);
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+          const int c = rq + 32 * it, g = tid & 7;
+          buf_st16<true>(rdt, tile_col8(t, 8 * g, c),
+                         (static_cast<uint32_t>(c) * ldt + static_cast<uint32_t>(r0) + 8u * g) * 2u);
         }
       }
+      __syncthreads();
     }
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int rr = (tid >> 3) + 32 * it;
-      const int64_t row = r0 + rr;
-      u32x4 out = {0u, 0u, 0u, 0u};
-      if (row < n && cf[it] != 0.f && c0 < a.V) {
-        const float f = -cf[it] * hw_exp2(ms_ref(m2[it]) - l2[it]);
-        const uint32_t ww[4] = {w[it][0], w[it][1], w[it][2], w[it][3]};
-        const int64_t rel = static_cast<int64_t>(id[it]) - c0;
-        float d[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float e = F32 ? __uint_as_float(k < 4 ? w[it][k] : w2[it][k - 4]) : F16T::unpack(ww, k);
-          d[k] = c0 + k < a.V ? f * e : 0.f;
-        }
-        if (rel >= 0 && rel < 8) {
-          const float pt = hw_exp2(fmaf(tg[it], kLog2e, -l2[it]));
-#pragma unroll
-          for (int k = 0; k < 8; ++k) d[k] = k == rel ? -cf[it] * pt + cf[it] : d[k];
-        }
-        out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
-                    pack2<BF16T>(d[6], d[7])};
-      }
-      if (row < n) __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(a.d + row * a.ld + c0));
-      tile_put8(t, rr, cc, out);
-    }
-    __syncthreads();
-    // Dt row v0 + c, tokens r0 + 8g .. +7: eight lanes write one row's 128 bytes.
-#pragma unroll
-    for (int it = 0; it < 2 && a.dt; ++it) {
-      const int c = (tid >> 3) + 32 * it, g = tid & 7;
-      __builtin_nontemporal_store(tile_col8(t, 8 * g, c), reinterpret_cast<u32x4*>(a.dt + (v0 + c) * a.ldt + r0 + 8 * g));
-    }
-    __syncthreads();
   }
 }
 
-__global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) { lm_dcache_body<false>(a); }
+__global__ void __launch_bounds__(256) lm_dcache_kernel(LmDcacheArgs a) {
+  lm_dcache_body<false>(a);
+}
 __global__ void __launch_bounds__(256) lm_dcache32_kernel(LmDcacheArgs a) { lm_dcache_body<true>(a); }
 
 // GRPO terms per token from logp / ref logp (token_terms); also masks logp for
@@ -1263,6 +1293,9 @@ hipError_t launch_lm_reduce(const LmReduceArgs& a, hipStream_t st) {
 
 hipError_t launch_lm_dcache(const LmDcacheArgs& a, hipStream_t st) {
   if (a.ldt <= 0 || a.ld <= 0) return hipSuccess;
+  // 32-bit offsets within a tile's descriptors: 64 rows of f32 terms, 64 Dt rows.
+  if (a.ld >= (int64_t{1} << 24) || a.ldt >= (int64_t{1} << 25) || static_cast<int64_t>(a.ldp) * 64 * 8 >= (int64_t{1} << 32))
+    return hipErrorInvalidValue;
   // Token tiles are the grid's fast dimension: the blocks past the live count (the grid
   // is sized for every token) are interleaved with live ones instead of forming a tail.
   // At config 5, 1.95 ms with an exact grid (host-read count), 2.08 ms with the dead
