@@ -615,10 +615,58 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
   // the ring reloads of (kb, 1) and (kb + 1, 0) (none in the forward): vmcnt(2 NJ16),
   // or vmcnt(0), leaves only those in flight.
   const int nk = K / BK;
+  // The forward's policy tiles also write W^T [H, ldwt] (the dhidden product's token
+  // operand, fragment-major) from the W slabs they hold: stage st of vocab tile tn by
+  // token tile st % ntt, so each stage is written once and every token tile writes
+  // about nk / ntt of them. Wave w writes the four fragments of vocab rows v0 + 32 w +
+  // [0, 32) and the stage's 64 hidden columns; lane l holds hidden column 16 bb + l % 16
+  // and vocab rows 8 (l / 16) + [0, 8), read from the swizzled LDS rows as 16-bit
+  // pairs. Called at the end of the iteration whose barrier landed stage st (after its
+  // MFMAs are issued): the buffer is refilled only after the next barrier, whose
+  // vmcnt(0) also covers these stores. Vocab rows past V hold zeros (the W
+  // descriptor's range); fragments past ldwt are not written. At config 5 this costs
+  // the forward 0.34 ms and saves the 0.49 ms transpose kernel that wrote W^T.
+  const bool wt_on = FWD && a.wt != nullptr && prod == 0 && v0 + 32 * wave < a.ldwt;
+  auto wt_write = [&](int st) {
+    if constexpr (FWD) {
+      if (!wt_on || st % ntt != tm) return;
+      const char* wb = smem + (st % NST) * kBuf;
+      // The thread index through an opaque copy: the addresses below are then formed
+      // here rather than hoisted out of the main loop, where they would hold VGPRs
+      // through every stage.
+      int ti = tid;
+      asm volatile("" : "+v"(ti));
+      const int ln = ti & 63, wv8 = ti >> 6;
+      const int r0 = 32 * wv8 + 8 * (ln >> 4);
+      // The stage's four fragment rows of W^T: ldwt / 32 fragments of 1 KB each.
+      const uint32_t frow = static_cast<uint32_t>(a.ldwt / 32) * 1024u;
+      const __amdgpu_buffer_rsrc_t rw =
+          row_rsrc(reinterpret_cast<const char*>(a.wt) + static_cast<int64_t>(4 * st) * frow, 4u * frow);
+      const uint32_t o0 = static_cast<uint32_t>(v0 / 32 + wv8) * 1024u + 16u * ln;
+      // Lane l: hidden column 16 bb + l % 16 of vocab rows r0 + [0, 8), read as 16-bit
+      // pairs. (ds_read_b64_tr_b16 would read the same eight values in two instructions,
+      // but hipcc waits for every direct-to-LDS load in flight before one, here the next
+      // stage's; as inline assembly with its own wait it measured the same as this.)
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        const int hl = 16 * bb + (ln & 15);
+        uint32_t w[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int r = r0 + 2 * jj;   // rows r and r + 1 share the swizzle (r even)
+          const char* p = wb + r * ROWB + (((hl >> 3) ^ lm_swz(r)) << 4) + (hl & 7) * 2;
+          w[jj] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p)) |
+                  (static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p + ROWB)) << 16);
+        }
+        buf_st16<true>(rw, u32x4{w[0], w[1], w[2], w[3]}, o0 + static_cast<uint32_t>(bb) * frow);
+      }
+    }
+  };
   issue(0, 0);
   ring_load(0, 0);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   lm_barrier();
+  wt_write(0);
   issue(min(1, nk - 1), 1);
   ring_load(1, 0);
   fload(0, 0, 0);
@@ -643,6 +691,10 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
     mf(1, 1);
     ring_load(1, n1);
     sched16(std::true_type{});
+    if constexpr (FWD) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (kb + 1 < nk) wt_write(kb + 1);
+    }
   }
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
@@ -1241,6 +1293,9 @@ hipError_t launch_lm_tiles(int mode, const LmTileArgs& args, hipStream_t st) {
   LmTileArgs a = args;
   const int grid = a.ntt * a.nvt * (mode == kLmFwd && a.n_model > 1 ? 2 : 1);   // tiles at the largest token count
   if (grid <= 0) return hipSuccess;
+  if (a.wt && (mode != kLmFwd || a.vt0 != 0 || a.ldwt % 64 != 0 || a.ldwt < a.V ||
+               static_cast<int64_t>(a.nvt) * lm::BV < a.V || a.ldwt >= (int64_t{1} << 25)))
+    return hipErrorInvalidValue;   // W^T from the forward: whole vocabulary, one stage's rows in 32-bit offsets
   if (mode == kLmFwd && a.ecache32) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_tile_fwd32_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lm::kSmem));

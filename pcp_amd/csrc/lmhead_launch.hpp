@@ -39,6 +39,8 @@ struct LmTileArgs {
   uint16_t* ecache;     // or nullptr: [N, lde] f16 softmax terms 2^(x*log2e - ref) of the
   int64_t lde;          //   partial's reference ref (lde % 64 == 0, >= V; 0 past V)
   float* ecache32;      // or nullptr: the same terms as f32 (ecache then nullptr)
+  uint16_t* wt;         // or nullptr: W^T [H, ldwt] fragment-major (launch_lm_transpose_frag's layout),
+  int64_t ldwt;         //   written by model 0's tiles from their W slabs (ldwt % 64 == 0, >= V)
   // kLmBwd
   const float* lse2;    // [N] base-2 log-sum-exp
   const float* coef;    // [N] d loss / d logp

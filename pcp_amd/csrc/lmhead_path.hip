@@ -288,6 +288,12 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   ta.ecache = cached && !exact ? static_cast<uint16_t*>(ctx->lm_dbuf) : nullptr;
   ta.ecache32 = cached && exact ? static_cast<float*>(ctx->lm_dbuf) : nullptr;
   ta.lde = ldv;
+  // W^T [H, ldv] fragment-major (the dhidden product's token operand) comes out of the
+  // forward: the policy's tiles write it from the W slabs they hold.
+  if (want_dy && (cached || chunk_frag)) {
+    ta.wt = reinterpret_cast<uint16_t*>(static_cast<char*>(ctx->lm_dbuf) + (cached ? o_wt : o_cwt));
+    ta.ldwt = ldv;
+  }
   ta.n_model = ref ? 2 : 1;
   if (ref) {
     ta.B2 = a->ref_weight;
@@ -301,6 +307,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
     if (timed && (e = hipEventRecord(ctx->prof_start[ctx->prof_used], st)) != hipSuccess)
       return hip_fail(ctx, e, "hipEventRecord");
     if ((e = launch_lm_tiles(kLmFwd, ta, st)) != hipSuccess) return hip_fail(ctx, e, "LM-head forward tiles");
+    ta.wt = nullptr;   // the backward's recompute tiles reuse ta
     if (timed && (e = hipEventRecord(ctx->prof_stop[ctx->prof_used++], st)) != hipSuccess)
       return hip_fail(ctx, e, "hipEventRecord");
   }
@@ -417,10 +424,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       int ng = 0;
       std::memset(g, 0, sizeof(g));
       if (want_dy) {
-        // W^T [H, ldv] (fragment-major), zero past V.
-        const LmTransposeArgs tw{static_cast<const uint16_t*>(a->weight), H, static_cast<int>(V), static_cast<int>(H),
-                                 wt, ldv, nullptr};
-        if ((e = launch_lm_transpose_frag(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
+        // W^T [H, ldv] (fragment-major, zero past V) was written by the forward.
         // dhidden_c[t][h] = sum_v D[t][v] * W^T[h][v].
         LmTileArgs::Gemm& d = g[ng++];
         d.B = dd;
@@ -465,12 +469,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       if (a->dweight && (e = chunk_frag ? launch_lm_transpose_frag(tr, st) : launch_lm_transpose(tr, st)) != hipSuccess)
         return hip_fail(ctx, e, "transposing hidden rows");
       uint16_t* cdt = chunk_frag && a->dweight ? reinterpret_cast<uint16_t*>(dbuf + o_cdt) : nullptr;
-      uint16_t* cwt = chunk_frag && want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_cwt) : nullptr;
-      if (cwt) {
-        const LmTransposeArgs tw{static_cast<const uint16_t*>(a->weight), H, static_cast<int>(V), static_cast<int>(H),
-                                 cwt, ldv, nullptr};
-        if ((e = launch_lm_transpose_frag(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
-      }
+      uint16_t* cwt = chunk_frag && want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_cwt) : nullptr;   // from the forward
       // The cached path's products over one chunk [vc0, vc0 + w): D_c token-major (rows of
       // chunk entries) with W^T's fragments of that range, and D_c^T with hidden^T.
       auto products_frag = [&](int64_t vc0, int64_t w) -> hipError_t {
