@@ -69,8 +69,8 @@ int collect_device_errors(pcp_ctx* ctx) {
   if (h & kErrBadRagged)
     return fail(ctx, PCP_ERR_INVALID_ARG, "rollout offsets decrease or run past the token array");
   if (h & kErrListedRow)
-    return fail(ctx, PCP_ERR_DEVICE, "a row listed as live was not live in the row kernel (ids or mask changed "
-                                     "during the call)");
+    return fail(ctx, PCP_ERR_INVALID_ARG, "a row listed as live was not live in the row kernel (ids or mask "
+                                          "changed during the call)");
   if (h & kErrBadBase64)
     return fail(ctx, PCP_ERR_INVALID_ARG, "base64 text has a character outside the alphabet or misplaced padding "
                                           "(InvalidCharacter / InvalidPadding)");
