@@ -713,7 +713,8 @@ def _full_config(key, mode, exact=False, n_seq=None, f32_out=False, zero_fill=Tr
              + (f" f32 dlogits, {S} sequences" if f32_out else "") + ("" if zero_fill else " no zero-fill"))
     print(f"full-size {label}", flush=True)
     sentinel = -3.5
-    dl = None if zero_fill else torch.full(inp["logits"].shape, sentinel, dtype=torch.bfloat16, device=DEV)
+    dl = None if zero_fill else torch.full(inp["logits"].shape, sentinel,
+                                           dtype=torch.float32 if f32_out else torch.bfloat16, device=DEV)
     out = grpo.grpo_loss_fwd_bwd(inp["logits"], inp["ids"], inp["mask"], rewards=inp["rewards"], group_size=cfg.group,
                                  ref_logits=inp["ref_logits"], old_logp=inp["old_logp"], loss_mode=mode,
                                  clip_eps=cfg.clip_eps, kl_beta=cfg.kl_beta, exact_bf16=exact,
@@ -776,6 +777,13 @@ def test_full_size_no_zero_fill(key):
     policy chunks during the current row's dlogits pass; config 2 (57% live) visits
     every row. Every live row against the oracle, dead rows untouched."""
     _full_config(key, LossMode.GRPO_CLIP_KL, zero_fill=False)
+
+
+def test_config4_rows_f32_dlogits_no_zero_fill():
+    """bf16 logits, f32 dlogits, no zero-fill at configuration 4 (21% of rows live): the
+    listed path with the next-row prefetch on the split-half instance, about 53 rows per
+    workgroup. Every live row against the oracle under the f32 bar, dead rows untouched."""
+    _full_config(4, LossMode.GRPO_CLIP_KL, f32_out=True, zero_fill=False)
 
 
 @pytest.mark.parametrize("V", [(1 << 29) - 4, (1 << 29) + 4])
