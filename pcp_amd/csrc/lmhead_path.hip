@@ -200,8 +200,13 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const size_t o_cwt = o_cdt + (a->dweight ? 2 * static_cast<size_t>(chunk) * ldt : 0);
   const size_t chunk_frag_bytes = o_cwt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
   bool cached = false, chunk_frag = false;
+  // The dlogits pass addresses a 64-token tile of the cache and 64 rows of D^T with
+  // 32-bit offsets (launch_lm_dcache): larger shapes take the chunked backward.
+  const bool cache_fits = ldv < (int64_t{1} << 24) && ldt < (int64_t{1} << 25);
+  // W^T comes out of the forward while one stage's four fragment rows fit 32-bit offsets.
+  const bool wt_fwd = ldv < (int64_t{1} << 25);
   if (bwd) {
-    if (a->vocab_chunk == 0 && cache_bytes <= cache_budget(ctx, cache_bytes)) {
+    if (a->vocab_chunk == 0 && cache_fits && cache_bytes <= cache_budget(ctx, cache_bytes)) {
       e = grow_dbuf(ctx, cache_bytes);
       if (e == hipSuccess) cached = true;
       else if (e != hipErrorOutOfMemory) return hip_fail(ctx, e, "allocating the softmax cache");
@@ -290,7 +295,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   ta.lde = ldv;
   // W^T [H, ldv] fragment-major (the dhidden product's token operand) comes out of the
   // forward: the policy's tiles write it from the W slabs they hold.
-  if (want_dy && (cached || chunk_frag)) {
+  if (want_dy && wt_fwd && (cached || chunk_frag)) {
     ta.wt = reinterpret_cast<uint16_t*>(static_cast<char*>(ctx->lm_dbuf) + (cached ? o_wt : o_cwt));
     ta.ldwt = ldv;
   }
@@ -424,7 +429,12 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       int ng = 0;
       std::memset(g, 0, sizeof(g));
       if (want_dy) {
-        // W^T [H, ldv] (fragment-major, zero past V) was written by the forward.
+        // W^T [H, ldv] (fragment-major, zero past V), written by the forward.
+        if (!wt_fwd) {
+          const LmTransposeArgs tw{static_cast<const uint16_t*>(a->weight), H, static_cast<int>(V),
+                                   static_cast<int>(H), wt, ldv, nullptr};
+          if ((e = launch_lm_transpose_frag(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
+        }
         // dhidden_c[t][h] = sum_v D[t][v] * W^T[h][v].
         LmTileArgs::Gemm& d = g[ng++];
         d.B = dd;
@@ -469,7 +479,12 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
       if (a->dweight && (e = chunk_frag ? launch_lm_transpose_frag(tr, st) : launch_lm_transpose(tr, st)) != hipSuccess)
         return hip_fail(ctx, e, "transposing hidden rows");
       uint16_t* cdt = chunk_frag && a->dweight ? reinterpret_cast<uint16_t*>(dbuf + o_cdt) : nullptr;
-      uint16_t* cwt = chunk_frag && want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_cwt) : nullptr;   // from the forward
+      uint16_t* cwt = chunk_frag && want_dy ? reinterpret_cast<uint16_t*>(dbuf + o_cwt) : nullptr;
+      if (cwt && !wt_fwd) {   // otherwise written by the forward
+        const LmTransposeArgs tw{static_cast<const uint16_t*>(a->weight), H, static_cast<int>(V), static_cast<int>(H),
+                                 cwt, ldv, nullptr};
+        if ((e = launch_lm_transpose_frag(tw, st)) != hipSuccess) return hip_fail(ctx, e, "transposing the LM head");
+      }
       // The cached path's products over one chunk [vc0, vc0 + w): D_c token-major (rows of
       // chunk entries) with W^T's fragments of that range, and D_c^T with hidden^T.
       auto products_frag = [&](int64_t vc0, int64_t w) -> hipError_t {
