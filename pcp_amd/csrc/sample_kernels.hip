@@ -297,8 +297,9 @@ __device__ __forceinline__ void sample_select(const SampleArgs& a, int64_t row, 
 
 // One launch: workgroup (g, row) writes its partials (coherent stores, complete before
 // its ticket), takes a ticket of its row, and the row's last workgroup selects with its
-// first wave (after an acquire fence) and returns the ticket to 0 for the next launch. A single-row call (the reference's one row per generated token) thus costs
-// one launch.
+// first wave (after an acquire fence) and returns the ticket to 0 for the next launch.
+// A single-row call (the reference's one row per generated token) thus costs one
+// launch.
 template <typename TI>
 __global__ void __launch_bounds__(64 * kWaves) sample_kernel(SampleArgs a) {
   __shared__ int last;
