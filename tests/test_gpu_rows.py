@@ -156,3 +156,51 @@ def test_no_zero_fill_leaves_dead_rows(kind, dt, V, odt, stream, shifted, live):
     assert_dlogits(got[~dead], want.dlogits[~dead], fl[~dead], odt == "bf16")
     assert abs(float(out.loss.cpu()) - want.loss) <= full_loss_tol(want, x, ids, mask, rows, off, odt_orc, False,
                                                                    0.04, S)
+
+
+# (logits dtype, V, dlogits dtype): aligned rows, several listed rows per workgroup
+LISTED_CASES = [("bf16", 32768, "bf16"), ("bf16", 32768, "f32"), ("f32", 8192, "f32")]
+
+
+@pytest.mark.parametrize("dt,V,odt", LISTED_CASES, ids=[f"{c[0]}-{c[1]}-{c[2]}" for c in LISTED_CASES])
+def test_no_zero_fill_listed_rows_prefetch(dt, V, odt):
+    """Without zero-fill and a quarter of the rows live, the resident kernel walks the
+    listed live rows, several per workgroup here, loading each next row's policy chunks
+    during the current row's dlogits pass (on 1024-lane instances of 2 and 4 chunks and
+    the split-half bf16 -> f32 instance). Every live row against the oracle, dead rows
+    untouched bit for bit."""
+    rng = np.random.default_rng(V + len(dt) + len(odt))
+    S, T, G = 16, 512, 4
+    x32 = rng.standard_normal((S, T, V)).astype(np.float32) * 3
+    r32 = x32 + rng.standard_normal((S, T, V)).astype(np.float32) * 0.1
+    if dt == "bf16":
+        x, ref, odt_orc = orc.bf16_from_f32(x32), orc.bf16_from_f32(r32), orc.BF16
+    else:
+        x, ref, odt_orc = x32, r32, orc.F32
+    del x32, r32
+    ids = rng.integers(0, V, size=(S, T)).astype(np.int64)
+    ids[rng.random((S, T)) < 0.05] = -100
+    mask = (rng.random((S, T)) < 0.27).astype(np.float32)
+    rewards = rng.random(S).astype(np.float32)
+    lp, _ = orc.logprob(np.ascontiguousarray(x).reshape(S * T, V), np.clip(ids.reshape(-1), 0, None), dtype=odt_orc)
+    old = (lp.reshape(S, T) + rng.standard_normal((S, T)) * 0.05).astype(np.float32)
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32}[odt]
+    sentinel = -3.5
+    dl = torch.full((S, T, V), sentinel, dtype=tdt, device=DEV)
+    dead = (mask == 0) | (ids == -100)
+    assert 2 * int((~dead).sum()) < S * T          # the listed path
+    print(f"listed rows: {dt}->{odt} V={V}, {int((~dead).sum())} live of {S * T}", flush=True)
+    out = grpo.grpo_loss_fwd_bwd(dev(x), dev(ids), dev(mask), rewards=dev(rewards), group_size=G,
+                                 ref_logits=dev(ref), old_logp=dev(old), loss_mode=LossMode.GRPO_CLIP_KL,
+                                 dlogits=dl, zero_fill=False)
+    torch.cuda.synchronize()
+    want = orc.grpo_full(x, ids, mask, rows=T, rewards=rewards, group_size=G, ref_logits=ref, old_logp=old,
+                         loss_mode=orc.CLIP_KL, dtype=odt_orc)
+    got_bits = host_bits(out.dlogits)
+    sent_bits = host_bits(torch.full((1,), sentinel, dtype=tdt))[0]
+    assert np.all(got_bits[dead] == sent_bits), "a dead row was written"
+    ts = token_scale(x, ids, T, 0, odt_orc)
+    fl = tok_to_rows(full_floor(want, mask, old, S, False, 0.04, 0.2, ts), T, 0, T)
+    got = orc.bf16_to_f32(got_bits) if odt == "bf16" else got_bits.astype(np.float32)
+    assert_dlogits(got[~dead], want.dlogits[~dead], fl[~dead], odt == "bf16")
+    assert abs(float(out.loss.cpu()) - want.loss) <= full_loss_tol(want, x, ids, mask, T, 0, odt_orc, False, 0.04, S)
