@@ -207,8 +207,8 @@ __device__ __forceinline__ int64_t resident_row(const RowArgs& a, const int64_t 
     if constexpr (PF) {
       // live_rows_kernel listed this row as live from the same ids and mask, so the
       // inputs changed under the launch. Fail loudly (PCP_ERR_INVALID_ARG); this
-      // workgroup's claimed rows stay unprocessed. (Loading the next row here as well as in the live path's
-      // dlogits pass made hipcc spill 75-110 VGPRs.)
+      // workgroup's claimed rows stay unprocessed. (Loading the next row here as well
+      // as in the live path's dlogits pass made hipcc spill 75-110 VGPRs.)
       if (tid == 0) atomicOr(a.err, kErrListedRow);
     }
     return -1;
