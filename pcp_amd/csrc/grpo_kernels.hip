@@ -917,6 +917,46 @@ __device__ __forceinline__ void group_advantages(const float* r, int64_t i, int6
   }
 }
 
+// group_advantages with the group's rewards loaded by the 64 lanes of one wave at once
+// (chunks of 64), so the sequential sums run on registers instead of one dependent
+// load per reward: every lane forms the same sums from the same values in the same
+// order (readlane copies bits), hence the same bits as group_advantages. Called by all
+// 64 lanes of a wave.
+__device__ __forceinline__ void group_advantages_wave(const float* r, int64_t i, int64_t e, float eps, float* adv,
+                                                      float* adv2) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const float cnt = static_cast<float>(e - i);
+  // Chunk c of 64 rewards: lane l holds r[i + 64 c + l]; the first chunk is kept.
+  const int n0 = static_cast<int>(min<int64_t>(64, e - i));
+  const float v0 = lane < n0 ? r[i + lane] : 0.f;
+  auto chunk = [&](int64_t c0) { return c0 == i ? v0 : (c0 + lane < e ? r[c0 + lane] : 0.f); };
+  float sum = 0.f;
+  for (int64_t c0 = i; c0 < e; c0 += 64) {
+    const int n = static_cast<int>(min<int64_t>(64, e - c0));
+    const float v = chunk(c0);
+    for (int k = 0; k < n; ++k) sum = sum + __shfl(v, k);
+  }
+  const float mean = sum / cnt;
+  float ssd = 0.f;
+  for (int64_t c0 = i; c0 < e; c0 += 64) {
+    const int n = static_cast<int>(min<int64_t>(64, e - c0));
+    const float v = chunk(c0);
+    for (int k = 0; k < n; ++k) {
+      const float d = __shfl(v, k) - mean;
+      const float d2 = d * d;
+      ssd = ssd + d2;
+    }
+  }
+  const float sd = sqrtf(ssd / cnt) + eps;
+  for (int64_t c0 = i; c0 < e; c0 += 64) {
+    if (c0 + lane >= e) break;
+    const float x = (chunk(c0) - mean) / sd;
+    adv[c0 + lane] = x;
+    if (adv2) adv2[c0 + lane] = x;
+  }
+}
+
 __global__ void __launch_bounds__(64)
 advantages_kernel(const float* r, int64_t n, int64_t group, float eps, float* adv) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
@@ -961,27 +1001,36 @@ loss_final_kernel(const float* seq_val, int64_t n_seq, float loss_norm, float* l
 //  * workgroup 0 zeroes the counters the row kernel and loss_reduce_kernel start from.
 __global__ void __launch_bounds__(kSmallBlock) step_prep_kernel(StepPrepArgs a) {
   const int64_t s = blockIdx.x;
-  if (threadIdx.x == 0) {
-    if (s == 0) {
-#pragma unroll
-      for (int k = 0; k < 3; ++k)
-        if (a.zero[k]) *a.zero[k] = 0;
-    }
-    if (a.rewards) {
-      if (s % a.group == 0) group_advantages(a.rewards, s, min(s + a.group, a.n_seq), a.std_eps, a.adv, a.adv_out);
-    } else if (a.adv_out) {
-      a.adv_out[s] = a.adv_in[s];
-    }
-  }
   __shared__ float lds[kSmallBlock / 64];
+  // The mask terms first, in batches of four per lane with every load of a batch in
+  // flight before its additions (each lane still adds its terms in row order).
   float acc = 0.f;
   const int64_t base = s * a.tok_stride + a.tok_offset;
-  for (int64_t t = threadIdx.x; t < a.rows; t += kSmallBlock) {
-    float m;
-    if (a.mask == nullptr) m = 1.f;
-    else if (a.mask_u8) m = static_cast<const uint8_t*>(a.mask)[base + t] ? 1.f : 0.f;
-    else m = static_cast<const float*>(a.mask)[base + t];
-    acc += m;
+  constexpr int kB = 4;
+  for (int64_t t0 = threadIdx.x; t0 < a.rows; t0 += kB * kSmallBlock) {
+    float m[kB];
+#pragma unroll
+    for (int q = 0; q < kB; ++q) {
+      const int64_t t = t0 + q * kSmallBlock;
+      m[q] = 1.f;
+      if (a.mask != nullptr && t < a.rows)
+        m[q] = a.mask_u8 ? (static_cast<const uint8_t*>(a.mask)[base + t] ? 1.f : 0.f)
+                         : static_cast<const float*>(a.mask)[base + t];
+    }
+#pragma unroll
+    for (int q = 0; q < kB; ++q)
+      if (t0 + q * kSmallBlock < a.rows) acc += m[q];
+  }
+  if (threadIdx.x == 0 && s == 0) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      if (a.zero[k]) *a.zero[k] = 0;
+  }
+  if (a.rewards) {
+    if (s % a.group == 0 && threadIdx.x < 64)
+      group_advantages_wave(a.rewards, s, min(s + a.group, a.n_seq), a.std_eps, a.adv, a.adv_out);
+  } else if (a.adv_out && threadIdx.x == 0) {
+    a.adv_out[s] = a.adv_in[s];
   }
   const float tot = block_sum<kSmallBlock>(acc, lds);
   if (threadIdx.x == 0) {
@@ -1002,12 +1051,27 @@ __global__ void __launch_bounds__(kSmallBlock) loss_reduce_kernel(LossReduceArgs
   __shared__ int last;
   const int64_t s = blockIdx.x;
   const int64_t base = s * a.tok_stride + a.tok_offset;
+  // The sequence's scalars and token losses all in flight before any addition (each
+  // lane still adds its terms in row order, batches of four).
+  const float len = a.seq_len[s];
+  const float av = a.reinforce ? a.adv[s] : 1.f;
   float acc = 0.f;
-  for (int64_t t = threadIdx.x; t < a.rows; t += kSmallBlock) acc += a.token_loss[base + t];
+  constexpr int kB = 4;
+  for (int64_t t0 = threadIdx.x; t0 < a.rows; t0 += kB * kSmallBlock) {
+    float m[kB];
+#pragma unroll
+    for (int q = 0; q < kB; ++q) {
+      const int64_t t = t0 + q * kSmallBlock;
+      m[q] = t < a.rows ? a.token_loss[base + t] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < kB; ++q)
+      if (t0 + q * kSmallBlock < a.rows) acc += m[q];
+  }
   const float tot = block_sum<kSmallBlock>(acc, lds);
   if (threadIdx.x == 0) {
-    const float v = tot / a.seq_len[s];
-    store_coherent(a.seq_val + s, a.reinforce ? v * a.adv[s] : v);
+    const float v = tot / len;
+    store_coherent(a.seq_val + s, a.reinforce ? v * av : v);
     wait_stores();     // seq_val[s] at the coherent level before the ticket
     last = atomicAdd(a.done, 1) == static_cast<int>(a.n_seq - 1);
   }
