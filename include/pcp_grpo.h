@@ -93,7 +93,10 @@ typedef enum pcp_loss_mode {
 
 /* pcp_grpo_args.flags */
 #define PCP_FLAG_ASYNC 0x1u            /* return after enqueueing; errors surface in pcp_sync */
-#define PCP_FLAG_NO_ZERO_FILL 0x2u     /* leave dlogits rows of masked / pad tokens untouched */
+#define PCP_FLAG_NO_ZERO_FILL 0x2u     /* leave dlogits rows of masked / pad tokens untouched
+                                          (ids and mask must not change while the call runs:
+                                          a row first listed live and then found dead fails
+                                          the call with PCP_ERR_INVALID_ARG)                  */
 #define PCP_FLAG_FORCE_STREAMING 0x4u  /* use the two-read streaming kernel even when the
                                           register-resident one fits (testing / comparison);
                                           on pcp_grpo_lmhead_fwd_bwd with a vocab_chunk: the
