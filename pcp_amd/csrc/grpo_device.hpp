@@ -133,6 +133,8 @@ __device__ __forceinline__ uint32_t fresh_off(uint32_t base, uint32_t add) {
 
 // Cache-policy bits of buffer accesses: 2 = NT (streaming, not retained).
 constexpr int kBufNT = 2;
+// sc0 | sc1 | nt: nontemporal at system scope (stores written through to memory).
+constexpr int kBufNTSystem = 19;
 
 // 16-byte load / store at byte offset `off` of a row buffer (range-checked).
 template <bool NT>
@@ -145,26 +147,27 @@ __device__ __forceinline__ u32x2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off)
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, NT ? kBufNT : 0));
 }
 
-template <bool NT>
+// POL: the cache policy of an NT access (kBufNT or kBufNTSystem).
+template <bool NT, int POL = kBufNT>
 __device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, u32x4 v, uint32_t off) {
   typedef int i32x4 __attribute__((ext_vector_type(4)));
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, off, 0, NT ? kBufNT : 0);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, off, 0, NT ? POL : 0);
 }
 
 // Store one output element at byte offset `off` of a row buffer (range-checked).
-template <typename TO, bool NT>
+template <typename TO, bool NT, int POL = kBufNT>
 __device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
   if constexpr (TO::kBytes == 4) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, NT ? kBufNT : 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, NT ? POL : 0);
   } else {
     __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(pack2<TO>(v, 0.f) & 0xffffu), r, off, 0,
-                                          NT ? kBufNT : 0);
+                                          NT ? POL : 0);
   }
 }
 
 // Pack N floats into N output elements (N * kBytes = 16 or 32 bytes) and store them
 // through a row buffer at byte offset `off` (range-checked).
-template <typename TO, int N, bool NT>
+template <typename TO, int N, bool NT, int POL = kBufNT>
 __device__ __forceinline__ void buf_store_vals(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&v)[N]) {
   if constexpr (TO::kBytes == 4) {
     static_assert(N % 4 == 0, "f32 output stores whole 16-byte vectors");
@@ -172,7 +175,7 @@ __device__ __forceinline__ void buf_store_vals(__amdgpu_buffer_rsrc_t r, uint32_
     for (int q = 0; q < N / 4; ++q) {
       u32x4 w = {__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]), __float_as_uint(v[4 * q + 2]),
                  __float_as_uint(v[4 * q + 3])};
-      buf_st16<NT>(r, w, off + 16 * q);
+      buf_st16<NT, POL>(r, w, off + 16 * q);
     }
   } else {
     static_assert(N % 8 == 0, "16-bit output stores whole 16-byte vectors");
@@ -180,7 +183,7 @@ __device__ __forceinline__ void buf_store_vals(__amdgpu_buffer_rsrc_t r, uint32_
     for (int q = 0; q < N / 8; ++q) {
       u32x4 w = {pack2<TO>(v[8 * q], v[8 * q + 1]), pack2<TO>(v[8 * q + 2], v[8 * q + 3]),
                  pack2<TO>(v[8 * q + 4], v[8 * q + 5]), pack2<TO>(v[8 * q + 6], v[8 * q + 7])};
-      buf_st16<NT>(r, w, off + 16 * q);
+      buf_st16<NT, POL>(r, w, off + 16 * q);
     }
   }
 }

@@ -148,7 +148,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t policy_rsrc(const RowArgs& a, 
 // dlogits pass then loads that row's chunks into xv as it frees them, so the next
 // row's policy loads are in flight under this row's stores. Returns the next row (PF,
 // -1 for none) or -1.
-template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE, bool CACHE, bool PF = false>
+template <typename TI, typename TO, int BLOCK, int NCH, int RB, bool EDGE, bool CACHE, bool PF = false,
+          int SP = kBufNT>
 __device__ __forceinline__ int64_t resident_row(const RowArgs& a, const int64_t row, float* lds, u32x4 (&xv)[NCH],
                                                 int next_listed = -1, bool next_ok = false, int* s_pub = nullptr) {
   static_assert(!(PF && EDGE), "prefetching rows are aligned rows");
@@ -189,18 +190,17 @@ __device__ __forceinline__ int64_t resident_row(const RowArgs& a, const int64_t 
   if (!r.live) {
     write_token_outputs(a, r, 0.f, 0.f, 0.f);
     if (a.dlogits && a.zero_fill) {
-      float z[EPV];
-#pragma unroll
-      for (int j = 0; j < EPV; ++j) z[j] = 0.f;
+      const u32x4 z = {0u, 0u, 0u, 0u};   // 0 bits are 0 in every output type
       if constexpr (kSplit) {
-        const float (&z4)[4] = reinterpret_cast<const float (&)[4]>(z);
 #pragma unroll
         for (int k = 0; k < NCH; ++k)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) buf_store_vals<TO, 4, true>(drow, (k * 2 * BLOCK + 64 * h + sgrp) * 16u, z4);
+          for (int h = 0; h < 2; ++h) buf_st16<true, SP>(drow, z, (k * 2 * BLOCK + 64 * h + sgrp) * 16u);
       } else {
 #pragma unroll
-        for (int k = 0; k < NCH; ++k) buf_store_vals<TO, EPV, true>(drow, (k * BLOCK + tid) * kOutVec, z);
+        for (int k = 0; k < NCH; ++k)
+#pragma unroll
+          for (uint32_t q = 0; q < kOutVec; q += 16) buf_st16<true, SP>(drow, z, (k * BLOCK + tid) * kOutVec + q);
       }
       if (EDGE && ek >= 0) store1<TO>(a.dlogits, row_elem + ek, 0.f);
     }
@@ -427,10 +427,10 @@ __device__ __forceinline__ int64_t resident_row(const RowArgs& a, const int64_t 
       // Groups past the row end sit past the descriptor: their stores are dropped.
       const float (&o0)[4] = reinterpret_cast<const float (&)[4]>(o[0]);
       const float (&o1)[4] = reinterpret_cast<const float (&)[4]>(o[4]);
-      buf_store_vals<TO, 4, true>(drow, fresh_off(sgrp * 16u, k * 2 * BLOCK * 16u), o0);
-      buf_store_vals<TO, 4, true>(drow, fresh_off(sgrp * 16u, k * 2 * BLOCK * 16u + 1024u), o1);
+      buf_store_vals<TO, 4, true, SP>(drow, fresh_off(sgrp * 16u, k * 2 * BLOCK * 16u), o0);
+      buf_store_vals<TO, 4, true, SP>(drow, fresh_off(sgrp * 16u, k * 2 * BLOCK * 16u + 1024u), o1);
     } else {
-      buf_store_vals<TO, EPV, true>(drow, fresh_off(tid * kOutVec, k * BLOCK * kOutVec), o);
+      buf_store_vals<TO, EPV, true, SP>(drow, fresh_off(tid * kOutVec, k * BLOCK * kOutVec), o);
     }
     if constexpr (PF) xv[k] = load_chunk<TI, TO, BLOCK>(nbuf, k, voff, sgrp);
   }
@@ -442,7 +442,7 @@ __device__ __forceinline__ int64_t resident_row(const RowArgs& a, const int64_t 
                             : static_cast<int>((it / EPV) % BLOCK);
   if (it >= 0 && it < static_cast<int64_t>(nv) * EPV && tid == t_lane) {
     const float dy = c - c * hw_exp2(fmaf(xy, kLog2e, -lse2));
-    buf_store1<TO, true>(drow, static_cast<uint32_t>(it) * TO::kBytes, dy);
+    buf_store1<TO, true, SP>(drow, static_cast<uint32_t>(it) * TO::kBytes, dy);
   }
   if constexpr (EDGE) {
     if (ek >= 0) {
@@ -523,11 +523,18 @@ __global__ void __launch_bounds__(BLOCK) grpo_resident_kernel(RowArgs a) {
     }
   }
   {
+    // Zero-fill launches store nontemporal at system scope (written through to memory):
+    // interleaved on one box, 8 / 4 / 4 runs, config 2 3.579 -> 3.546 ms, config 3
+    // 7.007 -> 6.949, config 4 4.718 -> 4.684, exact rounding 3.687 -> 3.631, f32
+    // dlogits 5.470 -> 5.387. Launches without zero-fill keep device-scope nontemporal
+    // stores, which measured 1-1.6% faster there (config 2 3.009 against 3.059 ms,
+    // config 4 2.131 against 2.150).
+    constexpr int kSP = LIST ? kBufNT : kBufNTSystem;
     int64_t row = blockIdx.x;
     for (int i = 0; row < a.nrows; ++i) {
       if (threadIdx.x == 0) s_next[i & 1] = atomicAdd(a.next_row, 1) + static_cast<int>(gridDim.x);
       u32x4 xv[NCH];
-      resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE>(a, row, lds, xv);
+      resident_row<TI, TO, BLOCK, NCH, RB, EDGE, CACHE, false, kSP>(a, row, lds, xv);
       __syncthreads();   // s_next visible; this row's LDS reads done before the next row writes
       row = s_next[i & 1];
     }
