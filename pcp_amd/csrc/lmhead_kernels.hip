@@ -983,6 +983,8 @@ constexpr int kDcacheVocabTiles = 4;
 // nontemporal accesses: each byte is touched once here and read back only by the next
 // launch, so keeping the lines in L2 only delays other traffic (config 5, kernel
 // traces: 2.07 -> 1.85 ms; the same hint on the forward's cache stores cost 0.5 ms).
+// D and Dt stores are nontemporal at system scope (written through to memory): 1.836 ->
+// 1.801 ms at config 5 (kernel traces, three interleaved runs each).
 // A block takes one 64-token tile and kDcacheVocabTiles vocab tiles in turn: the
 // rows' scalars are read once, and each vocab tile's loads are issued before the
 // previous tile's stores, so a wave's wait for them (vector-memory counts retire in
@@ -1072,7 +1074,7 @@ __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
           out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
                       pack2<BF16T>(d[6], d[7])};
         }
-        buf_st16<true>(rd, out, (static_cast<uint32_t>(rr) * ld + static_cast<uint32_t>(c0)) * 2u);
+        buf_st16<true, kBufNTSystem>(rd, out, (static_cast<uint32_t>(rr) * ld + static_cast<uint32_t>(c0)) * 2u);
         tile_put8(t, rr, cc, out);
       }
       __syncthreads();
@@ -1082,7 +1084,7 @@ __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
           const int c = rq + 32 * it, g = tid & 7;
-          buf_st16<true>(rdt, tile_col8(t, 8 * g, c),
+          buf_st16<true, kBufNTSystem>(rdt, tile_col8(t, 8 * g, c),
                          (static_cast<uint32_t>(c) * ldt + static_cast<uint32_t>(r0) + 8u * g) * 2u);
         }
       }
