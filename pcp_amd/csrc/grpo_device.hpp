@@ -147,6 +147,20 @@ __device__ __forceinline__ u32x2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off)
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, NT ? kBufNT : 0));
 }
 
+// Global streaming stores at system scope (sc0 sc1 nt: written through to memory), for
+// kernels that write each byte once and whose output the next launch reads back. No
+// builtin sets these bits on a global store, hence the inline assembly; the compiler
+// does not track these stores, which is safe as nothing in the kernel reads them back.
+__device__ __forceinline__ void store_nt_sys(u32x4 v, void* p) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_nt_sys(u32x2 v, void* p) {
+  asm volatile("global_store_dwordx2 %0, %1, off sc0 sc1 nt" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_nt_sys(uint32_t v, void* p) {
+  asm volatile("global_store_dword %0, %1, off sc0 sc1 nt" ::"v"(p), "v"(v) : "memory");
+}
+
 // POL: the cache policy of an NT access (kBufNT or kBufNTSystem).
 template <bool NT, int POL = kBufNT>
 __device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, u32x4 v, uint32_t off) {
