@@ -128,11 +128,16 @@ def test_noalloc_without_zero_fill_walks_the_listed_rows():
         assert abs(float(got["loss"]) - exp.loss) <= 1e-5 * scale, (got["loss"], exp.loss)
 
 
-def test_noalloc_rejects_requests_beyond_its_array():
-    # 2^20 + 1 tokens of per-token losses do not fit next to the other buffers in 4 MiB.
+@pytest.mark.parametrize("overflow", ["token_loss", "row_list"])
+def test_noalloc_rejects_requests_beyond_its_array(overflow):
+    # 2^20 + 1 rows do not fit next to the other buffers in 4 MiB: as per-token losses
+    # (token_loss NULL), or as the live-row list alone (token_loss given, dlogits without
+    # zero-fill: one 4-byte entry per row).
     a = _lib.default_args()
     a.n_seq, a.rows, a.vocab, a.group_size = 1, (1 << 20) + 1, 16, 1
     a.logits, a.ids, a.advantages = 0x1000, 0x2000, 0x3000
+    if overflow == "row_list":
+        a.token_loss, a.dlogits, a.flags = 0x4000, 0x5000, _lib.FLAG_NO_ZERO_FILL
     ctx = grpo.default_context(0)
     rc = lib().pcp_grpo_loss_fwd_bwd_noalloc(ctx.handle, ctypes.byref(a))
     assert rc == -9
