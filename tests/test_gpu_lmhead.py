@@ -567,6 +567,43 @@ def test_lmhead_graph_capture_replays(chunk, exact):
     ctx.sync()
 
 
+def test_release_workspace_then_call_again():
+    """pcp_release_workspace frees the context's work buffers (the loss path's scratch and
+    the LM head's softmax cache); calls after it allocate again and give the same bits as
+    before (no state lives only in a freed buffer), and pcp_workspace_bytes reads 0 in
+    between. A private context, so the other tests' default context keeps its buffers."""
+    c = make_case(2, 70, 128, 900, 2, seed=47, lengths=[70, 33])
+    old = np.full((2, 70), -7.0, np.float32)
+    args = (dev(c["hb"]), dev(c["wb"]), dev(c["ids"]), dev(c["mask"]))
+    kw = dict(ref_weight=dev(c["rb"]), rewards=dev(c["rewards"]), group_size=2, old_logp=dev(old),
+              loss_mode=LossMode.GRPO_CLIP_KL)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(5)
+    logits = (torch.randn((4, 64, 1000), generator=gen, device="cuda:0") * 3).to(torch.bfloat16)
+    ids = torch.randint(0, 1000, (4, 64), generator=gen, device="cuda:0")
+    mask = (torch.arange(64, device="cuda:0")[None] < torch.tensor([[64], [10], [40], [1]], device="cuda:0")).float()
+    rewards = torch.rand((4,), generator=gen, device="cuda:0")
+    ctx = grpo.Context(0)
+    try:
+        def run():
+            lm = grpo.lmhead_fwd_bwd(*args, ctx=ctx, **kw)
+            loss = grpo.grpo_loss_fwd_bwd(logits, ids, mask, rewards=rewards, group_size=2, ctx=ctx)
+            return lm, loss
+        want_lm, want_loss = run()
+        assert ctx.workspace_bytes() > 0
+        ctx.release_workspace()
+        assert ctx.workspace_bytes() == 0
+        ctx.release_workspace()   # nothing held: returns at once
+        got_lm, got_loss = run()
+        assert ctx.workspace_bytes() > 0
+        for f in ("loss", "logp", "ref_logp", "token_loss", "advantages", "dhidden", "dweight"):
+            assert torch.equal(getattr(got_lm, f), getattr(want_lm, f)), f
+        for f in ("loss", "dlogits", "logp", "token_loss", "advantages"):
+            assert torch.equal(getattr(got_loss, f), getattr(want_loss, f)), f
+    finally:
+        ctx.close()
+
+
 def test_synth_lmhead_tokens_gumbel_argmax():
     """pcp_synth_lmhead_tokens (config 5's target ids) draws argmax_v(logit + g) per row
     with g = -log(-log u), u from Philox(seed + chunk index, tag 3, row-in-chunk * V + v)
