@@ -204,3 +204,54 @@ def test_no_zero_fill_listed_rows_prefetch(dt, V, odt):
     got = orc.bf16_to_f32(got_bits) if odt == "bf16" else got_bits.astype(np.float32)
     assert_dlogits(got[~dead], want.dlogits[~dead], fl[~dead], odt == "bf16")
     assert abs(float(out.loss.cpu()) - want.loss) <= full_loss_tol(want, x, ids, mask, T, 0, odt_orc, False, 0.04, S)
+
+
+# Live-row counts around the persistent grid's size (one workgroup per resident slot,
+# a few hundred to about a thousand here): none, one, fewer than the grid, between one
+# and two grids (the second rows come from the first claim, not the counter), more,
+# and either side of the switch to visiting every row (half of 8192 rows).
+LIVE_COUNTS = [0, 1, 37, 255, 256, 257, 511, 512, 513, 767, 1023, 1024, 1025, 1537, 2049, 4095, 4096]
+
+
+@pytest.fixture(scope="module")
+def count_inputs():
+    S, T, V = 16, 512, 4096
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(77)
+    x = torch.randn((S, T, V), generator=gen, device=DEV) * 3
+    r = x + torch.randn((S, T, V), generator=gen, device=DEV) * 0.1
+    ids = torch.randint(0, V, (S, T), generator=gen, device=DEV)
+    old = torch.randn((S, T), generator=gen, device=DEV) * 0.05 - float(np.log(V))
+    rewards = torch.rand((S,), generator=gen, device=DEV)
+    return dict(S=S, T=T, V=V, x={"bf16": x.to(torch.bfloat16), "f32": x}, r={"bf16": r.to(torch.bfloat16), "f32": r},
+                ids=ids, old=old, rewards=rewards)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("n_live", LIVE_COUNTS)
+def test_no_zero_fill_live_counts(count_inputs, n_live, dt):
+    """Exactly n_live live rows at random places: the call without zero-fill (listed rows
+    with the next-row prefetch below half live, every row in order from half on) gives
+    the zero-fill call's outputs bit for bit on live rows and leaves every dead row's
+    dlogits as they were."""
+    c = count_inputs
+    S, T, V = c["S"], c["T"], c["V"]
+    rng = np.random.default_rng(1000 + n_live)
+    flat = np.zeros(S * T, np.float32)
+    flat[rng.choice(S * T, size=n_live, replace=False)] = 1.0
+    mask = torch.from_numpy(flat.reshape(S, T)).to(DEV)
+    kw = dict(rewards=c["rewards"], group_size=4, ref_logits=c["r"][dt], old_logp=c["old"],
+              loss_mode=LossMode.GRPO_CLIP_KL)
+    x = c["x"][dt]
+    sentinel = -3.5
+    dl = torch.full((S, T, V), sentinel, dtype=x.dtype, device=DEV)
+    print(f"live rows {n_live} of {S * T} ({dt})", flush=True)
+    got = grpo.grpo_loss_fwd_bwd(x, c["ids"], mask, dlogits=dl, zero_fill=False, **kw)
+    want = grpo.grpo_loss_fwd_bwd(x, c["ids"], mask, **kw)
+    torch.cuda.synchronize()
+    live = mask != 0
+    assert torch.equal(got.dlogits[live], want.dlogits[live])
+    assert bool((got.dlogits[~live] == sentinel).all()), "a dead row was written"
+    assert bool((want.dlogits[~live] == 0).all())
+    for f in ("loss", "logp", "ref_logp", "token_loss", "advantages"):
+        assert torch.equal(getattr(got, f), getattr(want, f)), f
