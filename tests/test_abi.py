@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -493,3 +494,13 @@ def test_mfma_peak_argument_errors_without_device():
     assert L.pcp_mfma_peak(None, 0, 1, 2, 0, 0x1000, 0x2004, None) == -1
     assert L.pcp_mfma_peak(None, 1, 1, 2, 0, 0x1000, 0x2000, None) == -1
     assert "context is NULL" in L.pcp_last_error(None).decode()
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 exits with status 2 and a JSON line that says this
+    build runs on one GPU (before it touches a device)."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    p = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], cwd=root,
+                       capture_output=True, text=True, timeout=300)
+    assert p.returncode == 2, (p.returncode, p.stderr[-500:])
+    assert "one GPU only" in p.stdout
