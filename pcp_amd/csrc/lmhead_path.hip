@@ -11,8 +11,9 @@
 // (the same kernels as the logits-input path).
 // Backward, by default: the policy forward also stored its softmax terms (f16, or f32
 // with PCP_FLAG_EXACT_BF16); one pass turns them into bf16 dlogits D (in place over
-// f16 terms, beside f32 ones) and writes D^T, W is transposed once, and one launch of
-// the MFMA tile kernel (kLmGemm, both operands K-contiguous) runs
+// f16 terms, beside f32 ones) and writes D^T, the policy forward's tiles also write W^T
+// from the W slabs they hold, and one launch of the MFMA tile kernel (kLmGemm, both
+// operands K-contiguous) runs
 //   dhidden = D * W      over the whole vocabulary (rows: live tokens), and
 //   dW      = D^T * hidden over the live tokens (rows: vocab).
 // Chunked backward (an explicit vocab_chunk, or a workspace past cache_budget):
