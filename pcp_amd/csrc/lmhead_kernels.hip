@@ -508,8 +508,16 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
   constexpr int kBuf = TL ? kStageBytes : kOpBytes;
   const uint32_t wbytes = static_cast<uint32_t>(ldb) * 2u, hbytes = static_cast<uint32_t>(lda) * 2u;
   const int rows_w = min(BV, V - v0), rows_h = min(BT, N - m0);
+  // A tile-major B (the cached backward's D, D^T; lm_tile_block_off): the tile's stages
+  // are consecutive 32 KB blocks. Its rows past V hold whatever was there; they only
+  // reach result rows past V, which are not stored.
+  const bool btile = !TL && g.b_tiled;
   const __amdgpu_buffer_rsrc_t rw =
-      row_rsrc(reinterpret_cast<const char*>(opB) + static_cast<int64_t>(v0) * wbytes, rows_w * wbytes);
+      btile ? row_rsrc(reinterpret_cast<const char*>(opB) + static_cast<int64_t>(v0 / BV) * (ldb / BK) * kOpBytes,
+                       static_cast<uint32_t>(ldb / BK) * kOpBytes)
+            : row_rsrc(reinterpret_cast<const char*>(opB) + static_cast<int64_t>(v0) * wbytes, rows_w * wbytes);
+  const uint32_t wrow = btile ? static_cast<uint32_t>(ROWB) : wbytes;   // bytes between B rows
+  const uint32_t wstage = btile ? static_cast<uint32_t>(kOpBytes) : static_cast<uint32_t>(ROWB);
   const __amdgpu_buffer_rsrc_t rh =
       row_rsrc(reinterpret_cast<const char*>(opA) + static_cast<int64_t>(m0) * hbytes, TL ? rows_h * hbytes : 0u);
   uint32_t dofw[QN], dofh[QN];
@@ -517,15 +525,16 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
   for (int q = 0; q < QN; ++q) {
     const int row = 8 * (QN * wave + q) + (lane >> 3);
     const uint32_t c16 = 16u * static_cast<uint32_t>((lane & 7) ^ lm_swz(row));
-    dofw[q] = static_cast<uint32_t>(row) * wbytes + c16;
+    dofw[q] = static_cast<uint32_t>(row) * wrow + c16;
     dofh[q] = static_cast<uint32_t>(row) * hbytes + c16;
   }
   auto issue = [&](int st, int buf) {
     char* base = smem + buf * kBuf;
     const uint32_t koff = static_cast<uint32_t>(st) * ROWB;
+    const uint32_t kofw = static_cast<uint32_t>(st) * wstage;
 #pragma unroll
     for (int q = 0; q < QN; ++q) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (QN * wave + q) * 1024), 16, dofw[q] + koff, 0, 0,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, LM_LDS(base + (QN * wave + q) * 1024), 16, dofw[q] + kofw, 0, 0,
                                                0);
       if constexpr (TL)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, LM_LDS(base + kOpBytes + (QN * wave + q) * 1024), 16,
@@ -764,8 +773,9 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
             dst[1] = w1;
           }
         } else if (ECACHE && prod == 0) {
-          // Softmax cache: ecache[n][v] = f16(2^(x*log2e - ref)), token-major rows of lde
-          // (vocab past V holds 0). The lane's terms of block (i, j) are vocab rows
+          // Softmax cache: ecache[n][v] = f16(2^(x*log2e - ref)) in the products' tile-major
+          // layout (lm_tile_block_off, K extent lde; vocab past V holds 0), which the
+          // dlogits pass rewrites in place as D. The lane's terms of block (i, j) are vocab rows
           // 16 i + 4 grp + 0..3 of token column 16 j + lane % 16. One v_permlane16_swap
           // per register trades the odd groups' block-jj terms with the even groups'
           // block-(jj+1) terms, after which lanes of an even group hold 8 consecutive rows
@@ -777,7 +787,7 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
           const int64_t c = vw + 16 * i + 8 * (grp >> 1);
           if (n < N && c < a.lde) {
             const u32x4 w = {lo[0], hi[0], lo[1], hi[1]};
-            *reinterpret_cast<u32x4*>(a.ecache + static_cast<int64_t>(n) * a.lde + c) = w;
+            *reinterpret_cast<u32x4*>(a.ecache + lm_tile_block_off(n, c, a.lde)) = w;
           }
         }
       }
@@ -973,9 +983,10 @@ __device__ __forceinline__ u32x4 tile_col8(const uint16_t* t, int r, int c) {
 constexpr int kDcacheVocabTiles = 4;
 
 // dlogits from the forward's softmax cache, per 64 x 64 tile (tokens x vocab): D is
-// written in place over the cache (f16 terms -> bf16, token-major, the dhidden
-// product's operand) and transposed through LDS into Dt [ldv, ldt] (vocab-major,
-// the dW product's operand; tokens past n are 0). D[n][v] = -c_n * e * 2^(ref -
+// written in place over the cache (f16 terms -> bf16; the dhidden product's operand,
+// tile-major with K extent ld: lm_tile_block_off) and transposed through LDS into Dt
+// (the dW product's operand: vocab rows, tile-major with K extent ldt; tokens past n
+// are 0). Each 64 x 64 tile is 8 KB contiguous in both. D[n][v] = -c_n * e * 2^(ref -
 // lse2_n), with ref the exponent reference of v's 128-entry partial (from the
 // policy's partials), except at the target, where D = c_n - c_n * 2^(tgt_n*log2e -
 // lse2_n) from the f32 target logit, as the recomputing backward forms it. Columns
@@ -989,10 +1000,9 @@ constexpr int kDcacheVocabTiles = 4;
 // rows' scalars are read once, and each vocab tile's loads are issued before the
 // previous tile's stores, so a wave's wait for them (vector-memory counts retire in
 // issue order) does not include those stores. All accesses go through per-tile
-// buffer descriptors with 32-bit offsets (the host checks ld and ldt), which keeps the
-// kernel at 64 VGPRs, eight waves per SIMD.
-// F32: the terms are f32 at a.src32 (the exact-rounding forward) and D goes to a.d
-// beside them, not in place.
+// buffer descriptors with 32-bit offsets (the host checks ld and ldt).
+// F32: the terms are f32 at a.src32 (the exact-rounding forward, token-major rows of
+// ld) and D goes to a.d beside them, not in place.
 template <bool F32>
 __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
   __shared__ uint16_t t[64 * kTilePitch];    // [token][vocab] bf16
@@ -1001,13 +1011,14 @@ __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
   const int64_t ntile = (n + 63) / 64;     // token tiles that the dW product reads
   const int cc = (tid & 7) * 8;            // the thread's 8 columns of a vocab tile
   const int rq = tid >> 3;                 // and its rows rq, rq + 32 of the token tile
-  const uint32_t ld = static_cast<uint32_t>(a.ld), ldt = static_cast<uint32_t>(a.ldt);
+  const uint32_t ld = static_cast<uint32_t>(a.ld);   // the f32 terms' row stride (F32)
   const int64_t vbase = static_cast<int64_t>(blockIdx.y) * kDcacheVocabTiles * 64;
   for (int64_t tb = blockIdx.x; tb < ntile; tb += gridDim.x) {
     const int64_t r0 = tb * 64;
     const uint32_t nr = static_cast<uint32_t>(min<int64_t>(64, n - r0));   // rows past n read 0, stores drop
-    const __amdgpu_buffer_rsrc_t rd = row_rsrc(a.d + r0 * a.ld, nr * ld * 2u);
-    const __amdgpu_buffer_rsrc_t rs = F32 ? row_rsrc(a.src32 + r0 * a.ld, nr * ld * 4u) : rd;
+    // D's 64 x 64 tile at vocab v0: 8 KB, row rr at 128 rr (rows past n: reads 0, stores drop).
+    auto dtile = [&](int64_t v0) { return row_rsrc(a.d + lm_tile_block_off(r0, v0, a.ld), nr * 128u); };
+    const __amdgpu_buffer_rsrc_t rs = row_rsrc(F32 ? a.src32 + r0 * a.ld : nullptr, F32 ? nr * ld * 4u : 0u);
     const __amdgpu_buffer_rsrc_t rp = row_rsrc(a.part + r0 * a.ldp, nr * static_cast<uint32_t>(a.ldp) * 8u);
     float cf[2], l2[2], tg[2];
     int id[2];
@@ -1038,7 +1049,7 @@ __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
           w[q][it] = buf_ld16<true>(rs, (rr * ld + c0) * 4u);
           w2[q][it] = buf_ld16<true>(rs, (rr * ld + c0) * 4u + 16u);
         } else {
-          w[q][it] = buf_ld16<true>(rd, (rr * ld + c0) * 2u);
+          w[q][it] = buf_ld16<true>(dtile(v0), rr * 128u + static_cast<uint32_t>(cc) * 2u);
         }
         m2[q][it] = __uint_as_float(
             __builtin_amdgcn_raw_buffer_load_b32(rp, (rr * static_cast<uint32_t>(a.ldp) + pi) * 8u, 0, 0));
@@ -1074,18 +1085,18 @@ __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
           out = u32x4{pack2<BF16T>(d[0], d[1]), pack2<BF16T>(d[2], d[3]), pack2<BF16T>(d[4], d[5]),
                       pack2<BF16T>(d[6], d[7])};
         }
-        buf_st16<true, kBufNTSystem>(rd, out, (static_cast<uint32_t>(rr) * ld + static_cast<uint32_t>(c0)) * 2u);
+        buf_st16<true, kBufNTSystem>(dtile(v0), out, static_cast<uint32_t>(rr) * 128u + static_cast<uint32_t>(cc) * 2u);
         tile_put8(t, rr, cc, out);
       }
       __syncthreads();
-      // Dt row v0 + c, tokens r0 + 8g .. +7: eight lanes write one row's 128 bytes.
+      // Dt row v0 + c, tokens r0 + 8g .. +7: eight lanes write one row's 128 bytes, the
+      // tile's 64 rows one 8 KB block piece.
       if (a.dt) {
-        const __amdgpu_buffer_rsrc_t rdt = row_rsrc(a.dt + v0 * a.ldt, 64u * ldt * 2u);
+        const __amdgpu_buffer_rsrc_t rdt = row_rsrc(a.dt + lm_tile_block_off(v0, r0, a.ldt), 64u * 128u);
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
           const int c = rq + 32 * it, g = tid & 7;
-          buf_st16<true, kBufNTSystem>(rdt, tile_col8(t, 8 * g, c),
-                         (static_cast<uint32_t>(c) * ldt + static_cast<uint32_t>(r0) + 8u * g) * 2u);
+          buf_st16<true, kBufNTSystem>(rdt, tile_col8(t, 8 * g, c), static_cast<uint32_t>(c) * 128u + 16u * g);
         }
       }
       __syncthreads();
@@ -1324,6 +1335,13 @@ hipError_t launch_lm_gemms(const LmTileArgs::Gemm* g, int n_gemm, bool k_major_a
   const bool frag = a.n_gemm > 0 && a.gemm[0].a_frag;
   if (a.n_gemm > 1 && (a.gemm[1].a_frag != 0) != frag) return hipErrorInvalidValue;   // one layout per launch
   if (frag && k_major_a) return hipErrorInvalidValue;
+  for (int p = 0; p < a.n_gemm; ++p) {
+    const LmTileArgs::Gemm& q = a.gemm[p];
+    // Tile-major B: fragment-major launches only (the 16x16x32 tile reads it), whole
+    // 64-deep blocks, a tile's K extent (ldb / 64 blocks of 32 KB) in 32-bit offsets.
+    if (q.b_tiled && (!frag || q.ldb % 64 != 0 || q.K > q.ldb || static_cast<int64_t>(q.ldb / 64) * 32768 >= (int64_t{1} << 32)))
+      return hipErrorInvalidValue;
+  }
   if (frag) return launch_tiles_mode<kLmGemm, false, false, true>(a, grid, st);
   if (!k_major_a) return launch_tiles_mode<kLmGemm, false, false>(a, grid, st);
   return launch_tiles_mode<kLmGemm>(a, grid, st);

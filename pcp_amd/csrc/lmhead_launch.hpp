@@ -14,6 +14,15 @@ constexpr int kLmTileV = 256;    // vocab entries per tile
 constexpr int kLmTileT = 256;    // tokens per tile
 constexpr int kLmPart = 128;     // vocab entries per log-sum-exp partial
 
+// Tile-major bf16 operand of the products (the cached backward's D and D^T): 32 KB
+// blocks of [256 rows][64 k], block (r / 256, k / 64) at element
+// ((r / 256) * (ld / 64) + k / 64) * 16384, row r % 256 at 64 (r % 256) within it, so
+// one product stage (256 rows x 64 k) is one contiguous block and a 64 x 64 tile of
+// the dlogits pass is 8 KB contiguous. ld: the K extent, a multiple of 64.
+__host__ __device__ __forceinline__ int64_t lm_tile_block_off(int64_t r, int64_t k, int64_t ld) {
+  return ((r >> 8) * (ld >> 6) + (k >> 6)) * 16384 + (r & 255) * 64 + (k & 63);
+}
+
 // One launch covers token tiles [0, ntt) x vocab tiles [vt0, vt0 + nvt) of
 // kLmTileT x kLmTileV. kLmGemm reuses the roles for plain products
 // C[v][t] = sum_k B[v][k] * A[t][k] (both operands K-contiguous, bf16): "vocab" rows
@@ -36,8 +45,9 @@ struct LmTileArgs {
   const void* B2;       // [V, H] bf16: model 1's weight
   float2* part2;
   float* tgt2;
-  uint16_t* ecache;     // or nullptr: [N, lde] f16 softmax terms 2^(x*log2e - ref) of the
-  int64_t lde;          //   partial's reference ref (lde % 64 == 0, >= V; 0 past V)
+  uint16_t* ecache;     // or nullptr: f16 softmax terms 2^(x*log2e - ref) of the partial's
+  int64_t lde;          //   reference ref, tile-major (lm_tile_block_off: token rows, K extent
+                        //   lde; lde % 64 == 0, >= V; 0 past V)
   float* ecache32;      // or nullptr: the same terms as f32 (ecache then nullptr)
   uint16_t* wt;         // or nullptr: W^T [H, ldwt] fragment-major (launch_lm_transpose_frag's layout),
   int64_t ldwt;         //   written by model 0's tiles from their W slabs (ldwt % 64 == 0, >= V)
@@ -59,6 +69,9 @@ struct LmTileArgs {
     int krows_a;        // K-major A: rows that exist; rows [krows_a, K) read as 0
     int a_frag;         // A stored fragment-major (launch_lm_transpose_frag, K extent lda): read
                         //   straight into registers; both products of a launch alike
+    int b_tiled;        // (a_frag only) B stored tile-major: 32 KB blocks of [256 rows][64 k],
+                        //   block (v / 256, k / 64) at byte ((v / 256) * (ldb / 64) + k / 64) * 32768,
+                        //   row v % 256 at 128 (v % 256) within it (lm_tile_block_off)
     const int* vcount;  // or nullptr: V = *vcount (<= V; tiles past it exit)
     const int* kcount;  // or nullptr: K = *kcount rounded up to 64 (<= K), krows_a = *kcount
     float* C;           // f32 result: row v, column t at C[v * ldc + t], or at
@@ -85,11 +98,12 @@ struct LmTransposeArgs {
 // and the same values transposed into dt[v][n], zero for *count <= n < *count rounded
 // up to 64 (columns past that are not written).
 struct LmDcacheArgs {
-  uint16_t* d;            // [ldt, ld] bf16 D, written over the f16 terms there (src32 nullptr)
-  const float* src32;     // or [ldt, ld] f32 terms, read in place of d's
+  uint16_t* d;            // bf16 D, tile-major (lm_tile_block_off: token rows, K extent ld),
+                          //   written over the f16 terms the forward stored there (src32 nullptr)
+  const float* src32;     // or [ldt, ld] f32 terms (token-major), read in place of d's
   int64_t ld;             // multiple of 64, >= V
   const int* count;       // [1] live tokens (device)
-  uint16_t* dt;           // [ld, ldt] or nullptr
+  uint16_t* dt;           // D^T, tile-major (vocab rows, K extent ldt), or nullptr
   int64_t ldt;            // multiple of 64, >= *count
   int64_t V;
   const float2* part;     // [n, ldp] the policy's forward partials

@@ -183,27 +183,32 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const int mask_u8 = a->mask_dtype == PCP_BOOL;
 
   // The backward's bf16 operands, sized for all N tokens (the live count stays on the
-  // device). By default: the whole-vocabulary softmax cache [N, ldv] (the policy forward
-  // stores its f16 terms there; a pass rewrites them as dlogits D and writes D^T
-  // [ldv, ldt] beside it) and W^T [H, ldv], so both products read K-contiguous
-  // operands. With PCP_FLAG_EXACT_BF16 the terms are f32 [N, ldv] and D follows them
+  // device). By default: the whole-vocabulary softmax cache (the policy forward stores
+  // its f16 terms there, tile-major over token rows with K extent ldv; a pass rewrites
+  // them in place as dlogits D and writes D^T, tile-major over vocab rows with K extent
+  // ldt, beside it) and W^T [H, ldv], so both products read K-contiguous operands.
+  // With PCP_FLAG_EXACT_BF16 the terms are f32 [N, ldv] (token-major) and D follows them
   // (D is then the f32 value rounded once). With an explicit vocab_chunk, more than
   // cache_budget bytes, or no memory for them: one dlogits chunk [N, chunk] that the
   // backward refills by recomputing the logits.
+  // D and D^T are tile-major (lm_tile_block_off: 32 KB blocks of 256 rows x 64 k), so
+  // their rows round up to 256: D's token rows ldr, D^T's vocab rows ldv256.
   const bool exact = (a->flags & PCP_FLAG_EXACT_BF16) != 0;
   const int64_t ldv = (V + 63) / 64 * 64;
   const int64_t ldt = ldt_max;
+  const int64_t ldr = (ldt + 255) / 256 * 256, ldv256 = (ldv + 255) / 256 * 256;
   const size_t o_d = exact ? 4 * static_cast<size_t>(ldt) * ldv : 0;
-  const size_t o_dt = o_d + 2 * static_cast<size_t>(ldt) * ldv;
-  const size_t o_wt = o_dt + (a->dweight ? 2 * static_cast<size_t>(ldv) * ldt : 0);
+  const size_t o_dt = o_d + 2 * static_cast<size_t>(ldr) * ldv;
+  const size_t o_wt = o_dt + (a->dweight ? 2 * static_cast<size_t>(ldv256) * ldt : 0);
   const size_t cache_bytes = o_wt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
   const size_t o_cdt = 2 * static_cast<size_t>(ldt) * chunk;
   const size_t o_cwt = o_cdt + (a->dweight ? 2 * static_cast<size_t>(chunk) * ldt : 0);
   const size_t chunk_frag_bytes = o_cwt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
   bool cached = false, chunk_frag = false;
-  // The dlogits pass addresses a 64-token tile of the cache and 64 rows of D^T with
-  // 32-bit offsets (launch_lm_dcache): larger shapes take the chunked backward.
-  const bool cache_fits = ldv < (int64_t{1} << 24) && ldt < (int64_t{1} << 25);
+  // 32-bit offsets: a 64-token tile of f32 terms in the dlogits pass (launch_lm_dcache)
+  // and a product tile's K extent of tile-major D or D^T (ld / 64 blocks of 32 KB,
+  // launch_lm_gemms): larger shapes take the chunked backward.
+  const bool cache_fits = ldv < (int64_t{1} << 23) && ldt < (int64_t{1} << 23);
   // W^T comes out of the forward while one stage's four fragment rows fit 32-bit offsets.
   const bool wt_fwd = ldv < (int64_t{1} << 25);
   if (bwd) {
@@ -439,6 +444,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         // dhidden_c[t][h] = sum_v D[t][v] * W^T[h][v].
         LmTileArgs::Gemm& d = g[ng++];
         d.B = dd;
+        d.b_tiled = 1;
         d.ldb = static_cast<int>(ldv);
         d.V = static_cast<int>(N);
         d.vcount = cnt;
@@ -456,6 +462,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
         // dW[v][h] = sum_t D^T[v][t] * hidden^T[h][t].
         LmTileArgs::Gemm& d = g[ng++];
         d.B = dt;
+        d.b_tiled = 1;
         d.ldb = static_cast<int>(ldt);
         d.V = static_cast<int>(V);
         d.A = sp + o_ht;
