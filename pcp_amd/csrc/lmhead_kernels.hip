@@ -767,8 +767,8 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
           }
           const int n = m0 + wt * TW + 16 * (jj + (grp & 1)) + (lane & 15);
           const int64_t c = vw + 16 * i + 8 * (grp >> 1);
-          if (n < N && c < a.lde) {
-            u32x4* dst = reinterpret_cast<u32x4*>(a.ecache32 + static_cast<int64_t>(n) * a.lde + c);
+          if (n < N && c < a.lde) {   // tile-major as the f16 cache (64 KB blocks of f32)
+            u32x4* dst = reinterpret_cast<u32x4*>(a.ecache32 + lm_tile_block_off(n, c, a.lde));
             dst[0] = w0;
             dst[1] = w1;
           }
@@ -1001,8 +1001,8 @@ constexpr int kDcacheVocabTiles = 4;
 // previous tile's stores, so a wave's wait for them (vector-memory counts retire in
 // issue order) does not include those stores. All accesses go through per-tile
 // buffer descriptors with 32-bit offsets (the host checks ld and ldt).
-// F32: the terms are f32 at a.src32 (the exact-rounding forward, token-major rows of
-// ld) and D goes to a.d beside them, not in place.
+// F32: the terms are f32 at a.src32 (the exact-rounding forward, tile-major as D) and D
+// goes to a.d beside them, not in place.
 template <bool F32>
 __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
   __shared__ uint16_t t[64 * kTilePitch];    // [token][vocab] bf16
@@ -1011,14 +1011,14 @@ __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
   const int64_t ntile = (n + 63) / 64;     // token tiles that the dW product reads
   const int cc = (tid & 7) * 8;            // the thread's 8 columns of a vocab tile
   const int rq = tid >> 3;                 // and its rows rq, rq + 32 of the token tile
-  const uint32_t ld = static_cast<uint32_t>(a.ld);   // the f32 terms' row stride (F32)
   const int64_t vbase = static_cast<int64_t>(blockIdx.y) * kDcacheVocabTiles * 64;
   for (int64_t tb = blockIdx.x; tb < ntile; tb += gridDim.x) {
     const int64_t r0 = tb * 64;
     const uint32_t nr = static_cast<uint32_t>(min<int64_t>(64, n - r0));   // rows past n read 0, stores drop
     // D's 64 x 64 tile at vocab v0: 8 KB, row rr at 128 rr (rows past n: reads 0, stores drop).
     auto dtile = [&](int64_t v0) { return row_rsrc(a.d + lm_tile_block_off(r0, v0, a.ld), nr * 128u); };
-    const __amdgpu_buffer_rsrc_t rs = row_rsrc(F32 ? a.src32 + r0 * a.ld : nullptr, F32 ? nr * ld * 4u : 0u);
+    // F32: the terms' 64 x 64 tile at vocab v0, tile-major as D (rows of 256 bytes).
+    auto stile = [&](int64_t v0) { return row_rsrc(a.src32 + lm_tile_block_off(r0, v0, a.ld), nr * 256u); };
     const __amdgpu_buffer_rsrc_t rp = row_rsrc(a.part + r0 * a.ldp, nr * static_cast<uint32_t>(a.ldp) * 8u);
     float cf[2], l2[2], tg[2];
     int id[2];
@@ -1046,8 +1046,9 @@ __device__ __forceinline__ void lm_dcache_body(const LmDcacheArgs& a) {
       for (int it = 0; it < 2; ++it) {
         const uint32_t rr = static_cast<uint32_t>(rq + 32 * it);
         if constexpr (F32) {
-          w[q][it] = buf_ld16<true>(rs, (rr * ld + c0) * 4u);
-          w2[q][it] = buf_ld16<true>(rs, (rr * ld + c0) * 4u + 16u);
+          const __amdgpu_buffer_rsrc_t rs = stile(v0);
+          w[q][it] = buf_ld16<true>(rs, rr * 256u + static_cast<uint32_t>(cc) * 4u);
+          w2[q][it] = buf_ld16<true>(rs, rr * 256u + static_cast<uint32_t>(cc) * 4u + 16u);
         } else {
           w[q][it] = buf_ld16<true>(dtile(v0), rr * 128u + static_cast<uint32_t>(cc) * 2u);
         }

@@ -48,7 +48,7 @@ struct LmTileArgs {
   uint16_t* ecache;     // or nullptr: f16 softmax terms 2^(x*log2e - ref) of the partial's
   int64_t lde;          //   reference ref, tile-major (lm_tile_block_off: token rows, K extent
                         //   lde; lde % 64 == 0, >= V; 0 past V)
-  float* ecache32;      // or nullptr: the same terms as f32 (ecache then nullptr)
+  float* ecache32;      // or nullptr: the same terms as f32, in the same layout (ecache then nullptr)
   uint16_t* wt;         // or nullptr: W^T [H, ldwt] fragment-major (launch_lm_transpose_frag's layout),
   int64_t ldwt;         //   written by model 0's tiles from their W slabs (ldwt % 64 == 0, >= V)
   // kLmBwd
@@ -100,7 +100,7 @@ struct LmTransposeArgs {
 struct LmDcacheArgs {
   uint16_t* d;            // bf16 D, tile-major (lm_tile_block_off: token rows, K extent ld),
                           //   written over the f16 terms the forward stored there (src32 nullptr)
-  const float* src32;     // or [ldt, ld] f32 terms (token-major), read in place of d's
+  const float* src32;     // or the f32 terms (tile-major as d), read in place of d's
   int64_t ld;             // multiple of 64, >= V
   const int* count;       // [1] live tokens (device)
   uint16_t* dt;           // D^T, tile-major (vocab rows, K extent ldt), or nullptr

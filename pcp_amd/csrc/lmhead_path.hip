@@ -187,7 +187,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   // its f16 terms there, tile-major over token rows with K extent ldv; a pass rewrites
   // them in place as dlogits D and writes D^T, tile-major over vocab rows with K extent
   // ldt, beside it) and W^T [H, ldv], so both products read K-contiguous operands.
-  // With PCP_FLAG_EXACT_BF16 the terms are f32 [N, ldv] (token-major) and D follows them
+  // With PCP_FLAG_EXACT_BF16 the terms are f32, in the same layout, and D follows them
   // (D is then the f32 value rounded once). With an explicit vocab_chunk, more than
   // cache_budget bytes, or no memory for them: one dlogits chunk [N, chunk] that the
   // backward refills by recomputing the logits.
@@ -197,7 +197,7 @@ int run_lm(pcp_ctx* ctx, const pcp_lmhead_args* a) {
   const int64_t ldv = (V + 63) / 64 * 64;
   const int64_t ldt = ldt_max;
   const int64_t ldr = (ldt + 255) / 256 * 256, ldv256 = (ldv + 255) / 256 * 256;
-  const size_t o_d = exact ? 4 * static_cast<size_t>(ldt) * ldv : 0;
+  const size_t o_d = exact ? 4 * static_cast<size_t>(ldr) * ldv : 0;
   const size_t o_dt = o_d + 2 * static_cast<size_t>(ldr) * ldv;
   const size_t o_wt = o_dt + (a->dweight ? 2 * static_cast<size_t>(ldv256) * ldt : 0);
   const size_t cache_bytes = o_wt + (want_dy ? 2 * static_cast<size_t>(H) * ldv : 0);
