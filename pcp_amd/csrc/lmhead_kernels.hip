@@ -978,9 +978,10 @@ __device__ __forceinline__ u32x4 tile_col8(const uint16_t* t, int r, int c) {
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
-// Vocab tiles of 64 per lm_dcache_kernel block: fewer blocks, so fewer of them idle
-// past the live token count.
-constexpr int kDcacheVocabTiles = 4;
+// Vocab tiles of 64 per lm_dcache_kernel block. With tile-major D and D^T, config 5
+// (kernel traces, interleaved on one box): 1 tile 1.685 ms, 2 tiles 1.616-1.621 ms,
+// 4 tiles 1.679, 8 tiles 1.696.
+constexpr int kDcacheVocabTiles = 2;
 
 // dlogits from the forward's softmax cache, per 64 x 64 tile (tokens x vocab): D is
 // written in place over the cache (f16 terms -> bf16; the dhidden product's operand,
