@@ -192,8 +192,8 @@ const char* pcp_last_error(const pcp_ctx* ctx);
 /* Wait for work enqueued with PCP_FLAG_ASYNC; returns the first device-side error. */
 int pcp_sync(pcp_ctx* ctx);
 /* Free the context's grow-only device work buffers: the per-call scratch and the
- * LM-head backward workspace (the softmax cache: 11.2 GB at 16,384 tokens, V =
- * 151,936, H = 4,096; 21.2 GB with PCP_FLAG_EXACT_BF16), which otherwise stay held
+ * LM-head backward workspace (the softmax cache: 11.3 GB at 16,384 tokens, V =
+ * 151,936, H = 4,096; 21.4 GB with PCP_FLAG_EXACT_BF16), which otherwise stay held
  * until pcp_destroy. Synchronises the device first (every stream: calls enqueued with
  * PCP_FLAG_ASYNC may still use the buffers). The next call allocates again. No
  * counterpart in the reference (IREE holds its own device pools). */
@@ -301,7 +301,7 @@ int pcp_grpo_loss_fwd_bwd_noalloc(pcp_ctx* ctx, const pcp_grpo_args* a);
  * normal range) plus 2^-25 * |c| * 2^(m_b - lse) (terms below it; m_b = the largest
  * logit of the entry's 128-entry block): PCP_FLAG_EXACT_BF16 keeps the terms as f32
  * (4 bytes per live token and vocab entry), so each dlogit is the f32 value rounded
- * once. The backward workspace (softmax cache, dlogits^T, weight^T; 11.2 GB at 16,384
+ * once. The backward workspace (softmax cache, dlogits^T, weight^T; 11.3 GB at 16,384
  * tokens, V = 151,936, H = 4,096) is allocated when it fits the budget: at most 64 GiB
  * and at most half of the device memory free at the call plus what the context holds.
  * It stays held until pcp_release_workspace or pcp_destroy; growing it synchronises

@@ -41,7 +41,7 @@ namespace {
 
 constexpr int64_t kDefaultChunk = 16384;
 // Cap on the backward workspace (softmax cache, D^T, W^T; sized for all N tokens) the
-// default path allocates: 11.2 GB at configuration 5 (16,384 tokens, V = 151,936,
+// default path allocates: 11.3 GB at configuration 5 (16,384 tokens, V = 151,936,
 // H = 4,096). 64 GiB holds it up to about 110,000 tokens at that vocabulary.
 constexpr size_t kCacheBudgetCap = size_t{64} << 30;
 
