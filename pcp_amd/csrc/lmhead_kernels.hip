@@ -97,6 +97,31 @@ __device__ __forceinline__ void lm_tile_of(int p, int ntt, int nvt, int group_m,
   tn = q / gm;
 }
 
+// The forward's order while the live hidden rows fit in half of the 256 MB MALL (the
+// token tiles times 256 rows of H bf16 within 128 MiB): groups of two vocab tiles
+// sweep every token tile, so the hidden slabs come back from the MALL and each W slab
+// pair is shared by the XCD's resident tiles. Forward-only launches at H = 4096,
+// interleaved on one box (ms, this order against lm_tile_of's): 10 / 20 / 32 token
+// tiles equal; 38: 18.92-19.04 against 19.11-19.18 (the full step's forward, with the
+// softmax cache and W^T stores, 18.75-18.77 against 19.12-19.16; groups of 1, 3 and
+// 4: 19.04-19.06, 19.78-19.85 and 20.22-20.24 against 19.52-19.55 for 2 on a slower
+// box); 48: 23.58-23.70 against 23.75-24.08; 64: 31.55-31.60 against 31.65-31.69; but
+// 96: 48.50-48.56 against 47.47-48.23 and 128: 65.41-65.50 against 63.30-63.65, where
+// the hidden rows no longer fit.
+constexpr int kLmFwdVocabGroup = 2;
+__device__ __forceinline__ bool lm_fwd_vocab_groups(int ntt, int H) {
+  return static_cast<int64_t>(ntt) * kLmTileT * H * 2 <= (int64_t{128} << 20);
+}
+__device__ __forceinline__ void lm_tile_of_vgroups(int p, int ntt, int nvt, int group_n, int& tm, int& tn) {
+  const int group = group_n * ntt;
+  const int g = p / group;
+  const int first_n = g * group_n;
+  const int gn = min(nvt - first_n, group_n);
+  const int q = p - g * group;
+  tn = first_n + q % gn;
+  tm = q / gn;
+}
+
 // Token tiles per group in the tile order. lm_tile_coords gives each XCD a
 // contiguous eighth of the work items; the forward measured fastest with the
 // smallest group (at least 8 token tiles) whose boundaries fall on those eighths:
@@ -497,7 +522,10 @@ __device__ __forceinline__ void lm_tile16(const LmTileArgs& a, int prod, int p, 
     if (g.kcount) K = min(K, (min(K, *g.kcount) + BK - 1) / BK * BK);
   }
   int tm, tn;
-  lm_tile_of(p, ntt, nvt, gm, tm, tn);
+  if (FWD && lm_fwd_vocab_groups(ntt, K))
+    lm_tile_of_vgroups(p, ntt, nvt, kLmFwdVocabGroup, tm, tn);
+  else
+    lm_tile_of(p, ntt, nvt, gm, tm, tn);
   const int m0 = tm * BT, v0 = (vt0 + tn) * BV;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
